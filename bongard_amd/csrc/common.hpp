@@ -1,0 +1,159 @@
+// Shared device helpers and the C-ABI error plumbing of libbongard_fp8.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/bongard_fp8.h"
+
+namespace bf8 {
+
+// ---- error reporting --------------------------------------------------------------
+void set_error(const char* fmt, ...);
+
+#define BF8_CHECK(cond, ...)            \
+  do {                                  \
+    if (!(cond)) {                      \
+      ::bf8::set_error(__VA_ARGS__);    \
+      return BF8_EINVAL;                \
+    }                                   \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+int launch_status(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- format constants -------------------------------------------------------------
+// OCP e4m3 (fn): max finite 448. OCP e5m2: max finite 57344.
+template <int FMT>
+struct Fp8Max;
+template <>
+struct Fp8Max<BF8_E4M3> {
+  static constexpr float value = 448.0f;
+};
+template <>
+struct Fp8Max<BF8_E5M2> {
+  static constexpr float value = 57344.0f;
+};
+
+inline float fp8_max_host(int fmt) { return fmt == BF8_E4M3 ? 448.0f : 57344.0f; }
+
+// ---- vector memory helpers (device) ----------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte loads/stores with the non-temporal hint (streamed data that is not re-read).
+__device__ __forceinline__ uint4 load_nt(const void* p) {
+  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_nt(void* p, uint4 v) {
+  u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+}
+
+// ---- bit helpers (device) ---------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays NaN (quietened, sign kept).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x0040u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_round(float f) {
+  return __uint_as_float(f32_to_bf16_bits(f) << 16);
+}
+
+// Byte for an fp32 product p = f32(x) * scale that is NaN. It follows torch's CPU
+// result for clamp(x.float() * scale).to(float8): the NaN carries the scale's sign if
+// the scale is NaN, else x's sign if x is NaN, else (inf * 0) the x86 default NaN, which
+// is negative. Both formats encode NaN as 0x7F | sign.
+__device__ __forceinline__ uint32_t nan_byte(float x, float scale) {
+  uint32_t s;
+  if (scale != scale)
+    s = __float_as_uint(scale) >> 31;
+  else if (x != x)
+    s = __float_as_uint(x) >> 31;
+  else
+    s = 1u;
+  return 0x7Fu | (s << 7);
+}
+
+// Saturating RNE conversion of four fp32 values (already multiplied by the scale) to
+// four fp8 bytes packed little-endian. xs are the unscaled inputs (for NaN signs).
+template <int FMT>
+__device__ __forceinline__ uint32_t quant4(float p0, float p1, float p2, float p3, float x0,
+                                           float x1, float x2, float x3, float scale) {
+  constexpr float M = Fp8Max<FMT>::value;
+  float c0 = __builtin_amdgcn_fmed3f(p0, -M, M);
+  float c1 = __builtin_amdgcn_fmed3f(p1, -M, M);
+  float c2 = __builtin_amdgcn_fmed3f(p2, -M, M);
+  float c3 = __builtin_amdgcn_fmed3f(p3, -M, M);
+  uint32_t w;
+  if constexpr (FMT == BF8_E4M3) {
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c2, c3, w, true);
+  } else {
+    w = __builtin_amdgcn_cvt_pk_bf8_f32(c0, c1, 0, false);
+    w = __builtin_amdgcn_cvt_pk_bf8_f32(c2, c3, w, true);
+  }
+  // NaN products are rare: patch them bytewise.
+  if (__builtin_expect((p0 != p0) | (p1 != p1) | (p2 != p2) | (p3 != p3), 0)) {
+    if (p0 != p0) w = (w & 0xFFFFFF00u) | nan_byte(x0, scale);
+    if (p1 != p1) w = (w & 0xFFFF00FFu) | (nan_byte(x1, scale) << 8);
+    if (p2 != p2) w = (w & 0xFF00FFFFu) | (nan_byte(x2, scale) << 16);
+    if (p3 != p3) w = (w & 0x00FFFFFFu) | (nan_byte(x3, scale) << 24);
+  }
+  return w;
+}
+
+// Quantize 8 bf16 values (two packed per uint32) to 8 fp8 bytes (two uint32).
+template <int FMT>
+__device__ __forceinline__ uint2 quant8_bf16(uint4 v, float scale) {
+  float x0 = bf16_lo(v.x), x1 = bf16_hi(v.x), x2 = bf16_lo(v.y), x3 = bf16_hi(v.y);
+  float x4 = bf16_lo(v.z), x5 = bf16_hi(v.z), x6 = bf16_lo(v.w), x7 = bf16_hi(v.w);
+  uint2 r;
+  r.x = quant4<FMT>(x0 * scale, x1 * scale, x2 * scale, x3 * scale, x0, x1, x2, x3, scale);
+  r.y = quant4<FMT>(x4 * scale, x5 * scale, x6 * scale, x7 * scale, x4, x5, x6, x7, scale);
+  return r;
+}
+
+// Max of |bf16| over the 8 values of v, as an fp32 bit pattern key: for non-negative
+// floats the unsigned order of the bits is the numeric order, and NaN keys sort above
+// +inf (as torch's NaN-propagating max does).
+__device__ __forceinline__ uint32_t absmax_key8(uint4 v) {
+  uint32_t a = v.x & 0x7FFF7FFFu, b = v.y & 0x7FFF7FFFu;
+  uint32_t c = v.z & 0x7FFF7FFFu, d = v.w & 0x7FFF7FFFu;
+  uint32_t m0 = max(max(a & 0xFFFFu, a >> 16), max(b & 0xFFFFu, b >> 16));
+  uint32_t m1 = max(max(c & 0xFFFFu, c >> 16), max(d & 0xFFFFu, d >> 16));
+  return max(m0, m1) << 16;
+}
+
+// Wavefront (64-lane) max reduction.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  return v;
+}
+
+// Block max reduction for blockDim.x == NT (multiple of 64). Result valid in all threads.
+template <int NT>
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v) {
+  __shared__ uint32_t red[NT / 64];
+  v = wave_max_u32(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) r = max(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
+}  // namespace bf8

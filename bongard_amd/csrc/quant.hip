@@ -1,0 +1,339 @@
+// Per-tensor amax, scale and saturating bf16 -> fp8 cast kernels for gfx950.
+//
+// Arithmetic follows torchao's tensorwise current scaling (tensor_to_amax,
+// amax_to_scale, to_fp8_saturated) as reached from bongard/float8_training.py:22 and
+// TE Float8CurrentScaling (bongard/te_linear.py:38-39,73-74): amax = max|x| (exact for
+// bf16), scale = fp32(fp8_max / clamp(f64(amax), 1e-12)), q = fp8_rne(clamp(f32(x) *
+// scale, +-fp8_max)).
+//
+// All kernels are HBM-bound streaming passes: 16-byte vector loads, several loads in
+// flight per lane, non-temporal hints on data that is not re-read.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "common.hpp"
+
+namespace bf8 {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return BF8_ELAUNCH;
+  }
+  return BF8_OK;
+}
+
+namespace {
+
+constexpr int kNT = 256;            // threads per block for streaming kernels
+constexpr int kVecPerThread = 4;    // 16-byte vectors per lane per iteration
+constexpr int64_t kMaxAmaxBlocks = 2048;
+
+int64_t amax_blocks(int64_t n) {
+  int64_t per_block = (int64_t)kNT * kVecPerThread * 8;  // bf16 elements per block pass
+  int64_t b = (n + per_block - 1) / per_block;
+  if (b < 1) b = 1;
+  return b < kMaxAmaxBlocks ? b : kMaxAmaxBlocks;
+}
+
+// partials[b] = max over block b's grid-stride share of |x| keys.
+__global__ __launch_bounds__(kNT) void amax_partials_kernel(const uint16_t* __restrict__ x,
+                                                            int64_t n,
+                                                            uint32_t* __restrict__ partials) {
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  const int64_t nvec = n >> 3;
+  const int64_t stride = (int64_t)gridDim.x * kNT;
+  uint32_t m = 0;
+  int64_t i = (int64_t)blockIdx.x * kNT + threadIdx.x;
+  for (; i + 3 * stride < nvec; i += 4 * stride) {
+    uint4 v0 = load_nt(xv + i);
+    uint4 v1 = load_nt(xv + i + stride);
+    uint4 v2 = load_nt(xv + i + 2 * stride);
+    uint4 v3 = load_nt(xv + i + 3 * stride);
+    m = max(m, max(max(absmax_key8(v0), absmax_key8(v1)), max(absmax_key8(v2), absmax_key8(v3))));
+  }
+  for (; i < nvec; i += stride) m = max(m, absmax_key8(load_nt(xv + i)));
+  // scalar tail (n % 8), handled by block 0
+  if (blockIdx.x == 0) {
+    for (int64_t j = (nvec << 3) + threadIdx.x; j < n; j += kNT)
+      m = max(m, (uint32_t)(x[j] & 0x7FFFu) << 16);
+  }
+  m = block_max_u32<kNT>(m);
+  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
+__device__ void write_meta_from_amax(uint32_t key, float fp8_max, float* meta) {
+  const float amax = __uint_as_float(key);
+  float scale, scale_inv;
+  if (amax != amax) {
+    // torch: clamp(NaN) is NaN; fp8_max / NaN returns that NaN (quietened).
+    scale = __uint_as_float(key | 0x00400000u);
+    scale_inv = scale;
+  } else {
+    double a = (double)amax;
+    if (a < 1e-12) a = 1e-12;
+    // f64 division is correctly rounded; rounding it to fp32 equals the correctly
+    // rounded fp32 quotient (53 >= 2 * 24 + 2).
+    scale = (float)((double)fp8_max / a);
+    scale_inv = (float)(1.0 / (double)scale);
+  }
+  meta[0] = amax;
+  meta[1] = scale;
+  meta[2] = scale_inv;
+  meta[3] = 0.0f;
+}
+
+__global__ __launch_bounds__(kNT) void scale_from_partials_kernel(
+    const uint32_t* __restrict__ partials, int64_t np, float fp8_max, float* __restrict__ meta) {
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < np; i += kNT) m = max(m, partials[i]);
+  m = block_max_u32<kNT>(m);
+  if (threadIdx.x == 0) write_meta_from_amax(m, fp8_max, meta);
+}
+
+// Row-major cast: each lane converts 16 consecutive bf16 (two 16-byte loads) into one
+// 16-byte store. n16 = number of 16-element groups; the n % 16 tail is done bytewise.
+template <int FMT>
+__global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ x, int64_t n,
+                                                   const float* __restrict__ scale_ptr,
+                                                   uint8_t* __restrict__ out) {
+  const float scale = *scale_ptr;
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  uint4* ov = reinterpret_cast<uint4*>(out);
+  const int64_t n16 = n >> 4;
+  const int64_t stride = (int64_t)gridDim.x * kNT;
+  int64_t i = (int64_t)blockIdx.x * kNT + threadIdx.x;
+  for (; i + stride < n16; i += 2 * stride) {
+    uint4 a0 = load_nt(xv + 2 * i);
+    uint4 a1 = load_nt(xv + 2 * i + 1);
+    uint4 b0 = load_nt(xv + 2 * (i + stride));
+    uint4 b1 = load_nt(xv + 2 * (i + stride) + 1);
+    uint2 qa0 = quant8_bf16<FMT>(a0, scale), qa1 = quant8_bf16<FMT>(a1, scale);
+    uint2 qb0 = quant8_bf16<FMT>(b0, scale), qb1 = quant8_bf16<FMT>(b1, scale);
+    store_nt(ov + i, make_uint4(qa0.x, qa0.y, qa1.x, qa1.y));
+    store_nt(ov + i + stride, make_uint4(qb0.x, qb0.y, qb1.x, qb1.y));
+  }
+  for (; i < n16; i += stride) {
+    uint4 a0 = load_nt(xv + 2 * i);
+    uint4 a1 = load_nt(xv + 2 * i + 1);
+    uint2 qa0 = quant8_bf16<FMT>(a0, scale), qa1 = quant8_bf16<FMT>(a1, scale);
+    store_nt(ov + i, make_uint4(qa0.x, qa0.y, qa1.x, qa1.y));
+  }
+  if (blockIdx.x == 0) {
+    for (int64_t j = (n16 << 4) + threadIdx.x; j < n; j += kNT) {
+      float xf = __uint_as_float((uint32_t)x[j] << 16);
+      float p = xf * scale;
+      out[j] = (uint8_t)(quant4<FMT>(p, 0.f, 0.f, 0.f, xf, 0.f, 0.f, 0.f, scale) & 0xFFu);
+    }
+  }
+}
+
+// Cast with a transposed copy. One block handles a 64 x 64 tile of x:
+//  - each lane loads 16 bf16 of one row (4 lanes cover a 128-byte row segment),
+//    quantizes, stores 16 bytes of `out` (if requested) and stages the bytes in LDS;
+//  - after a barrier each lane gathers 16 bytes of one tile column and stores them as a
+//    16-byte row segment of out_t.
+// rows and cols need not be multiples of 64; cols % 16 == 0.
+constexpr int kTT = 64;
+constexpr int kTPitch = kTT + 4;  // LDS row pitch (bytes), staggers banks for the gather
+
+template <int FMT>
+__global__ __launch_bounds__(kNT) void cast_transpose_kernel(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols,
+    const float* __restrict__ scale_ptr, uint8_t* __restrict__ out,
+    uint8_t* __restrict__ out_t) {
+  __shared__ uint32_t tile[kTT * kTPitch / 4];
+  uint8_t* tb = reinterpret_cast<uint8_t*>(tile);
+  const float scale = *scale_ptr;
+  const int64_t r0 = (int64_t)blockIdx.y * kTT, c0 = (int64_t)blockIdx.x * kTT;
+  const int t = threadIdx.x;
+  {
+    const int lr = t >> 2, lc = (t & 3) * 16;
+    const int64_t r = r0 + lr, c = c0 + lc;
+    uint32_t q[4] = {0u, 0u, 0u, 0u};
+    if (r < rows && c < cols) {
+      const uint4* src = reinterpret_cast<const uint4*>(x + r * cols + c);
+      uint4 a0 = load_nt(src);
+      uint4 a1 = load_nt(src + 1);
+      uint2 q0 = quant8_bf16<FMT>(a0, scale), q1 = quant8_bf16<FMT>(a1, scale);
+      q[0] = q0.x; q[1] = q0.y; q[2] = q1.x; q[3] = q1.y;
+      if (out) *reinterpret_cast<uint4*>(out + r * cols + c) = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(tb + lr * kTPitch + lc);
+    dst[0] = q[0]; dst[1] = q[1]; dst[2] = q[2]; dst[3] = q[3];
+  }
+  __syncthreads();
+  {
+    const int oc = t >> 2, orow = (t & 3) * 16;  // out_t row = tile column oc
+    const int64_t tr = c0 + oc, tc = r0 + orow;  // position in out_t [cols, rows]
+    if (tr < cols && tc < rows) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t b0 = tb[(orow + 4 * j + 0) * kTPitch + oc];
+        uint32_t b1 = tb[(orow + 4 * j + 1) * kTPitch + oc];
+        uint32_t b2 = tb[(orow + 4 * j + 2) * kTPitch + oc];
+        uint32_t b3 = tb[(orow + 4 * j + 3) * kTPitch + oc];
+        w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+      }
+      uint8_t* dst = out_t + tr * rows + tc;
+      if (tc + 16 <= rows && (rows & 15) == 0) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+        for (int j = 0; j < 16 && tc + j < rows; ++j) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+      }
+    }
+  }
+}
+
+// ---- delayed scaling ------------------------------------------------------------------
+// state layout: history[len], then meta {amax_last, scale, scale_inv, pos}; a fresh
+// state is zero except scale = scale_inv = 1. The new scale is fp8_max / max(history)
+// when that maximum is finite and positive, else the previous scale is kept (TE's
+// default scaling-factor update with margin 0).
+__global__ void delayed_begin_kernel(float* state, int len, float fp8_max) {
+  if (threadIdx.x != 0) return;
+  float h = 0.0f;
+  bool finite = true;
+  for (int i = 0; i < len; ++i) {
+    float v = state[i];
+    finite &= (v == v) && (fabsf(v) != INFINITY);
+    h = fmaxf(h, v);
+  }
+  float* meta = state + len;
+  if (finite && h > 0.0f) {
+    const float scale = (float)((double)fp8_max / (double)h);
+    meta[1] = scale;
+    meta[2] = (float)(1.0 / (double)scale);
+  }
+}
+
+__global__ __launch_bounds__(kNT) void delayed_end_kernel(float* state, int len,
+                                                          const uint32_t* __restrict__ partials,
+                                                          int64_t np) {
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < np; i += kNT) m = max(m, partials[i]);
+  m = block_max_u32<kNT>(m);
+  if (threadIdx.x == 0) {
+    float* meta = state + len;
+    int pos = (int)meta[3];
+    if (pos < 0 || pos >= len) pos = 0;
+    const float amax = __uint_as_float(m);
+    state[pos] = amax;
+    meta[0] = amax;
+    meta[3] = (float)((pos + 1) % len);
+  }
+}
+
+int grid_for_stream(int64_t work_items, int64_t per_block, int64_t cap) {
+  int64_t b = (work_items + per_block - 1) / per_block;
+  if (b < 1) b = 1;
+  return (int)(b < cap ? b : cap);
+}
+
+}  // namespace
+}  // namespace bf8
+
+using namespace bf8;
+
+extern "C" {
+
+const char* bf8_last_error(void) { return bf8::g_err; }
+int bf8_abi_version(void) { return 1; }
+
+int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
+
+int bf8_amax_bf16(const void* x, int64_t n, uint32_t* partials, void* stream) {
+  BF8_CHECK(n >= 0, "bf8_amax_bf16: n < 0");
+  BF8_CHECK(partials != nullptr, "bf8_amax_bf16: partials is NULL");
+  BF8_CHECK(n == 0 || x != nullptr, "bf8_amax_bf16: x is NULL");
+  BF8_CHECK(((uintptr_t)x & 15) == 0, "bf8_amax_bf16: x must be 16-byte aligned");
+  const int64_t nb = amax_blocks(n);
+  hipLaunchKernelGGL(amax_partials_kernel, dim3((unsigned)nb), dim3(kNT), 0, as_stream(stream),
+                     (const uint16_t*)x, n, partials);
+  return launch_status("amax_partials_kernel");
+}
+
+int bf8_scale_from_partials(const uint32_t* partials, int64_t n_partials, int fmt, float* meta,
+                            void* stream) {
+  BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "bf8_scale_from_partials: bad fmt %d", fmt);
+  BF8_CHECK(partials && meta, "bf8_scale_from_partials: NULL pointer");
+  BF8_CHECK(n_partials >= 1, "bf8_scale_from_partials: n_partials < 1");
+  hipLaunchKernelGGL(scale_from_partials_kernel, dim3(1), dim3(kNT), 0, as_stream(stream),
+                     partials, n_partials, fp8_max_host(fmt), meta);
+  return launch_status("scale_from_partials_kernel");
+}
+
+int bf8_cast_bf16(const void* x, int64_t rows, int64_t cols, const float* scale, int fmt,
+                  uint8_t* out, uint8_t* out_t, void* stream) {
+  BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "bf8_cast_bf16: bad fmt %d", fmt);
+  BF8_CHECK(rows >= 0 && cols >= 0, "bf8_cast_bf16: negative shape");
+  BF8_CHECK(scale != nullptr, "bf8_cast_bf16: scale is NULL");
+  BF8_CHECK(out || out_t, "bf8_cast_bf16: out and out_t are both NULL");
+  BF8_CHECK(((uintptr_t)x & 15) == 0 && (!out || ((uintptr_t)out & 15) == 0),
+            "bf8_cast_bf16: x and out must be 16-byte aligned");
+  const int64_t n = rows * cols;
+  if (n == 0) return BF8_OK;
+  hipStream_t s = as_stream(stream);
+  if (out_t == nullptr) {
+    const int grid = grid_for_stream((n + 15) / 16, 2 * kNT, 8192);
+    if (fmt == BF8_E4M3)
+      hipLaunchKernelGGL(cast_kernel<BF8_E4M3>, dim3(grid), dim3(kNT), 0, s, (const uint16_t*)x, n, scale, out);
+    else
+      hipLaunchKernelGGL(cast_kernel<BF8_E5M2>, dim3(grid), dim3(kNT), 0, s, (const uint16_t*)x, n, scale, out);
+    return launch_status("cast_kernel");
+  }
+  BF8_CHECK(cols % 16 == 0, "bf8_cast_bf16: transposed cast needs cols %% 16 == 0 (got %lld)",
+            (long long)cols);
+  BF8_CHECK(((uintptr_t)out_t & 15) == 0, "bf8_cast_bf16: out_t must be 16-byte aligned");
+  BF8_CHECK((cols + kTT - 1) / kTT < (1LL << 31) && (rows + kTT - 1) / kTT < 65536,
+            "bf8_cast_bf16: shape too large for the transposed cast grid");
+  dim3 grid((unsigned)((cols + kTT - 1) / kTT), (unsigned)((rows + kTT - 1) / kTT));
+  if (fmt == BF8_E4M3)
+    hipLaunchKernelGGL(cast_transpose_kernel<BF8_E4M3>, grid, dim3(kNT), 0, s, (const uint16_t*)x, rows, cols, scale, out, out_t);
+  else
+    hipLaunchKernelGGL(cast_transpose_kernel<BF8_E5M2>, grid, dim3(kNT), 0, s, (const uint16_t*)x, rows, cols, scale, out, out_t);
+  return launch_status("cast_transpose_kernel");
+}
+
+int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
+                      uint8_t* out_t, float* meta, uint32_t* partials, void* stream) {
+  BF8_CHECK(rows >= 0 && cols >= 0, "bf8_quantize_bf16: negative shape");
+  const int64_t n = rows * cols;
+  int rc = bf8_amax_bf16(x, n, partials, stream);
+  if (rc) return rc;
+  rc = bf8_scale_from_partials(partials, amax_blocks(n), fmt, meta, stream);
+  if (rc) return rc;
+  return bf8_cast_bf16(x, rows, cols, meta + 1, fmt, out, out_t, stream);
+}
+
+int bf8_delayed_scale_begin(float* state, int len, int fmt, void* stream) {
+  BF8_CHECK(state && len >= 1 && len <= 1024, "bf8_delayed_scale_begin: bad state/len");
+  BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "bf8_delayed_scale_begin: bad fmt %d", fmt);
+  hipLaunchKernelGGL(delayed_begin_kernel, dim3(1), dim3(64), 0, as_stream(stream), state, len,
+                     fp8_max_host(fmt));
+  return launch_status("delayed_begin_kernel");
+}
+
+int bf8_delayed_scale_end(float* state, int len, const uint32_t* partials, int64_t n_partials,
+                          void* stream) {
+  BF8_CHECK(state && len >= 1 && len <= 1024, "bf8_delayed_scale_end: bad state/len");
+  BF8_CHECK(partials && n_partials >= 1, "bf8_delayed_scale_end: bad partials");
+  hipLaunchKernelGGL(delayed_end_kernel, dim3(1), dim3(kNT), 0, as_stream(stream), state, len,
+                     partials, n_partials);
+  return launch_status("delayed_end_kernel");
+}
+
+}  // extern "C"

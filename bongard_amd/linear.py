@@ -1,0 +1,171 @@
+"""FP8 linear and gated-MLP autograd functions on the gfx950 kernels.
+
+Forward: X and W are quantized to e4m3 with per-tensor current scaling, the GEMM runs on
+the FP8 MFMA with fp32 accumulation and a dequant epilogue, output bf16.
+Backward (torchao tensorwise / TE Float8CurrentScaling "HYBRID" formats): grad_out is
+quantized to e5m2 with its own per-tensor scale;
+  dgrad  dX = dY8 . W8          (TN GEMM against W8's transposed copy)
+  wgrad  dW = dY8^T . X8        (TN GEMM on the transposed copies of dY8 and X8)
+The transposed copies come from the same cast kernels (LDS-staged transpose), so each
+operand is read from HBM once per quantization.
+
+Reference behaviour these replace: torchao Float8Linear.forward/backward reached from
+bongard/float8_training.py:16-22, te.Linear under TELinear.forward
+(bongard/te_linear.py:59-77), and TEMLP/FusedMLP (bongard/te_linear.py:98-103,
+bongard/fused_mlp.py:62-79).
+"""
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import ops
+from .ops import E4M3, E5M2
+
+
+@dataclass
+class QuantizedWeight:
+    """Cached FP8 copy of a weight: rowwise [N, K], transposed [K, N], meta."""
+
+    q: ops.Fp8Tensor
+    version: int
+
+
+def quantize_weight(weight, *, transpose=True):
+    return ops.quantize(weight.detach(), E4M3, rowwise=True, transpose=transpose)
+
+
+class Fp8LinearFunction(torch.autograd.Function):
+    """y = x @ W^T (+ b) in FP8; x: bf16 [M, K] with M % 16 == 0 when grads are needed."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, wq):
+        need_dx = ctx.needs_input_grad[0]
+        need_dw = ctx.needs_input_grad[1]
+        xq = ops.quantize(x, E4M3, rowwise=True, transpose=need_dw)
+        if wq is None:
+            wq = quantize_weight(weight, transpose=need_dx)
+        y = ops.gemm(xq.data, E4M3, xq.meta, wq.data, E4M3, wq.meta, bias=bias)
+        ctx.has_bias = bias is not None
+        ctx.save_for_backward(xq.data_t if need_dw else None, xq.meta,
+                              wq.data_t if need_dx else None, wq.meta)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x8t, x_meta, w8t, w_meta = ctx.saved_tensors
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dy = dy.contiguous()
+        dyq = ops.quantize(dy, E5M2, rowwise=need_dx, transpose=need_dw)
+        dx = dw = db = None
+        if need_dx:
+            dx = ops.gemm(dyq.data, E5M2, dyq.meta, w8t, E4M3, w_meta)
+        if need_dw:
+            dw = ops.gemm(dyq.data_t, E5M2, dyq.meta, x8t, E4M3, x_meta)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = dy.sum(0)
+        return dx, dw, db, None
+
+
+class Fp8GegluMlpFunction(torch.autograd.Function):
+    """y = down(gelu_tanh(x Wg^T) * (x Wu^T)) with every GEMM in FP8.
+
+    w_gu: bf16 [2I, K] (gate rows then up rows), w_down: bf16 [K_out, I]. ``gu_q`` and
+    ``down_q`` are optional cached quantized weights. ``split_scales`` selects one scale
+    per gate/up half (torchao / split TE) instead of one shared scale (fused TE gate_up).
+    """
+
+    @staticmethod
+    def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate, split_scales):
+        I = int(intermediate)
+        train = any(ctx.needs_input_grad[:3])
+        xq = ops.quantize(x, E4M3, rowwise=True, transpose=ctx.needs_input_grad[1])
+        if gu_q is None:
+            gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=ctx.needs_input_grad[0])
+        stride = 4 if split_scales else 0
+        H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
+                                       w_meta_stride=stride, keep_gu=train)
+        h_meta = ops.scale_from_partials(hparts, E4M3)
+        hq = ops.cast(H, h_meta, E4M3, rowwise=True, transpose=ctx.needs_input_grad[2])
+        if down_q is None:
+            down_q = quantize_weight(
+                w_down, transpose=ctx.needs_input_grad[0] or ctx.needs_input_grad[1])
+        y = ops.gemm(hq.data, E4M3, h_meta, down_q.data, E4M3, down_q.meta)
+        ctx.intermediate = I
+        ctx.split_scales = split_scales
+        ctx.save_for_backward(GU, xq.data_t, xq.meta, hq.data_t, h_meta, gu_q.data_t,
+                              gu_q.meta, down_q.data_t, down_q.meta)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (GU, x8t, x_meta, h8t, h_meta, gu8t, gu_meta, d8t, d_meta) = ctx.saved_tensors
+        I = ctx.intermediate
+        need_dx, need_dgu, need_dd = ctx.needs_input_grad[:3]
+        dy = dy.contiguous()
+        dyq = ops.quantize(dy, E5M2, rowwise=True, transpose=need_dd)
+        dx = dgu = dd = None
+        if need_dd:
+            dd = ops.gemm(dyq.data_t, E5M2, dyq.meta, h8t, E4M3, h_meta)
+        if not (need_dx or need_dgu):
+            return dx, dgu, dd, None, None, None, None
+        dH = ops.gemm(dyq.data, E5M2, dyq.meta, d8t, E4M3, d_meta)
+        dGU, parts = ops.geglu_bwd(dH, GU)
+        if not ctx.split_scales:
+            g_meta = ops.scale_from_partials(parts, E5M2)
+            dq = ops.cast(dGU, g_meta, E5M2, rowwise=need_dx, transpose=need_dgu)
+            if need_dx:
+                dx = ops.gemm(dq.data, E5M2, g_meta, gu8t, E4M3, gu_meta[0])
+            if need_dgu:
+                dgu = ops.gemm(dq.data_t, E5M2, g_meta, x8t, E4M3, x_meta)
+        else:
+            # Separate gate/up projections: each gradient has its own e5m2 scale and its
+            # own dgrad GEMM; the input gradient is their bf16 sum (autograd of x used twice).
+            dx_parts, dw_parts = [], []
+            for half in range(2):
+                d_half = dGU[:, half * I:(half + 1) * I].contiguous()
+                dq = ops.quantize(d_half, E5M2, rowwise=need_dx, transpose=need_dgu)
+                if need_dx:
+                    dx_parts.append(ops.gemm(dq.data, E5M2, dq.meta,
+                                             gu8t[:, half * I:(half + 1) * I], E4M3,
+                                             gu_meta[half]))
+                if need_dgu:
+                    dw_parts.append(ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta))
+            if need_dx:
+                dx = dx_parts[0] + dx_parts[1]
+            if need_dgu:
+                dgu = torch.cat(dw_parts, 0)
+        return dx, dgu, dd, None, None, None, None
+
+
+def quantize_gate_up(w_gu, intermediate, split_scales, *, transpose=True):
+    """Quantize [W_gate; W_up] into one [2I, K] fp8 buffer (+ [K, 2I] transposed copy).
+
+    split_scales: gate and up halves get separate metas (meta is then [2, 4]).
+    """
+    I = int(intermediate)
+    if not split_scales:
+        q = ops.quantize(w_gu.detach(), E4M3, rowwise=True, transpose=transpose)
+        return _GateUp(q.data, q.data_t, q.meta.view(1, 4))
+    K = w_gu.shape[1]
+    dev = w_gu.device
+    data = torch.empty((2 * I, K), dtype=torch.float8_e4m3fn, device=dev)
+    meta = ops.new_meta(dev, 2)
+    halves_t = []
+    for half in range(2):
+        part = w_gu.detach()[half * I:(half + 1) * I]
+        q = ops.quantize(part, E4M3, rowwise=True, transpose=transpose, meta=meta[half],
+                         out=data[half * I:(half + 1) * I])
+        halves_t.append(q.data_t)
+    data_t = torch.cat(halves_t, 1) if transpose else None
+    return _GateUp(data, data_t, meta)
+
+
+@dataclass
+class _GateUp:
+    """Quantized gate/up weight: data [2I, K], data_t [K, 2I], meta [1 or 2, 4]."""
+
+    data: torch.Tensor
+    data_t: Optional[torch.Tensor]
+    meta: torch.Tensor

@@ -1,0 +1,242 @@
+"""Tensor-level FP8 ops on top of libbongard_fp8.so (gfx950 HIP kernels).
+
+Every op runs on the caller's current HIP stream, allocates its outputs with PyTorch's
+caching allocator, and never synchronises with the host. Inputs must be CUDA (HIP)
+tensors; there is no CPU path.
+
+Quantized tensors are returned as :class:`Fp8Tensor`: fp8 payload(s) plus a 4-float
+device "meta" record ``{amax, scale, scale_inv, 0}`` with
+``scale = fp32(fp8_max / max(f64(amax), 1e-12))`` and ``q = fp8(clamp(x * scale))``,
+the semantics of torchao's tensorwise recipe (tensor_to_amax / amax_to_scale /
+to_fp8_saturated) behind bongard/float8_training.py:22 and of TE's
+Float8CurrentScaling behind bongard/te_linear.py:38-39,73-74.
+"""
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+E4M3 = 0
+E5M2 = 1
+FP8_MAX = {E4M3: 448.0, E5M2: 57344.0}
+TORCH_FP8 = {E4M3: torch.float8_e4m3fn, E5M2: torch.float8_e5m2}
+OUT_BF16 = 0
+OUT_F32 = 1
+
+
+@dataclass
+class Fp8Tensor:
+    """A per-tensor-scaled FP8 tensor: ``data`` [rows, cols] and/or ``data_t`` [cols, rows]."""
+
+    data: Optional[torch.Tensor]
+    data_t: Optional[torch.Tensor]
+    meta: torch.Tensor  # float32 [4] (or a view into a larger buffer)
+    fmt: int
+    rows: int
+    cols: int
+
+    @property
+    def scale(self):
+        return self.meta[1]
+
+    @property
+    def scale_inv(self):
+        return self.meta[2]
+
+    @property
+    def amax(self):
+        return self.meta[0]
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("bongard_amd FP8 ops need tensors on the HIP device (no CPU path)")
+
+
+def _bf16_2d(x):
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"expected a bfloat16 tensor, got {x.dtype}")
+    if x.dim() != 2:
+        x = x.reshape(-1, x.shape[-1])
+    if not x.is_contiguous():
+        x = x.contiguous()
+    return x
+
+
+def amax_partials_count(n):
+    return int(_lib.lib().bf8_amax_partials(int(n)))
+
+
+def new_meta(device, count=1):
+    """Zeroed meta record(s): float32 [count, 4] (or [4] when count == 1)."""
+    m = torch.zeros((count, 4) if count > 1 else (4,), dtype=torch.float32, device=device)
+    return m
+
+
+def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None, out_t=None):
+    """Current-scaling quantization of a bf16 tensor (flattened to 2-D [rows, cols]).
+
+    Returns an :class:`Fp8Tensor` whose ``data`` is [rows, cols] (if ``rowwise``) and
+    ``data_t`` [cols, rows] (if ``transpose``), both as torch float8 tensors.
+    """
+    _require_gpu(x)
+    x = _bf16_2d(x)
+    rows, cols = x.shape
+    dev = x.device
+    if meta is None:
+        meta = new_meta(dev)
+    if rowwise and out is None:
+        out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=dev)
+    if transpose and out_t is None:
+        out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=dev)
+    partials = torch.empty(amax_partials_count(rows * cols), dtype=torch.int32, device=dev)
+    L = _lib.lib()
+    _lib.check(L.bf8_quantize_bf16(_ptr(x), rows, cols, fmt, _ptr(out if rowwise else None),
+                                   _ptr(out_t if transpose else None), _ptr(meta),
+                                   _ptr(partials), _stream(dev)), "bf8_quantize_bf16")
+    return Fp8Tensor(out if rowwise else None, out_t if transpose else None, meta, fmt, rows, cols)
+
+
+def amax(x):
+    """Per-block partial amax keys (int32 view of fp32 bits) of a bf16 tensor."""
+    _require_gpu(x)
+    x = _bf16_2d(x)
+    partials = torch.empty(amax_partials_count(x.numel()), dtype=torch.int32, device=x.device)
+    _lib.check(_lib.lib().bf8_amax_bf16(_ptr(x), x.numel(), _ptr(partials), _stream(x.device)),
+               "bf8_amax_bf16")
+    return partials
+
+
+def scale_from_partials(partials, fmt, meta=None):
+    if meta is None:
+        meta = new_meta(partials.device)
+    _lib.check(_lib.lib().bf8_scale_from_partials(_ptr(partials), partials.numel(), fmt,
+                                                  _ptr(meta), _stream(partials.device)),
+               "bf8_scale_from_partials")
+    return meta
+
+
+def cast(x, meta, fmt=E4M3, *, rowwise=True, transpose=False, out=None, out_t=None):
+    """Cast with an existing scale (``meta[1]``), e.g. delayed scaling."""
+    _require_gpu(x, meta)
+    x = _bf16_2d(x)
+    rows, cols = x.shape
+    if rowwise and out is None:
+        out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=x.device)
+    if transpose and out_t is None:
+        out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=x.device)
+    scale_ptr = ctypes.c_void_p(meta.data_ptr() + 4)
+    _lib.check(_lib.lib().bf8_cast_bf16(_ptr(x), rows, cols, scale_ptr, fmt,
+                                        _ptr(out if rowwise else None),
+                                        _ptr(out_t if transpose else None), _stream(x.device)),
+               "bf8_cast_bf16")
+    return Fp8Tensor(out if rowwise else None, out_t if transpose else None, meta, fmt, rows, cols)
+
+
+def _sinv_ptr(meta):
+    return ctypes.c_void_p(meta.data_ptr() + 8)
+
+
+def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=None,
+         seg_ends: Optional[Sequence[int]] = None, b_meta_stride=4, out=None):
+    """``C = (a @ b.T) * a_scale_inv * b_scale_inv (+ bias)`` on fp8 operands.
+
+    a: fp8 [M, K], b: fp8 [N, K] (row-major, K contiguous). ``b_meta`` is the meta of b,
+    or for ``seg_ends`` (fused projections) the first of ``len(seg_ends)`` meta records
+    ``b_meta_stride`` floats apart.
+    """
+    _require_gpu(a, b, a_meta, b_meta)
+    M, K = a.shape
+    N, Kb = b.shape
+    if K != Kb:
+        raise ValueError(f"gemm: inner dims differ ({K} vs {Kb})")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("gemm: out_dtype must be bfloat16 or float32")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    n_seg = 1
+    seg = None
+    if seg_ends is not None:
+        n_seg = len(seg_ends)
+        seg = (ctypes.c_int64 * n_seg)(*[int(s) for s in seg_ends])
+    if bias is not None:
+        if bias.dtype != torch.bfloat16:
+            raise TypeError("gemm: bias must be bfloat16")
+        bias = bias.contiguous()
+    L = _lib.lib()
+    ws_bytes = int(L.bf8_gemm_workspace(M, N, K))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
+    _lib.check(L.bf8_gemm(_ptr(a), a_fmt, a.stride(0), _ptr(b), b_fmt, b.stride(0), M, N, K,
+                          _sinv_ptr(a_meta), _sinv_ptr(b_meta), b_meta_stride, seg, n_seg,
+                          _ptr(bias), _ptr(out), OUT_BF16 if out_dtype == torch.bfloat16 else OUT_F32,
+                          out.stride(0), _ptr(ws), ws_bytes, _stream(a.device)), "bf8_gemm")
+    return out
+
+
+def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu=False):
+    """Gate/up GEMM with the gated-GELU epilogue.
+
+    x8: fp8 e4m3 [M, K]; w8: fp8 e4m3 [2I, K] (gate rows then up rows). Returns
+    ``(H bf16 [M, I], GU bf16 [M, 2I] or None, h_partials int32)``.
+    """
+    _require_gpu(x8, w8, x_meta, w_meta)
+    M, K = x8.shape
+    I = int(intermediate)
+    if w8.shape != (2 * I, K):
+        raise ValueError(f"gemm_geglu: weight must be [{2 * I}, {K}], got {tuple(w8.shape)}")
+    L = _lib.lib()
+    H = torch.empty((M, I), dtype=torch.bfloat16, device=x8.device)
+    GU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=x8.device) if keep_gu else None
+    parts = torch.empty(int(L.bf8_geglu_partials(M, I)), dtype=torch.int32, device=x8.device)
+    _lib.check(L.bf8_gemm_geglu(_ptr(x8), x8.stride(0), _ptr(w8), w8.stride(0), M, I, K,
+                                _sinv_ptr(x_meta), _sinv_ptr(w_meta), w_meta_stride, _ptr(H),
+                                H.stride(0), _ptr(GU), _ptr(parts), _stream(x8.device)),
+               "bf8_gemm_geglu")
+    return H, GU, parts
+
+
+def geglu_bwd(dH, GU):
+    """dGU bf16 [M, 2I] (d_gate | d_up) from dH [M, I] and the forward's GU; + amax partials."""
+    _require_gpu(dH, GU)
+    dH = dH.contiguous()
+    M, I = dH.shape
+    L = _lib.lib()
+    dGU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=dH.device)
+    parts = torch.empty(int(L.bf8_geglu_bwd_partials(M, I)), dtype=torch.int32, device=dH.device)
+    _lib.check(L.bf8_geglu_bwd(_ptr(dH), _ptr(GU), M, I, _ptr(dGU), _ptr(parts),
+                               _stream(dH.device)), "bf8_geglu_bwd")
+    return dGU, parts
+
+
+def new_delayed_state(length, device):
+    """Delayed-scaling state: float32 [length + 4] = history, {amax, scale, scale_inv, pos}."""
+    st = torch.zeros(length + 4, dtype=torch.float32, device=device)
+    st[length + 1] = 1.0
+    st[length + 2] = 1.0
+    return st
+
+
+def delayed_scale_begin(state, length, fmt):
+    _lib.check(_lib.lib().bf8_delayed_scale_begin(_ptr(state), length, fmt,
+                                                  _stream(state.device)),
+               "bf8_delayed_scale_begin")
+    return state[length:length + 4]
+
+
+def delayed_scale_end(state, length, partials):
+    _lib.check(_lib.lib().bf8_delayed_scale_end(_ptr(state), length, _ptr(partials),
+                                                partials.numel(), _stream(state.device)),
+               "bf8_delayed_scale_end")

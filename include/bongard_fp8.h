@@ -1,0 +1,160 @@
+/*
+ * bongard_fp8.h - C ABI of the MI355X (gfx950) FP8 linear path.
+ *
+ * Built as libbongard_fp8.so from the HIP sources in bongard_amd/csrc. Every entry point:
+ *   - returns 0 on success, a non-zero BF8_E* code otherwise; bf8_last_error() then
+ *     gives a thread-local message;
+ *   - takes raw device pointers allocated by the caller (PyTorch), never allocates,
+ *     frees or synchronises, and enqueues its kernels on the given HIP stream
+ *     (`stream` is a hipStream_t; NULL means the legacy default stream);
+ *   - keeps no mutable global state besides the error message, so calls on different
+ *     streams are independent.
+ *
+ * Formats are OCP FP8: BF8_E4M3 (max 448, no inf, NaN = 0x7F/0xFF) and BF8_E5M2
+ * (max 57344, IEEE-like inf/NaN). Payloads are one byte per element.
+ *
+ * A "meta" record is four fp32 values in device memory: {amax, scale, scale_inv, 0}.
+ * scale = fp32(fp8_max / max(f64(amax), 1e-12)) (correctly rounded),
+ * scale_inv = fp32(1 / scale); the quantized value is q = fp8(clamp(f32(x) * scale)).
+ *
+ * The reference (AgentBull/bongard) has no native FFI for this path: it reaches the same
+ * arithmetic through torchao's Float8Linear and TransformerEngine's te.Linear /
+ * te.LayerNormMLP from Python. Each declaration names the reference call site whose
+ * arithmetic it replaces; the Python binding is bongard_amd/_lib.py (ctypes).
+ */
+#ifndef BONGARD_FP8_H
+#define BONGARD_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { BF8_E4M3 = 0, BF8_E5M2 = 1 };
+enum { BF8_OUT_BF16 = 0, BF8_OUT_F32 = 1 };
+enum {
+  BF8_OK = 0,
+  BF8_EINVAL = 1,   /* bad argument: shape, alignment, format, null pointer */
+  BF8_ELAUNCH = 2,  /* a kernel launch failed (hipGetLastError after launch) */
+  BF8_ESIZE = 3     /* caller-provided workspace too small */
+};
+
+/* Thread-local message for the last non-zero return code on this thread. */
+const char* bf8_last_error(void);
+/* ABI version of this library (bumped on any signature change). */
+int bf8_abi_version(void);
+
+/* ---------------------------------------------------------------------------------
+ * Per-tensor amax and scale (current scaling).
+ * Replaces torchao tensor_to_amax + amax_to_scale, reached from TrainingLinear.forward
+ * (bongard/float8_training.py:22, Float8Linear.forward) and the amax step of TE's
+ * Float8CurrentScaling quantizer used by TELinear / TEMLP (bongard/te_linear.py:73-74)
+ * and FusedMLP (bongard/fused_mlp.py:76-78).
+ * ------------------------------------------------------------------------------- */
+
+/* Number of uint32 partial-amax slots bf8_amax_bf16 writes for n elements. */
+int64_t bf8_amax_partials(int64_t n);
+
+/* partials[i] = fp32 bit pattern of max|x| over block i's share of x (NaN sorts above
+ * inf). x: bf16 [n], 16-byte aligned. partials: uint32 [bf8_amax_partials(n)]. */
+int bf8_amax_bf16(const void* x, int64_t n, uint32_t* partials, void* stream);
+
+/* meta = {amax, scale, scale_inv, 0} from n_partials partial-amax slots.
+ * `history` (nullable) selects delayed scaling instead: see bf8_delayed_scale. */
+int bf8_scale_from_partials(const uint32_t* partials, int64_t n_partials, int fmt,
+                            float* meta, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Saturating cast bf16 -> e4m3/e5m2, optional transposed copy.
+ * Replaces torchao to_fp8_saturated (+ the .t().contiguous() layouts fed to
+ * torch._scaled_mm) and TE's cast / cast-transpose kernels
+ * (bongard/te_linear.py:73-74, bongard/fused_mlp.py:76-78).
+ * x: bf16 [rows, cols] row-major, cols % 16 == 0. scale: device fp32 (meta + 1).
+ * out: fp8 [rows, cols] (nullable if out_t given); out_t: fp8 [cols, rows] or NULL.
+ * ------------------------------------------------------------------------------- */
+int bf8_cast_bf16(const void* x, int64_t rows, int64_t cols, const float* scale, int fmt,
+                  uint8_t* out, uint8_t* out_t, void* stream);
+
+/* amax -> scale -> cast in one call: meta gets {amax, scale, scale_inv, 0}.
+ * partials: uint32 workspace of bf8_amax_partials(rows * cols) slots. */
+int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
+                      uint8_t* out_t, float* meta, uint32_t* partials, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * FP8 GEMM, TN: C[m, n] = (sum_k A[m, k] * B[n, k]) * a_scale_inv * b_scale_inv(n)
+ *                          (+ bias[n]), fp32 accumulation, bf16 or fp32 output.
+ * Replaces torch._scaled_mm (cuBLASLt) under torchao Float8Linear (forward, and the
+ * dgrad/wgrad GEMMs of its backward) and TE's FP8 GEMM under te.Linear
+ * (bongard/te_linear.py:73-74); the emulated form is
+ * ((Aq.float() / sa) @ (Bq.float() / sb).T).to(out_dtype).
+ * A: fp8 [M, K] (row stride lda bytes), B: fp8 [N, K] (row stride ldb bytes),
+ * K % 16 == 0, lda % 16 == ldb % 16 == 0, N % 8 == 0.
+ * b_scale_inv: n_seg fp32 values at stride b_scale_stride floats; seg_ends (host array,
+ * n_seg <= 4, ascending, last == N) assigns column n to the first segment whose end
+ * exceeds n (fused QKV keeps one weight scale per projection). seg_ends may be NULL when
+ * n_seg == 1. bias: bf16 [N] or NULL. C: [M, N] with row stride ldc elements.
+ * ws: fp32 workspace for split-K partial sums, bf8_gemm_workspace(M, N, K) bytes
+ * (0 when the shape runs without split-K; ws may then be NULL).
+ * ------------------------------------------------------------------------------- */
+size_t bf8_gemm_workspace(int64_t M, int64_t N, int64_t K);
+int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt_b,
+             int64_t ldb, int64_t M, int64_t N, int64_t K, const float* a_scale_inv,
+             const float* b_scale_inv, int b_scale_stride, const int64_t* seg_ends,
+             int n_seg, const void* bias, void* C, int out_dtype, int64_t ldc, void* ws,
+             size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Gate/up GEMM with the gated-GELU(tanh) epilogue.
+ * Replaces TEMLP.forward's gate_up GEMM + F.gelu(gate, approximate='tanh') * up
+ * (bongard/te_linear.py:98-103; HF T5Gemma2MLP.forward) and TE LayerNormMLP's
+ * fc1 + geglu (bongard/fused_mlp.py:25-30). Rounding chain, per element:
+ *   g = bf16(acc_g * sx_inv * sg_inv), u = bf16(acc_u * sx_inv * su_inv),
+ *   h = bf16(f32(bf16(gelu_tanh(f32(g)))) * f32(u)).
+ * X: fp8 [M, K]; W: fp8 [2I, K] = [W_gate; W_up] (up rows start at row I).
+ * w_scale_inv[0] scales gate rows, w_scale_inv[w_scale_stride] up rows
+ * (w_scale_stride == 0: one shared scale, as TE's stacked gate_up weight).
+ * H: bf16 [M, I] (row stride ldh). GU: bf16 [M, 2I] (gate | up, bf16-rounded
+ * pre-activations kept for the backward) or NULL. h_partials: uint32
+ * [bf8_geglu_partials(M, I)] per-tile amax of |H| (fp32 bits), reduced by
+ * bf8_scale_from_partials into H's quantization meta. I % 128 == 0.
+ * ------------------------------------------------------------------------------- */
+int64_t bf8_geglu_partials(int64_t M, int64_t I);
+int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw, int64_t M,
+                   int64_t I, int64_t K, const float* x_scale_inv, const float* w_scale_inv,
+                   int w_scale_stride, void* H, int64_t ldh, void* GU,
+                   uint32_t* h_partials, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Backward of the gated GELU: given dH bf16 [M, I] and GU bf16 [M, 2I] (from the
+ * forward), write dGU bf16 [M, 2I] with
+ *   d_gate = bf16(dH * u * gelu'(g)), d_up = bf16(dH * bf16(gelu(g)))
+ * following autograd of F.gelu(g, approximate='tanh') * u in bf16
+ * (bongard/te_linear.py:103), and per-block amax partials of |dGU| (for its e5m2
+ * quantization) into partials [bf8_geglu_bwd_partials(M, I)].
+ * ------------------------------------------------------------------------------- */
+int64_t bf8_geglu_bwd_partials(int64_t M, int64_t I);
+int bf8_geglu_bwd(const void* dH, const void* GU, int64_t M, int64_t I, void* dGU,
+                  uint32_t* partials, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Delayed scaling with an amax history (no counterpart in the reference, which uses
+ * only current scaling: bongard/te_linear.py:38-39, bongard/fused_mlp.py:31-33).
+ * Semantics (TE DelayedScaling, margin 0, amax_compute_algo "max"):
+ *   the scale used at step t is fp8_max / max(history before step t) (1.0 while the
+ *   history is all zero); after the step, amax_t (reduced from partials) is written
+ *   into the ring at *pos and pos advances modulo len.
+ * state: fp32 [len + 4] = {history[len], amax_t, scale, scale_inv, pos}; the last
+ * three live at state + len + 1 .. + 3 so that state + len is a meta record.
+ * bf8_delayed_scale_begin writes meta = state + len (scale for this step) before the
+ * cast; bf8_delayed_scale_end pushes this step's amax after it.
+ * ------------------------------------------------------------------------------- */
+int bf8_delayed_scale_begin(float* state, int len, int fmt, void* stream);
+int bf8_delayed_scale_end(float* state, int len, const uint32_t* partials,
+                          int64_t n_partials, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BONGARD_FP8_H */

@@ -1,0 +1,303 @@
+"""CPU oracle of the FP8 linear path -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+module, and only as the checker (or the timed CPU baseline). The product path
+(bongard_amd) never calls it and has no CPU fallback.
+
+What it restates. The reference (AgentBull/bongard) ships no FP8 arithmetic of its own:
+its FP8 linears call torchao 0.17.0 (pyproject.toml:29; bongard/float8_training.py:14,
+35-36,57) and TransformerEngine 2.19.0 (pyproject.toml:30; bongard/te_linear.py:31-36,
+41,73; bongard/fused_mlp.py:14-19,21,76), neither of which is present here. This module
+restates their published per-tensor current-scaling algorithm, the arithmetic torchao
+runs on CPU under ``emulate=True`` (bongard/float8_training.py:28):
+
+  amax      = max(|x|)                              torchao tensor_to_amax
+  scale     = f32(fp8_max / clamp(f64(amax), 1e-12)) torchao amax_to_scale
+  q         = clamp(f32(x) * scale, +-fp8_max).to(fp8)   torchao to_fp8_saturated
+  Y         = ((Aq.f32 / sa) @ (Bq.f32 / sb).T).to(out)  emulated scaled mm
+  H         = bf16(bf16(gelu_tanh(g)) * u)           bongard/te_linear.py:103
+  RMSNorm   = x * rsqrt(mean(x^2) + eps) * (1 + w)   HF T5Gemma2RMSNorm, fused_mlp.py:25-30
+
+and adds the delayed-scaling closed form that config 5 asks for (no reference symbol).
+
+Two independent witnesses pin the cast: ``quantize`` (torch's own float8 conversion,
+the emulate path) and ``encode_fp8_np`` (a table-driven encoder built from the OCP FP8
+bit layout). tests/test_oracle.py checks them against each other on all 65,536 bf16
+bit patterns, against hand-computed known answers, and pins scale/matmul against fp64
+closed forms; tests/golden/ holds fixtures this module wrote.
+
+NaN conventions (this torch build's CPU kernels, x86): a NaN product carries the scale's
+sign if the scale is NaN, else x's sign if x is NaN, else (inf * 0) the x86 default NaN,
+which is negative; both fp8 formats encode NaN as 0x7F | sign.
+"""
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+E4M3 = 0
+E5M2 = 1
+FP8_MAX = {E4M3: 448.0, E5M2: 57344.0}
+TORCH_FP8 = {E4M3: torch.float8_e4m3fn, E5M2: torch.float8_e5m2}
+EPS = 1e-12  # torchao float8 EPS
+
+
+# ---------------------------------------------------------------------------------------
+# amax / scale  (torchao tensor_to_amax, amax_to_scale)
+# ---------------------------------------------------------------------------------------
+def amax(x: torch.Tensor) -> torch.Tensor:
+    """max(|x|) in x's dtype (exact for bf16), NaN-propagating; returned as fp32 scalar."""
+    return x.abs().max().to(torch.float32)
+
+
+def amax_to_scale(amax_f32: torch.Tensor, fmt: int):
+    """(scale, scale_inv) as fp32 scalars: scale = f32(fp8_max / clamp(f64(amax), EPS))."""
+    a = amax_f32.to(torch.float64)
+    scale = (FP8_MAX[fmt] / torch.clamp(a, min=EPS)).to(torch.float32)
+    return scale, scale.reciprocal()
+
+
+def scale_np(amax_value: float, fmt: int) -> np.float32:
+    """Closed form of the scale in plain Python floats (fp64), rounded once to fp32."""
+    a = float(amax_value)
+    if math.isnan(a):
+        return np.float32("nan")
+    return np.float32(FP8_MAX[fmt] / max(a, EPS))
+
+
+# ---------------------------------------------------------------------------------------
+# saturating cast  (torchao to_fp8_saturated)
+# ---------------------------------------------------------------------------------------
+def _nan_sign_bytes(xf: torch.Tensor, prod: torch.Tensor, scale: torch.Tensor, fmt: int):
+    """Bytes for NaN products per the conventions in the module docstring."""
+    xnan = torch.isnan(xf)
+    xsign = (xf.view(torch.int32) < 0)
+    if bool(torch.isnan(scale)):
+        sign = torch.full_like(xsign, bool(scale.view(torch.int32) < 0))
+    else:
+        sign = torch.where(xnan, xsign, torch.ones_like(xsign))
+    return torch.where(sign, 0xFF, 0x7F).to(torch.uint8)
+
+
+def cast(x: torch.Tensor, scale: torch.Tensor, fmt: int) -> torch.Tensor:
+    """q bytes (uint8) of clamp(f32(x) * scale, +-max).to(fp8) with explicit NaN bytes."""
+    xf = x.to(torch.float32)
+    prod = xf * scale.to(torch.float32)
+    m = FP8_MAX[fmt]
+    q = torch.clamp(prod, -m, m).to(TORCH_FP8[fmt]).view(torch.uint8)
+    nan = torch.isnan(prod)
+    if bool(nan.any()):
+        q = torch.where(nan, _nan_sign_bytes(xf, prod, scale, fmt), q)
+    return q
+
+
+def quantize(x: torch.Tensor, fmt: int = E4M3):
+    """Current scaling: returns (q uint8 same shape, amax, scale, scale_inv) fp32 scalars."""
+    a = amax(x)
+    s, si = amax_to_scale(a, fmt)
+    return cast(x, s, fmt), a, s, si
+
+
+def dequant(q: torch.Tensor, scale: torch.Tensor, fmt: int) -> torch.Tensor:
+    """q.float() / scale (the emulated dequantization) in fp32."""
+    return q.view(TORCH_FP8[fmt]).to(torch.float32) / scale
+
+
+# ---------------------------------------------------------------------------------------
+# Independent witness: table-driven OCP FP8 encoder (numpy)
+# ---------------------------------------------------------------------------------------
+def fp8_value_table(fmt: int) -> np.ndarray:
+    """float64 value of every byte 0..255 (NaN for NaN codes, +-inf for e5m2 inf)."""
+    vals = np.empty(256, dtype=np.float64)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        if fmt == E4M3:
+            e, m = (b >> 3) & 0xF, b & 0x7
+            if e == 0xF and m == 0x7:
+                v = math.nan
+            elif e == 0:
+                v = (m / 8.0) * 2.0 ** -6
+            else:
+                v = (1 + m / 8.0) * 2.0 ** (e - 7)
+        else:
+            e, m = (b >> 2) & 0x1F, b & 0x3
+            if e == 0x1F:
+                v = math.inf if m == 0 else math.nan
+            elif e == 0:
+                v = (m / 4.0) * 2.0 ** -14
+            else:
+                v = (1 + m / 4.0) * 2.0 ** (e - 15)
+        vals[b] = s * v
+    return vals
+
+
+def encode_fp8_np(v: np.ndarray, fmt: int) -> np.ndarray:
+    """Round-to-nearest-even encoding of finite fp32 values with |v| <= fp8_max.
+
+    Non-negative finite codes 0..max_code are monotone in value, so the nearest code is
+    found by bisection on the magnitude table; ties go to the even code (mantissa LSB 0).
+    The sign bit is copied from v (so -0.0 and negative underflow give 0x80).
+    """
+    v = np.asarray(v, dtype=np.float32)
+    table = fp8_value_table(fmt)
+    max_code = 0x7E if fmt == E4M3 else 0x7B
+    mags = table[: max_code + 1]
+    a = np.abs(v.astype(np.float64))
+    if np.any(a > FP8_MAX[fmt]) or np.any(~np.isfinite(a)):
+        raise ValueError("encode_fp8_np expects finite values within +-fp8_max")
+    hi = np.searchsorted(mags, a, side="left")  # first code with mag >= a
+    hi = np.clip(hi, 0, max_code)
+    lo = np.clip(hi - 1, 0, max_code)
+    d_hi = mags[hi] - a
+    d_lo = a - mags[lo]
+    pick_lo = (d_lo < d_hi) | ((d_lo == d_hi) & (lo % 2 == 0))
+    code = np.where(pick_lo, lo, hi).astype(np.uint8)
+    sign = (np.signbit(v)).astype(np.uint8) << 7
+    return code | sign
+
+
+def cast_np(x_f32: np.ndarray, scale: np.float32, fmt: int) -> np.ndarray:
+    """Numpy witness of ``cast``: fp32 product, clamp, table encoder, NaN convention."""
+    x_f32 = np.asarray(x_f32, dtype=np.float32)
+    scale = np.float32(scale)
+    with np.errstate(invalid="ignore", over="ignore"):
+        prod = (x_f32 * scale).astype(np.float32)
+    nan = np.isnan(prod)
+    m = np.float32(FP8_MAX[fmt])
+    clamped = np.clip(np.where(nan, np.float32(0), prod), -m, m)
+    q = encode_fp8_np(clamped, fmt)
+    if nan.any():
+        if np.isnan(scale):
+            sign = np.full(x_f32.shape, bool(np.signbit(scale)))
+        else:
+            sign = np.where(np.isnan(x_f32), np.signbit(x_f32), True)
+        q = np.where(nan, np.where(sign, 0xFF, 0x7F), q).astype(np.uint8)
+    return q
+
+
+# ---------------------------------------------------------------------------------------
+# dequantized matmul  (torchao emulated _scaled_mm / TE GEMM)
+# ---------------------------------------------------------------------------------------
+def scaled_mm(aq, a_scale, a_fmt, bq, b_scale, b_fmt, *, bias=None, precise=True,
+              seg_ends=None, b_scales=None):
+    """fp32 result of (Aq/sa) @ (Bq/sb).T (+ bias).
+
+    ``precise``: accumulate in fp64 (the reference truth for tolerance checks); else
+    fp32 torch.mm, exactly the emulated path (used for the CPU baseline timing).
+    ``seg_ends``/``b_scales``: per-column-segment weight scales (fused projections).
+    """
+    a = dequant(aq, a_scale, a_fmt)
+    if seg_ends is None:
+        b = dequant(bq, b_scale, b_fmt)
+    else:
+        parts, start = [], 0
+        for end, s in zip(seg_ends, b_scales):
+            parts.append(dequant(bq[start:end], s, b_fmt))
+            start = end
+        b = torch.cat(parts, 0)
+    if precise:
+        y = (a.double() @ b.double().T)
+        if bias is not None:
+            y = y + bias.double()
+        return y.to(torch.float32)
+    y = a @ b.T
+    if bias is not None:
+        y = y + bias.float()
+    return y
+
+
+# ---------------------------------------------------------------------------------------
+# gated GELU chain and its backward  (bongard/te_linear.py:98-103, HF T5Gemma2MLP)
+# ---------------------------------------------------------------------------------------
+def geglu(g_bf16: torch.Tensor, u_bf16: torch.Tensor) -> torch.Tensor:
+    """H = F.gelu(g, approximate='tanh') * u, on bf16 tensors (torch CPU kernels)."""
+    return F.gelu(g_bf16, approximate="tanh") * u_bf16
+
+
+def geglu_bwd(g_bf16, u_bf16, dh_bf16):
+    """(d_g, d_u) from autograd of the bf16 chain geglu(g, u)."""
+    g = g_bf16.detach().clone().requires_grad_(True)
+    u = u_bf16.detach().clone().requires_grad_(True)
+    h = geglu(g, u)
+    h.backward(dh_bf16)
+    return g.grad, u.grad
+
+
+def mlp_forward(x_bf16, w_gate, w_up, w_down, *, shared_gate_up_scale=True, precise=True):
+    """FP8 gated MLP as the reference's TEMLP computes it (bf16 tensors in, fp32 Y out).
+
+    Returns a dict with every intermediate (quantized bytes, scales, G, U, H, H8, Y).
+    """
+    xq, xa, xs, xsi = quantize(x_bf16, E4M3)
+    if shared_gate_up_scale:
+        wgu = torch.cat([w_gate, w_up], 0)
+        wq, wa, ws, wsi = quantize(wgu, E4M3)
+        I = w_gate.shape[0]
+        gate = scaled_mm(xq, xs, E4M3, wq[:I], ws, E4M3, precise=precise)
+        up = scaled_mm(xq, xs, E4M3, wq[I:], ws, E4M3, precise=precise)
+        w_scales = (ws, ws)
+    else:
+        gq, _, gs, _ = quantize(w_gate, E4M3)
+        uq, _, us, _ = quantize(w_up, E4M3)
+        gate = scaled_mm(xq, xs, E4M3, gq, gs, E4M3, precise=precise)
+        up = scaled_mm(xq, xs, E4M3, uq, us, E4M3, precise=precise)
+        w_scales = (gs, us)
+    g = gate.to(torch.bfloat16)
+    u = up.to(torch.bfloat16)
+    h = geglu(g, u)
+    hq, ha, hs, hsi = quantize(h, E4M3)
+    dq, da, ds, dsi = quantize(w_down, E4M3)
+    y = scaled_mm(hq, hs, E4M3, dq, ds, E4M3, precise=precise)
+    return dict(xq=xq, x_scale=xs, w_scales=w_scales, g=g, u=u, h=h, hq=hq, h_scale=hs,
+                wd_scale=ds, y=y)
+
+
+# ---------------------------------------------------------------------------------------
+# RMSNorm with zero-centred gamma  (HF T5Gemma2RMSNorm; TE LayerNormMLP, fused_mlp.py:25-30)
+# ---------------------------------------------------------------------------------------
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    out = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    out = out * (1.0 + weight.float())
+    return out.type_as(x)
+
+
+# ---------------------------------------------------------------------------------------
+# delayed scaling (config 5; TE DelayedScaling semantics, margin 0, algo "max")
+# ---------------------------------------------------------------------------------------
+class DelayedScaling:
+    """Reference closed form of the amax-history scaling used by config 5.
+
+    Step t quantizes with ``scale_t``; afterwards its amax enters a ring of ``length``.
+    scale_{t+1} = fp8_max / max(history) if that maximum is finite and > 0, else scale_t.
+    The initial scale is 1.
+    """
+
+    def __init__(self, length: int, fmt: int):
+        self.length = length
+        self.fmt = fmt
+        self.history = np.zeros(length, dtype=np.float32)
+        self.pos = 0
+        self.scale = np.float32(1.0)
+
+    def begin(self):
+        h = self.history
+        if np.all(np.isfinite(h)) and h.max() > 0:
+            self.scale = np.float32(FP8_MAX[self.fmt] / float(h.max()))
+        return self.scale, np.float32(1.0 / float(self.scale))
+
+    def end(self, amax_value):
+        self.history[self.pos] = np.float32(amax_value)
+        self.pos = (self.pos + 1) % self.length
+
+
+# ---------------------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------------------
+def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |x| (fp32), 2^(e-7) for normal x; min-normal spacing below."""
+    a = x.abs().float().clamp(min=2.0 ** -126)
+    e = torch.floor(torch.log2(a))
+    return torch.pow(2.0, e - 7)

@@ -1,0 +1,58 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared symbol, and rejects
+bad arguments with an error message before touching the GPU."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from bongard_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "bongard_fp8.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b(bf8_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_loads_and_exports_header_symbols():
+    L = _lib.lib()
+    declared = _declared_functions()
+    assert len(declared) >= 14
+    for name in declared:
+        assert hasattr(L, name), f"{name} declared in the header but not exported"
+    assert set(declared) == set(_lib.SIGNATURES), "ctypes table and header disagree"
+    assert L.bf8_abi_version() == _lib.ABI_VERSION
+
+
+def test_bad_arguments_report_errors_without_gpu():
+    L = _lib.lib()
+    null = ctypes.c_void_p(0)
+    rc = L.bf8_gemm(null, 0, 16, null, 0, 16, 32, 32, 24, null, null, 4, None, 1, null, null,
+                    0, 32, null, 0, null)
+    assert rc == 1
+    assert b"multiples of 16" in L.bf8_last_error()
+    rc = L.bf8_cast_bf16(null, 4, 16, null, 0, null, null, null)
+    assert rc == 1 and b"scale is NULL" in L.bf8_last_error()
+    rc = L.bf8_scale_from_partials(null, 1, 7, null, null)
+    assert rc == 1 and b"bad fmt" in L.bf8_last_error()
+    rc = L.bf8_gemm_geglu(null, 16, null, 16, 4, 100, 16, null, null, 0, null, 100, null, null,
+                          null)
+    assert rc == 1 and b"multiple of 128" in L.bf8_last_error()
+    with pytest.raises(_lib.Fp8LibError, match="bf8_gemm"):
+        _lib.check(L.bf8_gemm(null, 0, 16, null, 0, 16, 32, 32, 24, null, null, 4, None, 1,
+                              null, null, 0, 32, null, 0, null), "bf8_gemm")
+
+
+def test_partials_counts():
+    L = _lib.lib()
+    assert L.bf8_amax_partials(0) == 1
+    assert L.bf8_amax_partials(512 * 2560) >= 1
+    assert L.bf8_amax_partials(1 << 30) == 2048
+    assert L.bf8_geglu_partials(4096, 10240) == 16 * 80
+    assert L.bf8_gemm_workspace(4096, 2560, 10240) >= 0

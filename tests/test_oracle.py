@@ -1,0 +1,223 @@
+"""Pins the CPU oracle (oracle/fp8_oracle.py) before it is trusted as the GPU checker.
+
+The reference ships no tests, fixtures or golden vectors for this path, and torchao /
+TransformerEngine are not installed, so each oracle function is pinned by checks a
+plausible mistake would fail: hand-computed known answers, a second independent encoder
+(table-driven, from the OCP bit layout) on all 65,536 bf16 patterns, fp64 closed forms,
+integer-exact matmuls, and torch's own ops where the oracle restates them.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import fp8_oracle as orc
+
+E4M3, E5M2 = orc.E4M3, orc.E5M2
+
+
+# ---- known answers (hand-computed from the OCP formats) ---------------------------------
+E4M3_KNOWN = [
+    (0.0, 0x00), (-0.0, 0x80), (1.0, 0x38), (-1.0, 0xB8), (448.0, 0x7E), (-448.0, 0xFE),
+    (17.0, 0x58),            # 17 = 16 + 1, tie between 16 and 18 -> even mantissa (16)
+    (19.0, 0x5A),            # tie between 18 and 20 -> 20
+    (2.0 ** -6, 0x08),       # min normal
+    (2.0 ** -9, 0x01),       # min subnormal
+    (2.0 ** -10, 0x00),      # half the min subnormal: tie -> 0
+    (1.5 * 2.0 ** -10, 0x01),
+    (7 * 2.0 ** -9, 0x07),   # max subnormal
+    (240.0, 0x77), (256.0, 0x78), (0.1, 0x1D),
+    (500.0, 0x7E), (1e30, 0x7E), (-1e30, 0xFE),  # saturate
+]
+E5M2_KNOWN = [
+    (0.0, 0x00), (-0.0, 0x80), (1.0, 0x3C), (57344.0, 0x7B), (-57344.0, 0xFB),
+    (2.0 ** -14, 0x04), (2.0 ** -16, 0x01), (2.0 ** -17, 0x00), (3 * 2.0 ** -17, 0x02),
+    (1.125, 0x3C),           # tie between 1 and 1.25 -> even (1)
+    (1.375, 0x3E),           # tie between 1.25 and 1.5 -> 1.5
+    (61440.0, 0x7B), (1e30, 0x7B),  # saturate (no inf through the saturating cast)
+]
+
+
+@pytest.mark.parametrize("fmt,table", [(E4M3, E4M3_KNOWN), (E5M2, E5M2_KNOWN)])
+def test_known_answers(fmt, table):
+    vals = torch.tensor([v for v, _ in table], dtype=torch.float32)
+    want = torch.tensor([b for _, b in table], dtype=torch.uint8)
+    got = orc.cast(vals, torch.tensor(1.0), fmt)
+    assert got.tolist() == want.tolist()
+    got_np = orc.cast_np(vals.numpy(), np.float32(1.0), fmt)
+    assert got_np.tolist() == want.tolist()
+
+
+def test_value_table_round_trip():
+    for fmt, dt in ((E4M3, torch.float8_e4m3fn), (E5M2, torch.float8_e5m2)):
+        table = orc.fp8_value_table(fmt)
+        torch_vals = torch.arange(256, dtype=torch.uint8).view(dt).to(torch.float64).numpy()
+        same = (table == torch_vals) | (np.isnan(table) & np.isnan(torch_vals))
+        assert same.all()
+
+
+# ---- two witnesses on every bf16 bit pattern ---------------------------------------------
+ALL_BF16 = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+@pytest.mark.parametrize("scale", [1.0, 6.9457, 2.0 ** -13, 3.0e4, 4.48e14, 0.0, float("nan")])
+def test_torch_cast_equals_table_encoder(fmt, scale):
+    s = torch.tensor(scale, dtype=torch.float32)
+    a = orc.cast(ALL_BF16, s, fmt).numpy()
+    b = orc.cast_np(ALL_BF16.float().numpy(), np.float32(scale), fmt)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_nan_convention_is_torch_cpu(fmt):
+    """The explicit NaN rule equals what torch's own clamp(x*s).to(fp8) yields on this CPU."""
+    m = orc.FP8_MAX[fmt]
+    xs = torch.tensor([float("nan"), -float("nan"), float("inf"), -float("inf"), 1.0, -2.0])
+    for scale in (torch.tensor(2.0), torch.tensor(0.0), torch.tensor(float("nan"))):
+        raw = torch.clamp(xs * scale, -m, m).to(orc.TORCH_FP8[fmt]).view(torch.uint8)
+        assert orc.cast(xs, scale, fmt).tolist() == raw.tolist()
+
+
+# ---- amax / scale ---------------------------------------------------------------------
+def test_amax_exact_and_nan_propagating():
+    x = torch.tensor([[1.0, -3.5], [2.0, 0.25]], dtype=torch.bfloat16)
+    assert orc.amax(x).item() == 3.5
+    x[0, 0] = float("nan")
+    assert math.isnan(orc.amax(x).item())
+    g = torch.Generator().manual_seed(0)
+    y = torch.randn(300, 17, generator=g).to(torch.bfloat16)
+    brute = max(abs(float(v)) for v in y.flatten().tolist())
+    assert orc.amax(y).item() == brute
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_scale_closed_form(fmt):
+    g = torch.Generator().manual_seed(1)
+    amaxes = torch.cat([torch.rand(2000, generator=g) * 100,
+                        torch.tensor([0.0, 1e-13, 1e-12, 64.5, 0.1035, 3.0e38])])
+    for a in amaxes.tolist():
+        s, si = orc.amax_to_scale(torch.tensor(a, dtype=torch.float32), fmt)
+        want = np.float32(orc.FP8_MAX[fmt] / max(float(np.float32(a)), 1e-12))
+        assert s.item() == float(want)
+        assert si.item() == float(np.float32(1.0) / want)
+        assert s.item() == float(orc.scale_np(float(np.float32(a)), fmt))
+
+
+def test_scale_config1_probe_value():
+    # BASELINE config 1 note: amax 64.5 -> scale 448 / 64.5 = 6.9457
+    s, _ = orc.amax_to_scale(torch.tensor(64.5), E4M3)
+    assert abs(s.item() - 448 / 64.5) < 1e-6 and s.dtype == torch.float32
+
+
+# ---- dequantized matmul -----------------------------------------------------------------
+def test_scaled_mm_integer_exact():
+    """Power-of-two scales and small integers: the dequant matmul is exact."""
+    a = torch.tensor([[1.0, 2.0, -3.0], [0.5, 0.0, 4.0]])
+    b = torch.tensor([[2.0, 1.0, 1.0], [-1.0, 0.25, 2.0]])
+    sa, sb = torch.tensor(4.0), torch.tensor(0.5)
+    aq = orc.cast(a, sa, E4M3)
+    bq = orc.cast(b, sb, E4M3)
+    y = orc.scaled_mm(aq, sa, E4M3, bq, sb, E4M3)
+    assert torch.equal(y, a @ b.T)
+    y32 = orc.scaled_mm(aq, sa, E4M3, bq, sb, E4M3, precise=False)
+    assert torch.equal(y32, a @ b.T)
+
+
+def test_scaled_mm_transposition_and_bias():
+    g = torch.Generator().manual_seed(2)
+    a = torch.randn(5, 32, generator=g).to(torch.bfloat16)
+    b = torch.randn(7, 32, generator=g).to(torch.bfloat16)
+    bias = torch.randn(7, generator=g).to(torch.bfloat16)
+    aq, _, sa, _ = orc.quantize(a, E4M3)
+    bq, _, sb, _ = orc.quantize(b, E4M3)
+    y = orc.scaled_mm(aq, sa, E4M3, bq, sb, E4M3, bias=bias)
+    deq_a = orc.dequant(aq, sa, E4M3).double()
+    deq_b = orc.dequant(bq, sb, E4M3).double()
+    for i in range(5):
+        for j in range(7):
+            want = sum(deq_a[i, k] * deq_b[j, k] for k in range(32)) + float(bias[j])
+            assert abs(y[i, j].item() - want) <= 1e-6 * max(1.0, abs(want))
+
+
+def test_segment_scales_equal_separate_mms():
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(4, 16, generator=g).to(torch.bfloat16)
+    ws = [torch.randn(n, 16, generator=g).to(torch.bfloat16) * s for n, s in ((3, 1), (5, 9))]
+    aq, _, sa, _ = orc.quantize(a, E4M3)
+    qs = [orc.quantize(w, E4M3) for w in ws]
+    fused = orc.scaled_mm(aq, sa, E4M3, torch.cat([q[0] for q in qs]), None, E4M3,
+                          seg_ends=[3, 8], b_scales=[q[2] for q in qs])
+    sep = torch.cat([orc.scaled_mm(aq, sa, E4M3, q[0], q[2], E4M3) for q in qs], 1)
+    assert torch.equal(fused, sep)
+
+
+# ---- gated GELU chain --------------------------------------------------------------------
+def test_geglu_matches_formula_and_hf_mlp():
+    g = torch.Generator().manual_seed(4)
+    gate = (torch.randn(64, 32, generator=g) * 3).to(torch.bfloat16)
+    up = torch.randn(64, 32, generator=g).to(torch.bfloat16)
+    h = orc.geglu(gate, up)
+    x = gate.double()
+    want = 0.5 * x * (1 + torch.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)))
+    want = (want.to(torch.bfloat16).double() * up.double()).to(torch.bfloat16)
+    diff = (h.double() - want.double()).abs()
+    # a one-ulp change of the bf16 gelu moves the rounded product by at most two ulps
+    # (plus an absolute 2^-20 * max|h| where fp32 cancels 1 + tanh to exactly zero)
+    slack = 2.0 ** -20 * want.double().abs().max()
+    assert (diff <= 2 * orc.bf16_ulp(want.float()).double() + slack).all()
+    # fp32 evaluation of 1 + tanh(inner) cancels in the negative tail, so torch's fp32
+    # chain and the fp64 formula differ by one bf16 ulp on a few percent of elements
+    assert (diff > 0).float().mean() < 0.15
+    # HF activation used by T5Gemma2MLP (gelu_pytorch_tanh) is the same op
+    from transformers.activations import ACT2FN
+    assert torch.equal(ACT2FN["gelu_pytorch_tanh"](gate) * up, h)
+
+
+def test_geglu_bwd_against_finite_differences():
+    g = torch.Generator().manual_seed(5)
+    gate = torch.randn(8, 8, generator=g, dtype=torch.float64)
+    up = torch.randn(8, 8, generator=g, dtype=torch.float64)
+    dh = torch.randn(8, 8, generator=g, dtype=torch.float64)
+    dg, du = orc.geglu_bwd(gate.to(torch.bfloat16), up.to(torch.bfloat16), dh.to(torch.bfloat16))
+
+    def f(x):
+        return 0.5 * x * (1 + torch.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)))
+
+    gb, ub = gate.to(torch.bfloat16).double(), up.to(torch.bfloat16).double()
+    eps = 1e-6
+    dfdx = (f(gb + eps) - f(gb - eps)) / (2 * eps)
+    want_dg = dh.to(torch.bfloat16).double() * ub * dfdx
+    want_du = dh.to(torch.bfloat16).double() * f(gb)
+    assert torch.allclose(dg.double(), want_dg, rtol=3e-2, atol=1e-3)
+    assert torch.allclose(du.double(), want_du, rtol=2e-2, atol=1e-3)
+
+
+# ---- RMSNorm ------------------------------------------------------------------------------
+def test_rmsnorm_matches_hf_module():
+    from transformers.models.t5gemma2.modeling_t5gemma2 import T5Gemma2RMSNorm
+    norm = T5Gemma2RMSNorm(64, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.normal_()
+    x = torch.randn(10, 64).to(torch.bfloat16)
+    assert torch.equal(orc.rmsnorm(x, norm.weight, 1e-6), norm(x))
+
+
+# ---- delayed scaling ----------------------------------------------------------------------
+def test_delayed_scaling_closed_form():
+    d = orc.DelayedScaling(4, E4M3)
+    s, si = d.begin()
+    assert s == 1.0 and si == 1.0          # empty history keeps the initial scale
+    d.end(2.0)
+    s, _ = d.begin()
+    assert s == np.float32(224.0)          # 448 / 2
+    for a in (8.0, 1.0, 1.0, 1.0):
+        d.end(a)
+    s, _ = d.begin()                        # ring of 4 now holds 8, 1, 1, 1 (2 evicted)
+    assert s == np.float32(56.0)
+    d.end(float("inf"))
+    s2, _ = d.begin()
+    assert s2 == s                          # non-finite history keeps the previous scale
