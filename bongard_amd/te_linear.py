@@ -1,0 +1,302 @@
+"""FP8 projections with ordinary Hugging Face checkpoint weights (MI355X).
+
+Drop-in for bongard/te_linear.py (TransformerEngine te.Linear path): same ``RECIPES``,
+``TELinear(linears, recipe)``, ``TEMLP(mlp, recipe)``, ``enable_te_linear(model, *,
+mlp=None, attention=None) -> dict``, ``present(backbone)`` and
+``restore_hf_layout(backbone, state)``, with the reference's attributes
+(``bongard_recipe``, ``recipe``, ``splits``, ``counts``, ``_cached_weight_version``,
+``intermediate_size``, ``fused_gate_up``), state-dict keys (``weight`` and an empty
+``_extra_state`` per projection), pad-to-32 rows, the ``weight._version`` quantization
+cache (first microbatch quantizes, later ones reuse) and the
+``BONGARD_TE_SPLIT_GATE_UP`` switch.
+
+The 'fp8' recipe is per-tensor current scaling with HYBRID formats (e4m3 forward, e5m2
+gradients), on the gfx950 kernels. In training, TEMLP runs the gate/up GEMM with the
+gated-GELU fused into its epilogue and feeds H's FP8 copy to the down projection
+(bongard_amd.linear.Fp8GegluMlpFunction) instead of three separate passes.
+'mxfp8' and 'nvfp4' are accepted by name but raise NotImplementedError when a module is
+built: their block-scaled kernels do not exist yet.
+"""
+
+import os
+from collections import Counter
+from dataclasses import dataclass
+
+import torch
+from torch.nn import functional as F
+
+from . import linear as _linear
+
+RECIPES = ('nvfp4', 'mxfp8', 'fp8')
+ATTENTION_PROJECTIONS = ('q_proj', 'k_proj', 'v_proj', 'o_proj')
+
+
+@dataclass(frozen=True)
+class Float8CurrentScaling:
+    """Per-tensor current scaling; HYBRID = e4m3 forward tensors, e5m2 gradients."""
+
+    fp8_format: str = "HYBRID"
+
+
+def _make_recipe(name):
+    if name == 'fp8':
+        return Float8CurrentScaling()
+    raise NotImplementedError(
+        f"TE recipe {name!r} (block scaling) has no gfx950 kernels yet; use 'fp8'")
+
+
+def _te_linear(module):
+    return hasattr(module, 'bongard_recipe') and hasattr(module, 'splits')
+
+
+def _te_mlp(module):
+    return hasattr(module, 'bongard_recipe') and hasattr(module, 'fused_gate_up')
+
+
+def _pad_rows(flat, multiple=32):
+    length = flat.shape[0]
+    aligned = (length + multiple - 1) // multiple * multiple
+    if aligned != length:
+        flat = F.pad(flat, (0, 0, 0, aligned - length))
+    return flat, length, aligned
+
+
+class _StatelessExtraState:
+    """``_extra_state`` of a stateless-scaling module: an empty uint8 tensor."""
+
+    def get_extra_state(self):
+        return torch.empty(0, dtype=torch.uint8)
+
+    def set_extra_state(self, state):
+        if state is not None and getattr(state, 'numel', lambda: 0)():
+            raise ValueError('stateless FP8 scaling has no extra state to load')
+
+
+class TELinear(_StatelessExtraState, torch.nn.Module):
+    """One FP8 linear serving one or more stacked HF Linear weights of the same input."""
+
+    def __init__(self, linears, recipe):
+        super().__init__()
+        if any(linear.bias is not None for linear in linears):
+            raise ValueError('TE projections require bias-free HF linears')
+        splits = [linear.out_features for linear in linears]
+        self.in_features = linears[0].in_features
+        self.out_features = sum(splits)
+        self.bongard_recipe = recipe
+        self.recipe = _make_recipe(recipe)
+        self.weight = torch.nn.Parameter(torch.zeros(
+            self.out_features, self.in_features, dtype=torch.bfloat16,
+            device=linears[0].weight.device))
+        self.splits = splits
+        with torch.no_grad():
+            self.weight.copy_(torch.cat([linear.weight for linear in linears], 0))
+        self.counts = Counter()
+        self._cached_weight_version = None
+        self._fp8_weight = None
+
+    def extra_repr(self):
+        return f"in={self.in_features}, out={self.out_features}, recipe={self.bongard_recipe}"
+
+    def _apply(self, fn, recurse=True):
+        super()._apply(fn, recurse=recurse)
+        self._fp8_weight = None
+        self._cached_weight_version = None
+        return self
+
+    def fp8_weight(self, is_first_microbatch):
+        """Quantized weight (+ transposed copy); cached across microbatches like TE."""
+        if is_first_microbatch or self._fp8_weight is None:
+            q = _linear.quantize_weight(self.weight, transpose=True)
+            if is_first_microbatch is not None:
+                self._fp8_weight = q
+            return q
+        return self._fp8_weight
+
+    def _note_microbatch(self):
+        version = self.weight._version
+        first_microbatch = version != self._cached_weight_version
+        self._cached_weight_version = version
+        self.counts['weight_quantizations' if first_microbatch else 'cached_weights'] += 1
+        return first_microbatch
+
+    @torch.compiler.disable
+    def forward(self, x):
+        if not self.training:
+            return F.linear(x, self.weight)
+        flat = x.reshape(-1, x.shape[-1])
+        first_microbatch = self._note_microbatch()
+        # Pad to a multiple of 32 rows (zeros leave the amax unchanged), slice after.
+        flat, length, aligned = _pad_rows(flat)
+        if flat.dtype != torch.bfloat16:
+            flat = flat.to(torch.bfloat16)
+        out = _linear.Fp8LinearFunction.apply(flat, self.weight, None,
+                                              self.fp8_weight(first_microbatch))
+        if aligned != length:
+            out = out[:length]
+        return out.reshape(*x.shape[:-1], out.shape[-1])
+
+
+class TEMLP(torch.nn.Module):
+    """The HF gated MLP with its three projections as two FP8 GEMMs."""
+
+    def __init__(self, mlp, recipe):
+        super().__init__()
+        if mlp.config.hidden_activation != 'gelu_pytorch_tanh' or mlp.dropout.p:
+            raise ValueError('TE MLP requires tanh GELU and zero dropout')
+        self.bongard_recipe = recipe
+        self.intermediate_size = mlp.intermediate_size
+        # Default: one stacked [gate; up] weight sharing one scale; the environment switch
+        # keeps two projections (two scales), as in the reference.
+        self.fused_gate_up = os.environ.get('BONGARD_TE_SPLIT_GATE_UP', '0') != '1'
+        if self.fused_gate_up:
+            self.gate_up = TELinear([mlp.gate_proj, mlp.up_proj], recipe)
+        else:
+            self.gate_proj = TELinear([mlp.gate_proj], recipe)
+            self.up_proj = TELinear([mlp.up_proj], recipe)
+        self.down = TELinear([mlp.down_proj], recipe)
+        self._split_cache = None
+
+    def _gate_up_weight(self):
+        if self.fused_gate_up:
+            return self.gate_up.weight
+        return torch.cat([self.gate_proj.weight, self.up_proj.weight], 0)
+
+    def forward(self, x):
+        if not self.training:
+            if self.fused_gate_up:
+                gate, up = self.gate_up(x).split(self.intermediate_size, dim=-1)
+            else:
+                gate, up = self.gate_proj(x), self.up_proj(x)
+            return self.down(F.gelu(gate, approximate='tanh') * up)
+        return self._fp8_forward(x)
+
+    @torch.compiler.disable
+    def _fp8_forward(self, x):
+        I = self.intermediate_size
+        flat = x.reshape(-1, x.shape[-1])
+        flat, length, aligned = _pad_rows(flat)
+        if flat.dtype != torch.bfloat16:
+            flat = flat.to(torch.bfloat16)
+        down_first = self.down._note_microbatch()
+        down_q = self.down.fp8_weight(down_first)
+        if self.fused_gate_up:
+            first = self.gate_up._note_microbatch()
+            if first or self.gate_up._fp8_weight is None:
+                self.gate_up._fp8_weight = _linear.quantize_gate_up(
+                    self.gate_up.weight, I, split_scales=False)
+            gu_q = self.gate_up._fp8_weight
+            w_gu = self.gate_up.weight
+        else:
+            first_g = self.gate_proj._note_microbatch()
+            first_u = self.up_proj._note_microbatch()
+            if first_g or first_u or self._split_cache is None:
+                self._split_cache = _linear.quantize_gate_up(
+                    torch.cat([self.gate_proj.weight, self.up_proj.weight], 0), I,
+                    split_scales=True)
+            gu_q = self._split_cache
+            w_gu = _SplitGateUp.apply(self.gate_proj.weight, self.up_proj.weight)
+        out = _linear.Fp8GegluMlpFunction.apply(flat, w_gu, self.down.weight, gu_q, down_q, I,
+                                                not self.fused_gate_up)
+        if aligned != length:
+            out = out[:length]
+        return out.reshape(*x.shape[:-1], out.shape[-1])
+
+
+class _SplitGateUp(torch.autograd.Function):
+    """Stacks separate gate/up weights for the fused kernel; splits the gradient back."""
+
+    @staticmethod
+    def forward(ctx, wg, wu):
+        ctx.rows = wg.shape[0]
+        return torch.cat([wg, wu], 0)
+
+    @staticmethod
+    def backward(ctx, d):
+        return d[:ctx.rows], d[ctx.rows:]
+
+
+def _text_layers(model):
+    """Every encoder and decoder text layer, in model order."""
+    backbone = model.backbone
+    yield from backbone.encoder.text_model.layers
+    yield from backbone.decoder.layers
+
+
+def _keep_or_replace(current, cls, recipe, build, message):
+    """Return ``current`` if already converted with ``recipe``; else a new module."""
+    if isinstance(current, cls):
+        if current.bongard_recipe != recipe:
+            raise ValueError(message)
+        return current
+    return build()
+
+
+def enable_te_linear(model, *, mlp=None, attention=None):
+    """Convert the MLP and/or the q/k/v/o projections of every text layer.
+
+    Returns ``{'mlp': layers converted, 'attention': projections converted}`` (keys only
+    for the kinds requested). Sets ``model.pack_multiple = 32``: the packed forward then
+    hands every projection a row count that needs no padding.
+    """
+    if not (mlp or attention) or model.device.type != 'cuda':
+        raise ValueError('TE projections require CUDA and at least one recipe')
+    if any(r is not None and r not in RECIPES for r in (mlp, attention)):
+        raise ValueError(f'TE recipe must be one of {RECIPES}')
+    model.pack_multiple = 32
+    counts = Counter()
+    for layer in _text_layers(model):
+        if mlp:
+            layer.mlp = _keep_or_replace(
+                layer.mlp, TEMLP, mlp, lambda: TEMLP(layer.mlp, mlp),
+                'An existing TE MLP must retain its recipe')
+            counts['mlp'] += 1
+        if not attention:
+            continue
+        attn = layer.self_attn
+        for proj in ATTENTION_PROJECTIONS:
+            current = getattr(attn, proj)
+            setattr(attn, proj, _keep_or_replace(
+                current, TELinear, attention, lambda: TELinear([current], attention),
+                'An existing TE projection must retain its recipe'))
+            counts['attention'] += 1
+    return dict(counts)
+
+
+def present(backbone):
+    """True if any module of ``backbone`` is one of this file's FP8 projections."""
+    for module in backbone.modules():
+        if _te_linear(module) or _te_mlp(module):
+            return True
+    return False
+
+
+def _pop_empty_extra_state(state, key):
+    if state.pop(key).numel() != 0:
+        raise ValueError('TE export requires stateless quantization scaling')
+
+
+def _mlp_export(prefix, module, state):
+    """HF keys for one TEMLP: gate_proj/up_proj/down_proj weights, no extra state."""
+    own = ['gate_up'] if module.fused_gate_up else ['gate_proj', 'up_proj']
+    for sub in own + ['down']:
+        _pop_empty_extra_state(state, f'{prefix}{sub}._extra_state')
+    if module.fused_gate_up:
+        stacked = state.pop(f'{prefix}gate_up.weight')
+        halves = stacked.split(module.intermediate_size)
+        state[f'{prefix}gate_proj.weight'], state[f'{prefix}up_proj.weight'] = halves
+    state[f'{prefix}down_proj.weight'] = state.pop(f'{prefix}down.weight')
+
+
+def restore_hf_layout(backbone, state):
+    """Rewrite ``state`` (a backbone state dict) to the Hugging Face module keys.
+
+    TEMLP weights go back to gate_proj/up_proj/down_proj; attention projections keep
+    their ``weight`` key. Every ``_extra_state`` entry is removed and must be empty:
+    exporting a module with stateful (delayed) scaling raises ValueError.
+    """
+    for name, module in backbone.named_modules():
+        if _te_mlp(module):
+            _mlp_export(name + '.', module, state)
+        elif _te_linear(module) and name.rpartition('.')[2] in ATTENTION_PROJECTIONS:
+            _pop_empty_extra_state(state, name + '._extra_state')
+    return state

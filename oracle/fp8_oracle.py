@@ -254,6 +254,46 @@ def mlp_forward(x_bf16, w_gate, w_up, w_down, *, shared_gate_up_scale=True, prec
                 wd_scale=ds, y=y)
 
 
+def linear_fwd_bwd(x, w, dy, *, precise=True):
+    """FP8 linear forward and backward (torchao tensorwise / TE HYBRID).
+
+    y = X8 W8^T; dX = dY8 W8; dW = dY8^T X8 with X, W in e4m3 and dY in e5m2, each with
+    its own current scale. Returns fp32 (y, dx, dw).
+    """
+    xq, _, xs, _ = quantize(x, E4M3)
+    wq, _, ws, _ = quantize(w, E4M3)
+    dq, _, ds, _ = quantize(dy, E5M2)
+    y = scaled_mm(xq, xs, E4M3, wq, ws, E4M3, precise=precise)
+    dx = scaled_mm(dq, ds, E5M2, wq.t().contiguous(), ws, E4M3, precise=precise)
+    dw = scaled_mm(dq.t().contiguous(), ds, E5M2, xq.t().contiguous(), xs, E4M3,
+                   precise=precise)
+    return y, dx, dw
+
+
+def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True):
+    """Backward of ``mlp_forward`` (shared gate/up scale) through the FP8 GEMMs.
+
+    dH = dY8 Wd8 (bf16), dWd = dY8^T H8, (dG, dU) = autograd of the bf16 gelu chain,
+    dGU quantized to e5m2 with one scale, dX = dGU8 Wgu8, dWgu = dGU8^T X8.
+    Returns fp32 (dx, dw_gate_up [2I, K], dw_down) and the bf16 dGU.
+    """
+    I = w_gate.shape[0]
+    dq, _, ds, _ = quantize(dy_bf16, E5M2)
+    wdq, _, wds, _ = quantize(w_down, E4M3)
+    dh = scaled_mm(dq, ds, E5M2, wdq.t().contiguous(), wds, E4M3, precise=precise)
+    dwd = scaled_mm(dq.t().contiguous(), ds, E5M2, fwd["hq"].t().contiguous(), fwd["h_scale"],
+                    E4M3, precise=precise)
+    dg, du = geglu_bwd(fwd["g"], fwd["u"], dh.to(torch.bfloat16))
+    dgu = torch.cat([dg, du], 1)
+    gq, _, gs, _ = quantize(dgu, E5M2)
+    wgu = torch.cat([w_gate, w_up], 0)
+    wq, _, wsc, _ = quantize(wgu, E4M3)
+    dx = scaled_mm(gq, gs, E5M2, wq.t().contiguous(), wsc, E4M3, precise=precise)
+    dwgu = scaled_mm(gq.t().contiguous(), gs, E5M2, fwd["xq"].t().contiguous(), fwd["x_scale"],
+                     E4M3, precise=precise)
+    return dx, dwgu, dwd, dgu
+
+
 # ---------------------------------------------------------------------------------------
 # RMSNorm with zero-centred gamma  (HF T5Gemma2RMSNorm; TE LayerNormMLP, fused_mlp.py:25-30)
 # ---------------------------------------------------------------------------------------
