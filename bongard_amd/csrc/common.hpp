@@ -59,10 +59,11 @@ __device__ __forceinline__ void store_nt(void* p, uint4 v) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays NaN (quietened, sign kept).
+// fp32 -> bf16 bits, round to nearest even; any NaN becomes 0x7FC0 (as torch's
+// c10::BFloat16 conversion does).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x0040u;
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 __device__ __forceinline__ float bf16_round(float f) {

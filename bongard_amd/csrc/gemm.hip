@@ -7,10 +7,11 @@
 // (+ bias), "TN" layout (both operands K-contiguous, as nn.Linear weights are).
 //
 // Design (one workgroup = 4 wave64, 256 x 256 output tile, K step 128 bytes):
-//  - global -> LDS through 16-byte buffer loads (out-of-range rows/K read as zero),
-//    staged in VGPRs one K step ahead, double-buffered LDS (2 x 64 KB);
-//  - LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at c ^ (r & 7) so
-//    that the MFMA fragment reads (8 rows x 16 bytes per lane group) hit all banks;
+//  - global -> LDS by direct 16-byte buffer loads into LDS (no VGPR staging;
+//    out-of-range rows/K read as zero), two LDS stages (2 x 64 KB);
+//  - LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at c ^ ((r >> 1) & 7)
+//    so that a fragment read (16 lanes = 16 rows x 16 bytes per LDS cycle on the 64-bank,
+//    256 B/clk gfx950 LDS) touches every bank once;
 //  - each wave owns a 128 x 128 sub-tile = 4 x 4 MFMA 32x32x64 tiles (256 fp32 acc);
 //    the MFMA "A" operand is the B (weight) tile, so every lane ends up holding four
 //    consecutive output columns of one row -> 8-byte bf16 / 16-byte fp32 stores;
@@ -19,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -30,6 +32,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 256, kBN = 256, kBK = 128;
+constexpr int kStages = 2;  // LDS pipeline depth (2 x 64 KB)
 constexpr int kThreads = 256;
 constexpr int kGroupM = 8;
 constexpr int kNumXcd = 8;
@@ -85,40 +88,103 @@ __device__ __forceinline__ v16f mfma(v8i a, v8i b, v16f c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
 }
 
+// Swizzled position of logical 16-byte chunk c in tile row r (128-byte rows).
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
 // Reads one MFMA operand fragment: 32 rows starting at `row0` of an LDS tile, K bytes
 // [kk*64, kk*64+64): lane l holds row row0 + (l & 31), bytes (l >> 5)*32 .. +31.
 __device__ __forceinline__ v8i read_frag(const uint8_t* tile, int row0, int kk, int lane) {
   const int row = row0 + (lane & 31);
   const int c = kk * 4 + (lane >> 5) * 2;
-  const int sw = row & 7;
   const uint8_t* base = tile + row * kBK;
-  v4u lo = *reinterpret_cast<const v4u*>(base + ((c ^ sw) << 4));
-  v4u hi = *reinterpret_cast<const v4u*>(base + (((c + 1) ^ sw) << 4));
+  v4u lo = *reinterpret_cast<const v4u*>(base + (swz(row, c) << 4));
+  v4u hi = *reinterpret_cast<const v4u*>(base + (swz(row, c + 1) << 4));
   v8i r;
   r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
   r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
   return r;
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16x2 with round-to-nearest-even (gfx950 v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Epilogue staging in LDS: rows of CHUNKS 16-byte chunks; chunk c of row r lives at
+// c ^ (r & (CHUNKS - 1)). Lanes put 8-byte runs (4 bf16) and get 16-byte chunks.
+template <int CHUNKS>
+__device__ __forceinline__ void stage_put(uint8_t* buf, int row, int col, uint2 v) {
+  const int c = col >> 3, half = (col >> 2) & 1;
+  *reinterpret_cast<uint2*>(buf + row * (CHUNKS * 16) + ((c ^ (row & (CHUNKS - 1))) << 4) +
+                            half * 8) = v;
+}
+template <int CHUNKS>
+__device__ __forceinline__ uint4 stage_get(const uint8_t* buf, int row, int c) {
+  return *reinterpret_cast<const uint4*>(buf + row * (CHUNKS * 16) +
+                                         ((c ^ (row & (CHUNKS - 1))) << 4));
+}
+// 8 bf16 to global: one 16-byte store when the row stride keeps it aligned.
+__device__ __forceinline__ void store_bf16x8(uint16_t* dst, uint4 d, int64_t ld) {
+  if ((ld & 7) == 0) {
+    *reinterpret_cast<uint4*>(dst) = d;
+  } else {
+    reinterpret_cast<uint2*>(dst)[0] = make_uint2(d.x, d.y);
+    reinterpret_cast<uint2*>(dst)[1] = make_uint2(d.z, d.w);
+  }
+}
+
+// gelu_tanh(x) = 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
+// the identical x / (1 + exp(-2u)): no cancellation of 1 + tanh(u) for negative x, and
+// two transcendental instructions (v_exp_f32, v_rcp_f32) instead of a libm tanh.
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
-  // 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), evaluated in fp32 in the
-  // order of PyTorch's CPU kernel for reduced-precision inputs, without FMA contraction.
-#pragma clang fp contract(off)
   const float kBeta = 0.7978845608028654f;
   const float kKappa = 0.044715f;
-  float x3 = x * x * x;
-  float inner = kBeta * (x + kKappa * x3);
-  return 0.5f * x * (1.0f + tanhf(inner));
+  const float kM2Log2e = -2.8853900817779268f;  // -2 / ln 2
+  const float u = kBeta * (x + kKappa * (x * x * x));
+  const float e = __builtin_amdgcn_exp2f(u * kM2Log2e);  // exp(-2u)
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
+
+// Stage layout in LDS: [A tile | B tile], each kBM (= kBN) rows of kBK bytes.
+constexpr int kStageBytes = 2 * kTileBytes;
+constexpr int kBlocksPerTile = kTileBytes / 1024;   // 1 KB DMA blocks per operand tile
+constexpr int kRowsPerBlock = 1024 / kBK;           // tile rows covered by one DMA block
+constexpr int kChunksPerRow = kBK / 16;
+constexpr int kDmaPerWave = kBlocksPerTile / 4;     // per operand, per wave, per stage
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Issues one stage of direct global->LDS loads (16 bytes per lane). Lane l of DMA block
+// b fills LDS bytes [b*1024 + 16 l, +16): tile row b*kRowsPerBlock + l / kChunksPerRow,
+// physical chunk l % kChunksPerRow, i.e. logical chunk swz(row, physical).
+__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                          const uint32_t* a_off, const uint32_t* b_off,
+                                          uint8_t* stage, int wid, uint32_t k0) {
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int blk = wid * kDmaPerWave + j;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(stage + blk * 1024), 16, a_off[j],
+                                             k0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(stage + kTileBytes + blk * 1024),
+                                             16, b_off[j], k0, 0, 0);
+  }
+}
+
+struct Frags {
+  v8i b[4];  // MFMA "A" operand: weight-tile rows (output columns)
+  v8i a[4];  // MFMA "B" operand: activation-tile rows (output rows)
+};
 
 template <int FA, int FB, int EPI, int OUT>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(1, 1))) void
 gemm_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * kTileBytes];
-  // stage s: A tile at smem + 2s * kTileBytes, B tile right after it.
-  auto sA = [&](int s) { return smem + (2 * s) * kTileBytes; };
-  auto sB = [&](int s) { return smem + (2 * s + 1) * kTileBytes; };
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
+  static_assert(kStages == 2, "the main loop below alternates two stages");
 
   int tm, tn;
   tile_coords(p, tm, tn);
@@ -133,44 +199,42 @@ gemm_kernel(GemmParams p) {
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)((int64_t)p.M * p.lda));
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)((int64_t)p.N * p.ldb));
 
-  // Loader mapping: thread t moves chunk (t & 7) of rows (t >> 3) + 32 j, j = 0..7.
-  const int lrow = t >> 3;
-  const int lchunk = t & 7;
-  const int lds_chunk = lchunk ^ (lrow & 7);
-  uint32_t a_off[8], b_off[8];
+  // Per-lane DMA source offsets (without k0) for this wave's blocks of each operand.
+  const int lrow = lane / kChunksPerRow;
+  const int pchunk = lane % kChunksPerRow;
+  uint32_t a_off[kDmaPerWave], b_off[kDmaPerWave];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int r = lrow + 32 * j;
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int r = (wid * kDmaPerWave + j) * kRowsPerBlock + lrow;  // tile row
+    const int c = swz(r, pchunk);                                   // logical chunk
     const int am = m0 + r;
-    a_off[j] = am < p.M ? (uint32_t)((int64_t)am * p.lda + lchunk * 16) : kOob;
+    a_off[j] = am < p.M ? (uint32_t)((int64_t)am * p.lda + c * 16) : kOob;
     int bn;
-    if (EPI == EPI_GEGLU)
+    bool bvalid;
+    if (EPI == EPI_GEGLU) {
       bn = r < 128 ? n0 + r : p.I + n0 + (r - 128);
-    else
+      bvalid = n0 + (r & 127) < p.I;
+    } else {
       bn = n0 + r;
-    const bool bvalid = (EPI == EPI_GEGLU) ? (n0 + (r & 127) < p.I) : (bn < p.N);
-    b_off[j] = bvalid ? (uint32_t)((int64_t)bn * p.ldb + lchunk * 16) : kOob;
+      bvalid = bn < p.N;
+    }
+    b_off[j] = bvalid ? (uint32_t)((int64_t)bn * p.ldb + c * 16) : kOob;
   }
-
-  v4u pa[8], pb[8];
-  auto gload = [&](int k0) {
-    const bool kvalid = k0 + lchunk * 16 < p.K;
+  // K tail (K % kBK != 0): chunks at or beyond K must read as zero; only the last stage
+  // can contain them, and it gets masked offsets.
+  const int ksteps = (p.K + kBK - 1) / kBK;
+  const bool k_tail = (p.K % kBK) != 0;
+  uint32_t a_off_t[kDmaPerWave], b_off_t[kDmaPerWave];
+  if (k_tail) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t oa = (kvalid && a_off[j] != kOob) ? a_off[j] + k0 : kOob;
-      const uint32_t ob = (kvalid && b_off[j] != kOob) ? b_off[j] + k0 : kOob;
-      pa[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, oa, 0, 0);
-      pb[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, ob, 0, 0);
+    for (int j = 0; j < kDmaPerWave; ++j) {
+      const int r = (wid * kDmaPerWave + j) * kRowsPerBlock + lrow;
+      const int c = swz(r, pchunk);
+      const bool cvalid = (ksteps - 1) * kBK + c * 16 < p.K;
+      a_off_t[j] = cvalid ? a_off[j] : kOob;
+      b_off_t[j] = cvalid ? b_off[j] : kOob;
     }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = lrow + 32 * j;
-      *reinterpret_cast<v4u*>(sA(buf) + r * kBK + lds_chunk * 16) = pa[j];
-      *reinterpret_cast<v4u*>(sB(buf) + r * kBK + lds_chunk * 16) = pb[j];
-    }
-  };
+  }
 
   // MFMA-A rows (weight tile rows) per n-subtile, MFMA-B rows (activation rows) per m.
   int brow[4];
@@ -182,6 +246,13 @@ gemm_kernel(GemmParams p) {
       brow[s] = wn * 128 + s * 32;
   }
 
+  auto load_frags = [&](Frags& f, const uint8_t* stage, int kk) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f.b[s] = read_frag(stage + kTileBytes, brow[s], kk, lane);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f.a[s] = read_frag(stage, wm * 128 + s * 32, kk, lane);
+  };
+
   v16f acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -190,38 +261,93 @@ gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const int ksteps = (p.K + kBK - 1) / kBK;
-  gload(0);
-  sstore(0);
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma<FB, FA>(f.b[i], f.a[j], acc[i][j]);
+  };
+
+  // Pipeline (2 LDS stages, 2 MFMA sub-steps of 64 K-bytes per stage). Iteration ks:
+  //   read frags(ks, kk=1) | 16 MFMAs (kk=0) | wait DMA(ks+1) + barrier |
+  //   read frags(ks+1, kk=0) | DMA(ks+2) into the stage just released | 16 MFMAs (kk=1)
+  // The MFMA pipe always consumes operands read one sub-step earlier, each DMA has two
+  // sub-steps (~2k MFMA cycles) to land, and the one barrier per stage sits mid-stream.
+  // sched_barrier pins this order.
+  auto dma = [&](int kstep, uint8_t* stage) {
+    const uint32_t k0 = (uint32_t)kstep * kBK;
+    if (k_tail && kstep == ksteps - 1)
+      dma_stage(ra, rb, a_off_t, b_off_t, stage, wid, k0);
+    else
+      dma_stage(ra, rb, a_off, b_off, stage, wid, k0);
+  };
+  dma(0, smem);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  int cur = 0;
+  Frags f0, f1;
+  load_frags(f0, smem, 0);
+  if (ksteps > 1) dma(1, smem + kStageBytes);
   for (int ks = 0; ks < ksteps; ++ks) {
-    const bool more = ks + 1 < ksteps;
-    if (more) gload((ks + 1) * kBK);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      v8i fb[4], fa[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) fb[s] = read_frag(sB(cur), brow[s], kk, lane);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) fa[s] = read_frag(sA(cur), wm * 128 + s * 32, kk, lane);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma<FB, FA>(fb[i], fa[j], acc[i][j]);
-    }
-    if (more) sstore(cur ^ 1);
+    uint8_t* cur = smem + (ks & 1) * kStageBytes;
+    uint8_t* nxt = smem + ((ks & 1) ^ 1) * kStageBytes;
+    load_frags(f1, cur, 1);
+    mma(f0);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    cur ^= 1;
+    __builtin_amdgcn_sched_barrier(0);
+    if (ks + 1 < ksteps) load_frags(f0, nxt, 0);
+    if (ks + 2 < ksteps) dma(ks + 2, cur);
+    mma(f1);
   }
+  __syncthreads();  // every wave is done with the stages before the epilogue reuses them
 
   // ---- epilogue --------------------------------------------------------------------
-  // acc[i][j][r]: n-subtile i, m-subtile j; row m = m0 + wm*128 + j*32 + (lane & 31),
-  // column (within the n-subtile) 8*(r/4) + (lane >> 5)*4 + (r & 3).
+  // acc[i][j][r]: n-subtile i, m-subtile j; row m = wm*128 + j*32 + (lane & 31) of the
+  // tile, column (within the n-subtile) 8*(r/4) + (lane >> 5)*4 + (r & 3): each lane
+  // holds runs of four consecutive columns. bf16 results are staged through this wave's
+  // own LDS region of the (now idle) pipeline ring and leave as 16-byte row segments,
+  // 16 lanes per 256-byte row.
   const float sa = *p.a_sinv;
   const int lrow_m = lane & 31;
   const int lcol = (lane >> 5) * 4;
-  if (EPI == EPI_LINEAR) {
+  if (EPI == EPI_LINEAR && OUT == BF8_OUT_BF16) {
+    uint8_t* wbuf = smem + wid * (128 * 256);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = i * 32 + 8 * q + lcol;  // within the wave's 128 columns
+        const int n = n0 + wn * 128 + col;
+        int seg = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < p.n_seg && n >= p.seg_end[s2]) ? 1 : 0;
+        const float alpha = sa * p.b_sinv[seg * p.b_stride];
+        float bias[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias && n < p.N) {
+          const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
+          bias[0] = bf16_lo(bb.x); bias[1] = bf16_hi(bb.x);
+          bias[2] = bf16_lo(bb.y); bias[3] = bf16_hi(bb.y);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint2 w;
+          w.x = pack_bf16x2(acc[i][j][4 * q + 0] * alpha + bias[0], acc[i][j][4 * q + 1] * alpha + bias[1]);
+          w.y = pack_bf16x2(acc[i][j][4 * q + 2] * alpha + bias[2], acc[i][j][4 * q + 3] * alpha + bias[3]);
+          stage_put<16>(wbuf, j * 32 + lrow_m, col, w);
+        }
+      }
+    }
+    const int gn = n0 + wn * 128 + (lane & 15) * 8;
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {
+      const int row = it * 4 + (lane >> 4);
+      const uint4 d = stage_get<16>(wbuf, row, lane & 15);
+      const int gm = m0 + wm * 128 + row;
+      if (gm < p.M && gn < p.N)
+        store_bf16x8(reinterpret_cast<uint16_t*>(p.C) + (int64_t)gm * p.ldc + gn, d, p.ldc);
+    }
+  } else if (EPI == EPI_LINEAR) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -230,7 +356,7 @@ gemm_kernel(GemmParams p) {
         if (n >= p.N) continue;
         int seg = 0;
 #pragma unroll
-        for (int s = 0; s < 3; ++s) seg += (s + 1 < p.n_seg && n >= p.seg_end[s]) ? 1 : 0;
+        for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < p.n_seg && n >= p.seg_end[s2]) ? 1 : 0;
         const float alpha = sa * p.b_sinv[seg * p.b_stride];
         float bias[4] = {0.f, 0.f, 0.f, 0.f};
         if (p.bias) {
@@ -242,58 +368,74 @@ gemm_kernel(GemmParams p) {
         for (int j = 0; j < 4; ++j) {
           const int m = m0 + wm * 128 + j * 32 + lrow_m;
           if (m >= p.M) continue;
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e] * alpha + bias[e];
-          if (OUT == BF8_OUT_BF16) {
-            uint16_t* c = reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n;
-            uint2 w;
-            w.x = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-            w.y = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-            *reinterpret_cast<uint2*>(c) = w;
-          } else {
-            float* c = reinterpret_cast<float*>(p.C) + (int64_t)m * p.ldc + n;
-            *reinterpret_cast<float4*>(c) = make_float4(v[0], v[1], v[2], v[3]);
-          }
+          float* c = reinterpret_cast<float*>(p.C) + (int64_t)m * p.ldc + n;
+          *reinterpret_cast<float4*>(c) =
+              make_float4(acc[i][j][4 * q + 0] * alpha + bias[0], acc[i][j][4 * q + 1] * alpha + bias[1],
+                          acc[i][j][4 * q + 2] * alpha + bias[2], acc[i][j][4 * q + 3] * alpha + bias[3]);
         }
       }
     }
   } else {
-    // Gated GELU: acc[i] (gate) pairs with acc[i + 2] (up) for i = 0, 1.
+    // Gated GELU: acc[i] (gate) pairs with acc[i + 2] (up) for i = 0, 1. The wave owns
+    // H rows wm*128 .. +128 and columns wn*64 .. +64 of this tile (128-byte LDS rows).
+    // Pass 0 stages H (and accumulates its amax); passes 1, 2 stage the bf16 gate / up
+    // pre-activations when the caller keeps them for the backward.
     const float ag = sa * p.b_sinv[0];
     const float au = sa * p.b_sinv[p.b_stride];
+    uint8_t* wbuf = smem + wid * (128 * 128);
     uint32_t hmax = 0;
+    auto run_pass = [&](auto pass_tag) {
+      constexpr int pass = decltype(pass_tag)::value;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < 2; ++i) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = n0 + wn * 64 + i * 32 + 8 * q + lcol;  // column of H (index into I)
-        if (col >= p.I) continue;
+        for (int q = 0; q < 4; ++q) {
+          const int col = i * 32 + 8 * q + lcol;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = m0 + wm * 128 + j * 32 + lrow_m;
-          if (m >= p.M) continue;
-          uint32_t hb[4], gb[4], ub[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            gb[e] = f32_to_bf16_bits(acc[i][j][4 * q + e] * ag);
-            ub[e] = f32_to_bf16_bits(acc[i + 2][j][4 * q + e] * au);
-            const float g = __uint_as_float(gb[e] << 16);
-            const float u = __uint_as_float(ub[e] << 16);
-            const float gl = bf16_round(gelu_tanh_f32(g));
-            hb[e] = f32_to_bf16_bits(gl * u);
-            hmax = max(hmax, (hb[e] & 0x7FFFu) << 16);
-          }
-          uint16_t* h = reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + col;
-          *reinterpret_cast<uint2*>(h) = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
-          if (p.GU) {
-            uint16_t* g = p.GU + (int64_t)m * (2 * (int64_t)p.I) + col;
-            *reinterpret_cast<uint2*>(g) = make_uint2(gb[0] | (gb[1] << 16), gb[2] | (gb[3] << 16));
-            *reinterpret_cast<uint2*>(g + p.I) =
-                make_uint2(ub[0] | (ub[1] << 16), ub[2] | (ub[3] << 16));
+          for (int j = 0; j < 4; ++j) {
+            const float ga[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                 acc[i][j][4 * q + 3]};
+            const float ua[4] = {acc[i + 2][j][4 * q], acc[i + 2][j][4 * q + 1],
+                                 acc[i + 2][j][4 * q + 2], acc[i + 2][j][4 * q + 3]};
+            uint32_t w0, w1;  // packed bf16 pairs (columns 0-1, 2-3 of the run)
+            if constexpr (pass == 0) {
+              const uint32_t g01 = pack_bf16x2(ga[0] * ag, ga[1] * ag);
+              const uint32_t g23 = pack_bf16x2(ga[2] * ag, ga[3] * ag);
+              const uint32_t u01 = pack_bf16x2(ua[0] * au, ua[1] * au);
+              const uint32_t u23 = pack_bf16x2(ua[2] * au, ua[3] * au);
+              const uint32_t l01 = pack_bf16x2(gelu_tanh_f32(bf16_lo(g01)), gelu_tanh_f32(bf16_hi(g01)));
+              const uint32_t l23 = pack_bf16x2(gelu_tanh_f32(bf16_lo(g23)), gelu_tanh_f32(bf16_hi(g23)));
+              w0 = pack_bf16x2(bf16_lo(l01) * bf16_lo(u01), bf16_hi(l01) * bf16_hi(u01));
+              w1 = pack_bf16x2(bf16_lo(l23) * bf16_lo(u23), bf16_hi(l23) * bf16_hi(u23));
+              const uint32_t a0 = w0 & 0x7FFF7FFFu, a1 = w1 & 0x7FFF7FFFu;
+              hmax = max(hmax, max(max(a0 << 16, a0 & 0xFFFF0000u), max(a1 << 16, a1 & 0xFFFF0000u)));
+            } else if constexpr (pass == 1) {
+              w0 = pack_bf16x2(ga[0] * ag, ga[1] * ag);
+              w1 = pack_bf16x2(ga[2] * ag, ga[3] * ag);
+            } else {
+              w0 = pack_bf16x2(ua[0] * au, ua[1] * au);
+              w1 = pack_bf16x2(ua[2] * au, ua[3] * au);
+            }
+            stage_put<8>(wbuf, j * 32 + lrow_m, col, make_uint2(w0, w1));
           }
         }
       }
+      uint16_t* dst = pass == 0 ? reinterpret_cast<uint16_t*>(p.C) : p.GU;
+      const int64_t ld = pass == 0 ? p.ldc : 2 * (int64_t)p.I;
+      const int coff = pass == 2 ? p.I : 0;
+      const int gcol = coff + n0 + wn * 64 + (lane & 7) * 8;
+#pragma unroll 4
+      for (int it = 0; it < 16; ++it) {
+        const int row = it * 8 + (lane >> 3);
+        const uint4 d = stage_get<8>(wbuf, row, lane & 7);
+        const int gm = m0 + wm * 128 + row;
+        if (gm < p.M) store_bf16x8(dst + (int64_t)gm * ld + gcol, d, ld);
+      }
+    };
+    run_pass(std::integral_constant<int, 0>{});
+    if (p.GU) {
+      run_pass(std::integral_constant<int, 1>{});
+      run_pass(std::integral_constant<int, 2>{});
     }
     hmax = block_max_u32<kThreads>(hmax);
     if (t == 0) p.partials[blockIdx.x] = hmax;

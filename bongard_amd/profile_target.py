@@ -1,0 +1,61 @@
+"""Profiling target: launches the FP8 path's kernels a few times at BASELINE config-2 size.
+
+Run under rocprofv3 (kernel trace or PMC counters). Besides the FP8 kernels it launches a
+plain device-to-device copy of a known byte count, the calibration that turns the
+FETCH_SIZE / WRITE_SIZE counters into bytes.
+
+    python -m bongard_amd.profile_target [--iters N] [--rows M] [--case c2|square]
+
+``c2``: the whole config-2 MLP forward (quantize X and weights, gate/up GEMM + gated-GELU
+epilogue, H scale + cast, down GEMM). ``square``: one 8192^3 e4m3 GEMM, the steady-state
+main loop with no epilogue-heavy work.
+"""
+
+import argparse
+
+import torch
+
+from . import ops, workloads
+
+COPY_BYTES = 256 << 20
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--iters", type=int, default=5)
+    p.add_argument("--rows", type=int, default=4096)
+    p.add_argument("--case", choices=("c2", "square"), default="c2")
+    args = p.parse_args()
+    dev = torch.device("cuda:0")
+    if args.case == "square":
+        g = torch.Generator(device=dev).manual_seed(0)
+        a = torch.randn(8192, 8192, device=dev, generator=g).to(torch.bfloat16)
+        b = (torch.randn(8192, 8192, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        aq, bq = ops.quantize(a), ops.quantize(b)
+        for _ in range(args.iters):
+            ops.gemm(aq.data, ops.E4M3, aq.meta, bq.data, ops.E4M3, bq.meta)
+        torch.cuda.synchronize()
+        print(f"profile_target done: {args.iters} x 8192^3 GEMM", flush=True)
+        return
+    c = workloads.config2(rows=args.rows)
+    I = workloads.INTERMEDIATE
+    x = c["x"].to(dev)
+    w_gu = torch.cat([c["w_gate"], c["w_up"]], 0).to(dev)
+    w_d = c["w_down"].to(dev)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(args.iters):
+        dst.copy_(src)
+        xq = ops.quantize(x, ops.E4M3)
+        gq = ops.quantize(w_gu, ops.E4M3)
+        dq = ops.quantize(w_d, ops.E4M3)
+        H, _, parts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
+        hm = ops.scale_from_partials(parts, ops.E4M3)
+        hq = ops.cast(H, hm, ops.E4M3)
+        ops.gemm(hq.data, ops.E4M3, hm, dq.data, ops.E4M3, dq.meta)
+    torch.cuda.synchronize()
+    print(f"profile_target done: {args.iters} iterations, copy {COPY_BYTES} bytes", flush=True)
+
+
+if __name__ == "__main__":
+    main()
