@@ -60,9 +60,39 @@ struct GemmParams {
   uint32_t* partials;
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           0x00020000);
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource (4 SGPRs): base, stride 0, `bytes` valid bytes (offsets at or beyond
+// read as zero), raw-buffer flags of gfx9/gfx950.
+__device__ __forceinline__ i32x4 make_srd(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xFFFFu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16-byte-per-lane load from a buffer straight into LDS: lane l's bytes land at
+// lds_addr + 16 l. Written as inline asm so that the compiler's wait-count pass does
+// not serialise it against LDS reads of other stages (it cannot prove they do not
+// alias); the kernel orders it with explicit vmcnt waits and barriers instead. M0 is
+// set inside the same asm block, immediately before its only use.
+__device__ __forceinline__ void dma16(i32x4 srd, uint32_t lds_addr, uint32_t voff,
+                                      uint32_t soff) {
+  // lds_addr and soff are wave-uniform; readfirstlane puts them in SGPRs
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0v), "v"(voff), "s"(srd), "s"(so)
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const uint8_t*)(p));
 }
 
 __device__ __forceinline__ void tile_coords(const GemmParams& p, int& tm, int& tn) {
@@ -91,8 +121,16 @@ __device__ __forceinline__ v16f mfma(v8i a, v8i b, v16f c) {
 // Swizzled position of logical 16-byte chunk c in tile row r (128-byte rows).
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
-// Reads one MFMA operand fragment: 32 rows starting at `row0` of an LDS tile, K bytes
-// [kk*64, kk*64+64): lane l holds row row0 + (l & 31), bytes (l >> 5)*32 .. +31.
+// Reads 16 bytes of an MFMA operand fragment: 32 rows starting at `row0` of an LDS tile,
+// K bytes [kk*64, kk*64+64); lane l holds row row0 + (l & 31), bytes (l >> 5)*32 + 16*half
+// .. +15 (two halves make the lane's 32 bytes).
+__device__ __forceinline__ v4u read_half(const uint8_t* tile, int row0, int kk, int half,
+                                         int lane) {
+  const int row = row0 + (lane & 31);
+  const int c = kk * 4 + (lane >> 5) * 2 + half;
+  return *reinterpret_cast<const v4u*>(tile + row * kBK + (swz(row, c) << 4));
+}
+
 __device__ __forceinline__ v8i read_frag(const uint8_t* tile, int row0, int kk, int lane) {
   const int row = row0 + (lane & 31);
   const int c = kk * 4 + (lane >> 5) * 2;
@@ -156,28 +194,48 @@ constexpr int kRowsPerBlock = 1024 / kBK;           // tile rows covered by one 
 constexpr int kChunksPerRow = kBK / 16;
 constexpr int kDmaPerWave = kBlocksPerTile / 4;     // per operand, per wave, per stage
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
 // Issues one stage of direct global->LDS loads (16 bytes per lane). Lane l of DMA block
 // b fills LDS bytes [b*1024 + 16 l, +16): tile row b*kRowsPerBlock + l / kChunksPerRow,
 // physical chunk l % kChunksPerRow, i.e. logical chunk swz(row, physical).
-__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
-                                          const uint32_t* a_off, const uint32_t* b_off,
-                                          uint8_t* stage, int wid, uint32_t k0) {
+__device__ __forceinline__ void dma_stage(i32x4 ra, i32x4 rb, const uint32_t* a_off,
+                                          const uint32_t* b_off, uint8_t* stage, int wid,
+                                          uint32_t k0) {
+  const uint32_t base = lds_addr(stage);
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
     const int blk = wid * kDmaPerWave + j;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(stage + blk * 1024), 16, a_off[j],
-                                             k0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(stage + kTileBytes + blk * 1024),
-                                             16, b_off[j], k0, 0, 0);
+    dma16(ra, base + blk * 1024, a_off[j], k0);
+    dma16(rb, base + kTileBytes + blk * 1024, b_off[j], k0);
   }
 }
 
+// One of the wave's DMA loads of a stage: x = 0..15 -> operand (x & 1: 0 = A, 1 = B),
+// block j = x >> 1 of this wave.
+__device__ __forceinline__ void dma_one(i32x4 ra, i32x4 rb, const uint32_t* a_off,
+                                        const uint32_t* b_off, uint8_t* stage, int wid,
+                                        uint32_t k0, int x) {
+  const int j = x >> 1;
+  const uint32_t dst = lds_addr(stage) + (wid * kDmaPerWave + j) * 1024;
+  if ((x & 1) == 0)
+    dma16(ra, dst, a_off[j], k0);
+  else
+    dma16(rb, dst + kTileBytes, b_off[j], k0);
+}
+
+// The 8 operand fragments of one MFMA sub-step as 16 halves (16 bytes each), in the order
+// the MFMAs of the sub-step consume them: b0, a0, a1, a2, a3, b1, b2, b3.
 struct Frags {
-  v8i b[4];  // MFMA "A" operand: weight-tile rows (output columns)
-  v8i a[4];  // MFMA "B" operand: activation-tile rows (output rows)
+  v4u h[16];
 };
+__device__ __forceinline__ int half_b(int i) { return i == 0 ? 0 : 8 + 2 * i; }
+__device__ __forceinline__ int half_a(int j) { return 2 + 2 * j; }
+__device__ __forceinline__ v8i frag_of(const Frags& f, int first) {
+  const v4u lo = f.h[first], hi = f.h[first + 1];
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
 
 template <int FA, int FB, int EPI, int OUT>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
@@ -196,8 +254,8 @@ gemm_kernel(GemmParams p) {
   const int wid = t >> 6;
   const int wm = wid & 1, wn = wid >> 1;
 
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)((int64_t)p.M * p.lda));
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, (uint32_t)((int64_t)p.N * p.ldb));
+  const i32x4 ra = make_srd(p.A, (uint32_t)((int64_t)p.M * p.lda));
+  const i32x4 rb = make_srd(p.B, (uint32_t)((int64_t)p.N * p.ldb));
 
   // Per-lane DMA source offsets (without k0) for this wave's blocks of each operand.
   const int lrow = lane / kChunksPerRow;
@@ -246,11 +304,24 @@ gemm_kernel(GemmParams p) {
       brow[s] = wn * 128 + s * 32;
   }
 
+  // Row of the LDS tile where half h of the sub-step's fragments starts, and its tile.
+  auto half_src = [&](int h, const uint8_t* stage, int& row0) -> const uint8_t* {
+    const int fr = h >> 1;  // 0: b0, 1..4: a0..a3, 5..7: b1..b3
+    if (fr == 0 || fr >= 5) {
+      row0 = brow[fr == 0 ? 0 : fr - 4];
+      return stage + kTileBytes;
+    }
+    row0 = wm * 128 + (fr - 1) * 32;
+    return stage;
+  };
+  auto read_one = [&](Frags& f, const uint8_t* stage, int kk, int h) {
+    int row0;
+    const uint8_t* tile = half_src(h, stage, row0);
+    f.h[h] = read_half(tile, row0, kk, h & 1, lane);
+  };
   auto load_frags = [&](Frags& f, const uint8_t* stage, int kk) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) f.b[s] = read_frag(stage + kTileBytes, brow[s], kk, lane);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) f.a[s] = read_frag(stage, wm * 128 + s * 32, kk, lane);
+    for (int h = 0; h < 16; ++h) read_one(f, stage, kk, h);
   };
 
   v16f acc[4][4];
@@ -261,19 +332,21 @@ gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  auto mma = [&](const Frags& f) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma<FB, FA>(f.b[i], f.a[j], acc[i][j]);
+  // MFMA number x of a sub-step: n-subtile x >> 2, m-subtile x & 3.
+  auto mma_one = [&](const Frags& f, int x) {
+    const int i = x >> 2, j = x & 3;
+    acc[i][j] = mfma<FB, FA>(frag_of(f, half_b(i)), frag_of(f, half_a(j)), acc[i][j]);
   };
 
   // Pipeline (2 LDS stages, 2 MFMA sub-steps of 64 K-bytes per stage). Iteration ks:
-  //   read frags(ks, kk=1) | 16 MFMAs (kk=0) | wait DMA(ks+1) + barrier |
-  //   read frags(ks+1, kk=0) | DMA(ks+2) into the stage just released | 16 MFMAs (kk=1)
-  // The MFMA pipe always consumes operands read one sub-step earlier, each DMA has two
-  // sub-steps (~2k MFMA cycles) to land, and the one barrier per stage sits mid-stream.
-  // sched_barrier pins this order.
+  //   16 x {MFMA(ks, kk=0), read 1/16 of frags(ks, kk=1)} | wait DMA(ks+1) + barrier |
+  //   16 x {MFMA(ks, kk=1), read 1/16 of frags(ks+1, kk=0), 1 DMA load of stage ks+2}
+  // Each MFMA consumes operands read one sub-step earlier; each DMA has two sub-steps
+  // (~2k MFMA cycles) to land; one LDS read and one texture-unit load sit between
+  // consecutive MFMAs, so neither unit (both shared by the four waves) blocks MFMA issue.
+  // sched_barrier(0) pins the order. Loads past the last stage read zeros (kOob) into a
+  // stage that is never read again, which keeps the loop free of branches.
+  const uint32_t kend = (uint32_t)ksteps * kBK;
   auto dma = [&](int kstep, uint8_t* stage) {
     const uint32_t k0 = (uint32_t)kstep * kBK;
     if (k_tail && kstep == ksteps - 1)
@@ -290,17 +363,34 @@ gemm_kernel(GemmParams p) {
   for (int ks = 0; ks < ksteps; ++ks) {
     uint8_t* cur = smem + (ks & 1) * kStageBytes;
     uint8_t* nxt = smem + ((ks & 1) ^ 1) * kStageBytes;
-    load_frags(f1, cur, 1);
-    mma(f0);
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      mma_one(f0, x);
+      read_one(f1, cur, 1, x);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    if (ks + 1 < ksteps) load_frags(f0, nxt, 0);
-    if (ks + 2 < ksteps) dma(ks + 2, cur);
-    mma(f1);
+    // stage ks+2's DMA: zero-fill offsets past K; the K-tail stage uses masked offsets
+    const uint32_t k2 = (uint32_t)(ks + 2) * kBK;
+    const bool tail2 = k_tail && ks + 2 == ksteps - 1;
+    const uint32_t* ao = tail2 ? a_off_t : a_off;
+    const uint32_t* bo = tail2 ? b_off_t : b_off;
+    const uint32_t k2s = k2 < kend ? k2 : 0x40000000u;  // beyond K: offset >= 2^30 -> OOB
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      mma_one(f1, x);
+      read_one(f0, nxt, 0, x);
+      dma_one(ra, rb, ao, bo, cur, wid, k2s, x);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
-  __syncthreads();  // every wave is done with the stages before the epilogue reuses them
+  // The last iteration's zero-fill loads still target LDS: drain them, and let every wave
+  // finish with the stages, before the epilogue reuses the space.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 
   // ---- epilogue --------------------------------------------------------------------
   // acc[i][j][r]: n-subtile i, m-subtile j; row m = wm*128 + j*32 + (lane & 31) of the
