@@ -1,0 +1,46 @@
+"""Summaries of rocprofv3 result databases (kernel trace and PMC counters).
+
+    python -m bongard_amd.profile_summary trace <results.db>
+    python -m bongard_amd.profile_summary pmc <results.db>
+
+``trace``: per-kernel call count and average / min / max duration (us) from the
+kernel-dispatch records. ``pmc``: per-kernel, per-counter average value per dispatch.
+"""
+import sqlite3, sys, re
+def short(n):
+    n = n.replace("(anonymous namespace)", "anon")
+    depth = 0
+    for i, ch in enumerate(n):
+        if ch == '<': depth += 1
+        elif ch == '>': depth -= 1
+        elif ch == '(' and depth == 0:
+            n = n[:i]; break
+    n = n.replace("void ", "").replace("bf8::anon::", "")
+    return n[:70]
+def kernel_stats(path):
+    db = sqlite3.connect(path); cur = db.cursor()
+    rows = cur.execute("select name, start, end from kernels").fetchall()
+    agg = {}
+    for name, s, e in rows:
+        d = (e - s) / 1e3
+        a = agg.setdefault(short(name), [0, 0.0, 1e18, 0])
+        a[0] += 1; a[1] += d; a[2] = min(a[2], d); a[3] = max(a[3], d)
+    tot = sum(v[1] for v in agg.values())
+    out = [f"{'kernel':70s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'time%':>7s}"]
+    for k, v in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"{k:70s} {v[0]:6d} {v[1]/v[0]:9.2f} {v[2]:9.2f} {v[3]:9.2f} {100*v[1]/tot:7.2f}")
+    return "\n".join(out)
+def pmc(path):
+    db = sqlite3.connect(path); cur = db.cursor()
+    rows = cur.execute("select kernel_name, counter_name, value, grid_size from counters_collection").fetchall()
+    agg = {}
+    for name, c, v, g in rows:
+        a = agg.setdefault((short(name), c, g), [0, 0.0])
+        a[0] += 1; a[1] += v
+    return {k: v[1] / v[0] for k, v in agg.items()}
+if __name__ == "__main__":
+    if sys.argv[1] == "trace":
+        print(kernel_stats(sys.argv[2]))
+    else:
+        for k, v in sorted(pmc(sys.argv[2]).items()):
+            print(f"{k[0]:70s} {k[1]:11s} grid={k[2]:<10d} {v:14.1f} KiB/dispatch")
