@@ -81,9 +81,9 @@ def main():
             dq = ops.quantize(w_d, ops.E4M3)
         else:
             gq, dq = cached
-        H, _, parts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
-        hm = ops.scale_from_partials(parts, ops.E4M3)
-        hq = ops.cast(H, hm, ops.E4M3)
+        H, _, hparts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
+        hq = ops.cast_partials(H, hparts, ops.E4M3)
+        hm = hq.meta
         return ops.gemm(hq.data, ops.E4M3, hm, dq.data, ops.E4M3, dq.meta)
 
     def timed(fn, steps, warmup):
@@ -118,9 +118,9 @@ def main():
     achieved = geglu_flop / geglu_s / 1e12
 
     # ---- down GEMM and the activation quantize (HBM-bound), same method
-    H, _, parts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
-    hm = ops.scale_from_partials(parts, ops.E4M3)
-    hq = ops.cast(H, hm, ops.E4M3)
+    H, _, hparts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
+    hq = ops.cast_partials(H, hparts, ops.E4M3)
+    hm = hq.meta
     dq = cached[1]
 
     def ev_time(fn, n=n_launch):

@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 1
+ABI_VERSION = 3
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -18,6 +18,8 @@ SIGNATURES = {
     "bf8_amax_partials": (c_int64, [c_int64]),
     "bf8_amax_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_void_p]),
     "bf8_scale_from_partials": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p]),
+    "bf8_cast_partials_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int,
+                                       c_void_p, c_void_p, c_void_p, c_void_p]),
     "bf8_cast_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int, c_void_p, c_void_p,
                               c_void_p]),
     "bf8_quantize_bf16": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,

@@ -157,4 +157,80 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v) {
   return r;
 }
 
+// gelu_tanh(x) = 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
+// the identical x / (1 + exp(-2u)): no cancellation of 1 + tanh(u) for negative x, and
+// two transcendental instructions (v_exp_f32, v_rcp_f32) instead of a libm tanh.
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+  const float kBeta = 0.7978845608028654f;
+  const float kKappa = 0.044715f;
+  const float kM2Log2e = -2.8853900817779268f;  // -2 / ln 2
+  const float u = kBeta * (x + kKappa * (x * x * x));
+  const float e = __builtin_amdgcn_exp2f(u * kM2Log2e);  // exp(-2u)
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// gelu_tanh and its derivative, both from s = 1 / (1 + exp(-2u)) = 0.5 (1 + tanh(u)):
+//   y = x s,   dy/dx = s + 2 x s (1 - s) u',  u' = sqrt(2/pi) (1 + 3 * 0.044715 x^2),
+// with 1 - s = e s (e = exp(-2u)) to avoid cancellation. y is bit-identical to
+// gelu_tanh_f32(x), so the backward sees the forward's activation.
+__device__ __forceinline__ void gelu_tanh_fwd_bwd(float x, float& y, float& dydx) {
+  const float kBeta = 0.7978845608028654f;
+  const float kKappa = 0.044715f;
+  const float kM2Log2e = -2.8853900817779268f;
+  const float u = kBeta * (x + kKappa * (x * x * x));
+  const float e = __builtin_amdgcn_exp2f(u * kM2Log2e);
+  const float s = __builtin_amdgcn_rcpf(1.0f + e);
+  y = x * s;
+  const float du = kBeta * (1.0f + 3.0f * kKappa * (x * x));
+  dydx = s + 2.0f * x * (s * s * e) * du;
+}
+
+// ---- per-tensor scale from block partials, finished by the last block ---------------
+// meta = {amax, scale, scale_inv, 0}: scale = fp32(fp8_max / max(f64(amax), 1e-12))
+// (f64 division, correctly rounded, then one rounding to fp32: equal to the correctly
+// rounded fp32 quotient since 53 >= 2 * 24 + 2); a NaN amax gives its quietened NaN.
+__device__ inline void write_meta_from_amax(uint32_t key, float fp8_max, float* meta) {
+  const float amax = __uint_as_float(key);
+  float scale, scale_inv;
+  if (amax != amax) {
+    scale = __uint_as_float(key | 0x00400000u);
+    scale_inv = scale;
+  } else {
+    double a = (double)amax;
+    if (a < 1e-12) a = 1e-12;
+    scale = (float)((double)fp8_max / a);
+    scale_inv = (float)(1.0 / (double)scale);
+  }
+  meta[0] = amax;
+  meta[1] = scale;
+  meta[2] = scale_inv;
+  meta[3] = 0.0f;
+}
+
+// Scale of a tensor from the per-block amax partials its producer wrote, computed by
+// every block of the consumer (each reads the <= 2048 partials once); block 0 also
+// publishes the meta record. Result valid in all threads.
+template <int NT>
+__device__ inline float scale_from_partials_block(const uint32_t* __restrict__ partials,
+                                                  int64_t np, float fp8_max,
+                                                  float* __restrict__ meta_out) {
+  __shared__ float s_scale;
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < np; i += NT) m = max(m, partials[i]);
+  m = block_max_u32<NT>(m);
+  if (threadIdx.x == 0) {
+    float meta[4];
+    write_meta_from_amax(m, fp8_max, meta);
+    s_scale = meta[1];
+    if (meta_out && blockIdx.x == 0 && blockIdx.y == 0) {
+      meta_out[0] = meta[0];
+      meta_out[1] = meta[1];
+      meta_out[2] = meta[2];
+      meta_out[3] = meta[3];
+    }
+  }
+  __syncthreads();
+  return s_scale;
+}
+
 }  // namespace bf8

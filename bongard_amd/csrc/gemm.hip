@@ -57,7 +57,7 @@ struct GemmParams {
   void* C;
   int64_t ldc;
   uint16_t* GU;
-  uint32_t* partials;
+  uint32_t* partials;  // GEGLU: one amax key of |H| per tile
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -175,17 +175,6 @@ __device__ __forceinline__ void store_bf16x8(uint16_t* dst, uint4 d, int64_t ld)
   }
 }
 
-// gelu_tanh(x) = 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
-// the identical x / (1 + exp(-2u)): no cancellation of 1 + tanh(u) for negative x, and
-// two transcendental instructions (v_exp_f32, v_rcp_f32) instead of a libm tanh.
-__device__ __forceinline__ float gelu_tanh_f32(float x) {
-  const float kBeta = 0.7978845608028654f;
-  const float kKappa = 0.044715f;
-  const float kM2Log2e = -2.8853900817779268f;  // -2 / ln 2
-  const float u = kBeta * (x + kKappa * (x * x * x));
-  const float e = __builtin_amdgcn_exp2f(u * kM2Log2e);  // exp(-2u)
-  return x * __builtin_amdgcn_rcpf(1.0f + e);
-}
 
 // Stage layout in LDS: [A tile | B tile], each kBM (= kBN) rows of kBK bytes.
 constexpr int kStageBytes = 2 * kTileBytes;

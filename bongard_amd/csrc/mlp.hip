@@ -2,14 +2,13 @@
 //
 // Forward (bongard/te_linear.py:103): h = bf16(bf16(gelu_tanh(g)) * u) on bf16 g, u.
 // Autograd of that bf16 chain gives, per element:
-//   a   = bf16(gelu_tanh(g))                 (recomputed)
+//   a   = bf16(gelu_tanh(g))                 (recomputed exactly as the forward kernel)
 //   d_a = bf16(dh * u)                       (mul backward, grad wrt a)
 //   d_u = bf16(dh * a)                       (mul backward, grad wrt u)
 //   d_g = bf16(d_a * gelu_tanh'(g))          (gelu backward, fp32 inside)
-// with gelu_tanh'(x) = 0.5 (1 + t) + 0.5 x (1 - t^2) beta (1 + 3 kappa x^2),
-// t = tanh(beta (x + kappa x^3)), evaluated in fp32 in PyTorch's CPU kernel order.
-// The kernel is one streaming pass (read dH, g, u; write d_g, d_u) that also emits
-// per-block amax partials of |dGU| for the e5m2 quantization of the gradient.
+// (gelu_tanh_fwd_bwd in common.hpp). The kernel is one streaming pass (read dH, g, u;
+// write d_g, d_u) that also writes per-block amax partials of |dGU|, from which the
+// e5m2 cast of dGU derives its scale.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -20,7 +19,7 @@ namespace bf8 {
 namespace {
 
 constexpr int kNT = 256;
-constexpr int64_t kMaxBlocks = 4096;
+constexpr int64_t kMaxBlocks = 2048;
 
 int64_t bwd_blocks(int64_t M, int64_t I) {
   const int64_t vec = M * I / 8;
@@ -29,24 +28,6 @@ int64_t bwd_blocks(int64_t M, int64_t I) {
   return b < kMaxBlocks ? b : kMaxBlocks;
 }
 
-__device__ __forceinline__ void gelu_fwd_bwd(float x, float& y, float& dydx) {
-#pragma clang fp contract(off)
-  const float kBeta = 0.7978845608028654f;
-  const float kKappa = 0.044715f;
-  const float x_sq = x * x;
-  const float x_cube = x_sq * x;
-  const float inner = kBeta * (x + kKappa * x_cube);
-  const float th = tanhf(inner);
-  // forward in the forward kernel's order: ((0.5 * x) * (1 + th)) with x^3 = (x*x)*x
-  y = 0.5f * x * (1.0f + th);
-  const float left = 0.5f * x;
-  const float right = 1.0f + th;
-  const float left_derivative = 0.5f * right;
-  const float tanh_derivative = 1.0f - th * th;
-  const float inner_derivative = kBeta * (1.0f + 3.0f * kKappa * x_sq);
-  const float right_derivative = left * tanh_derivative * inner_derivative;
-  dydx = left_derivative + right_derivative;
-}
 
 __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restrict__ dH,
                                                         const uint16_t* __restrict__ GU,
@@ -76,7 +57,7 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restri
         const float uu = h ? bf16_hi(uw[w]) : bf16_lo(uw[w]);
         const float d = h ? bf16_hi(dhw[w]) : bf16_lo(dhw[w]);
         float y, dydx;
-        gelu_fwd_bwd(x, y, dydx);
+        gelu_tanh_fwd_bwd(x, y, dydx);
         const float a = bf16_round(y);
         const float da = bf16_round(d * uu);
         const uint32_t bu = f32_to_bf16_bits(d * a);

@@ -6,8 +6,13 @@
 // bf16), scale = fp32(fp8_max / clamp(f64(amax), 1e-12)), q = fp8_rne(clamp(f32(x) *
 // scale, +-fp8_max)).
 //
-// All kernels are HBM-bound streaming passes: 16-byte vector loads, several loads in
-// flight per lane, non-temporal hints on data that is not re-read.
+// Current scaling needs the whole tensor's amax before the first byte is cast, so a
+// quantization is two streaming passes: amax_partials_kernel writes one max per block
+// (at most kMaxAmaxBlocks, plain stores, no atomics), and the cast kernel reduces those
+// partials in every block (a <= 2 KB read) to the scale before it streams the data;
+// its block 0 publishes the meta record. The same cast kernel consumes the per-tile
+// partials of H written by the gate/up GEMM epilogue and those of dGU written by the
+// gated-GELU backward. Streaming loads use 16-byte vectors, several in flight per lane.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -39,13 +44,19 @@ namespace {
 
 constexpr int kNT = 256;            // threads per block for streaming kernels
 constexpr int kVecPerThread = 4;    // 16-byte vectors per lane per iteration
-constexpr int64_t kMaxAmaxBlocks = 2048;
+constexpr int64_t kMaxAmaxBlocks = 512;  // keeps the consumers' partial reads at <= 2 KB
 
 int64_t amax_blocks(int64_t n) {
   int64_t per_block = (int64_t)kNT * kVecPerThread * 8;  // bf16 elements per block pass
   int64_t b = (n + per_block - 1) / per_block;
   if (b < 1) b = 1;
   return b < kMaxAmaxBlocks ? b : kMaxAmaxBlocks;
+}
+
+int grid_for_stream(int64_t work_items, int64_t per_block, int64_t cap) {
+  int64_t b = (work_items + per_block - 1) / per_block;
+  if (b < 1) b = 1;
+  return (int)(b < cap ? b : cap);
 }
 
 // partials[b] = max over block b's grid-stride share of |x| keys.
@@ -74,27 +85,6 @@ __global__ __launch_bounds__(kNT) void amax_partials_kernel(const uint16_t* __re
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
 }
 
-__device__ void write_meta_from_amax(uint32_t key, float fp8_max, float* meta) {
-  const float amax = __uint_as_float(key);
-  float scale, scale_inv;
-  if (amax != amax) {
-    // torch: clamp(NaN) is NaN; fp8_max / NaN returns that NaN (quietened).
-    scale = __uint_as_float(key | 0x00400000u);
-    scale_inv = scale;
-  } else {
-    double a = (double)amax;
-    if (a < 1e-12) a = 1e-12;
-    // f64 division is correctly rounded; rounding it to fp32 equals the correctly
-    // rounded fp32 quotient (53 >= 2 * 24 + 2).
-    scale = (float)((double)fp8_max / a);
-    scale_inv = (float)(1.0 / (double)scale);
-  }
-  meta[0] = amax;
-  meta[1] = scale;
-  meta[2] = scale_inv;
-  meta[3] = 0.0f;
-}
-
 __global__ __launch_bounds__(kNT) void scale_from_partials_kernel(
     const uint32_t* __restrict__ partials, int64_t np, float fp8_max, float* __restrict__ meta) {
   uint32_t m = 0;
@@ -103,13 +93,24 @@ __global__ __launch_bounds__(kNT) void scale_from_partials_kernel(
   if (threadIdx.x == 0) write_meta_from_amax(m, fp8_max, meta);
 }
 
+// The scale comes from scale_ptr, or (scale_ptr == NULL) from amax partials that every
+// block reduces itself (block 0 then also writes meta_out).
+template <int FMT>
+__device__ __forceinline__ float resolve_scale(const float* scale_ptr, const uint32_t* partials,
+                                               int64_t np, float* meta_out) {
+  if (scale_ptr) return *scale_ptr;
+  return scale_from_partials_block<kNT>(partials, np, Fp8Max<FMT>::value, meta_out);
+}
+
 // Row-major cast: each lane converts 16 consecutive bf16 (two 16-byte loads) into one
 // 16-byte store. n16 = number of 16-element groups; the n % 16 tail is done bytewise.
 template <int FMT>
 __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ x, int64_t n,
                                                    const float* __restrict__ scale_ptr,
+                                                   const uint32_t* __restrict__ partials,
+                                                   int64_t np, float* __restrict__ meta_out,
                                                    uint8_t* __restrict__ out) {
-  const float scale = *scale_ptr;
+  const float scale = resolve_scale<FMT>(scale_ptr, partials, np, meta_out);
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint4* ov = reinterpret_cast<uint4*>(out);
   const int64_t n16 = n >> 4;
@@ -152,11 +153,11 @@ constexpr int kTPitch = kTT + 4;  // LDS row pitch (bytes), staggers banks for t
 template <int FMT>
 __global__ __launch_bounds__(kNT) void cast_transpose_kernel(
     const uint16_t* __restrict__ x, int64_t rows, int64_t cols,
-    const float* __restrict__ scale_ptr, uint8_t* __restrict__ out,
-    uint8_t* __restrict__ out_t) {
+    const float* __restrict__ scale_ptr, const uint32_t* __restrict__ partials, int64_t np,
+    float* __restrict__ meta_out, uint8_t* __restrict__ out, uint8_t* __restrict__ out_t) {
   __shared__ uint32_t tile[kTT * kTPitch / 4];
   uint8_t* tb = reinterpret_cast<uint8_t*>(tile);
-  const float scale = *scale_ptr;
+  const float scale = resolve_scale<FMT>(scale_ptr, partials, np, meta_out);
   const int64_t r0 = (int64_t)blockIdx.y * kTT, c0 = (int64_t)blockIdx.x * kTT;
   const int t = threadIdx.x;
   {
@@ -237,10 +238,43 @@ __global__ __launch_bounds__(kNT) void delayed_end_kernel(float* state, int len,
   }
 }
 
-int grid_for_stream(int64_t work_items, int64_t per_block, int64_t cap) {
-  int64_t b = (work_items + per_block - 1) / per_block;
-  if (b < 1) b = 1;
-  return (int)(b < cap ? b : cap);
+int launch_cast(const void* x, int64_t rows, int64_t cols, const float* scale,
+                const uint32_t* partials, int64_t np, float* meta_out, int fmt, uint8_t* out,
+                uint8_t* out_t, void* stream, const char* who) {
+  BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "%s: bad fmt %d", who, fmt);
+  BF8_CHECK(rows >= 0 && cols >= 0, "%s: negative shape", who);
+  BF8_CHECK(scale != nullptr || (partials != nullptr && np >= 1 && np <= 4096),
+            "%s: no scale source (or more than 4096 partials)", who);
+  BF8_CHECK(out || out_t, "%s: out and out_t are both NULL", who);
+  BF8_CHECK(((uintptr_t)x & 15) == 0 && (!out || ((uintptr_t)out & 15) == 0),
+            "%s: x and out must be 16-byte aligned", who);
+  const int64_t n = rows * cols;
+  if (n == 0) return BF8_OK;
+  hipStream_t s = as_stream(stream);
+  const uint16_t* xs = (const uint16_t*)x;
+  if (out_t == nullptr) {
+    const int grid = grid_for_stream((n + 15) / 16, 2 * kNT, 2048);
+    if (fmt == BF8_E4M3)
+      hipLaunchKernelGGL(cast_kernel<BF8_E4M3>, dim3(grid), dim3(kNT), 0, s, xs, n, scale,
+                         partials, np, meta_out, out);
+    else
+      hipLaunchKernelGGL(cast_kernel<BF8_E5M2>, dim3(grid), dim3(kNT), 0, s, xs, n, scale,
+                         partials, np, meta_out, out);
+    return launch_status("cast_kernel");
+  }
+  BF8_CHECK(cols % 16 == 0, "%s: transposed cast needs cols %% 16 == 0 (got %lld)", who,
+            (long long)cols);
+  BF8_CHECK(((uintptr_t)out_t & 15) == 0, "%s: out_t must be 16-byte aligned", who);
+  BF8_CHECK((cols + kTT - 1) / kTT < (1LL << 31) && (rows + kTT - 1) / kTT < 65536,
+            "%s: shape too large for the transposed cast grid", who);
+  dim3 grid((unsigned)((cols + kTT - 1) / kTT), (unsigned)((rows + kTT - 1) / kTT));
+  if (fmt == BF8_E4M3)
+    hipLaunchKernelGGL(cast_transpose_kernel<BF8_E4M3>, grid, dim3(kNT), 0, s, xs, rows, cols,
+                       scale, partials, np, meta_out, out, out_t);
+  else
+    hipLaunchKernelGGL(cast_transpose_kernel<BF8_E5M2>, grid, dim3(kNT), 0, s, xs, rows, cols,
+                       scale, partials, np, meta_out, out, out_t);
+  return launch_status("cast_transpose_kernel");
 }
 
 }  // namespace
@@ -251,7 +285,7 @@ using namespace bf8;
 extern "C" {
 
 const char* bf8_last_error(void) { return bf8::g_err; }
-int bf8_abi_version(void) { return 1; }
+int bf8_abi_version(void) { return 3; }
 
 int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
 
@@ -278,34 +312,18 @@ int bf8_scale_from_partials(const uint32_t* partials, int64_t n_partials, int fm
 
 int bf8_cast_bf16(const void* x, int64_t rows, int64_t cols, const float* scale, int fmt,
                   uint8_t* out, uint8_t* out_t, void* stream) {
-  BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "bf8_cast_bf16: bad fmt %d", fmt);
-  BF8_CHECK(rows >= 0 && cols >= 0, "bf8_cast_bf16: negative shape");
   BF8_CHECK(scale != nullptr, "bf8_cast_bf16: scale is NULL");
-  BF8_CHECK(out || out_t, "bf8_cast_bf16: out and out_t are both NULL");
-  BF8_CHECK(((uintptr_t)x & 15) == 0 && (!out || ((uintptr_t)out & 15) == 0),
-            "bf8_cast_bf16: x and out must be 16-byte aligned");
-  const int64_t n = rows * cols;
-  if (n == 0) return BF8_OK;
-  hipStream_t s = as_stream(stream);
-  if (out_t == nullptr) {
-    const int grid = grid_for_stream((n + 15) / 16, 2 * kNT, 8192);
-    if (fmt == BF8_E4M3)
-      hipLaunchKernelGGL(cast_kernel<BF8_E4M3>, dim3(grid), dim3(kNT), 0, s, (const uint16_t*)x, n, scale, out);
-    else
-      hipLaunchKernelGGL(cast_kernel<BF8_E5M2>, dim3(grid), dim3(kNT), 0, s, (const uint16_t*)x, n, scale, out);
-    return launch_status("cast_kernel");
-  }
-  BF8_CHECK(cols % 16 == 0, "bf8_cast_bf16: transposed cast needs cols %% 16 == 0 (got %lld)",
-            (long long)cols);
-  BF8_CHECK(((uintptr_t)out_t & 15) == 0, "bf8_cast_bf16: out_t must be 16-byte aligned");
-  BF8_CHECK((cols + kTT - 1) / kTT < (1LL << 31) && (rows + kTT - 1) / kTT < 65536,
-            "bf8_cast_bf16: shape too large for the transposed cast grid");
-  dim3 grid((unsigned)((cols + kTT - 1) / kTT), (unsigned)((rows + kTT - 1) / kTT));
-  if (fmt == BF8_E4M3)
-    hipLaunchKernelGGL(cast_transpose_kernel<BF8_E4M3>, grid, dim3(kNT), 0, s, (const uint16_t*)x, rows, cols, scale, out, out_t);
-  else
-    hipLaunchKernelGGL(cast_transpose_kernel<BF8_E5M2>, grid, dim3(kNT), 0, s, (const uint16_t*)x, rows, cols, scale, out, out_t);
-  return launch_status("cast_transpose_kernel");
+  return launch_cast(x, rows, cols, scale, nullptr, 0, nullptr, fmt, out, out_t, stream,
+                     "bf8_cast_bf16");
+}
+
+int bf8_cast_partials_bf16(const void* x, int64_t rows, int64_t cols, const uint32_t* partials,
+                           int64_t n_partials, int fmt, float* meta, uint8_t* out,
+                           uint8_t* out_t, void* stream) {
+  BF8_CHECK(partials && meta && n_partials >= 1,
+            "bf8_cast_partials_bf16: bad partials or meta");
+  return launch_cast(x, rows, cols, nullptr, partials, n_partials, meta, fmt, out, out_t,
+                     stream, "bf8_cast_partials_bf16");
 }
 
 int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
@@ -314,9 +332,8 @@ int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_
   const int64_t n = rows * cols;
   int rc = bf8_amax_bf16(x, n, partials, stream);
   if (rc) return rc;
-  rc = bf8_scale_from_partials(partials, amax_blocks(n), fmt, meta, stream);
-  if (rc) return rc;
-  return bf8_cast_bf16(x, rows, cols, meta + 1, fmt, out, out_t, stream);
+  return bf8_cast_partials_bf16(x, rows, cols, partials, amax_blocks(n), fmt, meta, out, out_t,
+                                stream);
 }
 
 int bf8_delayed_scale_begin(float* state, int len, int fmt, void* stream) {

@@ -86,8 +86,8 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
         stride = 4 if split_scales else 0
         H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
                                        w_meta_stride=stride, keep_gu=train)
-        h_meta = ops.scale_from_partials(hparts, E4M3)
-        hq = ops.cast(H, h_meta, E4M3, rowwise=True, transpose=ctx.needs_input_grad[2])
+        hq = ops.cast_partials(H, hparts, E4M3, rowwise=True, transpose=ctx.needs_input_grad[2])
+        h_meta = hq.meta
         if down_q is None:
             down_q = quantize_weight(
                 w_down, transpose=ctx.needs_input_grad[0] or ctx.needs_input_grad[1])
@@ -111,10 +111,10 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
         if not (need_dx or need_dgu):
             return dx, dgu, dd, None, None, None, None
         dH = ops.gemm(dyq.data, E5M2, dyq.meta, d8t, E4M3, d_meta)
-        dGU, parts = ops.geglu_bwd(dH, GU)
+        dGU, gparts = ops.geglu_bwd(dH, GU)
         if not ctx.split_scales:
-            g_meta = ops.scale_from_partials(parts, E5M2)
-            dq = ops.cast(dGU, g_meta, E5M2, rowwise=need_dx, transpose=need_dgu)
+            dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=need_dx, transpose=need_dgu)
+            g_meta = dq.meta
             if need_dx:
                 dx = ops.gemm(dq.data, E5M2, g_meta, gu8t, E4M3, gu_meta[0])
             if need_dgu:

@@ -81,9 +81,23 @@ def amax_partials_count(n):
 
 
 def new_meta(device, count=1):
-    """Zeroed meta record(s): float32 [count, 4] (or [4] when count == 1)."""
-    m = torch.zeros((count, 4) if count > 1 else (4,), dtype=torch.float32, device=device)
-    return m
+    """Uninitialised meta record(s): float32 [count, 4] (or [4] when count == 1); the
+    kernels that produce a meta write all four words."""
+    return torch.empty((count, 4) if count > 1 else (4,), dtype=torch.float32, device=device)
+
+
+# Per-(device, stream) scratch for amax partials, reused in stream order.
+_PARTIALS = {}
+
+
+def partials_buffer(count, device):
+    device = torch.device(device)
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    buf = _PARTIALS.get(key)
+    if buf is None or buf.numel() < count:
+        buf = torch.empty(max(int(count), 4096), dtype=torch.int32, device=device)
+        _PARTIALS[key] = buf
+    return buf
 
 
 def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None, out_t=None):
@@ -102,11 +116,11 @@ def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None,
         out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=dev)
     if transpose and out_t is None:
         out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=dev)
-    partials = torch.empty(amax_partials_count(rows * cols), dtype=torch.int32, device=dev)
     L = _lib.lib()
+    parts = partials_buffer(L.bf8_amax_partials(rows * cols), dev)
     _lib.check(L.bf8_quantize_bf16(_ptr(x), rows, cols, fmt, _ptr(out if rowwise else None),
                                    _ptr(out_t if transpose else None), _ptr(meta),
-                                   _ptr(partials), _stream(dev)), "bf8_quantize_bf16")
+                                   _ptr(parts), _stream(dev)), "bf8_quantize_bf16")
     return Fp8Tensor(out if rowwise else None, out_t if transpose else None, meta, fmt, rows, cols)
 
 
@@ -127,6 +141,22 @@ def scale_from_partials(partials, fmt, meta=None):
                                                   _ptr(meta), _stream(partials.device)),
                "bf8_scale_from_partials")
     return meta
+
+
+def cast_partials(x, partials, fmt=E4M3, *, rowwise=True, transpose=False):
+    """Cast whose scale comes from amax partials (as returned by ``gemm_geglu`` /
+    ``geglu_bwd``); returns the Fp8Tensor with its freshly written meta."""
+    _require_gpu(x, partials)
+    x = _bf16_2d(x)
+    rows, cols = x.shape
+    meta = new_meta(x.device)
+    out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=x.device) if rowwise else None
+    out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=x.device) if transpose else None
+    _lib.check(_lib.lib().bf8_cast_partials_bf16(_ptr(x), rows, cols, _ptr(partials),
+                                                 partials.numel(), fmt, _ptr(meta), _ptr(out),
+                                                 _ptr(out_t), _stream(x.device)),
+               "bf8_cast_partials_bf16")
+    return Fp8Tensor(out, out_t, meta, fmt, rows, cols)
 
 
 def cast(x, meta, fmt=E4M3, *, rowwise=True, transpose=False, out=None, out_t=None):
@@ -190,7 +220,8 @@ def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu
     """Gate/up GEMM with the gated-GELU epilogue.
 
     x8: fp8 e4m3 [M, K]; w8: fp8 e4m3 [2I, K] (gate rows then up rows). Returns
-    ``(H bf16 [M, I], GU bf16 [M, 2I] or None, h_partials int32)``.
+    ``(H bf16 [M, I], GU bf16 [M, 2I] or None, h_partials int32 [tiles])``; the per-tile
+    amax partials of |H| feed ``cast_partials``.
     """
     _require_gpu(x8, w8, x_meta, w_meta)
     M, K = x8.shape
@@ -209,7 +240,8 @@ def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu
 
 
 def geglu_bwd(dH, GU):
-    """dGU bf16 [M, 2I] (d_gate | d_up) from dH [M, I] and the forward's GU; + amax partials."""
+    """dGU bf16 [M, 2I] (d_gate | d_up) from dH [M, I] and the forward's GU, and the
+    per-block amax partials of |dGU| (for ``cast_partials``)."""
     _require_gpu(dH, GU)
     dH = dH.contiguous()
     M, I = dH.shape

@@ -49,9 +49,9 @@ def main():
         xq = ops.quantize(x, ops.E4M3)
         gq = ops.quantize(w_gu, ops.E4M3)
         dq = ops.quantize(w_d, ops.E4M3)
-        H, _, parts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
-        hm = ops.scale_from_partials(parts, ops.E4M3)
-        hq = ops.cast(H, hm, ops.E4M3)
+        H, _, hparts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
+        hq = ops.cast_partials(H, hparts, ops.E4M3)
+        hm = hq.meta
         ops.gemm(hq.data, ops.E4M3, hm, dq.data, ops.E4M3, dq.meta)
     torch.cuda.synchronize()
     print(f"profile_target done: {args.iters} iterations, copy {COPY_BYTES} bytes", flush=True)

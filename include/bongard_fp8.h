@@ -61,10 +61,10 @@ int64_t bf8_amax_partials(int64_t n);
  * inf). x: bf16 [n], 16-byte aligned. partials: uint32 [bf8_amax_partials(n)]. */
 int bf8_amax_bf16(const void* x, int64_t n, uint32_t* partials, void* stream);
 
-/* meta = {amax, scale, scale_inv, 0} from n_partials partial-amax slots.
- * `history` (nullable) selects delayed scaling instead: see bf8_delayed_scale. */
+/* meta = {amax, scale, scale_inv, 0} from n_partials partial-amax slots. */
 int bf8_scale_from_partials(const uint32_t* partials, int64_t n_partials, int fmt,
                             float* meta, void* stream);
+
 
 /* ---------------------------------------------------------------------------------
  * Saturating cast bf16 -> e4m3/e5m2, optional transposed copy.
@@ -77,8 +77,15 @@ int bf8_scale_from_partials(const uint32_t* partials, int64_t n_partials, int fm
 int bf8_cast_bf16(const void* x, int64_t rows, int64_t cols, const float* scale, int fmt,
                   uint8_t* out, uint8_t* out_t, void* stream);
 
-/* amax -> scale -> cast in one call: meta gets {amax, scale, scale_inv, 0}.
- * partials: uint32 workspace of bf8_amax_partials(rows * cols) slots. */
+/* Cast with the scale derived from amax partials (as written by bf8_amax_bf16,
+ * bf8_gemm_geglu or bf8_geglu_bwd; n_partials <= 4096): every block reduces them to the
+ * scale before casting, and meta receives {amax, scale, scale_inv, 0}. */
+int bf8_cast_partials_bf16(const void* x, int64_t rows, int64_t cols, const uint32_t* partials,
+                           int64_t n_partials, int fmt, float* meta, uint8_t* out,
+                           uint8_t* out_t, void* stream);
+
+/* amax -> scale -> cast (two kernels: bf8_amax_bf16, bf8_cast_partials_bf16); meta gets
+ * {amax, scale, scale_inv, 0}. partials: uint32 [bf8_amax_partials(rows * cols)]. */
 int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
                       uint8_t* out_t, float* meta, uint32_t* partials, void* stream);
 
@@ -117,8 +124,10 @@ int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt
  * (w_scale_stride == 0: one shared scale, as TE's stacked gate_up weight).
  * H: bf16 [M, I] (row stride ldh). GU: bf16 [M, 2I] (gate | up, bf16-rounded
  * pre-activations kept for the backward) or NULL. h_partials: uint32
- * [bf8_geglu_partials(M, I)] per-tile amax of |H| (fp32 bits), reduced by
- * bf8_scale_from_partials into H's quantization meta. I % 128 == 0.
+ * [bf8_geglu_partials(M, I)] per-tile amax of |H| (fp32 bits), for
+ * bf8_cast_partials_bf16. I % 128 == 0.
+ * gelu_tanh is evaluated as x / (1 + exp(-2u)), the same function as
+ * 0.5 x (1 + tanh(u)) without the cancellation of 1 + tanh(u) for negative x.
  * ------------------------------------------------------------------------------- */
 int64_t bf8_geglu_partials(int64_t M, int64_t I);
 int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw, int64_t M,
@@ -131,8 +140,8 @@ int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw,
  * forward), write dGU bf16 [M, 2I] with
  *   d_gate = bf16(dH * u * gelu'(g)), d_up = bf16(dH * bf16(gelu(g)))
  * following autograd of F.gelu(g, approximate='tanh') * u in bf16
- * (bongard/te_linear.py:103), and per-block amax partials of |dGU| (for its e5m2
- * quantization) into partials [bf8_geglu_bwd_partials(M, I)].
+ * (bongard/te_linear.py:103), and per-block amax partials of |dGU| into partials
+ * [bf8_geglu_bwd_partials(M, I)] for its e5m2 cast (bf8_cast_partials_bf16).
  * ------------------------------------------------------------------------------- */
 int64_t bf8_geglu_bwd_partials(int64_t M, int64_t I);
 int bf8_geglu_bwd(const void* dH, const void* GU, int64_t M, int64_t I, void* dGU,

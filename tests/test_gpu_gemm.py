@@ -168,12 +168,12 @@ def _geglu_case(dev, M, I, K, seed, split=False):
         wm = ops.new_meta(dev, 2)
         ops.quantize(wg.to(dev), 0, meta=wm[0], out=w8[:I])
         ops.quantize(wu.to(dev), 0, meta=wm[1], out=w8[I:])
-        H, GU, parts = ops.gemm_geglu(xq.data, xq.meta, w8, wm, I, w_meta_stride=4, keep_gu=True)
+        H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, w8, wm, I, w_meta_stride=4, keep_gu=True)
     else:
         wq = _quant(torch.cat([wg, wu]), 0, dev)
-        H, GU, parts = ops.gemm_geglu(xq.data, xq.meta, wq.data, wq.meta, I, keep_gu=True)
-    hmeta = ops.scale_from_partials(parts, ops.E4M3)
-    hq = ops.cast(H, hmeta, ops.E4M3)
+        H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, wq.data, wq.meta, I, keep_gu=True)
+    hq = ops.cast_partials(H, hparts, ops.E4M3)
+    hmeta = hq.meta
     torch.cuda.synchronize()
     rx, _, sx, _ = orc.quantize(x, 0)
     if split:
@@ -235,7 +235,7 @@ def test_geglu_bwd(gpu):
     GU = (torch.randn(M, 2 * I, generator=g) * 2).to(torch.bfloat16)
     dH = (torch.randn(M, I, generator=g) * 1e-3).to(torch.bfloat16)
     dGU, parts = ops.geglu_bwd(dH.to(gpu), GU.to(gpu))
-    meta = ops.scale_from_partials(parts, ops.E5M2)
+    meta = ops.cast_partials(dGU, parts, ops.E5M2).meta
     torch.cuda.synchronize()
     dg, du = orc.geglu_bwd(GU[:, :I], GU[:, I:], dH)
     got = dGU.cpu().float()
@@ -256,9 +256,9 @@ def test_mlp_down_gemm_on_own_h8(gpu):
     xq = _quant(x, 0, gpu)
     gq = _quant(wgu, 0, gpu)
     dq = _quant(wd, 0, gpu)
-    H, _, parts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
-    hm = ops.scale_from_partials(parts, 0)
-    hq = ops.cast(H, hm, 0)
+    H, _, hparts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
+    hq = ops.cast_partials(H, hparts, 0)
+    hm = hq.meta
     y32 = ops.gemm(hq.data, 0, hm, dq.data, 0, dq.meta, out_dtype=torch.float32)
     torch.cuda.synchronize()
     rq, _, rs, _ = orc.quantize(H.cpu(), 0)
