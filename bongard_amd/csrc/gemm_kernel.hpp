@@ -1,0 +1,58 @@
+// Shared declarations of the FP8 GEMM: launch parameters, block-tile shapes and the
+// per-tile launchers (each instantiated in its own gemm_tile_*.hip translation unit so
+// that the tile variants compile in parallel).
+#pragma once
+
+#include "common.hpp"
+
+namespace bf8 {
+
+enum GemmEpi { EPI_LINEAR = 0, EPI_GEGLU = 1 };
+
+struct GemmParams {
+  const uint8_t* A;  // [M, K] row-major, row stride lda bytes
+  const uint8_t* B;  // [N, K] row-major (nn.Linear weight layout), row stride ldb bytes
+  int64_t lda, ldb;
+  int M, N, K;           // for GEGLU, N = 2I (rows of [W_gate; W_up])
+  int I;                 // GEGLU intermediate size
+  int tiles_m, tiles_n;  // output tiles
+  int splits;            // K splits per output tile (LINEAR only; 1 = none)
+  int ksteps_per_split;  // 128-byte K steps per split
+  const float* a_sinv;
+  const float* b_sinv;
+  int b_stride;
+  int n_seg;
+  int seg_end[4];
+  const uint16_t* bias;
+  void* C;
+  int64_t ldc;
+  uint16_t* GU;
+  uint32_t* partials;     // GEGLU: one amax key of |H| per tile
+  int64_t split_stride;   // splits > 1: C is fp32 [splits][M][ldc], raw sums, this many
+                          // elements apart (a reduce kernel applies scales and bias)
+};
+
+// A workgroup is four wave64s arranged WM x WN; each wave owns FM x FN MFMA tiles of
+// 32 x 32 outputs, so the block tile is (WM*FM*32) x (WN*FN*32). NS LDS stages of
+// (BM + BN) x 128 bytes are in flight; OCC workgroups share a CU (the register budget
+// per wave is 512 / OCC VGPRs, LDS 160 KB / OCC).
+template <int WM_, int WN_, int FM_, int FN_, int NS_, int OCC_>
+struct GemmTile {
+  static constexpr int WM = WM_, WN = WN_, FM = FM_, FN = FN_, NS = NS_, OCC = OCC_;
+  static constexpr int BM = WM * FM * 32, BN = WN * FN * 32;
+  static_assert(WM * WN == 4, "four waves per workgroup");
+  static_assert(NS >= 2 && NS * (BM + BN) * 128 * OCC <= 160 * 1024, "LDS budget");
+};
+
+using Tile256x256 = GemmTile<2, 2, 4, 4, 2, 1>;
+using Tile256x160 = GemmTile<4, 1, 2, 5, 3, 1>;
+using Tile160x256 = GemmTile<1, 4, 5, 2, 3, 1>;
+using Tile128x128 = GemmTile<2, 2, 2, 2, 4, 1>;
+
+// Enqueues the GEMM for tile shape T (EPI_GEGLU: e4m3 x e4m3, bf16 H). Returns a BF8_*
+// status; the host entry points have validated p.
+template <class T>
+int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
+                     hipStream_t stream);
+
+}  // namespace bf8

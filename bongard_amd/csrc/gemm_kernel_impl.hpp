@@ -1,0 +1,516 @@
+// FP8 GEMM kernel for gfx950 (MI355X) on the double-rate f8f6f4 MFMA, with a dequant/bias
+// epilogue (or raw fp32 split-K partials), and a gated-GELU(tanh) epilogue for the MLP
+// gate/up projection. Included by the gemm_tile_*.hip files only.
+//
+// Semantics replace torch._scaled_mm / cuBLASLt under torchao Float8Linear
+// (bongard/float8_training.py:22) and TE's FP8 GEMM under te.Linear
+// (bongard/te_linear.py:73-74): C = (A8 . B8^T accumulated in fp32) * sa_inv * sb_inv
+// (+ bias), "TN" layout (both operands K-contiguous, as nn.Linear weights are).
+//
+// Design (one workgroup = 4 wave64, block tile BM x BN, K step 128 bytes):
+//  - global -> LDS by direct 16-byte buffer loads into LDS (no VGPR staging; out-of-range
+//    rows/K read as zero), NS LDS stages of (BM + BN) x 128 bytes in flight;
+//  - LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at c ^ ((r >> 1) & 7)
+//    so that a fragment read (16 lanes = 16 rows x 16 bytes per LDS cycle on the 64-bank,
+//    256 B/clk gfx950 LDS) touches every bank once;
+//  - each wave owns FM x FN MFMA 32x32x64 tiles; the MFMA "A" operand is the B (weight)
+//    tile, so every lane ends up holding four consecutive output columns of one row;
+//  - per 64-byte K sub-step a wave issues FM*FN MFMAs with the fragment reads of the next
+//    sub-step and the DMA loads of the stage after next spread evenly between them;
+//  - workgroups are renumbered so that each XCD (blockIdx % 8 on MI355X) owns a
+//    contiguous range of (split, tile) ids, walked in groups of kGroupM tile rows.
+#pragma once
+
+#include <type_traits>
+
+#include "gemm_kernel.hpp"
+
+namespace bf8 {
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBK = 128;       // K bytes per LDS stage
+constexpr int kThreads = 256;  // four wave64
+constexpr int kGroupM = 8;
+constexpr int kNumXcd = 8;
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset that always reads as zero
+
+// Buffer resource (4 SGPRs): base, stride 0, `bytes` valid bytes (offsets at or beyond
+// read as zero), raw-buffer flags of gfx9/gfx950.
+__device__ __forceinline__ i32x4 make_srd(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xFFFFu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16-byte-per-lane load from a buffer straight into LDS: lane l's bytes land at
+// lds_addr + 16 l. Written as inline asm so that the compiler's wait-count pass does
+// not serialise it against LDS reads of other stages (it cannot prove they do not
+// alias); the kernel orders it with explicit vmcnt waits and barriers instead. M0 is
+// set inside the same asm block, immediately before its only use.
+__device__ __forceinline__ void dma16(i32x4 srd, uint32_t lds_addr, uint32_t voff,
+                                      uint32_t soff) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0v), "v"(voff), "s"(srd), "s"(so)
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const uint8_t*)(p));
+}
+
+// (tile row, tile column, K split) of this workgroup.
+__device__ __forceinline__ void block_coords(const GemmParams& p, int& tm, int& tn,
+                                             int& split) {
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int nb = ntiles * p.splits;
+  const int b = blockIdx.x;
+  // XCD-contiguous renumbering: blocks dispatched to XCD x (b % 8 == x) get ids
+  // [x*q + min(x, r), ...) with q = nb / 8, r = nb % 8.
+  const int x = b % kNumXcd, idx = b / kNumXcd;
+  const int q = nb / kNumXcd, r = nb % kNumXcd;
+  int id = x * q + (x < r ? x : r) + idx;
+  split = id / ntiles;
+  id -= split * ntiles;
+  const int per_group = kGroupM * p.tiles_n;
+  const int g = id / per_group;
+  const int first_m = g * kGroupM;
+  const int gm = min(p.tiles_m - first_m, kGroupM);
+  const int in_g = id - g * per_group;
+  tm = first_m + in_g % gm;
+  tn = in_g / gm;
+}
+
+template <int FA, int FB>
+__device__ __forceinline__ v16f mfma(v8i a, v8i b, v16f c) {
+  // scale operands 0: plain (unscaled) f8f6f4 MFMA; FA/FB select e4m3 (0) / e5m2 (1).
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
+}
+
+// Swizzled position of logical 16-byte chunk c in tile row r (128-byte rows).
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+// Reads 16 bytes of an MFMA operand fragment: 32 rows starting at `row0` of an LDS tile,
+// K bytes [kk*64, kk*64+64); lane l holds row row0 + (l & 31), bytes (l >> 5)*32 + 16*half
+// .. +15 (two halves make the lane's 32 bytes).
+__device__ __forceinline__ v4u read_half(const uint8_t* tile, int row0, int kk, int half,
+                                         int lane) {
+  const int row = row0 + (lane & 31);
+  const int c = kk * 4 + (lane >> 5) * 2 + half;
+  return *reinterpret_cast<const v4u*>(tile + row * kBK + (swz(row, c) << 4));
+}
+
+__device__ __forceinline__ v8i join(v4u lo, v4u hi) {
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16x2 with round-to-nearest-even (gfx950 v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Epilogue staging in LDS: rows of CH 16-byte chunks; chunk c of row r lives at
+// c ^ (r & (CH - 1)) for power-of-two CH, else at (c + r) % CH, so that the 32 rows a
+// wave writes at once spread over the banks. Lanes put 8-byte runs (4 bf16) and get
+// 16-byte chunks.
+template <int CH>
+__device__ __forceinline__ int stage_pos(int row, int c) {
+  if constexpr ((CH & (CH - 1)) == 0)
+    return c ^ (row & (CH - 1));
+  else
+    return (c + row) % CH;
+}
+template <int CH>
+__device__ __forceinline__ void stage_put(uint8_t* buf, int row, int col, uint2 v) {
+  const int c = col >> 3, half = (col >> 2) & 1;
+  *reinterpret_cast<uint2*>(buf + row * (CH * 16) + (stage_pos<CH>(row, c) << 4) + half * 8) = v;
+}
+template <int CH>
+__device__ __forceinline__ uint4 stage_get(const uint8_t* buf, int row, int c) {
+  return *reinterpret_cast<const uint4*>(buf + row * (CH * 16) + (stage_pos<CH>(row, c) << 4));
+}
+// 8 bf16 to global: one 16-byte store when the row stride keeps it aligned.
+__device__ __forceinline__ void store_bf16x8(uint16_t* dst, uint4 d, int64_t ld) {
+  if ((ld & 7) == 0) {
+    *reinterpret_cast<uint4*>(dst) = d;
+  } else {
+    reinterpret_cast<uint2*>(dst)[0] = make_uint2(d.x, d.y);
+    reinterpret_cast<uint2*>(dst)[1] = make_uint2(d.z, d.w);
+  }
+}
+
+// The operand fragments of one MFMA sub-step as 16-byte halves, in the order the MFMAs
+// of the sub-step consume them: b0, a0 .. a(FM-1), b1 .. b(FN-1).
+template <int NH>
+struct Frags {
+  v4u h[NH];
+};
+
+template <class T, int FA, int FB, int EPI, int OUT>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(T::OCC, T::OCC))) void
+gemm_kernel(GemmParams p) {
+  constexpr int BM = T::BM, BN = T::BN, FM = T::FM, FN = T::FN, WM = T::WM, NS = T::NS;
+  constexpr int kA = BM * kBK;               // A tile bytes per stage
+  constexpr int kStage = (BM + BN) * kBK;    // [A tile | B tile]
+  constexpr int DA = BM / 32, DB = BN / 32;  // 1 KB DMA blocks per wave per stage
+  constexpr int ND = DA + DB;
+  constexpr int NM = FM * FN;                // MFMAs per sub-step
+  constexpr int NH = 2 * (FM + FN);          // 16-byte fragment halves per sub-step
+  static_assert(EPI != EPI_GEGLU || FN % 2 == 0, "GEGLU pairs gate and up sub-tiles");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage];
+
+  int tm, tn, split;
+  block_coords(p, tm, tn, split);
+  const int m0 = tm * BM;
+  const int n0 = tn * (EPI == EPI_GEGLU ? BN / 2 : BN);  // GEGLU: n0 indexes I
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wid = t >> 6;
+  const int wm = wid % WM, wn = wid / WM;
+  const int wave_m0 = wm * FM * 32;
+
+  const int ksteps = (p.K + kBK - 1) / kBK;
+  const int kbeg = split * p.ksteps_per_split;
+  const int nsteps = min(p.ksteps_per_split, ksteps - kbeg);  // >= 1 by construction
+
+  const i32x4 ra = make_srd(p.A, (uint32_t)((int64_t)p.M * p.lda));
+  const i32x4 rb = make_srd(p.B, (uint32_t)((int64_t)p.N * p.ldb));
+
+  static_assert(ND * (NS - 1) < 64, "vmcnt holds at most 63 outstanding loads");
+  // DMA: lane l of the wave's j-th 1 KB block (block j*4 + wid of the tile) covers tile
+  // row blk*8 + l/8, physical chunk l%8. Its logical chunk swz(row, l%8) only depends on
+  // l and wid & 1 (= blk & 1), so one K mask serves every block of the lane.
+  const int lrow = lane >> 3;
+  const int lchunk = (lane & 7) ^ (((wid & 1) << 2) | (lrow >> 1));
+  uint32_t a_off[DA], b_off[DB];
+#pragma unroll
+  for (int j = 0; j < DA; ++j) {
+    const int am = m0 + (j * 4 + wid) * 8 + lrow;
+    a_off[j] = am < p.M ? (uint32_t)((int64_t)am * p.lda + lchunk * 16) : kOob;
+  }
+#pragma unroll
+  for (int j = 0; j < DB; ++j) {
+    const int r = (j * 4 + wid) * 8 + lrow;
+    int bn;
+    bool bvalid;
+    if (EPI == EPI_GEGLU) {
+      const int rr = r < BN / 2 ? r : r - BN / 2;
+      bn = (r < BN / 2 ? 0 : p.I) + n0 + rr;
+      bvalid = n0 + rr < p.I;
+    } else {
+      bn = n0 + r;
+      bvalid = bn < p.N;
+    }
+    b_off[j] = bvalid ? (uint32_t)((int64_t)bn * p.ldb + lchunk * 16) : kOob;
+  }
+  // A partial last K step (K % 128 != 0) must read its chunks at or beyond K as zero.
+  const bool lane_ktail_dead = (p.K % kBK) != 0 && (ksteps - 1) * kBK + lchunk * 16 >= p.K;
+
+  // Load x of a stage (x < DA: A block x, else B block x - DA). `kill` zero-fills.
+  auto dma_load = [&](int x, uint8_t* stage, uint32_t k0, bool kill) {
+    const uint32_t base = lds_addr(stage);
+    if (x < DA)
+      dma16(ra, base + (x * 4 + wid) * 1024, kill ? kOob : a_off[x], k0);
+    else
+      dma16(rb, base + kA + ((x - DA) * 4 + wid) * 1024, kill ? kOob : b_off[x - DA], k0);
+  };
+  // Stages past this split's last step are filled with zeros (never read); the partial
+  // last K step of the tensor masks lanes beyond K.
+  auto stage_kill = [&](int ls) {
+    return ls >= nsteps || (kbeg + ls == ksteps - 1 && lane_ktail_dead);
+  };
+  auto stage_ptr = [&](int ls) { return smem + (ls % NS) * kStage; };
+
+  // B-tile row of each of the wave's n-subtiles; GEGLU puts gate rows in the first half
+  // of the B tile and the matching up rows in the second.
+  int brow[FN];
+#pragma unroll
+  for (int s = 0; s < FN; ++s) {
+    if (EPI == EPI_GEGLU)
+      brow[s] = (s < FN / 2 ? 0 : BN / 2) + wn * (FN / 2) * 32 + (s % (FN / 2)) * 32;
+    else
+      brow[s] = wn * FN * 32 + s * 32;
+  }
+  auto read_one = [&](Frags<NH>& f, const uint8_t* stage, int kk, int h) {
+    const int fr = h >> 1;  // 0: b0, 1..FM: a0.., FM+1..: b1..
+    if (fr == 0)
+      f.h[h] = read_half(stage + kA, brow[0], kk, h & 1, lane);
+    else if (fr <= FM)
+      f.h[h] = read_half(stage, wave_m0 + (fr - 1) * 32, kk, h & 1, lane);
+    else
+      f.h[h] = read_half(stage + kA, brow[fr - FM], kk, h & 1, lane);
+  };
+
+  v16f acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  // MFMA x of a sub-step: n-subtile x / FM, m-subtile x % FM.
+  auto mma_one = [&](const Frags<NH>& f, int x) {
+    const int i = x / FM, j = x % FM;
+    const int hb = i == 0 ? 0 : 2 * (FM + i);
+    const int ha = 2 * (1 + j);
+    acc[i][j] = mfma<FB, FA>(join(f.h[hb], f.h[hb + 1]), join(f.h[ha], f.h[ha + 1]), acc[i][j]);
+  };
+
+  // Pipeline (NS LDS stages, 2 MFMA sub-steps of 64 K-bytes per stage). Step ls:
+  //   NM x {MFMA(ls, kk=0), reads of frags(ls, kk=1)} | wait DMA(ls+1) + barrier |
+  //   NM x {MFMA(ls, kk=1), reads of frags(ls+1, kk=0), DMA loads of stage ls+NS}
+  // Each MFMA consumes operands read one sub-step earlier; stage ls+NS goes into the slot
+  // of stage ls, which the barrier has just released, and has about NS-1 steps to land;
+  // LDS reads and texture-unit loads sit between consecutive MFMAs, so neither unit
+  // (both shared by the four waves) blocks MFMA issue. sched_barrier(0) pins the order.
+  // Loads of stages past the split's end zero-fill a slot that is never read again,
+  // which keeps the loop free of branches.
+#pragma unroll
+  for (int ls = 0; ls < NS; ++ls) {
+#pragma unroll
+    for (int x = 0; x < ND; ++x)
+      dma_load(x, smem + ls * kStage, (uint32_t)(kbeg + ls) * kBK, stage_kill(ls));
+  }
+  // stage 0 landed: the NS-1 later stages (ND loads each) may still be in flight
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 1)) : "memory");
+  __syncthreads();
+  Frags<NH> f0, f1;
+#pragma unroll
+  for (int h = 0; h < NH; ++h) read_one(f0, smem, 0, h);
+  for (int ls = 0; ls < nsteps; ++ls) {
+    uint8_t* cur = stage_ptr(ls);
+    uint8_t* nxt = stage_ptr(ls + 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int x = 0; x < NM; ++x) {
+      mma_one(f0, x);
+#pragma unroll
+      for (int h = x * NH / NM; h < (x + 1) * NH / NM; ++h) read_one(f1, cur, 1, h);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // stage ls+1 landed (stages ls+2 .. ls+NS-1 may still be in flight)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 2)) : "memory");
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t kn = (uint32_t)(kbeg + ls + NS) * kBK;
+    const bool killn = stage_kill(ls + NS);
+#pragma unroll
+    for (int x = 0; x < NM; ++x) {
+      mma_one(f1, x);
+#pragma unroll
+      for (int h = x * NH / NM; h < (x + 1) * NH / NM; ++h) read_one(f0, nxt, 0, h);
+#pragma unroll
+      for (int d = x * ND / NM; d < (x + 1) * ND / NM; ++d) dma_load(d, cur, kn, killn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // The last steps' zero-fill loads still target LDS: drain them, and let every wave
+  // finish with the stages, before the epilogue reuses the space.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // ---- epilogue --------------------------------------------------------------------
+  // acc[i][j][r]: n-subtile i, m-subtile j; row m = wave_m0 + j*32 + (lane & 31) of the
+  // tile, column (within the n-subtile) 8*(r/4) + (lane >> 5)*4 + (r & 3): each lane
+  // holds runs of four consecutive columns. bf16 results are staged through this wave's
+  // own LDS region of the (now idle) pipeline ring and leave as 16-byte row segments.
+  constexpr int ROWS = FM * 32;  // rows of the wave's output tile
+  const float sa = *p.a_sinv;
+  const int lrow_m = lane & 31;
+  const int lcol = (lane >> 5) * 4;
+  if constexpr (EPI == EPI_LINEAR && OUT == BF8_OUT_BF16) {
+    constexpr int CH = FN * 4;  // 16-byte chunks per staged row (FN*32 bf16)
+    uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
+    const int wave_n0 = n0 + wn * FN * 32;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = i * 32 + 8 * q + lcol;  // within the wave's columns
+        const int n = wave_n0 + col;
+        int seg = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < p.n_seg && n >= p.seg_end[s2]) ? 1 : 0;
+        const float alpha = sa * p.b_sinv[seg * p.b_stride];
+        float bias[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias && n < p.N) {
+          const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
+          bias[0] = bf16_lo(bb.x); bias[1] = bf16_hi(bb.x);
+          bias[2] = bf16_lo(bb.y); bias[3] = bf16_hi(bb.y);
+        }
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          uint2 w;
+          w.x = pack_bf16x2(acc[i][j][4 * q + 0] * alpha + bias[0], acc[i][j][4 * q + 1] * alpha + bias[1]);
+          w.y = pack_bf16x2(acc[i][j][4 * q + 2] * alpha + bias[2], acc[i][j][4 * q + 3] * alpha + bias[3]);
+          stage_put<CH>(wbuf, j * 32 + lrow_m, col, w);
+        }
+      }
+    }
+#pragma unroll 4
+    for (int it = 0; it < ROWS * CH / 64; ++it) {
+      const int idx = it * 64 + lane;
+      const int row = idx / CH, c = idx % CH;
+      const uint4 d = stage_get<CH>(wbuf, row, c);
+      const int gm = m0 + wave_m0 + row;
+      const int gn = wave_n0 + c * 8;
+      if (gm < p.M && gn < p.N)
+        store_bf16x8(reinterpret_cast<uint16_t*>(p.C) + (int64_t)gm * p.ldc + gn, d, p.ldc);
+    }
+  } else if constexpr (EPI == EPI_LINEAR) {
+    // fp32 out; with a K split, raw partial sums into this split's slice of C
+    const bool raw = p.splits > 1;
+    float* cbase = reinterpret_cast<float*>(p.C) + (raw ? split * p.split_stride : 0);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * FN * 32 + i * 32 + 8 * q + lcol;
+        if (n >= p.N) continue;
+        int seg = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < p.n_seg && n >= p.seg_end[s2]) ? 1 : 0;
+        const float alpha = raw ? 1.0f : sa * p.b_sinv[seg * p.b_stride];
+        float bias[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias && !raw) {
+          const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
+          bias[0] = bf16_lo(bb.x); bias[1] = bf16_hi(bb.x);
+          bias[2] = bf16_lo(bb.y); bias[3] = bf16_hi(bb.y);
+        }
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const int m = m0 + wave_m0 + j * 32 + lrow_m;
+          if (m >= p.M) continue;
+          float* c = cbase + (int64_t)m * p.ldc + n;
+          *reinterpret_cast<float4*>(c) =
+              make_float4(acc[i][j][4 * q + 0] * alpha + bias[0], acc[i][j][4 * q + 1] * alpha + bias[1],
+                          acc[i][j][4 * q + 2] * alpha + bias[2], acc[i][j][4 * q + 3] * alpha + bias[3]);
+        }
+      }
+    }
+  } else {
+    // Gated GELU: acc[i] (gate) pairs with acc[i + FN/2] (up). The wave owns H rows
+    // wave_m0 .. +ROWS and HF*32 columns of this tile. Pass 0 stages H (and accumulates
+    // its amax); passes 1, 2 stage the bf16 gate / up pre-activations when the caller
+    // keeps them for the backward.
+    constexpr int HF = FN / 2;
+    constexpr int CH = HF * 4;  // 16-byte chunks per staged H row
+    const float ag = sa * p.b_sinv[0];
+    const float au = sa * p.b_sinv[p.b_stride];
+    uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
+    const int wave_h0 = n0 + wn * HF * 32;
+    uint32_t hmax = 0;
+    auto run_pass = [&](auto pass_tag) {
+      constexpr int pass = decltype(pass_tag)::value;
+#pragma unroll
+      for (int i = 0; i < HF; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = i * 32 + 8 * q + lcol;
+#pragma unroll
+          for (int j = 0; j < FM; ++j) {
+            const float ga[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                 acc[i][j][4 * q + 3]};
+            const float ua[4] = {acc[i + HF][j][4 * q], acc[i + HF][j][4 * q + 1],
+                                 acc[i + HF][j][4 * q + 2], acc[i + HF][j][4 * q + 3]};
+            uint32_t w0, w1;  // packed bf16 pairs (columns 0-1, 2-3 of the run)
+            if constexpr (pass == 0) {
+              const uint32_t g01 = pack_bf16x2(ga[0] * ag, ga[1] * ag);
+              const uint32_t g23 = pack_bf16x2(ga[2] * ag, ga[3] * ag);
+              const uint32_t u01 = pack_bf16x2(ua[0] * au, ua[1] * au);
+              const uint32_t u23 = pack_bf16x2(ua[2] * au, ua[3] * au);
+              const uint32_t l01 = pack_bf16x2(gelu_tanh_f32(bf16_lo(g01)), gelu_tanh_f32(bf16_hi(g01)));
+              const uint32_t l23 = pack_bf16x2(gelu_tanh_f32(bf16_lo(g23)), gelu_tanh_f32(bf16_hi(g23)));
+              w0 = pack_bf16x2(bf16_lo(l01) * bf16_lo(u01), bf16_hi(l01) * bf16_hi(u01));
+              w1 = pack_bf16x2(bf16_lo(l23) * bf16_lo(u23), bf16_hi(l23) * bf16_hi(u23));
+              const uint32_t a0 = w0 & 0x7FFF7FFFu, a1 = w1 & 0x7FFF7FFFu;
+              hmax = max(hmax, max(max(a0 << 16, a0 & 0xFFFF0000u), max(a1 << 16, a1 & 0xFFFF0000u)));
+            } else if constexpr (pass == 1) {
+              w0 = pack_bf16x2(ga[0] * ag, ga[1] * ag);
+              w1 = pack_bf16x2(ga[2] * ag, ga[3] * ag);
+            } else {
+              w0 = pack_bf16x2(ua[0] * au, ua[1] * au);
+              w1 = pack_bf16x2(ua[2] * au, ua[3] * au);
+            }
+            stage_put<CH>(wbuf, j * 32 + lrow_m, col, make_uint2(w0, w1));
+          }
+        }
+      }
+      uint16_t* dst = pass == 0 ? reinterpret_cast<uint16_t*>(p.C) : p.GU;
+      const int64_t ld = pass == 0 ? p.ldc : 2 * (int64_t)p.I;
+      const int coff = pass == 2 ? p.I : 0;
+#pragma unroll 4
+      for (int it = 0; it < ROWS * CH / 64; ++it) {
+        const int idx = it * 64 + lane;
+        const int row = idx / CH, c = idx % CH;
+        const uint4 d = stage_get<CH>(wbuf, row, c);
+        const int gm = m0 + wave_m0 + row;
+        if (gm < p.M) store_bf16x8(dst + (int64_t)gm * ld + coff + wave_h0 + c * 8, d, ld);
+      }
+    };
+    run_pass(std::integral_constant<int, 0>{});
+    if (p.GU) {
+      run_pass(std::integral_constant<int, 1>{});
+      run_pass(std::integral_constant<int, 2>{});
+    }
+    hmax = block_max_u32<kThreads>(hmax);
+    if (t == 0) p.partials[blockIdx.x] = hmax;
+  }
+}
+
+template <class T, int EPI, int OUT>
+int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads);
+  if (fa == BF8_E4M3 && fb == BF8_E4M3)
+    hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI, OUT>), grid, block, 0, s, p);
+  else if (fa == BF8_E5M2 && fb == BF8_E4M3)
+    hipLaunchKernelGGL((gemm_kernel<T, 1, 0, EPI, OUT>), grid, block, 0, s, p);
+  else if (fa == BF8_E4M3 && fb == BF8_E5M2)
+    hipLaunchKernelGGL((gemm_kernel<T, 0, 1, EPI, OUT>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_kernel<T, 1, 1, EPI, OUT>), grid, block, 0, s, p);
+  return launch_status("gemm_kernel");
+}
+
+}  // namespace
+
+template <class T>
+int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
+                     hipStream_t stream) {
+  if (epi == EPI_GEGLU) {
+    if constexpr (T::FN % 2 == 0) {
+      const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(kThreads);
+      hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI_GEGLU, BF8_OUT_BF16>), grid, block, 0, stream, p);
+      return launch_status("gemm_kernel(geglu)");
+    } else {
+      set_error("gemm: tile %dx%d has no gated-GELU variant", T::BM, T::BN);
+      return BF8_EINVAL;
+    }
+  }
+  if (out_dtype == BF8_OUT_BF16) return launch_typed<T, EPI_LINEAR, BF8_OUT_BF16>(p, fmt_a, fmt_b, stream);
+  return launch_typed<T, EPI_LINEAR, BF8_OUT_F32>(p, fmt_a, fmt_b, stream);
+}
+
+}  // namespace bf8

@@ -100,6 +100,21 @@ def partials_buffer(count, device):
     return buf
 
 
+# Per-(device, stream) split-K workspace of bf8_gemm (fp32 partial sums), reused in
+# stream order.
+_GEMM_WS = {}
+
+
+def gemm_workspace(nbytes, device):
+    device = torch.device(device)
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    buf = _GEMM_WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
+        _GEMM_WS[key] = buf
+    return buf
+
+
 def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None, out_t=None):
     """Current-scaling quantization of a bf16 tensor (flattened to 2-D [rows, cols]).
 
@@ -208,7 +223,8 @@ def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=N
         bias = bias.contiguous()
     L = _lib.lib()
     ws_bytes = int(L.bf8_gemm_workspace(M, N, K))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
+    ws = gemm_workspace(ws_bytes, a.device) if ws_bytes else None
+    ws_bytes = ws.numel() if ws is not None else 0
     _lib.check(L.bf8_gemm(_ptr(a), a_fmt, a.stride(0), _ptr(b), b_fmt, b.stride(0), M, N, K,
                           _sinv_ptr(a_meta), _sinv_ptr(b_meta), b_meta_stride, seg, n_seg,
                           _ptr(bias), _ptr(out), OUT_BF16 if out_dtype == torch.bfloat16 else OUT_F32,

@@ -271,3 +271,47 @@ def test_mlp_down_gemm_on_own_h8(gpu):
     print(f"[mlp end-to-end] RMS(err)/RMS = {rel_rms:.3e}, "
           f"max/RMS = {err.abs().max().item() / _rms(full):.3e}", flush=True)
     assert rel_rms <= 0.005
+
+
+# ---- block-tile shapes and split-K -------------------------------------------------------
+# BONGARD_FP8_GEMM_TILE forces the library's plan (read on every call), so each tile shape
+# and the split-K fix-up are checked on shapes with M, N and K tails.
+TILES = ["256x256", "256x160", "160x256", "128x128"]
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("tile", TILES)
+def test_tile_shapes(gpu, monkeypatch, tile, splits):
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", f"{tile}:{splits}")
+    _gemm_case(gpu, 300, 328, 1040, seed=17, bias=True)  # 9 K steps, the last partial
+    _gemm_case(gpu, 40, 520, 384, fa=ops.E5M2, seed=18, a_std=1e-3)
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_split_k_deterministic(gpu, monkeypatch, tile):
+    """Split partials are summed in split order, so repeated calls agree bit for bit."""
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", f"{tile}:4")
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(520, 2048, generator=g).to(torch.bfloat16)
+    b = (torch.randn(264, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    aq, bq = _quant(a, 0, gpu), _quant(b, 0, gpu)
+    outs = [ops.gemm(aq.data, 0, aq.meta, bq.data, 0, bq.meta, out_dtype=torch.float32)
+            for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ra, _, sa, _ = orc.quantize(a, 0)
+    rb, _, sb, _ = orc.quantize(b, 0)
+    _assert_fp32_close(outs[0], orc.scaled_mm(ra, sa, 0, rb, sb, 0), what=f"split4 {tile}")
+
+
+@pytest.mark.parametrize("tile", ["256x256", "160x256", "128x128"])
+def test_geglu_tiles(gpu, monkeypatch, tile):
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", tile)
+    _geglu_case(gpu, 300, 384, 528, seed=11)
+
+
+def test_skinny_down_projection_auto_plan(gpu):
+    """c4's down projection (M=512, K=10240): the automatic plan splits K."""
+    assert ops._lib.lib().bf8_gemm_workspace(512, 2560, 10240) > 0
+    _gemm_case(gpu, 512, 2560, 10240, seed=23, b_std=0.014)

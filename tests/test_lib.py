@@ -56,3 +56,17 @@ def test_partials_counts():
     assert L.bf8_amax_partials(1 << 30) == 512
     assert L.bf8_geglu_partials(4096, 10240) == 16 * 80
     assert L.bf8_gemm_workspace(4096, 2560, 10240) >= 0
+
+
+def test_plan_override_env(monkeypatch):
+    """BONGARD_FP8_GEMM_TILE forces the tile (and K split) of the next calls; the gated-GELU
+    partial count follows the forced tile, and a K split sizes the fp32 workspace."""
+    L = _lib.lib()
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "128x128")
+    assert L.bf8_geglu_partials(300, 384) == 3 * 6
+    assert L.bf8_gemm_workspace(512, 2560, 10240) == 0
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:4")
+    assert L.bf8_geglu_partials(300, 384) == 2 * 3
+    assert L.bf8_gemm_workspace(512, 2560, 10240) == 4 * 512 * 2560 * 4
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x160")  # no gated-GELU variant
+    assert L.bf8_geglu_partials(4096, 10240) >= 1
