@@ -233,4 +233,59 @@ __device__ inline float scale_from_partials_block(const uint32_t* __restrict__ p
   return s_scale;
 }
 
+// Delayed scaling (TE DelayedScaling, margin 0, amax_compute_algo "max") folded into a
+// consumer kernel. state = history[len], then meta {amax, scale, scale_inv, next slot}.
+// Every block reduces the previous step's amax partials (n_prev of them; none on the
+// first step) and forms w = max(history[i != pos], that amax), the window after the
+// amax is pushed into slot pos. scale = fp32(fp8_max / f64(w)) when the window is finite
+// and w > 0, else the stored scale is kept. Block (0,0) pushes the amax and publishes the
+// meta. All blocks compute the same values, so reading the words block 0 rewrites is
+// harmless: slot pos is excluded, and the stored scale is only used when it is written
+// back unchanged. Block (0,0) also writes {w, scale, scale_inv, 0} to meta_out (if any),
+// a copy of this step's scale that later steps do not overwrite. Result valid in all
+// threads.
+template <int NT>
+__device__ inline float delayed_scale_block(float* __restrict__ state, int len, int pos,
+                                            const uint32_t* __restrict__ prev, int64_t n_prev,
+                                            float fp8_max, float* __restrict__ meta_out) {
+  __shared__ float s_scale;
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < n_prev; i += NT) m = max(m, prev[i]);
+  m = block_max_u32<NT>(m);
+  if (threadIdx.x == 0) {
+    const bool have_new = n_prev > 0;
+    const float amax_new = __uint_as_float(m);
+    float w = have_new ? amax_new : 0.0f;
+    bool finite = !have_new || (m < 0x7F800000u);
+    for (int i = 0; i < len; ++i) {
+      if (have_new && i == pos) continue;
+      const float v = state[i];
+      finite &= (v == v) && (fabsf(v) != INFINITY);
+      w = fmaxf(w, v);
+    }
+    float* meta = state + len;
+    float scale = meta[1];
+    if (finite && w > 0.0f) scale = (float)((double)fp8_max / (double)w);
+    s_scale = scale;
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      if (have_new) {
+        state[pos] = amax_new;
+        meta[0] = amax_new;
+      }
+      const float scale_inv = (float)(1.0 / (double)scale);
+      meta[1] = scale;
+      meta[2] = scale_inv;
+      meta[3] = (float)((pos + (have_new ? 1 : 0)) % len);
+      if (meta_out) {
+        meta_out[0] = w;
+        meta_out[1] = scale;
+        meta_out[2] = scale_inv;
+        meta_out[3] = 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  return s_scale;
+}
+
 }  // namespace bf8

@@ -13,6 +13,11 @@
 // its block 0 publishes the meta record. The same cast kernel consumes the per-tile
 // partials of H written by the gate/up GEMM epilogue and those of dGU written by the
 // gated-GELU backward. Streaming loads use 16-byte vectors, several in flight per lane.
+//
+// Delayed scaling (amax history, TE DelayedScaling semantics) needs no pre-pass: the
+// cast kernel derives the scale from the history (after folding in the previous step's
+// amax partials) and writes this step's amax partials while it casts, so a delayed
+// quantization is one streaming pass and one launch.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -43,8 +48,8 @@ int launch_status(const char* what) {
 namespace {
 
 constexpr int kNT = 256;            // threads per block for streaming kernels
-constexpr int kVecPerThread = 4;    // 16-byte vectors per lane per iteration
-constexpr int64_t kMaxAmaxBlocks = 512;  // keeps the consumers' partial reads at <= 2 KB
+constexpr int kVecPerThread = 8;    // 16-byte loads in flight per lane (amax)
+constexpr int64_t kMaxAmaxBlocks = 1024;  // 4 blocks per CU; consumers read <= 4 KB of partials
 
 int64_t amax_blocks(int64_t n) {
   int64_t per_block = (int64_t)kNT * kVecPerThread * 8;  // bf16 elements per block pass
@@ -68,12 +73,14 @@ __global__ __launch_bounds__(kNT) void amax_partials_kernel(const uint16_t* __re
   const int64_t stride = (int64_t)gridDim.x * kNT;
   uint32_t m = 0;
   int64_t i = (int64_t)blockIdx.x * kNT + threadIdx.x;
-  for (; i + 3 * stride < nvec; i += 4 * stride) {
-    uint4 v0 = load_nt(xv + i);
-    uint4 v1 = load_nt(xv + i + stride);
-    uint4 v2 = load_nt(xv + i + 2 * stride);
-    uint4 v3 = load_nt(xv + i + 3 * stride);
-    m = max(m, max(max(absmax_key8(v0), absmax_key8(v1)), max(absmax_key8(v2), absmax_key8(v3))));
+  // kVecPerThread independent 16-byte loads per lane in flight (HBM latency x bandwidth
+  // needs ~32 MB in flight chip-wide)
+  for (; i + (kVecPerThread - 1) * stride < nvec; i += kVecPerThread * stride) {
+    uint4 v[kVecPerThread];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) v[j] = load_nt(xv + i + j * stride);
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) m = max(m, absmax_key8(v[j]));
   }
   for (; i < nvec; i += stride) m = max(m, absmax_key8(load_nt(xv + i)));
   // scalar tail (n % 8), handled by block 0
@@ -93,34 +100,61 @@ __global__ __launch_bounds__(kNT) void scale_from_partials_kernel(
   if (threadIdx.x == 0) write_meta_from_amax(m, fp8_max, meta);
 }
 
-// The scale comes from scale_ptr, or (scale_ptr == NULL) from amax partials that every
-// block reduces itself (block 0 then also writes meta_out).
+// Where a cast kernel takes its scale from (exactly one source):
+//  - `scale`: a device fp32 scalar;
+//  - current scaling: `partials` (np amax partials of x or of its producer), reduced in
+//    every block; block 0 publishes meta_out = {amax, scale, scale_inv, 0};
+//  - delayed scaling: `state` (amax history [len] + meta), which first absorbs the
+//    previous step's amax (`prev`, n_prev partials; none on the first step) at slot pos;
+//    block 0 copies this step's meta to meta_out (if not NULL).
+struct ScaleSrc {
+  const float* scale;
+  const uint32_t* partials;
+  int64_t np;
+  float* meta_out;
+  float* state;
+  int len, pos;
+  const uint32_t* prev;
+  int64_t n_prev;
+};
+
 template <int FMT>
-__device__ __forceinline__ float resolve_scale(const float* scale_ptr, const uint32_t* partials,
-                                               int64_t np, float* meta_out) {
-  if (scale_ptr) return *scale_ptr;
-  return scale_from_partials_block<kNT>(partials, np, Fp8Max<FMT>::value, meta_out);
+__device__ __forceinline__ float resolve_scale(const ScaleSrc& s) {
+  if (s.scale) return *s.scale;
+  if (s.state)
+    return delayed_scale_block<kNT>(s.state, s.len, s.pos, s.prev, s.n_prev, Fp8Max<FMT>::value,
+                                    s.meta_out);
+  return scale_from_partials_block<kNT>(s.partials, s.np, Fp8Max<FMT>::value, s.meta_out);
+}
+
+// Block max of the lanes' amax keys, stored as this block's partial (amax_out != NULL).
+__device__ __forceinline__ void store_block_amax(uint32_t m, uint32_t* amax_out, int64_t blk) {
+  if (!amax_out) return;
+  m = block_max_u32<kNT>(m);
+  if (threadIdx.x == 0) amax_out[blk] = m;
 }
 
 // Row-major cast: each lane converts 16 consecutive bf16 (two 16-byte loads) into one
 // 16-byte store. n16 = number of 16-element groups; the n % 16 tail is done bytewise.
+// With amax_out, each block also writes the max |x| key of the elements it cast.
 template <int FMT>
 __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ x, int64_t n,
-                                                   const float* __restrict__ scale_ptr,
-                                                   const uint32_t* __restrict__ partials,
-                                                   int64_t np, float* __restrict__ meta_out,
-                                                   uint8_t* __restrict__ out) {
-  const float scale = resolve_scale<FMT>(scale_ptr, partials, np, meta_out);
+                                                   ScaleSrc src, uint8_t* __restrict__ out,
+                                                   uint32_t* __restrict__ amax_out) {
+  const float scale = resolve_scale<FMT>(src);
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint4* ov = reinterpret_cast<uint4*>(out);
   const int64_t n16 = n >> 4;
   const int64_t stride = (int64_t)gridDim.x * kNT;
   int64_t i = (int64_t)blockIdx.x * kNT + threadIdx.x;
+  uint32_t m = 0;
   for (; i + stride < n16; i += 2 * stride) {
     uint4 a0 = load_nt(xv + 2 * i);
     uint4 a1 = load_nt(xv + 2 * i + 1);
     uint4 b0 = load_nt(xv + 2 * (i + stride));
     uint4 b1 = load_nt(xv + 2 * (i + stride) + 1);
+    if (amax_out)
+      m = max(m, max(max(absmax_key8(a0), absmax_key8(a1)), max(absmax_key8(b0), absmax_key8(b1))));
     uint2 qa0 = quant8_bf16<FMT>(a0, scale), qa1 = quant8_bf16<FMT>(a1, scale);
     uint2 qb0 = quant8_bf16<FMT>(b0, scale), qb1 = quant8_bf16<FMT>(b1, scale);
     store_nt(ov + i, make_uint4(qa0.x, qa0.y, qa1.x, qa1.y));
@@ -129,6 +163,7 @@ __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ 
   for (; i < n16; i += stride) {
     uint4 a0 = load_nt(xv + 2 * i);
     uint4 a1 = load_nt(xv + 2 * i + 1);
+    if (amax_out) m = max(m, max(absmax_key8(a0), absmax_key8(a1)));
     uint2 qa0 = quant8_bf16<FMT>(a0, scale), qa1 = quant8_bf16<FMT>(a1, scale);
     store_nt(ov + i, make_uint4(qa0.x, qa0.y, qa1.x, qa1.y));
   }
@@ -137,11 +172,14 @@ __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ 
       float xf = __uint_as_float((uint32_t)x[j] << 16);
       float p = xf * scale;
       out[j] = (uint8_t)(quant4<FMT>(p, 0.f, 0.f, 0.f, xf, 0.f, 0.f, 0.f, scale) & 0xFFu);
+      m = max(m, (uint32_t)(x[j] & 0x7FFFu) << 16);
     }
   }
+  store_block_amax(m, amax_out, blockIdx.x);
 }
 
-// Cast with a transposed copy. One block handles a 64 x 64 tile of x:
+// Cast with a transposed copy, over 64 x 64 tiles of x (grid-stride, so the grid and the
+// number of amax partials stay bounded). Per tile:
 //  - each lane loads 16 bf16 of one row (4 lanes cover a 128-byte row segment),
 //    quantizes, stores 16 bytes of `out` (if requested) and stages the bytes in LDS;
 //  - after a barrier each lane gathers 16 bytes of one tile column and stores them as a
@@ -149,55 +187,70 @@ __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ 
 // rows and cols need not be multiples of 64; cols % 16 == 0.
 constexpr int kTT = 64;
 constexpr int kTPitch = kTT + 4;  // LDS row pitch (bytes), staggers banks for the gather
+constexpr int kMaxTransposeBlocks = 1024;
 
 template <int FMT>
 __global__ __launch_bounds__(kNT) void cast_transpose_kernel(
-    const uint16_t* __restrict__ x, int64_t rows, int64_t cols,
-    const float* __restrict__ scale_ptr, const uint32_t* __restrict__ partials, int64_t np,
-    float* __restrict__ meta_out, uint8_t* __restrict__ out, uint8_t* __restrict__ out_t) {
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, ScaleSrc src,
+    uint8_t* __restrict__ out, uint8_t* __restrict__ out_t, uint32_t* __restrict__ amax_out) {
   __shared__ uint32_t tile[kTT * kTPitch / 4];
   uint8_t* tb = reinterpret_cast<uint8_t*>(tile);
-  const float scale = resolve_scale<FMT>(scale_ptr, partials, np, meta_out);
-  const int64_t r0 = (int64_t)blockIdx.y * kTT, c0 = (int64_t)blockIdx.x * kTT;
+  const float scale = resolve_scale<FMT>(src);
+  const int64_t tiles_c = (cols + kTT - 1) / kTT;
+  const int64_t ntiles = tiles_c * ((rows + kTT - 1) / kTT);
   const int t = threadIdx.x;
-  {
-    const int lr = t >> 2, lc = (t & 3) * 16;
-    const int64_t r = r0 + lr, c = c0 + lc;
-    uint32_t q[4] = {0u, 0u, 0u, 0u};
-    if (r < rows && c < cols) {
-      const uint4* src = reinterpret_cast<const uint4*>(x + r * cols + c);
-      uint4 a0 = load_nt(src);
-      uint4 a1 = load_nt(src + 1);
-      uint2 q0 = quant8_bf16<FMT>(a0, scale), q1 = quant8_bf16<FMT>(a1, scale);
-      q[0] = q0.x; q[1] = q0.y; q[2] = q1.x; q[3] = q1.y;
-      if (out) *reinterpret_cast<uint4*>(out + r * cols + c) = make_uint4(q[0], q[1], q[2], q[3]);
+  uint32_t m = 0;
+  for (int64_t tile_id = blockIdx.x; tile_id < ntiles; tile_id += gridDim.x) {
+    const int64_t r0 = (tile_id / tiles_c) * kTT, c0 = (tile_id % tiles_c) * kTT;
+    {
+      const int lr = t >> 2, lc = (t & 3) * 16;
+      const int64_t r = r0 + lr, c = c0 + lc;
+      uint32_t q[4] = {0u, 0u, 0u, 0u};
+      if (r < rows && c < cols) {
+        const uint4* src4 = reinterpret_cast<const uint4*>(x + r * cols + c);
+        uint4 a0 = load_nt(src4);
+        uint4 a1 = load_nt(src4 + 1);
+        if (amax_out) m = max(m, max(absmax_key8(a0), absmax_key8(a1)));
+        uint2 q0 = quant8_bf16<FMT>(a0, scale), q1 = quant8_bf16<FMT>(a1, scale);
+        q[0] = q0.x; q[1] = q0.y; q[2] = q1.x; q[3] = q1.y;
+        if (out) *reinterpret_cast<uint4*>(out + r * cols + c) = make_uint4(q[0], q[1], q[2], q[3]);
+      }
+      uint32_t* dst = reinterpret_cast<uint32_t*>(tb + lr * kTPitch + lc);
+      dst[0] = q[0]; dst[1] = q[1]; dst[2] = q[2]; dst[3] = q[3];
     }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(tb + lr * kTPitch + lc);
-    dst[0] = q[0]; dst[1] = q[1]; dst[2] = q[2]; dst[3] = q[3];
-  }
-  __syncthreads();
-  {
-    const int oc = t >> 2, orow = (t & 3) * 16;  // out_t row = tile column oc
-    const int64_t tr = c0 + oc, tc = r0 + orow;  // position in out_t [cols, rows]
-    if (tr < cols && tc < rows) {
-      uint32_t w[4];
+    __syncthreads();
+    {
+      const int oc = t >> 2, orow = (t & 3) * 16;  // out_t row = tile column oc
+      const int64_t tr = c0 + oc, tc = r0 + orow;  // position in out_t [cols, rows]
+      if (tr < cols && tc < rows) {
+        uint32_t w[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t b0 = tb[(orow + 4 * j + 0) * kTPitch + oc];
-        uint32_t b1 = tb[(orow + 4 * j + 1) * kTPitch + oc];
-        uint32_t b2 = tb[(orow + 4 * j + 2) * kTPitch + oc];
-        uint32_t b3 = tb[(orow + 4 * j + 3) * kTPitch + oc];
-        w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-      }
-      uint8_t* dst = out_t + tr * rows + tc;
-      if (tc + 16 <= rows && (rows & 15) == 0) {
-        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-      } else {
-        for (int j = 0; j < 16 && tc + j < rows; ++j) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+        for (int j = 0; j < 4; ++j) {
+          uint32_t b0 = tb[(orow + 4 * j + 0) * kTPitch + oc];
+          uint32_t b1 = tb[(orow + 4 * j + 1) * kTPitch + oc];
+          uint32_t b2 = tb[(orow + 4 * j + 2) * kTPitch + oc];
+          uint32_t b3 = tb[(orow + 4 * j + 3) * kTPitch + oc];
+          w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+        uint8_t* dst = out_t + tr * rows + tc;
+        if (tc + 16 <= rows && (rows & 15) == 0) {
+          *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+          for (int j = 0; j < 16 && tc + j < rows; ++j) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+        }
       }
     }
+    __syncthreads();  // the next tile reuses the LDS staging
   }
+  store_block_amax(m, amax_out, blockIdx.x);
 }
+
+int64_t transpose_blocks(int64_t rows, int64_t cols) {
+  const int64_t tiles = ((rows + kTT - 1) / kTT) * ((cols + kTT - 1) / kTT);
+  return tiles < kMaxTransposeBlocks ? (tiles > 0 ? tiles : 1) : kMaxTransposeBlocks;
+}
+
+int64_t row_cast_blocks(int64_t n) { return grid_for_stream((n + 15) / 16, 2 * kNT, 2048); }
 
 // ---- delayed scaling ------------------------------------------------------------------
 // state layout: history[len], then meta {amax_last, scale, scale_inv, pos}; a fresh
@@ -238,13 +291,10 @@ __global__ __launch_bounds__(kNT) void delayed_end_kernel(float* state, int len,
   }
 }
 
-int launch_cast(const void* x, int64_t rows, int64_t cols, const float* scale,
-                const uint32_t* partials, int64_t np, float* meta_out, int fmt, uint8_t* out,
-                uint8_t* out_t, void* stream, const char* who) {
+int launch_cast(const void* x, int64_t rows, int64_t cols, const ScaleSrc& src, int fmt,
+                uint8_t* out, uint8_t* out_t, uint32_t* amax_out, void* stream, const char* who) {
   BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "%s: bad fmt %d", who, fmt);
   BF8_CHECK(rows >= 0 && cols >= 0, "%s: negative shape", who);
-  BF8_CHECK(scale != nullptr || (partials != nullptr && np >= 1 && np <= 4096),
-            "%s: no scale source (or more than 4096 partials)", who);
   BF8_CHECK(out || out_t, "%s: out and out_t are both NULL", who);
   BF8_CHECK(((uintptr_t)x & 15) == 0 && (!out || ((uintptr_t)out & 15) == 0),
             "%s: x and out must be 16-byte aligned", who);
@@ -253,28 +303,40 @@ int launch_cast(const void* x, int64_t rows, int64_t cols, const float* scale,
   hipStream_t s = as_stream(stream);
   const uint16_t* xs = (const uint16_t*)x;
   if (out_t == nullptr) {
-    const int grid = grid_for_stream((n + 15) / 16, 2 * kNT, 2048);
+    const int grid = (int)row_cast_blocks(n);
     if (fmt == BF8_E4M3)
-      hipLaunchKernelGGL(cast_kernel<BF8_E4M3>, dim3(grid), dim3(kNT), 0, s, xs, n, scale,
-                         partials, np, meta_out, out);
+      hipLaunchKernelGGL(cast_kernel<BF8_E4M3>, dim3(grid), dim3(kNT), 0, s, xs, n, src, out,
+                         amax_out);
     else
-      hipLaunchKernelGGL(cast_kernel<BF8_E5M2>, dim3(grid), dim3(kNT), 0, s, xs, n, scale,
-                         partials, np, meta_out, out);
+      hipLaunchKernelGGL(cast_kernel<BF8_E5M2>, dim3(grid), dim3(kNT), 0, s, xs, n, src, out,
+                         amax_out);
     return launch_status("cast_kernel");
   }
   BF8_CHECK(cols % 16 == 0, "%s: transposed cast needs cols %% 16 == 0 (got %lld)", who,
             (long long)cols);
   BF8_CHECK(((uintptr_t)out_t & 15) == 0, "%s: out_t must be 16-byte aligned", who);
-  BF8_CHECK((cols + kTT - 1) / kTT < (1LL << 31) && (rows + kTT - 1) / kTT < 65536,
-            "%s: shape too large for the transposed cast grid", who);
-  dim3 grid((unsigned)((cols + kTT - 1) / kTT), (unsigned)((rows + kTT - 1) / kTT));
+  const dim3 grid((unsigned)transpose_blocks(rows, cols));
   if (fmt == BF8_E4M3)
     hipLaunchKernelGGL(cast_transpose_kernel<BF8_E4M3>, grid, dim3(kNT), 0, s, xs, rows, cols,
-                       scale, partials, np, meta_out, out, out_t);
+                       src, out, out_t, amax_out);
   else
     hipLaunchKernelGGL(cast_transpose_kernel<BF8_E5M2>, grid, dim3(kNT), 0, s, xs, rows, cols,
-                       scale, partials, np, meta_out, out, out_t);
+                       src, out, out_t, amax_out);
   return launch_status("cast_transpose_kernel");
+}
+
+ScaleSrc given_scale(const float* scale) {
+  ScaleSrc s{};
+  s.scale = scale;
+  return s;
+}
+
+ScaleSrc current_scale(const uint32_t* partials, int64_t np, float* meta) {
+  ScaleSrc s{};
+  s.partials = partials;
+  s.np = np;
+  s.meta_out = meta;
+  return s;
 }
 
 }  // namespace
@@ -285,7 +347,7 @@ using namespace bf8;
 extern "C" {
 
 const char* bf8_last_error(void) { return bf8::g_err; }
-int bf8_abi_version(void) { return 3; }
+int bf8_abi_version(void) { return 4; }
 
 int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
 
@@ -313,17 +375,41 @@ int bf8_scale_from_partials(const uint32_t* partials, int64_t n_partials, int fm
 int bf8_cast_bf16(const void* x, int64_t rows, int64_t cols, const float* scale, int fmt,
                   uint8_t* out, uint8_t* out_t, void* stream) {
   BF8_CHECK(scale != nullptr, "bf8_cast_bf16: scale is NULL");
-  return launch_cast(x, rows, cols, scale, nullptr, 0, nullptr, fmt, out, out_t, stream,
+  return launch_cast(x, rows, cols, given_scale(scale), fmt, out, out_t, nullptr, stream,
                      "bf8_cast_bf16");
 }
 
 int bf8_cast_partials_bf16(const void* x, int64_t rows, int64_t cols, const uint32_t* partials,
                            int64_t n_partials, int fmt, float* meta, uint8_t* out,
                            uint8_t* out_t, void* stream) {
-  BF8_CHECK(partials && meta && n_partials >= 1,
-            "bf8_cast_partials_bf16: bad partials or meta");
-  return launch_cast(x, rows, cols, nullptr, partials, n_partials, meta, fmt, out, out_t,
-                     stream, "bf8_cast_partials_bf16");
+  BF8_CHECK(partials && meta && n_partials >= 1 && n_partials <= 4096,
+            "bf8_cast_partials_bf16: bad partials or meta (1..4096 partials)");
+  return launch_cast(x, rows, cols, current_scale(partials, n_partials, meta), fmt, out, out_t,
+                     nullptr, stream, "bf8_cast_partials_bf16");
+}
+
+int64_t bf8_cast_amax_partials(int64_t rows, int64_t cols, int transpose) {
+  if (rows <= 0 || cols <= 0) return 1;
+  return transpose ? transpose_blocks(rows, cols) : row_cast_blocks(rows * cols);
+}
+
+int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* state, int len,
+                          int pos, const uint32_t* prev_partials, int64_t n_prev, int fmt,
+                          float* meta_out, uint8_t* out, uint8_t* out_t, uint32_t* partials_out,
+                          void* stream) {
+  BF8_CHECK(state && len >= 1 && len <= 1024, "bf8_cast_delayed_bf16: bad state/len");
+  BF8_CHECK(pos >= 0 && pos < len, "bf8_cast_delayed_bf16: pos %d outside [0, %d)", pos, len);
+  BF8_CHECK(n_prev >= 0 && n_prev <= 4096 && (n_prev == 0 || prev_partials),
+            "bf8_cast_delayed_bf16: bad previous partials (0..4096)");
+  ScaleSrc src{};
+  src.state = state;
+  src.len = len;
+  src.pos = pos;
+  src.prev = prev_partials;
+  src.n_prev = n_prev;
+  src.meta_out = meta_out;
+  return launch_cast(x, rows, cols, src, fmt, out, out_t, partials_out, stream,
+                     "bf8_cast_delayed_bf16");
 }
 
 int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,

@@ -9,6 +9,10 @@ quantized to e5m2 with its own per-tensor scale;
 The transposed copies come from the same cast kernels (LDS-staged transpose), so each
 operand is read from HBM once per quantization.
 
+Scaling is per-tensor current scaling by default; passing ``scaling``
+(:class:`bongard_amd.scaling.LinearScaling`) switches a linear to delayed scaling with an
+amax history (one-pass casts, the scale of each role taken from its history).
+
 Reference behaviour these replace: torchao Float8Linear.forward/backward reached from
 bongard/float8_training.py:16-22, te.Linear under TELinear.forward
 (bongard/te_linear.py:59-77), and TEMLP/FusedMLP (bongard/te_linear.py:98-103,
@@ -32,21 +36,32 @@ class QuantizedWeight:
     version: int
 
 
-def quantize_weight(weight, *, transpose=True):
-    return ops.quantize(weight.detach(), E4M3, rowwise=True, transpose=transpose)
+def quantize_weight(weight, *, transpose=True, scaler=None):
+    return _quantize(weight.detach(), E4M3, scaler, rowwise=True, transpose=transpose)
+
+
+def _quantize(x, fmt, scaler, *, rowwise=True, transpose=False):
+    """Current scaling (scaler None) or the scaler's delayed scaling."""
+    if scaler is None:
+        return ops.quantize(x, fmt, rowwise=rowwise, transpose=transpose)
+    return scaler.quantize(x, rowwise=rowwise, transpose=transpose)
 
 
 class Fp8LinearFunction(torch.autograd.Function):
-    """y = x @ W^T (+ b) in FP8; x: bf16 [M, K] with M % 16 == 0 when grads are needed."""
+    """y = x @ W^T (+ b) in FP8; x: bf16 [M, K] with M % 16 == 0 when grads are needed.
+
+    ``scaling``: None (current scaling) or a LinearScaling (delayed scaling)."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, wq):
+    def forward(ctx, x, weight, bias, wq, scaling=None):
         need_dx = ctx.needs_input_grad[0]
         need_dw = ctx.needs_input_grad[1]
-        xq = ops.quantize(x, E4M3, rowwise=True, transpose=need_dw)
+        xq = _quantize(x, E4M3, scaling and scaling.input, transpose=need_dw)
         if wq is None:
-            wq = quantize_weight(weight, transpose=need_dx)
+            wq = quantize_weight(weight, transpose=need_dx,
+                                 scaler=scaling and scaling.weight)
         y = ops.gemm(xq.data, E4M3, xq.meta, wq.data, E4M3, wq.meta, bias=bias)
+        ctx.scaling = scaling
         ctx.has_bias = bias is not None
         ctx.save_for_backward(xq.data_t if need_dw else None, xq.meta,
                               wq.data_t if need_dx else None, wq.meta)
@@ -57,7 +72,9 @@ class Fp8LinearFunction(torch.autograd.Function):
         x8t, x_meta, w8t, w_meta = ctx.saved_tensors
         need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         dy = dy.contiguous()
-        dyq = ops.quantize(dy, E5M2, rowwise=need_dx, transpose=need_dw)
+        scaling = ctx.scaling
+        dyq = _quantize(dy, E5M2, scaling and scaling.grad_output, rowwise=need_dx,
+                        transpose=need_dw)
         dx = dw = db = None
         if need_dx:
             dx = ops.gemm(dyq.data, E5M2, dyq.meta, w8t, E4M3, w_meta)
@@ -65,7 +82,7 @@ class Fp8LinearFunction(torch.autograd.Function):
             dw = ops.gemm(dyq.data_t, E5M2, dyq.meta, x8t, E4M3, x_meta)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = dy.sum(0)
-        return dx, dw, db, None
+        return dx, dw, db, None, None
 
 
 class Fp8GegluMlpFunction(torch.autograd.Function):
@@ -74,26 +91,44 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
     w_gu: bf16 [2I, K] (gate rows then up rows), w_down: bf16 [K_out, I]. ``gu_q`` and
     ``down_q`` are optional cached quantized weights. ``split_scales`` selects one scale
     per gate/up half (torchao / split TE) instead of one shared scale (fused TE gate_up).
+    ``scaling``: None (current scaling) or ``(gate_up, down)`` LinearScaling objects for
+    delayed scaling (roles: x, W_gu, dGU of gate_up; H, W_down, dY of down).
     """
 
     @staticmethod
-    def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate, split_scales):
+    def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scaling=None):
         I = int(intermediate)
         train = any(ctx.needs_input_grad[:3])
-        xq = ops.quantize(x, E4M3, rowwise=True, transpose=ctx.needs_input_grad[1])
+        if scaling is not None and split_scales:
+            raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
+        gs, ds = scaling if scaling is not None else (None, None)
+        xq = _quantize(x, E4M3, gs and gs.input, transpose=ctx.needs_input_grad[1])
         if gu_q is None:
-            gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=ctx.needs_input_grad[0])
+            gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=ctx.needs_input_grad[0],
+                                    scaler=gs and gs.weight)
         stride = 4 if split_scales else 0
-        H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
-                                       w_meta_stride=stride, keep_gu=train)
-        hq = ops.cast_partials(H, hparts, E4M3, rowwise=True, transpose=ctx.needs_input_grad[2])
+        M = xq.rows
+        if ds is None:
+            H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
+                                           w_meta_stride=stride, keep_gu=train)
+            hq = ops.cast_partials(H, hparts, E4M3, rowwise=True,
+                                   transpose=ctx.needs_input_grad[2])
+        else:
+            count = ops.geglu_partials_count(M, I)
+            H, GU, _ = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
+                                      keep_gu=train,
+                                      partials=ds.input.partials_for_producer(count, x.device))
+            hq = ds.input.quantize(H, rowwise=True, transpose=ctx.needs_input_grad[2],
+                                   producer_count=count)
         h_meta = hq.meta
         if down_q is None:
             down_q = quantize_weight(
-                w_down, transpose=ctx.needs_input_grad[0] or ctx.needs_input_grad[1])
+                w_down, transpose=ctx.needs_input_grad[0] or ctx.needs_input_grad[1],
+                scaler=ds and ds.weight)
         y = ops.gemm(hq.data, E4M3, h_meta, down_q.data, E4M3, down_q.meta)
         ctx.intermediate = I
         ctx.split_scales = split_scales
+        ctx.scaling = scaling
         ctx.save_for_backward(GU, xq.data_t, xq.meta, hq.data_t, h_meta, gu_q.data_t,
                               gu_q.meta, down_q.data_t, down_q.meta)
         return y
@@ -103,14 +138,27 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
         (GU, x8t, x_meta, h8t, h_meta, gu8t, gu_meta, d8t, d_meta) = ctx.saved_tensors
         I = ctx.intermediate
         need_dx, need_dgu, need_dd = ctx.needs_input_grad[:3]
+        gs, ds = ctx.scaling if ctx.scaling is not None else (None, None)
         dy = dy.contiguous()
-        dyq = ops.quantize(dy, E5M2, rowwise=True, transpose=need_dd)
+        dyq = _quantize(dy, E5M2, ds and ds.grad_output, rowwise=True, transpose=need_dd)
         dx = dgu = dd = None
         if need_dd:
             dd = ops.gemm(dyq.data_t, E5M2, dyq.meta, h8t, E4M3, h_meta)
         if not (need_dx or need_dgu):
-            return dx, dgu, dd, None, None, None, None
+            return dx, dgu, dd, None, None, None, None, None
         dH = ops.gemm(dyq.data, E5M2, dyq.meta, d8t, E4M3, d_meta)
+        if gs is not None:
+            M = dH.shape[0]
+            count = ops.geglu_bwd_partials_count(M, I)
+            dGU, _ = ops.geglu_bwd(
+                dH, GU, partials=gs.grad_output.partials_for_producer(count, dH.device))
+            dq = gs.grad_output.quantize(dGU, rowwise=need_dx, transpose=need_dgu,
+                                         producer_count=count)
+            if need_dx:
+                dx = ops.gemm(dq.data, E5M2, dq.meta, gu8t, E4M3, gu_meta[0])
+            if need_dgu:
+                dgu = ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta)
+            return dx, dgu, dd, None, None, None, None, None
         dGU, gparts = ops.geglu_bwd(dH, GU)
         if not ctx.split_scales:
             dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=need_dx, transpose=need_dgu)
@@ -136,18 +184,21 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
                 dx = dx_parts[0] + dx_parts[1]
             if need_dgu:
                 dgu = torch.cat(dw_parts, 0)
-        return dx, dgu, dd, None, None, None, None
+        return dx, dgu, dd, None, None, None, None, None
 
 
-def quantize_gate_up(w_gu, intermediate, split_scales, *, transpose=True):
+def quantize_gate_up(w_gu, intermediate, split_scales, *, transpose=True, scaler=None):
     """Quantize [W_gate; W_up] into one [2I, K] fp8 buffer (+ [K, 2I] transposed copy).
 
     split_scales: gate and up halves get separate metas (meta is then [2, 4]).
+    scaler: a DelayedScaler for the shared scale (delayed scaling), or None.
     """
     I = int(intermediate)
     if not split_scales:
-        q = ops.quantize(w_gu.detach(), E4M3, rowwise=True, transpose=transpose)
+        q = _quantize(w_gu.detach(), E4M3, scaler, rowwise=True, transpose=transpose)
         return _GateUp(q.data, q.data_t, q.meta.view(1, 4))
+    if scaler is not None:
+        raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
     K = w_gu.shape[1]
     dev = w_gu.device
     data = torch.empty((2 * I, K), dtype=torch.float8_e4m3fn, device=dev)

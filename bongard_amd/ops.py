@@ -232,12 +232,18 @@ def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=N
     return out
 
 
-def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu=False):
+def geglu_partials_count(M, intermediate):
+    return int(_lib.lib().bf8_geglu_partials(int(M), int(intermediate)))
+
+
+def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu=False,
+               partials=None):
     """Gate/up GEMM with the gated-GELU epilogue.
 
     x8: fp8 e4m3 [M, K]; w8: fp8 e4m3 [2I, K] (gate rows then up rows). Returns
     ``(H bf16 [M, I], GU bf16 [M, 2I] or None, h_partials int32 [tiles])``; the per-tile
-    amax partials of |H| feed ``cast_partials``.
+    amax partials of |H| feed ``cast_partials`` (or a delayed scaler). ``partials``: an
+    optional caller-owned buffer of at least ``geglu_partials_count(M, I)`` entries.
     """
     _require_gpu(x8, w8, x_meta, w_meta)
     M, K = x8.shape
@@ -247,7 +253,13 @@ def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu
     L = _lib.lib()
     H = torch.empty((M, I), dtype=torch.bfloat16, device=x8.device)
     GU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=x8.device) if keep_gu else None
-    parts = torch.empty(int(L.bf8_geglu_partials(M, I)), dtype=torch.int32, device=x8.device)
+    count = int(L.bf8_geglu_partials(M, I))
+    if partials is None:
+        parts = torch.empty(count, dtype=torch.int32, device=x8.device)
+    else:
+        if partials.numel() < count or partials.dtype != torch.int32:
+            raise ValueError(f"gemm_geglu: partials must be int32 with >= {count} entries")
+        parts = partials[:count]
     _lib.check(L.bf8_gemm_geglu(_ptr(x8), x8.stride(0), _ptr(w8), w8.stride(0), M, I, K,
                                 _sinv_ptr(x_meta), _sinv_ptr(w_meta), w_meta_stride, _ptr(H),
                                 H.stride(0), _ptr(GU), _ptr(parts), _stream(x8.device)),
@@ -255,15 +267,26 @@ def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu
     return H, GU, parts
 
 
-def geglu_bwd(dH, GU):
+def geglu_bwd_partials_count(M, intermediate):
+    return int(_lib.lib().bf8_geglu_bwd_partials(int(M), int(intermediate)))
+
+
+def geglu_bwd(dH, GU, *, partials=None):
     """dGU bf16 [M, 2I] (d_gate | d_up) from dH [M, I] and the forward's GU, and the
-    per-block amax partials of |dGU| (for ``cast_partials``)."""
+    per-block amax partials of |dGU| (for ``cast_partials`` or a delayed scaler;
+    ``partials``: an optional caller-owned buffer)."""
     _require_gpu(dH, GU)
     dH = dH.contiguous()
     M, I = dH.shape
     L = _lib.lib()
     dGU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=dH.device)
-    parts = torch.empty(int(L.bf8_geglu_bwd_partials(M, I)), dtype=torch.int32, device=dH.device)
+    count = int(L.bf8_geglu_bwd_partials(M, I))
+    if partials is None:
+        parts = torch.empty(count, dtype=torch.int32, device=dH.device)
+    else:
+        if partials.numel() < count or partials.dtype != torch.int32:
+            raise ValueError(f"geglu_bwd: partials must be int32 with >= {count} entries")
+        parts = partials[:count]
     _lib.check(L.bf8_geglu_bwd(_ptr(dH), _ptr(GU), M, I, _ptr(dGU), _ptr(parts),
                                _stream(dH.device)), "bf8_geglu_bwd")
     return dGU, parts
@@ -288,3 +311,33 @@ def delayed_scale_end(state, length, partials):
     _lib.check(_lib.lib().bf8_delayed_scale_end(_ptr(state), length, _ptr(partials),
                                                 partials.numel(), _stream(state.device)),
                "bf8_delayed_scale_end")
+
+
+def cast_amax_partials_count(rows, cols, transpose):
+    return int(_lib.lib().bf8_cast_amax_partials(int(rows), int(cols), int(bool(transpose))))
+
+
+def cast_delayed(x, state, length, pos, prev_partials, fmt=E4M3, *, rowwise=True,
+                 transpose=False, partials_out=None, meta_out=None):
+    """One-pass delayed-scaling cast (bf8_cast_delayed_bf16).
+
+    ``prev_partials``: the previous step's amax partials (None on the first step), pushed
+    into history slot ``pos`` before the scale is derived. ``partials_out``: buffer for
+    this step's amax partials of |x| (``cast_amax_partials_count`` entries), or None when
+    the producer of x wrote them. Returns an :class:`Fp8Tensor` whose meta is
+    ``meta_out`` (a fresh record if None): {history max, scale, scale_inv, 0}.
+    """
+    _require_gpu(x, state)
+    x = _bf16_2d(x)
+    rows, cols = x.shape
+    dev = x.device
+    if meta_out is None:
+        meta_out = new_meta(dev)
+    out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=dev) if rowwise else None
+    out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=dev) if transpose else None
+    n_prev = 0 if prev_partials is None else prev_partials.numel()
+    _lib.check(_lib.lib().bf8_cast_delayed_bf16(
+        _ptr(x), rows, cols, _ptr(state), int(length), int(pos), _ptr(prev_partials), n_prev,
+        fmt, _ptr(meta_out), _ptr(out), _ptr(out_t), _ptr(partials_out), _stream(dev)),
+        "bf8_cast_delayed_bf16")
+    return Fp8Tensor(out, out_t, meta_out, fmt, rows, cols)

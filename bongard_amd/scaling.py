@@ -1,0 +1,132 @@
+"""Delayed (amax-history) scaling for the FP8 path.
+
+Semantics are TransformerEngine's ``DelayedScaling`` with margin 0 and
+``amax_compute_algo='max'`` (the reference reaches TE only through Float8CurrentScaling,
+bongard/te_linear.py:38-39; delayed scaling is the extension BASELINE config 5 asks for):
+a tensor role quantized at step t uses ``scale_t = fp8_max / max(history)``, where the
+history holds the amaxes of the previous ``length`` quantizations of that role; while
+the history is all zero (or holds a non-finite value) the previous scale is kept, and
+the first scale is 1.
+
+On the GPU a delayed quantization is one kernel (``bf8_cast_delayed_bf16``): it folds the
+previous step's amax partials into the history, derives the scale, casts, and writes
+this step's amax partials, which the next quantization of the role folds in. No amax
+pre-pass and no host synchronisation are needed.
+"""
+
+import torch
+
+from . import ops
+from .ops import E4M3, E5M2
+
+DEFAULT_HISTORY = 16
+
+
+class DelayedScaler:
+    """Delayed scaling state of one tensor role (e.g. a linear's input)."""
+
+    def __init__(self, fmt, history=DEFAULT_HISTORY):
+        if fmt not in (E4M3, E5M2):
+            raise ValueError(f"bad fp8 format {fmt}")
+        if not 1 <= int(history) <= 1024:
+            raise ValueError("amax history length must be in [1, 1024]")
+        self.fmt = fmt
+        self.length = int(history)
+        self.state = None     # device float32 [length + 4]: history, meta
+        self.recorded = 0     # amaxes pushed into the history so far
+        self._bufs = [None, None]
+        self._slot = 0        # buffer for this step's partials; the other one is pending
+        self._pending = 0     # partial count of the previous step (0: none)
+
+    def _ensure(self, device):
+        if self.state is None:
+            self.state = ops.new_delayed_state(self.length, device)
+        elif self.state.device != device:
+            self.state = self.state.to(device)
+            self._bufs = [None, None]
+            self._pending = 0
+
+    def _buffer(self, slot, count, device):
+        buf = self._bufs[slot]
+        if buf is None or buf.numel() < count or buf.device != device:
+            buf = torch.empty(max(int(count), 1024), dtype=torch.int32, device=device)
+            self._bufs[slot] = buf
+        return buf[:count]
+
+    def partials_for_producer(self, count, device):
+        """Buffer the producer of the role's next tensor fills with its amax partials (the
+        gated-GELU GEMM for H, its backward for dGU); pass ``count`` to :meth:`quantize`."""
+        self._ensure(device)
+        return self._buffer(self._slot, count, device)
+
+    def quantize(self, x, *, rowwise=True, transpose=False, producer_count=None):
+        """Quantize ``x`` (bf16, flattened to 2-D) with this role's delayed scale."""
+        dev = x.device
+        self._ensure(dev)
+        rows = x.numel() // x.shape[-1] if x.dim() else 1
+        cols = x.shape[-1]
+        if producer_count is None:
+            count = ops.cast_amax_partials_count(rows, cols, transpose)
+            out_parts = self._buffer(self._slot, count, dev)
+        else:
+            count, out_parts = int(producer_count), None
+        prev = self._bufs[self._slot ^ 1][:self._pending] if self._pending else None
+        q = ops.cast_delayed(x, self.state, self.length, self.recorded % self.length, prev,
+                             self.fmt, rowwise=rowwise, transpose=transpose,
+                             partials_out=out_parts)
+        if prev is not None:
+            self.recorded += 1
+        self._pending = count
+        self._slot ^= 1
+        return q
+
+    # -- persistence (``_extra_state``) -------------------------------------------------
+    def to_tensor(self):
+        """float32 [3 + length + 4] on the CPU: length, amaxes recorded, format, state."""
+        head = torch.tensor([self.length, self.recorded, self.fmt], dtype=torch.float32)
+        if self.state is None:
+            body = _fresh_state_cpu(self.length)
+        else:
+            body = self.state.detach().float().cpu()
+        return torch.cat([head, body])
+
+    def load_tensor(self, t):
+        t = t.detach().float().cpu()
+        length, recorded, fmt = int(t[0]), int(t[1]), int(t[2])
+        if length != self.length or fmt != self.fmt or t.numel() != 3 + length + 4:
+            raise ValueError("delayed-scaling state does not match this role")
+        device = self.state.device if self.state is not None else None
+        state = t[3:].clone()
+        self.state = state.to(device) if device is not None else state
+        self.recorded = recorded
+        self._pending = 0
+
+
+def _fresh_state_cpu(length):
+    st = torch.zeros(length + 4, dtype=torch.float32)
+    st[length + 1] = 1.0
+    st[length + 2] = 1.0
+    return st
+
+
+class LinearScaling:
+    """Delayed scalers of one FP8 linear, as TE keeps per module: its input and weight
+    (e4m3, forward) and the gradient of its output (e5m2, backward)."""
+
+    ROLES = ('input', 'weight', 'grad_output')
+
+    def __init__(self, history=DEFAULT_HISTORY):
+        self.history = int(history)
+        self.input = DelayedScaler(E4M3, history)
+        self.weight = DelayedScaler(E4M3, history)
+        self.grad_output = DelayedScaler(E5M2, history)
+
+    def to_tensor(self):
+        return torch.cat([getattr(self, r).to_tensor() for r in self.ROLES])
+
+    def load_tensor(self, t):
+        n = 3 + self.history + 4
+        if t.numel() != len(self.ROLES) * n:
+            raise ValueError("delayed-scaling state has the wrong size")
+        for i, r in enumerate(self.ROLES):
+            getattr(self, r).load_tensor(t[i * n:(i + 1) * n])

@@ -163,6 +163,22 @@ int bf8_delayed_scale_begin(float* state, int len, int fmt, void* stream);
 int bf8_delayed_scale_end(float* state, int len, const uint32_t* partials,
                           int64_t n_partials, void* stream);
 
+/* Delayed-scaling cast in one pass (the begin / cast / amax / end sequence above fused):
+ * the kernel first pushes the previous step's amax (max of prev_partials, n_prev of them,
+ * n_prev = 0 on the first step) into slot pos (0 <= pos < len) of the history, derives
+ * this step's scale from the history, publishes {amax, scale, scale_inv, next slot} at
+ * state + len and {history max, scale, scale_inv, 0} at meta_out (nullable; a copy the
+ * next step does not overwrite, for a backward pass that runs after it), casts x like
+ * bf8_cast_bf16, and writes this step's amax partials of |x|
+ * into partials_out [bf8_cast_amax_partials(rows, cols, out_t != NULL)] (NULL when the
+ * producer of x supplies them, as the gated-GELU GEMM does for H). Keep partials_out
+ * until the next step's call, which reads it as prev_partials. */
+int64_t bf8_cast_amax_partials(int64_t rows, int64_t cols, int transpose);
+int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* state, int len,
+                          int pos, const uint32_t* prev_partials, int64_t n_prev, int fmt,
+                          float* meta_out, uint8_t* out, uint8_t* out_t, uint32_t* partials_out,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -225,33 +225,45 @@ def geglu_bwd(g_bf16, u_bf16, dh_bf16):
     return g.grad, u.grad
 
 
-def mlp_forward(x_bf16, w_gate, w_up, w_down, *, shared_gate_up_scale=True, precise=True):
+def _current(role, x, fmt):
+    """Current scaling for every tensor role: (q bytes, scale)."""
+    q, _, s, _ = quantize(x, fmt)
+    return q, s
+
+
+def mlp_forward(x_bf16, w_gate, w_up, w_down, *, shared_gate_up_scale=True, precise=True,
+                quant=None):
     """FP8 gated MLP as the reference's TEMLP computes it (bf16 tensors in, fp32 Y out).
 
-    Returns a dict with every intermediate (quantized bytes, scales, G, U, H, H8, Y).
+    ``quant(role, x, fmt) -> (q, scale)`` quantizes each tensor role ('x', 'w_gu', 'h',
+    'w_down'); the default is current scaling (bongard/te_linear.py:38-39, 98-103), a
+    DelayedQuantizer gives delayed scaling. Returns a dict with every intermediate
+    (quantized bytes, scales, G, U, H, H8, Y).
     """
-    xq, xa, xs, xsi = quantize(x_bf16, E4M3)
+    quant = quant or _current
+    xq, xs = quant("x", x_bf16, E4M3)
+    I = w_gate.shape[0]
     if shared_gate_up_scale:
         wgu = torch.cat([w_gate, w_up], 0)
-        wq, wa, ws, wsi = quantize(wgu, E4M3)
-        I = w_gate.shape[0]
+        wq, ws = quant("w_gu", wgu, E4M3)
         gate = scaled_mm(xq, xs, E4M3, wq[:I], ws, E4M3, precise=precise)
         up = scaled_mm(xq, xs, E4M3, wq[I:], ws, E4M3, precise=precise)
         w_scales = (ws, ws)
     else:
-        gq, _, gs, _ = quantize(w_gate, E4M3)
-        uq, _, us, _ = quantize(w_up, E4M3)
+        gq, gs = quant("w_gate", w_gate, E4M3)
+        uq, us = quant("w_up", w_up, E4M3)
         gate = scaled_mm(xq, xs, E4M3, gq, gs, E4M3, precise=precise)
         up = scaled_mm(xq, xs, E4M3, uq, us, E4M3, precise=precise)
         w_scales = (gs, us)
+        wq = torch.cat([gq, uq], 0)
     g = gate.to(torch.bfloat16)
     u = up.to(torch.bfloat16)
     h = geglu(g, u)
-    hq, ha, hs, hsi = quantize(h, E4M3)
-    dq, da, ds, dsi = quantize(w_down, E4M3)
+    hq, hs = quant("h", h, E4M3)
+    dq, ds = quant("w_down", w_down, E4M3)
     y = scaled_mm(hq, hs, E4M3, dq, ds, E4M3, precise=precise)
-    return dict(xq=xq, x_scale=xs, w_scales=w_scales, g=g, u=u, h=h, hq=hq, h_scale=hs,
-                wd_scale=ds, y=y)
+    return dict(xq=xq, x_scale=xs, w_scales=w_scales, wgu_q=wq, g=g, u=u, h=h, hq=hq,
+                h_scale=hs, wd_q=dq, wd_scale=ds, y=y)
 
 
 def linear_fwd_bwd(x, w, dy, *, precise=True):
@@ -270,24 +282,24 @@ def linear_fwd_bwd(x, w, dy, *, precise=True):
     return y, dx, dw
 
 
-def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True):
+def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True, quant=None):
     """Backward of ``mlp_forward`` (shared gate/up scale) through the FP8 GEMMs.
 
     dH = dY8 Wd8 (bf16), dWd = dY8^T H8, (dG, dU) = autograd of the bf16 gelu chain,
-    dGU quantized to e5m2 with one scale, dX = dGU8 Wgu8, dWgu = dGU8^T X8.
+    dGU quantized to e5m2 with one scale, dX = dGU8 Wgu8, dWgu = dGU8^T X8. The weights'
+    FP8 copies are the forward's; ``quant`` quantizes the roles 'dy' and 'dgu'.
     Returns fp32 (dx, dw_gate_up [2I, K], dw_down) and the bf16 dGU.
     """
-    I = w_gate.shape[0]
-    dq, _, ds, _ = quantize(dy_bf16, E5M2)
-    wdq, _, wds, _ = quantize(w_down, E4M3)
+    quant = quant or _current
+    dq, ds = quant("dy", dy_bf16, E5M2)
+    wdq, wds = fwd["wd_q"], fwd["wd_scale"]
     dh = scaled_mm(dq, ds, E5M2, wdq.t().contiguous(), wds, E4M3, precise=precise)
     dwd = scaled_mm(dq.t().contiguous(), ds, E5M2, fwd["hq"].t().contiguous(), fwd["h_scale"],
                     E4M3, precise=precise)
     dg, du = geglu_bwd(fwd["g"], fwd["u"], dh.to(torch.bfloat16))
     dgu = torch.cat([dg, du], 1)
-    gq, _, gs, _ = quantize(dgu, E5M2)
-    wgu = torch.cat([w_gate, w_up], 0)
-    wq, _, wsc, _ = quantize(wgu, E4M3)
+    gq, gs = quant("dgu", dgu, E5M2)
+    wq, wsc = fwd["wgu_q"], fwd["w_scales"][0]
     dx = scaled_mm(gq, gs, E5M2, wq.t().contiguous(), wsc, E4M3, precise=precise)
     dwgu = scaled_mm(gq.t().contiguous(), gs, E5M2, fwd["xq"].t().contiguous(), fwd["x_scale"],
                      E4M3, precise=precise)
@@ -331,6 +343,24 @@ class DelayedScaling:
     def end(self, amax_value):
         self.history[self.pos] = np.float32(amax_value)
         self.pos = (self.pos + 1) % self.length
+
+
+class DelayedQuantizer:
+    """``quant(role, x, fmt)`` for mlp_forward / mlp_backward with delayed scaling: one
+    DelayedScaling per tensor role; each call quantizes with the role's scale, then
+    pushes the tensor's amax into the role's history."""
+
+    def __init__(self, length: int):
+        self.length = length
+        self.roles = {}
+
+    def __call__(self, role, x, fmt):
+        ds = self.roles.setdefault(role, DelayedScaling(self.length, fmt))
+        scale, _ = ds.begin()
+        s = torch.tensor(scale, dtype=torch.float32)
+        q = cast(x, s, fmt)
+        ds.end(float(amax(x)))
+        return q, s
 
 
 # ---------------------------------------------------------------------------------------

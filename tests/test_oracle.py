@@ -221,3 +221,19 @@ def test_delayed_scaling_closed_form():
     d.end(float("inf"))
     s2, _ = d.begin()
     assert s2 == s                          # non-finite history keeps the previous scale
+
+
+def test_delayed_quantizer_uses_previous_amaxes():
+    """Each role's scale at step t comes from the amaxes of its steps < t only."""
+    g = torch.Generator().manual_seed(12)
+    xs = [(torch.randn(8, 16, generator=g) * s).to(torch.bfloat16) for s in (3.0, 0.5, 0.1)]
+    q = orc.DelayedQuantizer(16)
+    _, s1 = q("x", xs[0], E4M3)
+    assert float(s1) == 1.0
+    _, s2 = q("x", xs[1], E4M3)
+    assert float(s2) == float(np.float32(448.0 / float(orc.amax(xs[0]))))
+    _, s3 = q("x", xs[2], E4M3)
+    m = max(float(orc.amax(xs[0])), float(orc.amax(xs[1])))
+    assert float(s3) == float(np.float32(448.0 / m))
+    _, sw = q("w", xs[2], E5M2)                # roles keep separate histories
+    assert float(sw) == 1.0
