@@ -1,21 +1,31 @@
 """Benchmark of the MI355X FP8 linear path (one JSON line on stdout).
 
-Workload ("c2"): the fused gated-GELU MLP at Gemma-3-4B width,
-X bf16 [4096, 2560], W_gate/W_up [10240, 2560], W_down [2560, 10240]. One step is the
-whole FP8 forward with inputs resident in HBM:
+Headline workload ("c2"): the fused gated-GELU MLP at
+Gemma-3-4B width, X bf16 [4096, 2560], W_gate/W_up [10240, 2560], W_down [2560, 10240].
+One step is the whole FP8 forward with inputs resident in HBM:
   quantize X, [W_gate; W_up], W_down (amax -> scale -> e4m3 cast, per tensor)
   gate/up GEMM with the gated-GELU epilogue (+ per-tile amax of H)
-  H scale, H e4m3 cast, down GEMM -> Y bf16 [4096, 2560]
+  H e4m3 cast, down GEMM -> Y bf16 [4096, 2560]
 ``value`` = 2*M*(2I*K + K*I) FLOP per step / step time (TFLOP/s). Weight quantization is
 inside the step (the first-microbatch case); the cached-weight rate is reported beside it.
 
 ``roofline`` covers the dominant kernel (gate/up GEMM + gated-GELU epilogue): algorithmic
 FLOP per launch / its average launch time from HIP events on the launch stream, against
 the dense FP8 MFMA peak. ``traffic`` comes from rocprofv3 FETCH_SIZE/WRITE_SIZE runs
-summarised in profiles/ (null when no such summary exists).
+summarised in profiles/ (null when no such summary exists). ``quantize_roofline`` does
+the same for the H cast against HBM bandwidth.
+
+``configs`` reports the other BASELINE configurations, each timed the same way:
+  c1  one FP8 linear, X [512, 2560] (8 outlier columns) . W [2048, 2560]^T, both quantized
+  c3  an encoder layer's linears on a packed varlen batch (M = sum of 8 lengths ~ 16k):
+      fused QKV (3 per-segment scales), O, and the c2 MLP; cached weights
+  c4  decoder-branch skinny GEMMs (M = 512) on pre-quantized weights; reports HBM GB/s
+      (weights + activations + outputs) against peak as well as TFLOP/s
+  c5  FP8 training step of the c2 MLP at M = 8192 (forward + backward, grad_out e5m2),
+      delayed scaling with an amax history of 16 on every tensor role
 
 ``cpu_baseline`` times the CPU oracle (torch CPU: amax, clamp, .to(float8), fp32 matmul,
-bf16 gelu chain -- torchao's emulate path) on the same step, on this host's cores.
+bf16 gelu chain -- torchao's emulate path) on the same c2 step, on this host's cores.
 """
 
 import argparse
@@ -41,6 +51,7 @@ def _args():
     p.add_argument("--rows", type=int, default=4096)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-reps", type=int, default=1)
+    p.add_argument("--only-c2", action="store_true", help="skip the other configurations")
     return p.parse_args()
 
 
@@ -52,6 +63,32 @@ def _load_traffic():
         return json.loads(f.read_text())
     except (OSError, ValueError):
         return None
+
+
+def _timed(torch, fn, steps, warmup):
+    """Wall time per call of ``fn`` between two device synchronisations."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def _ev_time(torch, fn, n):
+    """Average time per call from HIP events recorded on the launch stream."""
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        fn()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(n):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / 1e3 / n
 
 
 def main():
@@ -83,65 +120,37 @@ def main():
             gq, dq = cached
         H, _, hparts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
         hq = ops.cast_partials(H, hparts, ops.E4M3)
-        hm = hq.meta
-        return ops.gemm(hq.data, ops.E4M3, hm, dq.data, ops.E4M3, dq.meta)
+        return ops.gemm(hq.data, ops.E4M3, hq.meta, dq.data, ops.E4M3, dq.meta)
 
-    def timed(fn, steps, warmup):
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            fn()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / steps
-
-    sec = timed(step, args.steps, args.warmup)
+    sec = _timed(torch, step, args.steps, args.warmup)
     cached = (ops.quantize(w_gu, ops.E4M3), ops.quantize(w_d, ops.E4M3))
-    sec_cached = timed(lambda: step(cached), args.steps, args.warmup)
+    sec_cached = _timed(torch, lambda: step(cached), args.steps, args.warmup)
 
     # ---- dominant kernel: gate/up GEMM + gated-GELU epilogue, HIP events on its stream
     xq = ops.quantize(x, ops.E4M3)
     gq = cached[0]
-    stream = torch.cuda.current_stream()
     n_launch = max(10, args.steps)
-    for _ in range(3):
-        ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(n_launch):
-        ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    geglu_s = ev0.elapsed_time(ev1) / 1e3 / n_launch
+    geglu_s = _ev_time(torch, lambda: ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I),
+                       n_launch)
     geglu_flop = 2.0 * M * (2 * I) * K
     achieved = geglu_flop / geglu_s / 1e12
 
-    # ---- down GEMM and the activation quantize (HBM-bound), same method
+    # ---- down GEMM and the quantize kernels (HBM-bound), same method
     H, _, hparts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
     hq = ops.cast_partials(H, hparts, ops.E4M3)
     hm = hq.meta
     dq = cached[1]
-
-    def ev_time(fn, n=n_launch):
-        for _ in range(3):
-            fn()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(n):
-            fn()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / 1e3 / n
-
-    down_s = ev_time(lambda: ops.gemm(hq.data, 0, hm, dq.data, 0, dq.meta))
-    qx_s = ev_time(lambda: ops.quantize(x, ops.E4M3))
-    qh_s = ev_time(lambda: ops.cast(H, hm, ops.E4M3))
-    qw_s = ev_time(lambda: ops.quantize(w_gu, ops.E4M3))
+    down_s = _ev_time(torch, lambda: ops.gemm(hq.data, 0, hm, dq.data, 0, dq.meta), n_launch)
+    qx_s = _ev_time(torch, lambda: ops.quantize(x, ops.E4M3), n_launch)
+    qh_s = _ev_time(torch, lambda: ops.cast(H, hm, ops.E4M3), n_launch)
+    qw_s = _ev_time(torch, lambda: ops.quantize(w_gu, ops.E4M3), n_launch)
+    amax_w_s = _ev_time(torch, lambda: ops.amax(w_gu), n_launch)
+    qht_s = _ev_time(torch, lambda: ops.cast(H, hm, ops.E4M3, rowwise=True, transpose=True),
+                     n_launch)
 
     traffic = _load_traffic()
     roofline = {
-        "kernel": "gemm_kernel<e4m3,e4m3,GEGLU,bf16> (gate/up GEMM + gated-GELU epilogue)",
+        "kernel": "gemm_kernel<256x256 tile, e4m3 x e4m3, gated-GELU epilogue> (gate/up GEMM)",
         "bound": "mfma",
         "achieved": round(achieved, 1),
         "peak": FP8_PEAK_TFLOPS,
@@ -151,6 +160,22 @@ def main():
         "flop_per_launch": geglu_flop,
         "avg_launch_us": round(geglu_s * 1e6, 2),
     }
+    cast_h_gbps = 3.0 * M * I / qh_s / 1e9
+    quant_roofline = {
+        "kernel": "cast_kernel<e4m3> (H [4096, 10240] bf16 -> e4m3, given scale)",
+        "bound": "hbm", "achieved": round(cast_h_gbps, 1), "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s", "frac": round(cast_h_gbps / HBM_PEAK_GBPS, 4),
+        "bytes_per_launch": 3 * M * I, "avg_launch_us": round(qh_s * 1e6, 2),
+    }
+
+    configs = None
+    if not args.only_c2:
+        configs = {
+            "c1": _bench_c1(torch, ops, workloads, dev),
+            "c3": _bench_c3(torch, ops, workloads, dev),
+            "c4": _bench_c4(torch, ops, workloads, dev),
+            "c5": _bench_c5(torch, workloads, dev),
+        }
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -180,15 +205,163 @@ def main():
             "gemm_down_tflops": round(2.0 * M * K * I / down_s / 1e12, 1),
             "quantize_x_us": round(qx_s * 1e6, 2),
             "quantize_x_gbps": round(3.0 * M * K / qx_s / 1e9, 1),
+            "amax_wgu_us": round(amax_w_s * 1e6, 2),
+            "amax_wgu_gbps": round(2.0 * 2 * I * K / amax_w_s / 1e9, 1),
             "cast_h_us": round(qh_s * 1e6, 2),
-            "cast_h_gbps": round(3.0 * M * I / qh_s / 1e9, 1),
+            "cast_h_gbps": round(cast_h_gbps, 1),
+            "cast_transpose_h_us": round(qht_s * 1e6, 2),
+            "cast_transpose_h_gbps": round(4.0 * M * I / qht_s / 1e9, 1),
             "quantize_wgu_us": round(qw_s * 1e6, 2),
             "quantize_wgu_gbps": round(3.0 * 2 * I * K / qw_s / 1e9, 1),
         },
         "roofline": roofline,
+        "quantize_roofline": quant_roofline,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def _bench_c1(torch, ops, workloads, dev, steps=50):
+    """c1: Y = X W^T with both operands quantized each call (TELinear, first microbatch)."""
+    c = workloads.config1()
+    x, w = c["x"].to(dev), c["w"].to(dev)
+    M, K = x.shape
+    N = w.shape[0]
+
+    def step():
+        xq = ops.quantize(x, ops.E4M3)
+        wq = ops.quantize(w, ops.E4M3)
+        return ops.gemm(xq.data, 0, xq.meta, wq.data, 0, wq.meta)
+
+    s = _timed(torch, step, steps, 5)
+    xq, wq = ops.quantize(x, ops.E4M3), ops.quantize(w, ops.E4M3)
+    g = _ev_time(torch, lambda: ops.gemm(xq.data, 0, xq.meta, wq.data, 0, wq.meta), steps)
+    flop = 2.0 * M * N * K
+    return {"workload": f"linear [{M},{K}] x [{N},{K}]^T, both quantized per call",
+            "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
+            "gemm_us": round(g * 1e6, 2), "gemm_tflops": round(flop / g / 1e12, 1)}
+
+
+def _qkv_weight(torch, ops, c, dev):
+    """[W_q; W_k; W_v] in one fp8 buffer with one meta per segment (fused QKV)."""
+    parts = [c["w_q"], c["w_k"], c["w_v"]]
+    K = parts[0].shape[1]
+    n = sum(p.shape[0] for p in parts)
+    w8 = torch.empty(n, K, dtype=torch.float8_e4m3fn, device=dev)
+    metas = ops.new_meta(dev, 3)
+    start, ends = 0, []
+    for i, p in enumerate(parts):
+        ops.quantize(p.to(dev), ops.E4M3, meta=metas[i], out=w8[start:start + p.shape[0]])
+        start += p.shape[0]
+        ends.append(start)
+    return w8, metas, ends
+
+
+def _bench_c3(torch, ops, workloads, dev, steps=20):
+    """c3: packed varlen encoder layer: fused QKV, O, MLP (cached weights)."""
+    c = workloads.config3()
+    x = c["x"].to(dev)
+    M, K = x.shape
+    I = c["w_gate"].shape[0]
+    g = torch.Generator().manual_seed(33)
+    attn = torch.randn(M, c["w_o"].shape[1], generator=g).to(torch.bfloat16).to(dev)
+    w8, metas, ends = _qkv_weight(torch, ops, c, dev)
+    oq = ops.quantize(c["w_o"].to(dev), ops.E4M3)
+    gq = ops.quantize(torch.cat([c["w_gate"], c["w_up"]]).to(dev), ops.E4M3)
+    dq = ops.quantize(c["w_down"].to(dev), ops.E4M3)
+
+    def step():
+        xq = ops.quantize(x, ops.E4M3)
+        qkv = ops.gemm(xq.data, 0, xq.meta, w8, 0, metas[0], seg_ends=ends, b_meta_stride=4)
+        aq = ops.quantize(attn, ops.E4M3)
+        o = ops.gemm(aq.data, 0, aq.meta, oq.data, 0, oq.meta)
+        H, _, hp = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
+        hq = ops.cast_partials(H, hp, ops.E4M3)
+        y = ops.gemm(hq.data, 0, hq.meta, dq.data, 0, dq.meta)
+        return qkv, o, y
+
+    s = _timed(torch, step, steps, 3)
+    flop = 2.0 * M * (K * ends[-1] + oq.cols * K + 2 * I * K + I * K)
+    return {"workload": f"packed varlen encoder layer, M={M} (8 lengths {c['lengths'].tolist()}): "
+                        "fused QKV (3 scales) + O + gated MLP, cached weights",
+            "M": M, "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
+            "frac_of_fp8_peak": round(flop / s / 1e12 / FP8_PEAK_TFLOPS, 4)}
+
+
+def _bench_c4(torch, ops, workloads, dev, steps=50):
+    """c4: decoder-branch skinny GEMMs at M=512 on pre-quantized weights."""
+    c = workloads.config4()
+    x = c["x"].to(dev)
+    M, K = x.shape
+    I = c["w_gate"].shape[0]
+    g = torch.Generator().manual_seed(44)
+    attn = torch.randn(M, c["w_o"].shape[1], generator=g).to(torch.bfloat16).to(dev)
+    w8, metas, ends = _qkv_weight(torch, ops, c, dev)
+    oq = ops.quantize(c["w_o"].to(dev), ops.E4M3)
+    gq = ops.quantize(torch.cat([c["w_gate"], c["w_up"]]).to(dev), ops.E4M3)
+    dq = ops.quantize(c["w_down"].to(dev), ops.E4M3)
+    xq = ops.quantize(x, ops.E4M3)
+    aq = ops.quantize(attn, ops.E4M3)
+    H, _, hp = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
+    hq = ops.cast_partials(H, hp, ops.E4M3)
+    gemms = {
+        "qkv": (lambda: ops.gemm(xq.data, 0, xq.meta, w8, 0, metas[0], seg_ends=ends,
+                                 b_meta_stride=4), ends[-1], K, True),
+        "o": (lambda: ops.gemm(aq.data, 0, aq.meta, oq.data, 0, oq.meta), K, oq.cols, True),
+        "gate_up_geglu": (lambda: ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I),
+                          2 * I, K, False),
+        "down": (lambda: ops.gemm(hq.data, 0, hq.meta, dq.data, 0, dq.meta), K, I, True),
+    }
+    out, tot_s, tot_b, tot_f = {}, 0.0, 0.0, 0.0
+    for name, (fn, N, KK, full_out) in gemms.items():
+        t = _ev_time(torch, fn, steps)
+        out_cols = N if full_out else N // 2
+        nbytes = N * KK + M * KK + 2 * M * out_cols  # fp8 W + fp8 X + bf16 out
+        f = 2.0 * M * N * KK
+        out[name] = {"us": round(t * 1e6, 2), "gbps": round(nbytes / t / 1e9, 1),
+                     "tflops": round(f / t / 1e12, 1)}
+        tot_s += t
+        tot_b += nbytes
+        tot_f += f
+    gbps = tot_b / tot_s / 1e9
+    return {"workload": "decoder-branch GEMMs at M=512 (QKV, O, gate/up+GELU, down), "
+                        "pre-quantized e4m3 weights",
+            "gemms": out, "us_total": round(tot_s * 1e6, 2), "hbm_gbps": round(gbps, 1),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "tflops": round(tot_f / tot_s / 1e12, 1),
+            "mfma_frac": round(tot_f / tot_s / 1e12 / FP8_PEAK_TFLOPS, 4),
+            "note": "arithmetic intensity 600-1000 FLOP/B is above the 625 FLOP/B ridge for "
+                    "most of these GEMMs, so the MFMA roof binds before HBM"}
+
+
+def _bench_c5(torch, workloads, dev, steps=10):
+    """c5: FP8 training step of the c2 MLP at M=8192 with delayed scaling (history 16)."""
+    from bongard_amd import linear, scaling
+
+    c = workloads.config5()
+    x = c["x"].to(dev)
+    dy = c["dy"].to(dev)
+    M, K = x.shape
+    I = c["w_gate"].shape[0]
+    w_gu = torch.cat([c["w_gate"], c["w_up"]]).to(dev).requires_grad_(True)
+    w_d = c["w_down"].to(dev).requires_grad_(True)
+    sc = (scaling.LinearScaling(c["history"]), scaling.LinearScaling(c["history"]))
+    xg = x.requires_grad_(True)
+
+    def step():
+        w_gu.grad = None
+        w_d.grad = None
+        xg.grad = None
+        y = linear.Fp8GegluMlpFunction.apply(xg, w_gu, w_d, None, None, I, False, sc)
+        y.backward(dy)
+
+    s = _timed(torch, step, steps, 3)
+    flop = 3 * 2.0 * M * (2 * I * K + K * I)
+    return {"workload": f"c2 MLP training step (fwd + dgrad + wgrad) at M={M}, e4m3 fwd / "
+                        f"e5m2 grads, delayed scaling with amax history {c['history']}, "
+                        "weights re-quantized every step",
+            "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
+            "frac_of_fp8_peak": round(flop / s / 1e12 / FP8_PEAK_TFLOPS, 4)}
 
 
 def _cpu_baseline(c, reps=1):

@@ -275,7 +275,7 @@ __device__ inline float delayed_scale_block(float* __restrict__ state, int len, 
       const float scale_inv = (float)(1.0 / (double)scale);
       meta[1] = scale;
       meta[2] = scale_inv;
-      meta[3] = (float)((pos + (have_new ? 1 : 0)) % len);
+      if (have_new) meta[3] = (float)((pos + 1) % len);
       if (meta_out) {
         meta_out[0] = w;
         meta_out[1] = scale;

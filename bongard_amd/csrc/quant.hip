@@ -50,6 +50,9 @@ namespace {
 constexpr int kNT = 256;            // threads per block for streaming kernels
 constexpr int kVecPerThread = 8;    // 16-byte loads in flight per lane (amax)
 constexpr int64_t kMaxAmaxBlocks = 1024;  // 4 blocks per CU; consumers read <= 4 KB of partials
+// Consumers reduce up to this many partials in every block; a longer list (the gated-GELU
+// GEMM writes one per tile: 5200 at M = 16.6k) is first reduced by a one-block kernel.
+constexpr int64_t kMaxInlinePartials = 2048;
 
 int64_t amax_blocks(int64_t n) {
   int64_t per_block = (int64_t)kNT * kVecPerThread * 8;  // bf16 elements per block pass
@@ -291,7 +294,23 @@ __global__ __launch_bounds__(kNT) void delayed_end_kernel(float* state, int len,
   }
 }
 
-int launch_cast(const void* x, int64_t rows, int64_t cols, const ScaleSrc& src, int fmt,
+// Delayed scaling with a long list of previous partials: pushes their max into slot pos
+// (and meta {amax, ., ., next slot}), so the cast itself then has none to fold.
+__global__ __launch_bounds__(kNT) void fold_amax_kernel(float* state, int len, int pos,
+                                                        const uint32_t* __restrict__ prev,
+                                                        int64_t n_prev) {
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < n_prev; i += kNT) m = max(m, prev[i]);
+  m = block_max_u32<kNT>(m);
+  if (threadIdx.x == 0) {
+    const float amax = __uint_as_float(m);
+    state[pos] = amax;
+    state[len] = amax;
+    state[len + 3] = (float)((pos + 1) % len);
+  }
+}
+
+int launch_cast(const void* x, int64_t rows, int64_t cols, ScaleSrc src, int fmt,
                 uint8_t* out, uint8_t* out_t, uint32_t* amax_out, void* stream, const char* who) {
   BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "%s: bad fmt %d", who, fmt);
   BF8_CHECK(rows >= 0 && cols >= 0, "%s: negative shape", who);
@@ -302,6 +321,25 @@ int launch_cast(const void* x, int64_t rows, int64_t cols, const ScaleSrc& src, 
   if (n == 0) return BF8_OK;
   hipStream_t s = as_stream(stream);
   const uint16_t* xs = (const uint16_t*)x;
+  if (!src.scale && !src.state && src.np > kMaxInlinePartials) {
+    // current scaling from many partials: meta first, then a cast with its scale
+    float* meta = src.meta_out;
+    hipLaunchKernelGGL(scale_from_partials_kernel, dim3(1), dim3(kNT), 0, s, src.partials,
+                       src.np, fp8_max_host(fmt), meta);
+    const int rc = launch_status("scale_from_partials_kernel");
+    if (rc != BF8_OK) return rc;
+    src = ScaleSrc{};
+    src.scale = meta + 1;
+  }
+  if (src.state && src.n_prev > kMaxInlinePartials) {
+    // delayed scaling after a producer with many partials: fold them in first
+    hipLaunchKernelGGL(fold_amax_kernel, dim3(1), dim3(kNT), 0, s, src.state, src.len, src.pos,
+                       src.prev, src.n_prev);
+    const int rc = launch_status("fold_amax_kernel");
+    if (rc != BF8_OK) return rc;
+    src.prev = nullptr;
+    src.n_prev = 0;
+  }
   if (out_t == nullptr) {
     const int grid = (int)row_cast_blocks(n);
     if (fmt == BF8_E4M3)
@@ -382,8 +420,7 @@ int bf8_cast_bf16(const void* x, int64_t rows, int64_t cols, const float* scale,
 int bf8_cast_partials_bf16(const void* x, int64_t rows, int64_t cols, const uint32_t* partials,
                            int64_t n_partials, int fmt, float* meta, uint8_t* out,
                            uint8_t* out_t, void* stream) {
-  BF8_CHECK(partials && meta && n_partials >= 1 && n_partials <= 4096,
-            "bf8_cast_partials_bf16: bad partials or meta (1..4096 partials)");
+  BF8_CHECK(partials && meta && n_partials >= 1, "bf8_cast_partials_bf16: bad partials or meta");
   return launch_cast(x, rows, cols, current_scale(partials, n_partials, meta), fmt, out, out_t,
                      nullptr, stream, "bf8_cast_partials_bf16");
 }
@@ -399,8 +436,8 @@ int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* stat
                           void* stream) {
   BF8_CHECK(state && len >= 1 && len <= 1024, "bf8_cast_delayed_bf16: bad state/len");
   BF8_CHECK(pos >= 0 && pos < len, "bf8_cast_delayed_bf16: pos %d outside [0, %d)", pos, len);
-  BF8_CHECK(n_prev >= 0 && n_prev <= 4096 && (n_prev == 0 || prev_partials),
-            "bf8_cast_delayed_bf16: bad previous partials (0..4096)");
+  BF8_CHECK(n_prev >= 0 && (n_prev == 0 || prev_partials),
+            "bf8_cast_delayed_bf16: bad previous partials");
   ScaleSrc src{};
   src.state = state;
   src.len = len;

@@ -3,7 +3,7 @@
 Drop-in for bongard/fused_mlp.py (TransformerEngine te.LayerNormMLP path): same
 ``RECIPES``, ``FusedMLP(mlp, norm, recipe)`` with parameters ``layer_norm_weight``
 [hidden], ``fc1_weight`` [2I, hidden] (= [gate; up]), ``fc2_weight`` [hidden, I] and an
-empty ``_extra_state``; HF eval views (``_hf_mlp``, ``_hf_norm``) sharing storage and
+``_extra_state`` (empty for 'fp8'; the amax histories for 'fp8_delayed'); HF eval views (``_hf_mlp``, ``_hf_norm``) sharing storage and
 refreshed by ``_apply``; counters ``weight_quantizations`` / ``cached_weights`` /
 ``real_tokens`` / ``kernel_tokens``; ``enable_fused_mlp(model, recipe) -> int``; and
 ``hf_state_dict(backbone)`` for export.
@@ -21,7 +21,7 @@ from collections import Counter
 import torch
 
 from . import linear as _linear
-from .te_linear import RECIPES, _StatelessExtraState, _make_recipe, _pad_rows, present
+from .te_linear import RECIPES, _ScalingExtraState, _make_recipe, _new_scaling, _pad_rows, present
 
 __all__ = ["RECIPES", "FusedMLP", "enable_fused_mlp", "hf_state_dict"]
 
@@ -32,7 +32,7 @@ def _rms_norm(x, weight, eps):
     return (y * (1.0 + weight.float())).type_as(x)
 
 
-class FusedMLP(_StatelessExtraState, torch.nn.Module):
+class FusedMLP(_ScalingExtraState, torch.nn.Module):
     """RMSNorm -> fc1 = [gate; up] -> gelu_tanh(gate) * up -> fc2, in FP8 while training."""
 
     def __init__(self, mlp, norm, recipe):
@@ -66,6 +66,12 @@ class FusedMLP(_StatelessExtraState, torch.nn.Module):
         self.counts = Counter()
         self._cached_weight_versions = None
         self._fp8_weights = None
+        # delayed scaling: (fc1 roles: norm output, fc1 weight, dGU), (fc2: H, fc2, dY)
+        fc1, fc2 = _new_scaling(self.recipe), _new_scaling(self.recipe)
+        self.scaling = (fc1, fc2) if fc1 is not None else None
+
+    def _delayed_scalings(self):
+        return list(self.scaling) if self.scaling is not None else []
 
     def _refresh_hf_views(self):
         inter = self.intermediate_size
@@ -97,15 +103,18 @@ class FusedMLP(_StatelessExtraState, torch.nn.Module):
         flat, length, aligned = _pad_rows(flat)
         self.counts['real_tokens'] += length
         self.counts['kernel_tokens'] += aligned
+        fc1, fc2 = self.scaling if self.scaling is not None else (None, None)
         if first:
             self._fp8_weights = (
                 _linear.quantize_gate_up(self.fc1_weight, self.intermediate_size,
-                                         split_scales=False),
-                _linear.quantize_weight(self.fc2_weight, transpose=True))
+                                         split_scales=False, scaler=fc1 and fc1.weight),
+                _linear.quantize_weight(self.fc2_weight, transpose=True,
+                                        scaler=fc2 and fc2.weight))
         gu_q, down_q = self._fp8_weights
         normed = _rms_norm(flat.to(torch.bfloat16), self.layer_norm_weight, self.eps)
         out = _linear.Fp8GegluMlpFunction.apply(normed, self.fc1_weight, self.fc2_weight, gu_q,
-                                                down_q, self.intermediate_size, False)
+                                                down_q, self.intermediate_size, False,
+                                                self.scaling)
         return out[:length].reshape_as(x)
 
 

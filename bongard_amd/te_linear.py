@@ -14,6 +14,10 @@ The 'fp8' recipe is per-tensor current scaling with HYBRID formats (e4m3 forward
 gradients), on the gfx950 kernels. In training, TEMLP runs the gate/up GEMM with the
 gated-GELU fused into its epilogue and feeds H's FP8 copy to the down projection
 (bongard_amd.linear.Fp8GegluMlpFunction) instead of three separate passes.
+'fp8_delayed' (an addition to the reference's names) is TE's DelayedScaling with an amax
+history of 16 and HYBRID formats: each projection keeps the histories of its input,
+weight and output gradient in ``_extra_state``, which is then non-empty, so export raises
+as the reference does for stateful scaling.
 'mxfp8' and 'nvfp4' are accepted by name but raise NotImplementedError when a module is
 built: their block-scaled kernels do not exist yet.
 """
@@ -26,8 +30,9 @@ import torch
 from torch.nn import functional as F
 
 from . import linear as _linear
+from .scaling import LinearScaling
 
-RECIPES = ('nvfp4', 'mxfp8', 'fp8')
+RECIPES = ('nvfp4', 'mxfp8', 'fp8', 'fp8_delayed')
 ATTENTION_PROJECTIONS = ('q_proj', 'k_proj', 'v_proj', 'o_proj')
 
 
@@ -38,11 +43,30 @@ class Float8CurrentScaling:
     fp8_format: str = "HYBRID"
 
 
+@dataclass(frozen=True)
+class DelayedScaling:
+    """Per-tensor delayed scaling from an amax history (TE DelayedScaling defaults)."""
+
+    fp8_format: str = "HYBRID"
+    amax_history_len: int = 16
+    margin: int = 0
+    amax_compute_algo: str = "max"
+
+
 def _make_recipe(name):
     if name == 'fp8':
         return Float8CurrentScaling()
+    if name == 'fp8_delayed':
+        return DelayedScaling()
     raise NotImplementedError(
         f"TE recipe {name!r} (block scaling) has no gfx950 kernels yet; use 'fp8'")
+
+
+def _new_scaling(recipe):
+    """The delayed-scaling state a module needs for ``recipe`` (None: stateless)."""
+    if isinstance(recipe, DelayedScaling):
+        return LinearScaling(recipe.amax_history_len)
+    return None
 
 
 def _te_linear(module):
@@ -61,18 +85,38 @@ def _pad_rows(flat, multiple=32):
     return flat, length, aligned
 
 
-class _StatelessExtraState:
-    """``_extra_state`` of a stateless-scaling module: an empty uint8 tensor."""
+class _ScalingExtraState:
+    """``_extra_state``: an empty uint8 tensor for stateless (current) scaling; the amax
+    histories (float32) of the module's delayed-scaling roles otherwise."""
+
+    def _delayed_scalings(self):
+        return []
 
     def get_extra_state(self):
-        return torch.empty(0, dtype=torch.uint8)
+        scalings = self._delayed_scalings()
+        if not scalings:
+            return torch.empty(0, dtype=torch.uint8)
+        return torch.cat([sc.to_tensor() for sc in scalings])
 
     def set_extra_state(self, state):
-        if state is not None and getattr(state, 'numel', lambda: 0)():
-            raise ValueError('stateless FP8 scaling has no extra state to load')
+        n = state.numel() if state is not None and hasattr(state, 'numel') else 0
+        scalings = self._delayed_scalings()
+        if not scalings:
+            if n:
+                raise ValueError('stateless FP8 scaling has no extra state to load')
+            return
+        if n == 0:
+            return
+        sizes = [sc.to_tensor().numel() for sc in scalings]
+        if n != sum(sizes):
+            raise ValueError('delayed-scaling extra state does not match this module')
+        start = 0
+        for sc, size in zip(scalings, sizes):
+            sc.load_tensor(state[start:start + size])
+            start += size
 
 
-class TELinear(_StatelessExtraState, torch.nn.Module):
+class TELinear(_ScalingExtraState, torch.nn.Module):
     """One FP8 linear serving one or more stacked HF Linear weights of the same input."""
 
     def __init__(self, linears, recipe):
@@ -93,6 +137,10 @@ class TELinear(_StatelessExtraState, torch.nn.Module):
         self.counts = Counter()
         self._cached_weight_version = None
         self._fp8_weight = None
+        self.scaling = _new_scaling(self.recipe)
+
+    def _delayed_scalings(self):
+        return [self.scaling] if self.scaling is not None else []
 
     def extra_repr(self):
         return f"in={self.in_features}, out={self.out_features}, recipe={self.bongard_recipe}"
@@ -106,7 +154,8 @@ class TELinear(_StatelessExtraState, torch.nn.Module):
     def fp8_weight(self, is_first_microbatch):
         """Quantized weight (+ transposed copy); cached across microbatches like TE."""
         if is_first_microbatch or self._fp8_weight is None:
-            q = _linear.quantize_weight(self.weight, transpose=True)
+            q = _linear.quantize_weight(self.weight, transpose=True,
+                                        scaler=self.scaling and self.scaling.weight)
             if is_first_microbatch is not None:
                 self._fp8_weight = q
             return q
@@ -130,7 +179,7 @@ class TELinear(_StatelessExtraState, torch.nn.Module):
         if flat.dtype != torch.bfloat16:
             flat = flat.to(torch.bfloat16)
         out = _linear.Fp8LinearFunction.apply(flat, self.weight, None,
-                                              self.fp8_weight(first_microbatch))
+                                              self.fp8_weight(first_microbatch), self.scaling)
         if aligned != length:
             out = out[:length]
         return out.reshape(*x.shape[:-1], out.shape[-1])
@@ -148,6 +197,8 @@ class TEMLP(torch.nn.Module):
         # Default: one stacked [gate; up] weight sharing one scale; the environment switch
         # keeps two projections (two scales), as in the reference.
         self.fused_gate_up = os.environ.get('BONGARD_TE_SPLIT_GATE_UP', '0') != '1'
+        if not self.fused_gate_up and recipe == 'fp8_delayed':
+            raise ValueError('delayed scaling needs the fused gate_up projection')
         if self.fused_gate_up:
             self.gate_up = TELinear([mlp.gate_proj, mlp.up_proj], recipe)
         else:
@@ -182,8 +233,9 @@ class TEMLP(torch.nn.Module):
         if self.fused_gate_up:
             first = self.gate_up._note_microbatch()
             if first or self.gate_up._fp8_weight is None:
+                gs = self.gate_up.scaling
                 self.gate_up._fp8_weight = _linear.quantize_gate_up(
-                    self.gate_up.weight, I, split_scales=False)
+                    self.gate_up.weight, I, split_scales=False, scaler=gs and gs.weight)
             gu_q = self.gate_up._fp8_weight
             w_gu = self.gate_up.weight
         else:
@@ -195,8 +247,11 @@ class TEMLP(torch.nn.Module):
                     split_scales=True)
             gu_q = self._split_cache
             w_gu = _SplitGateUp.apply(self.gate_proj.weight, self.up_proj.weight)
+        scaling = None
+        if self.fused_gate_up and self.gate_up.scaling is not None:
+            scaling = (self.gate_up.scaling, self.down.scaling)
         out = _linear.Fp8GegluMlpFunction.apply(flat, w_gu, self.down.weight, gu_q, down_q, I,
-                                                not self.fused_gate_up)
+                                                not self.fused_gate_up, scaling)
         if aligned != length:
             out = out[:length]
         return out.reshape(*x.shape[:-1], out.shape[-1])

@@ -239,3 +239,40 @@ def test_enable_float8_errors():
         recipe="tensorwise")
     with pytest.raises(ValueError, match="retain its FP8 recipe"):
         float8_training.enable_float8(model, "tensorwise", emulate=True)
+
+
+# ---- delayed scaling recipe ('fp8_delayed') ---------------------------------------------
+def test_delayed_recipe_extra_state_round_trip_and_export():
+    """'fp8_delayed' modules keep amax histories in _extra_state (non-empty), which load
+    back through load_state_dict and make export raise as stateful scaling does."""
+    lin = te_linear.TELinear([nn.Linear(H, 32, bias=False).to(torch.bfloat16)], "fp8_delayed")
+    assert lin.recipe.amax_history_len == 16
+    sd = lin.state_dict()
+    assert sd["_extra_state"].numel() == 3 * (3 + 16 + 4)
+    hist = sd["_extra_state"].clone()
+    hist[3] = 2.5                                   # input role, history slot 0
+    hist[1] = 1.0                                   # one amax recorded
+    lin2 = te_linear.TELinear([nn.Linear(H, 32, bias=False).to(torch.bfloat16)], "fp8_delayed")
+    lin2.load_state_dict({"weight": sd["weight"], "_extra_state": hist})
+    assert lin2.scaling.input.recorded == 1
+    assert lin2.scaling.input.state[0].item() == 2.5
+    assert torch.equal(lin2.state_dict()["_extra_state"], hist)
+    with pytest.raises(ValueError, match="stateless"):
+        te_linear.TELinear([nn.Linear(H, 32, bias=False)], "fp8").load_state_dict(
+            {"weight": sd["weight"], "_extra_state": hist})
+    model = _Model()
+    te_linear.enable_te_linear(model, mlp="fp8_delayed")
+    with pytest.raises(ValueError, match="stateless"):
+        te_linear.restore_hf_layout(model.backbone, model.backbone.state_dict())
+    model = _Model()
+    assert fused_mlp.enable_fused_mlp(model, "fp8_delayed") == 3
+    f = model.backbone.decoder.layers[0].mlp
+    assert f.state_dict()["_extra_state"].numel() == 2 * 3 * (3 + 16 + 4)
+    with pytest.raises(ValueError, match="stateless"):
+        fused_mlp.hf_state_dict(model.backbone)
+
+
+def test_delayed_recipe_needs_fused_gate_up(monkeypatch):
+    monkeypatch.setenv("BONGARD_TE_SPLIT_GATE_UP", "1")
+    with pytest.raises(ValueError, match="fused gate_up"):
+        te_linear.TEMLP(_mlp(4), "fp8_delayed")

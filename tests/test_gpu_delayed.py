@@ -121,3 +121,30 @@ def test_mlp_training_steps_delayed(gpu):
             assert rel <= 0.005 and mx <= tol, name
         w_gu.grad = None
         w_d.grad = None
+
+
+@pytest.mark.parametrize("count", [5, 2048, 5200])
+def test_long_partial_lists(gpu, count):
+    """Producers may hand over more partials than a cast folds inline (the gated-GELU GEMM
+    writes one per tile: 5200 at c3's M); current and delayed scaling both pre-reduce
+    them then, with the same result."""
+    g = torch.Generator().manual_seed(count)
+    x = torch.randn(64, 128, generator=g).to(torch.bfloat16)
+    vals = torch.rand(count, generator=g) * 3.0
+    keys = vals.view(torch.int32).clone()
+    amax = float(vals.max())
+    parts = keys.to(gpu)
+    q = ops.cast_partials(x.to(gpu), parts, ops.E4M3)
+    torch.cuda.synchronize()
+    scale = orc.scale_np(amax, ops.E4M3)
+    assert q.meta.cpu()[1].item() == float(scale)
+    assert torch.equal(q.data.view(torch.uint8).cpu(), orc.cast(x, torch.tensor(scale), 0))
+    # delayed: step 0 records nothing; step 1 folds this producer's `count` partials
+    sc = scaling.DelayedScaler(ops.E4M3, 4)
+    buf = sc.partials_for_producer(count, gpu)
+    buf.copy_(parts)
+    sc.quantize(x.to(gpu), producer_count=count)
+    q1 = sc.quantize(x.to(gpu))
+    torch.cuda.synchronize()
+    assert q1.meta.cpu()[1].item() == float(scale)
+    assert sc.state.cpu()[0].item() == amax

@@ -180,3 +180,35 @@ def test_fused_mlp_train_forward(gpu):
     f.eval()
     ref_eval = f._hf_mlp(f._hf_norm(xg.detach()))
     assert torch.equal(f(xg.detach()), ref_eval)
+
+
+def test_temlp_delayed_train_steps(gpu):
+    """'fp8_delayed': three training steps (an in-place update between them re-quantizes
+    the weights, as an optimizer step does) against the oracle chain whose every tensor
+    role is quantized by a DelayedQuantizer with the same history length."""
+    hidden, inter, rows = 256, 512, 256
+    g = torch.Generator().manual_seed(77)
+    mlp = _mlp(hidden, inter, 77, "cpu")
+    wg, wu, wd = (m.weight.detach().clone() for m in (mlp.gate_proj, mlp.up_proj, mlp.down_proj))
+    t = te_linear.TEMLP(mlp, "fp8_delayed").to(gpu).train()
+    quant = orc.DelayedQuantizer(16)
+    for step in range(3):
+        with torch.no_grad():                       # new weight versions: re-quantize
+            t.gate_up.weight.mul_(1.0)
+            t.down.weight.mul_(1.0)
+        x = (torch.randn(rows, hidden, generator=g) * (1 + step)).to(torch.bfloat16)
+        dy = (torch.randn(rows, hidden, generator=g) * 1e-3).to(torch.bfloat16)
+        xg = x.to(gpu).requires_grad_(True)
+        y = t(xg)
+        y.backward(dy.to(gpu))
+        torch.cuda.synchronize()
+        fwd = orc.mlp_forward(x, wg, wu, wd, quant=quant)
+        rdx, rdwgu, rdwd, _ = orc.mlp_backward(fwd, x, wg, wu, wd, dy, quant=quant)
+        _close_requant(y, fwd["y"], f"delayed y step {step}")
+        _close_requant(xg.grad, rdx, f"delayed dx step {step}", max_tol=0.2)
+        _close_requant(t.gate_up.weight.grad, rdwgu, f"delayed dWgu step {step}", max_tol=0.2)
+        _close_requant(t.down.weight.grad, rdwd, f"delayed dWd step {step}", max_tol=0.2)
+        t.gate_up.weight.grad = None
+        t.down.weight.grad = None
+    assert t.gate_up.scaling.input.recorded == 2    # amaxes of steps 0, 1 folded in
+    assert t.state_dict()["down._extra_state"].numel() == 3 * (3 + 16 + 4)
