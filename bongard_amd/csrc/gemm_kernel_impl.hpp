@@ -179,6 +179,17 @@ gemm_kernel(GemmParams p) {
   static_assert(EPI != EPI_GEGLU || FN % 2 == 0, "GEGLU pairs gate and up sub-tiles");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage];
 
+  // Dequant scales: read at the start, so their latency hides behind the first loads.
+  const float sa = *p.a_sinv;
+  float sb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) sb[s] = s < p.n_seg ? p.b_sinv[s * p.b_stride] : 0.0f;
+  float ag = 0.0f, au = 0.0f;
+  if constexpr (EPI == EPI_GEGLU) {
+    ag = sa * p.b_sinv[0];
+    au = sa * p.b_sinv[p.b_stride];
+  }
+
   int tm, tn, split;
   block_coords(p, tm, tn, split);
   const int m0 = tm * BM;
@@ -285,8 +296,10 @@ gemm_kernel(GemmParams p) {
   // of stage ls, which the barrier has just released, and has about NS-1 steps to land;
   // LDS reads and texture-unit loads sit between consecutive MFMAs, so neither unit
   // (both shared by the four waves) blocks MFMA issue. sched_barrier(0) pins the order.
-  // Loads of stages past the split's end zero-fill a slot that is never read again,
-  // which keeps the loop free of branches.
+  // The last NS steps load nothing (their stages would lie past the split's end); their
+  // mid-step wait drains every load instead (the next stage is then the last one issued,
+  // or none: the trailing fragment reads of the final step go to a stale slot and are
+  // never used). Prologue stages past the end are zero-filled.
 #pragma unroll
   for (int ls = 0; ls < NS; ++ls) {
 #pragma unroll
@@ -297,9 +310,15 @@ gemm_kernel(GemmParams p) {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 1)) : "memory");
   __syncthreads();
   Frags<NH> f0, f1;
+  // same read order as the loop's second half, so that the wait counts at the loop header
+  // agree on both incoming paths
 #pragma unroll
-  for (int h = 0; h < NH; ++h) read_one(f0, smem, 0, h);
-  for (int ls = 0; ls < nsteps; ++ls) {
+  for (int h = 0; h < NH; ++h) {
+    read_one(f0, smem, 0, h);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  auto step = [&](auto with_dma, int ls) __attribute__((always_inline)) {
+    constexpr bool kDma = decltype(with_dma)::value;
     uint8_t* cur = stage_ptr(ls);
     uint8_t* nxt = stage_ptr(ls + 1);
     __builtin_amdgcn_sched_barrier(0);
@@ -311,7 +330,10 @@ gemm_kernel(GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     // stage ls+1 landed (stages ls+2 .. ls+NS-1 may still be in flight)
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 2)) : "memory");
+    if constexpr (kDma)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 2)) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t kn = (uint32_t)(kbeg + ls + NS) * kBK;
@@ -321,13 +343,17 @@ gemm_kernel(GemmParams p) {
       mma_one(f1, x);
 #pragma unroll
       for (int h = x * NH / NM; h < (x + 1) * NH / NM; ++h) read_one(f0, nxt, 0, h);
+      if constexpr (kDma) {
 #pragma unroll
-      for (int d = x * ND / NM; d < (x + 1) * ND / NM; ++d) dma_load(d, cur, kn, killn);
+        for (int d = x * ND / NM; d < (x + 1) * ND / NM; ++d) dma_load(d, cur, kn, killn);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-  }
-  // The last steps' zero-fill loads still target LDS: drain them, and let every wave
-  // finish with the stages, before the epilogue reuses the space.
+  };
+  int ls = 0;
+  for (; ls < nsteps - NS; ++ls) step(std::true_type{}, ls);
+  for (; ls < nsteps; ++ls) step(std::false_type{}, ls);
+  // Let every wave finish with the stages before the epilogue reuses the space.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
@@ -337,7 +363,6 @@ gemm_kernel(GemmParams p) {
   // holds runs of four consecutive columns. bf16 results are staged through this wave's
   // own LDS region of the (now idle) pipeline ring and leave as 16-byte row segments.
   constexpr int ROWS = FM * 32;  // rows of the wave's output tile
-  const float sa = *p.a_sinv;
   const int lrow_m = lane & 31;
   const int lcol = (lane >> 5) * 4;
   if constexpr (EPI == EPI_LINEAR && OUT == BF8_OUT_BF16) {
@@ -353,7 +378,7 @@ gemm_kernel(GemmParams p) {
         int seg = 0;
 #pragma unroll
         for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < p.n_seg && n >= p.seg_end[s2]) ? 1 : 0;
-        const float alpha = sa * p.b_sinv[seg * p.b_stride];
+        const float alpha = sa * (seg == 0 ? sb[0] : seg == 1 ? sb[1] : seg == 2 ? sb[2] : sb[3]);
         float bias[4] = {0.f, 0.f, 0.f, 0.f};
         if (p.bias && n < p.N) {
           const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
@@ -392,7 +417,8 @@ gemm_kernel(GemmParams p) {
         int seg = 0;
 #pragma unroll
         for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < p.n_seg && n >= p.seg_end[s2]) ? 1 : 0;
-        const float alpha = raw ? 1.0f : sa * p.b_sinv[seg * p.b_stride];
+        const float alpha =
+            raw ? 1.0f : sa * (seg == 0 ? sb[0] : seg == 1 ? sb[1] : seg == 2 ? sb[2] : sb[3]);
         float bias[4] = {0.f, 0.f, 0.f, 0.f};
         if (p.bias && !raw) {
           const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
@@ -417,8 +443,6 @@ gemm_kernel(GemmParams p) {
     // keeps them for the backward.
     constexpr int HF = FN / 2;
     constexpr int CH = HF * 4;  // 16-byte chunks per staged H row
-    const float ag = sa * p.b_sinv[0];
-    const float au = sa * p.b_sinv[p.b_stride];
     uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
     const int wave_h0 = n0 + wn * HF * 32;
     uint32_t hmax = 0;
