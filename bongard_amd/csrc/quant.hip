@@ -9,10 +9,12 @@
 // Current scaling needs the whole tensor's amax before the first byte is cast, so a
 // quantization is two streaming passes: amax_partials_kernel writes one max per block
 // (at most kMaxAmaxBlocks, plain stores, no atomics), and the cast kernel reduces those
-// partials in every block (a <= 2 KB read) to the scale before it streams the data;
-// its block 0 publishes the meta record. The same cast kernel consumes the per-tile
-// partials of H written by the gate/up GEMM epilogue and those of dGU written by the
-// gated-GELU backward. Streaming loads use 16-byte vectors, several in flight per lane.
+// partials in every block (a <= 8 KB read, overlapped with the block's first data
+// loads) to the scale before it streams the data; its block 0 publishes the meta record.
+// The same cast kernel consumes the per-tile partials of H written by the gate/up GEMM
+// epilogue and those of dGU written by the gated-GELU backward. Streaming loads and
+// stores are plain 16-byte vector accesses, several in flight per lane (the non-temporal
+// hint measured up to 30% slower on gfx950 for these streams).
 //
 // Delayed scaling (amax history, TE DelayedScaling semantics) needs no pre-pass: the
 // cast kernel derives the scale from the history (after folding in the previous step's
@@ -49,7 +51,8 @@ namespace {
 
 constexpr int kNT = 256;            // threads per block for streaming kernels
 constexpr int kVecPerThread = 8;    // 16-byte loads in flight per lane (amax)
-constexpr int64_t kMaxAmaxBlocks = 1024;  // 4 blocks per CU; consumers read <= 4 KB of partials
+constexpr int64_t kMaxAmaxBlocks = 2048;  // 8 blocks per CU; consumers read <= 8 KB of partials
+constexpr int64_t kMaxCastBlocks = 4096;  // 16 blocks per CU (2048 when partials are written)
 // Consumers reduce up to this many partials in every block; a longer list (the gated-GELU
 // GEMM writes one per tile: 5200 at M = 16.6k) is first reduced by a one-block kernel.
 constexpr int64_t kMaxInlinePartials = 2048;
@@ -81,11 +84,11 @@ __global__ __launch_bounds__(kNT) void amax_partials_kernel(const uint16_t* __re
   for (; i + (kVecPerThread - 1) * stride < nvec; i += kVecPerThread * stride) {
     uint4 v[kVecPerThread];
 #pragma unroll
-    for (int j = 0; j < kVecPerThread; ++j) v[j] = load_nt(xv + i + j * stride);
+    for (int j = 0; j < kVecPerThread; ++j) v[j] = xv[i + j * stride];
 #pragma unroll
     for (int j = 0; j < kVecPerThread; ++j) m = max(m, absmax_key8(v[j]));
   }
-  for (; i < nvec; i += stride) m = max(m, absmax_key8(load_nt(xv + i)));
+  for (; i < nvec; i += stride) m = max(m, absmax_key8(xv[i]));
   // scalar tail (n % 8), handled by block 0
   if (blockIdx.x == 0) {
     for (int64_t j = (nvec << 3) + threadIdx.x; j < n; j += kNT)
@@ -144,31 +147,32 @@ template <int FMT>
 __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ x, int64_t n,
                                                    ScaleSrc src, uint8_t* __restrict__ out,
                                                    uint32_t* __restrict__ amax_out) {
-  const float scale = resolve_scale<FMT>(src);
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint4* ov = reinterpret_cast<uint4*>(out);
   const int64_t n16 = n >> 4;
   const int64_t stride = (int64_t)gridDim.x * kNT;
   int64_t i = (int64_t)blockIdx.x * kNT + threadIdx.x;
+  // Two 16-element groups (i, i + stride) per lane and iteration; the next iteration's
+  // four loads are issued before this one is converted, and the first iteration's before
+  // the scale is resolved (whose partial-amax reduction then overlaps them).
+  uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = a0, b0 = a0, b1 = a0;
+  if (i < n16) { a0 = xv[2 * i]; a1 = xv[2 * i + 1]; }
+  if (i + stride < n16) { b0 = xv[2 * (i + stride)]; b1 = xv[2 * (i + stride) + 1]; }
+  const float scale = resolve_scale<FMT>(src);
   uint32_t m = 0;
-  for (; i + stride < n16; i += 2 * stride) {
-    uint4 a0 = load_nt(xv + 2 * i);
-    uint4 a1 = load_nt(xv + 2 * i + 1);
-    uint4 b0 = load_nt(xv + 2 * (i + stride));
-    uint4 b1 = load_nt(xv + 2 * (i + stride) + 1);
-    if (amax_out)
-      m = max(m, max(max(absmax_key8(a0), absmax_key8(a1)), max(absmax_key8(b0), absmax_key8(b1))));
-    uint2 qa0 = quant8_bf16<FMT>(a0, scale), qa1 = quant8_bf16<FMT>(a1, scale);
-    uint2 qb0 = quant8_bf16<FMT>(b0, scale), qb1 = quant8_bf16<FMT>(b1, scale);
-    store_nt(ov + i, make_uint4(qa0.x, qa0.y, qa1.x, qa1.y));
-    store_nt(ov + i + stride, make_uint4(qb0.x, qb0.y, qb1.x, qb1.y));
-  }
-  for (; i < n16; i += stride) {
-    uint4 a0 = load_nt(xv + 2 * i);
-    uint4 a1 = load_nt(xv + 2 * i + 1);
-    if (amax_out) m = max(m, max(absmax_key8(a0), absmax_key8(a1)));
-    uint2 qa0 = quant8_bf16<FMT>(a0, scale), qa1 = quant8_bf16<FMT>(a1, scale);
-    store_nt(ov + i, make_uint4(qa0.x, qa0.y, qa1.x, qa1.y));
+  for (; i < n16; i += 2 * stride) {
+    const uint4 c0 = a0, c1 = a1, d0 = b0, d1 = b1;
+    const int64_t inext = i + 2 * stride;
+    if (inext < n16) { a0 = xv[2 * inext]; a1 = xv[2 * inext + 1]; }
+    if (inext + stride < n16) { b0 = xv[2 * (inext + stride)]; b1 = xv[2 * (inext + stride) + 1]; }
+    if (amax_out) m = max(m, max(absmax_key8(c0), absmax_key8(c1)));
+    const uint2 qc0 = quant8_bf16<FMT>(c0, scale), qc1 = quant8_bf16<FMT>(c1, scale);
+    ov[i] = make_uint4(qc0.x, qc0.y, qc1.x, qc1.y);
+    if (i + stride < n16) {
+      if (amax_out) m = max(m, max(absmax_key8(d0), absmax_key8(d1)));
+      const uint2 qd0 = quant8_bf16<FMT>(d0, scale), qd1 = quant8_bf16<FMT>(d1, scale);
+      ov[i + stride] = make_uint4(qd0.x, qd0.y, qd1.x, qd1.y);
+    }
   }
   if (blockIdx.x == 0) {
     for (int64_t j = (n16 << 4) + threadIdx.x; j < n; j += kNT) {
@@ -211,8 +215,8 @@ __global__ __launch_bounds__(kNT) void cast_transpose_kernel(
       uint32_t q[4] = {0u, 0u, 0u, 0u};
       if (r < rows && c < cols) {
         const uint4* src4 = reinterpret_cast<const uint4*>(x + r * cols + c);
-        uint4 a0 = load_nt(src4);
-        uint4 a1 = load_nt(src4 + 1);
+        uint4 a0 = src4[0];
+        uint4 a1 = src4[1];
         if (amax_out) m = max(m, max(absmax_key8(a0), absmax_key8(a1)));
         uint2 q0 = quant8_bf16<FMT>(a0, scale), q1 = quant8_bf16<FMT>(a1, scale);
         q[0] = q0.x; q[1] = q0.y; q[2] = q1.x; q[3] = q1.y;
@@ -253,7 +257,11 @@ int64_t transpose_blocks(int64_t rows, int64_t cols) {
   return tiles < kMaxTransposeBlocks ? (tiles > 0 ? tiles : 1) : kMaxTransposeBlocks;
 }
 
-int64_t row_cast_blocks(int64_t n) { return grid_for_stream((n + 15) / 16, 2 * kNT, 2048); }
+// Blocks of the row-major cast: up to kMaxCastBlocks, but no more than the consumers of
+// its amax partials reduce inline when it writes them.
+int64_t row_cast_blocks(int64_t n, bool with_amax) {
+  return grid_for_stream((n + 15) / 16, 2 * kNT, with_amax ? kMaxInlinePartials : kMaxCastBlocks);
+}
 
 // ---- delayed scaling ------------------------------------------------------------------
 // state layout: history[len], then meta {amax_last, scale, scale_inv, pos}; a fresh
@@ -341,7 +349,7 @@ int launch_cast(const void* x, int64_t rows, int64_t cols, ScaleSrc src, int fmt
     src.n_prev = 0;
   }
   if (out_t == nullptr) {
-    const int grid = (int)row_cast_blocks(n);
+    const int grid = (int)row_cast_blocks(n, amax_out != nullptr);
     if (fmt == BF8_E4M3)
       hipLaunchKernelGGL(cast_kernel<BF8_E4M3>, dim3(grid), dim3(kNT), 0, s, xs, n, src, out,
                          amax_out);
@@ -427,7 +435,7 @@ int bf8_cast_partials_bf16(const void* x, int64_t rows, int64_t cols, const uint
 
 int64_t bf8_cast_amax_partials(int64_t rows, int64_t cols, int transpose) {
   if (rows <= 0 || cols <= 0) return 1;
-  return transpose ? transpose_blocks(rows, cols) : row_cast_blocks(rows * cols);
+  return transpose ? transpose_blocks(rows, cols) : row_cast_blocks(rows * cols, true);
 }
 
 int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* state, int len,
