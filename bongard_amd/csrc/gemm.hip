@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 
@@ -23,7 +24,16 @@ constexpr int kStepBytes = 128;
 constexpr int kMaxSplits = 8;
 constexpr int kMinStepsPerSplit = 4;
 
-enum TileId { TILE_256x256 = 0, TILE_256x160, TILE_160x256, TILE_128x128, NUM_TILES };
+enum TileId {
+  TILE_256x256 = 0,
+  TILE_256x160,
+  TILE_160x256,
+  TILE_128x128,
+  TILE_192x256,
+  TILE_128x64,
+  TILE_64x128,
+  NUM_TILES
+};
 
 struct TileInfo {
   int bm, bn, occ;
@@ -40,6 +50,9 @@ constexpr TileInfo kTiles[NUM_TILES] = {
     {256, 160, 1, 9.2, 0.0, "256x160"},
     {160, 256, 1, 9.0, 7.6, "160x256"},
     {128, 128, 1, 8.0, 6.2, "128x128"},
+    {192, 256, 1, 9.0, 8.0, "192x256"},
+    {128, 64, 2, 6.5, 0.0, "128x64"},
+    {64, 128, 2, 6.5, 4.0, "64x128"},
 };
 // Gated-GELU plans may not depend on K (the amax partial count is sized from M and I
 // alone); they are costed at a typical 20 K steps (hidden size 2560).
@@ -68,15 +81,25 @@ Plan make_plan(int tile, int64_t M, int64_t N, int64_t ksteps, int splits) {
   return p;
 }
 
+// A K step never takes less than this, however little MFMA work it holds: with few
+// workgroups per CU the loads of the stages in flight no longer cover their latency
+// (measured at M = 512: ~520 ns per step for one workgroup per CU, ~450 ns when the tile
+// is small enough for two to share the CU).
+constexpr double kStepFloorNs = 520.0;
+constexpr double kStepFloorNsOcc2 = 450.0;
+
 // Modelled time (ns): rounds of co-resident workgroups, each running its K steps plus
 // about two steps of pipeline fill and epilogue, plus the split-K partials' HBM round
-// trip and the reduction's launch.
+// trip and the reduction's launch. A step costs the MFMA work of the workgroups sharing
+// a CU in the busiest round, or the latency floor.
 double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu) {
   const TileInfo& ti = kTiles[p.tile];
   const int64_t ctas = (int64_t)p.tiles_m * p.tiles_n * p.splits;
   const int64_t rounds = cdiv(ctas, (int64_t)kNumCus * ti.occ);
+  const int64_t per_cu = std::min<int64_t>(ti.occ, cdiv(ctas, (int64_t)kNumCus));
   const double rate = geglu ? ti.geglu_rate : ti.rate;
-  const double step_ns = ti.occ * 2.0 * ti.bm * ti.bn * kStepBytes / (rate * 1e3);
+  const double work_ns = per_cu * 2.0 * ti.bm * ti.bn * kStepBytes / (rate * 1e3);
+  const double step_ns = std::max(work_ns, ti.occ > 1 ? kStepFloorNsOcc2 : kStepFloorNs);
   double t = (double)rounds * (p.kps + 2) * step_ns;
   if (p.splits > 1) t += 2.0 * p.splits * M * N * 4 / 5e3 + 5000.0;
   return t;
@@ -128,6 +151,10 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail) {
     }
   }
   if (geglu) best.kps = (int)ksteps;
+  if (const char* d = std::getenv("BONGARD_FP8_GEMM_DEBUG"); d && d[0] == '1')
+    std::fprintf(stderr, "bf8 plan %s M=%lld N=%lld K=%lld: tile %s splits %d (%d x %d tiles)\n",
+                 geglu ? "geglu" : "gemm", (long long)M, (long long)N, (long long)K,
+                 kTiles[best.tile].name, best.splits, best.tiles_m, best.tiles_n);
   return best;
 }
 
@@ -137,6 +164,9 @@ int launch_tile(const Plan& pl, const GemmParams& p, int epi, int out_dtype, int
     case TILE_256x256: return launch_gemm_tile<Tile256x256>(p, epi, out_dtype, fa, fb, s);
     case TILE_256x160: return launch_gemm_tile<Tile256x160>(p, epi, out_dtype, fa, fb, s);
     case TILE_160x256: return launch_gemm_tile<Tile160x256>(p, epi, out_dtype, fa, fb, s);
+    case TILE_192x256: return launch_gemm_tile<Tile192x256>(p, epi, out_dtype, fa, fb, s);
+    case TILE_128x64: return launch_gemm_tile<Tile128x64>(p, epi, out_dtype, fa, fb, s);
+    case TILE_64x128: return launch_gemm_tile<Tile64x128>(p, epi, out_dtype, fa, fb, s);
     default: return launch_gemm_tile<Tile128x128>(p, epi, out_dtype, fa, fb, s);
   }
 }

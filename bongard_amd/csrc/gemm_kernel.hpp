@@ -48,6 +48,9 @@ using Tile256x256 = GemmTile<2, 2, 4, 4, 2, 1>;
 using Tile256x160 = GemmTile<4, 1, 2, 5, 3, 1>;
 using Tile160x256 = GemmTile<1, 4, 5, 2, 3, 1>;
 using Tile128x128 = GemmTile<2, 2, 2, 2, 4, 1>;
+using Tile192x256 = GemmTile<2, 2, 3, 4, 2, 1>;
+using Tile128x64 = GemmTile<2, 2, 2, 1, 3, 2>;
+using Tile64x128 = GemmTile<2, 2, 1, 2, 3, 2>;
 
 // Enqueues the GEMM for tile shape T (EPI_GEGLU: e4m3 x e4m3, bf16 H). Returns a BF8_*
 // status; the host entry points have validated p.

@@ -1,0 +1,6 @@
+// FP8 GEMM kernels for 192 x 256 block tiles (one translation unit per tile shape).
+#include "gemm_kernel_impl.hpp"
+
+namespace bf8 {
+template int launch_gemm_tile<Tile192x256>(const GemmParams&, int, int, int, int, hipStream_t);
+}  // namespace bf8
