@@ -215,6 +215,7 @@ def main():
             "c3": _bench_c3(torch, ops, workloads, dev),
             "c4": _bench_c4(torch, ops, workloads, dev),
             "c5": _bench_c5(torch, workloads, dev),
+            "fused_norm": _bench_norm(torch, ops, workloads, dev),
         }
 
     cpu = None
@@ -408,6 +409,42 @@ def _bench_c5(torch, workloads, dev, steps=10):
                         "weights re-quantized every step",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
             "frac_of_fp8_peak": round(flop / s / 1e12 / FP8_PEAK_TFLOPS, 4)}
+
+
+def _bench_norm(torch, ops, workloads, dev, steps=50):
+    """FusedMLP's norm -> e4m3 input of fc1 at the c5 shape: the fused RMSNorm (which writes
+    the amax partials of its output) + cast from those partials, against the same norm in
+    torch ops + the two-pass quantize. Both cast with the transposed copy (training)."""
+    from bongard_amd import fused_mlp
+
+    c = workloads.config5()
+    x = c["x"].to(dev)
+    M, K = x.shape
+    g = torch.Generator(device=dev).manual_seed(3)
+    w = (torch.randn(K, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+
+    def fused():
+        y, _, parts = ops.rmsnorm(x, w, 1e-6)
+        return ops.cast_partials(y, parts, ops.E4M3, rowwise=True, transpose=True)
+
+    def unfused():
+        y = fused_mlp._rms_norm(x, w, 1e-6)
+        return ops.quantize(y, ops.E4M3, rowwise=True, transpose=True)
+
+    a, b = fused(), unfused()
+    torch.cuda.synchronize()
+    # the norms' means are summed in different orders (fp64 vs torch's fp32), so a rare
+    # element may round to the neighbouring bf16 and then e4m3 value
+    flips = (a.data.view(torch.uint8) != b.data.view(torch.uint8)).float().mean().item()
+    s_f = _timed(torch, fused, steps, 5)
+    s_u = _timed(torch, unfused, steps, 5)
+    s_n = _ev_time(torch, lambda: ops.rmsnorm(x, w, 1e-6), steps)
+    gbps = 4.0 * M * K / s_n / 1e9
+    return {"workload": f"RMSNorm [{M},{K}] bf16 -> e4m3 (+ transposed copy)",
+            "fused_us": round(s_f * 1e6, 2), "torch_norm_then_quantize_us": round(s_u * 1e6, 2),
+            "rmsnorm_kernel_us": round(s_n * 1e6, 2), "rmsnorm_kernel_gbps": round(gbps, 1),
+            "rmsnorm_kernel_frac_hbm": round(gbps / HBM_PEAK_GBPS, 4),
+            "fp8_bytes_differing_from_torch_norm_path": flips}
 
 
 def _cpu_baseline(c, reps=1):

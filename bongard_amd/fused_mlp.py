@@ -9,11 +9,14 @@ refreshed by ``_apply``; counters ``weight_quantizations`` / ``cached_weights`` 
 ``hf_state_dict(backbone)`` for export.
 
 Training forward: RMSNorm with zero-centred gamma (``x * rsqrt(mean(x^2) + eps) *
-(1 + w)`` in fp32, rounded to bf16, as HF T5Gemma2RMSNorm), then the FP8 gated MLP of
-bongard_amd.linear.Fp8GegluMlpFunction (fc1 + gated-GELU epilogue, H quantized, fc2).
-fc1 keeps one shared scale for [gate; up], as TE's stacked fc1 weight does. Whether TE
-rounds the norm output to bf16 before its cast is not pinned by anything available; this
-path rounds it (the te_linear chain).
+(1 + w)`` in fp32, rounded to bf16, as HF T5Gemma2RMSNorm) in one HIP kernel that also
+writes the amax partials of its output, so the e4m3 cast of the norm output needs no amax
+pass (TE LayerNormMLP fuses norm and cast the same way, bongard/fused_mlp.py:25-30); then
+the FP8 gated MLP of bongard_amd.linear.Fp8GegluMlpFunction (fc1 + gated-GELU epilogue,
+H quantized, fc2). fc1 keeps one shared scale for [gate; up], as TE's stacked fc1 weight
+does. Whether TE rounds the norm output to bf16 before its cast is not pinned by anything
+available; this path rounds it (the te_linear chain). The norm's backward recomputes the
+HF formula under autograd (bf16 in, fp32 math).
 """
 
 from collections import Counter
@@ -21,6 +24,7 @@ from collections import Counter
 import torch
 
 from . import linear as _linear
+from . import ops as _ops
 from .te_linear import RECIPES, _ScalingExtraState, _make_recipe, _new_scaling, _pad_rows, present
 
 __all__ = ["RECIPES", "FusedMLP", "enable_fused_mlp", "hf_state_dict"]
@@ -30,6 +34,31 @@ def _rms_norm(x, weight, eps):
     xf = x.float()
     y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
     return (y * (1.0 + weight.float())).type_as(x)
+
+
+class _FusedRMSNorm(torch.autograd.Function):
+    """bf16 RMSNorm (zero-centred gamma) whose kernel also writes the amax partials of its
+    output into ``partials``; the backward differentiates :func:`_rms_norm`."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, partials):
+        y, _, _ = _ops.rmsnorm(x, weight, eps, zero_centered=True, partials=partials)
+        ctx.eps = eps
+        ctx.save_for_backward(x, weight)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight = ctx.saved_tensors
+        with torch.enable_grad():
+            xr = x.detach().requires_grad_(ctx.needs_input_grad[0])
+            wr = weight.detach().requires_grad_(ctx.needs_input_grad[1])
+            y = _rms_norm(xr, wr, ctx.eps)
+            inputs = [t for t in (xr, wr) if t.requires_grad]
+            grads = iter(torch.autograd.grad(y, inputs, dy))
+        dx = next(grads) if ctx.needs_input_grad[0] else None
+        dw = next(grads) if ctx.needs_input_grad[1] else None
+        return dx, dw, None, None
 
 
 class FusedMLP(_ScalingExtraState, torch.nn.Module):
@@ -111,10 +140,24 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
                 _linear.quantize_weight(self.fc2_weight, transpose=True,
                                         scaler=fc2 and fc2.weight))
         gu_q, down_q = self._fp8_weights
-        normed = _rms_norm(flat.to(torch.bfloat16), self.layer_norm_weight, self.eps)
+        flat = flat.to(torch.bfloat16).contiguous()
+        count = _ops.rmsnorm_partials_count(flat.shape[0])
+        if not _ops.rmsnorm_supported(flat.shape[1]):
+            # rows wider than the fused kernel holds in registers: norm in torch ops on the
+            # device, then the cast's own amax pass
+            parts, x_amax = None, None
+            normed = _rms_norm(flat, self.layer_norm_weight, self.eps)
+        elif fc1 is None:
+            parts = torch.empty(count, dtype=torch.int32, device=flat.device)
+            x_amax = parts
+        else:
+            parts = fc1.input.partials_for_producer(count, flat.device)
+            x_amax = count
+        if parts is not None:
+            normed = _FusedRMSNorm.apply(flat, self.layer_norm_weight, self.eps, parts)
         out = _linear.Fp8GegluMlpFunction.apply(normed, self.fc1_weight, self.fc2_weight, gu_q,
                                                 down_q, self.intermediate_size, False,
-                                                self.scaling)
+                                                self.scaling, x_amax)
         return out[:length].reshape_as(x)
 
 

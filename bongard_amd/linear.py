@@ -47,6 +47,18 @@ def _quantize(x, fmt, scaler, *, rowwise=True, transpose=False):
     return scaler.quantize(x, rowwise=rowwise, transpose=transpose)
 
 
+def _quantize_input(x, scaler, x_amax, transpose):
+    """e4m3 quantization of a GEMM input whose amax partials its producer may have written.
+
+    ``x_amax``: None (amax pass here), the producer's partials tensor (current scaling), or
+    the number of partials it wrote into ``scaler.partials_for_producer`` (delayed)."""
+    if x_amax is None:
+        return _quantize(x, E4M3, scaler, transpose=transpose)
+    if scaler is None:
+        return ops.cast_partials(x, x_amax, E4M3, rowwise=True, transpose=transpose)
+    return scaler.quantize(x, rowwise=True, transpose=transpose, producer_count=int(x_amax))
+
+
 class Fp8LinearFunction(torch.autograd.Function):
     """y = x @ W^T (+ b) in FP8; x: bf16 [M, K] with M % 16 == 0 when grads are needed.
 
@@ -93,16 +105,19 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
     per gate/up half (torchao / split TE) instead of one shared scale (fused TE gate_up).
     ``scaling``: None (current scaling) or ``(gate_up, down)`` LinearScaling objects for
     delayed scaling (roles: x, W_gu, dGU of gate_up; H, W_down, dY of down).
+    ``x_amax``: amax partials of x written by its producer (the fused RMSNorm): a partials
+    tensor under current scaling, the producer count under delayed scaling; None = none.
     """
 
     @staticmethod
-    def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scaling=None):
+    def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scaling=None,
+                x_amax=None):
         I = int(intermediate)
         train = any(ctx.needs_input_grad[:3])
         if scaling is not None and split_scales:
             raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
         gs, ds = scaling if scaling is not None else (None, None)
-        xq = _quantize(x, E4M3, gs and gs.input, transpose=ctx.needs_input_grad[1])
+        xq = _quantize_input(x, gs and gs.input, x_amax, ctx.needs_input_grad[1])
         if gu_q is None:
             gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=ctx.needs_input_grad[0],
                                     scaler=gs and gs.weight)
@@ -145,7 +160,7 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
         if need_dd:
             dd = ops.gemm(dyq.data_t, E5M2, dyq.meta, h8t, E4M3, h_meta)
         if not (need_dx or need_dgu):
-            return dx, dgu, dd, None, None, None, None, None
+            return dx, dgu, dd, None, None, None, None, None, None
         dH = ops.gemm(dyq.data, E5M2, dyq.meta, d8t, E4M3, d_meta)
         if gs is not None:
             M = dH.shape[0]
@@ -158,7 +173,7 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
                 dx = ops.gemm(dq.data, E5M2, dq.meta, gu8t, E4M3, gu_meta[0])
             if need_dgu:
                 dgu = ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta)
-            return dx, dgu, dd, None, None, None, None, None
+            return dx, dgu, dd, None, None, None, None, None, None
         dGU, gparts = ops.geglu_bwd(dH, GU)
         if not ctx.split_scales:
             dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=need_dx, transpose=need_dgu)
@@ -184,7 +199,7 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
                 dx = dx_parts[0] + dx_parts[1]
             if need_dgu:
                 dgu = torch.cat(dw_parts, 0)
-        return dx, dgu, dd, None, None, None, None, None
+        return dx, dgu, dd, None, None, None, None, None, None
 
 
 def quantize_gate_up(w_gu, intermediate, split_scales, *, transpose=True, scaler=None):

@@ -292,6 +292,48 @@ def geglu_bwd(dH, GU, *, partials=None):
     return dGU, parts
 
 
+RMSNORM_MAX_COLS = 4096
+
+
+def rmsnorm_supported(cols):
+    """Whether the fused RMSNorm kernel takes rows of ``cols`` elements."""
+    return cols % 8 == 0 and 0 < cols <= RMSNORM_MAX_COLS
+
+
+def rmsnorm_partials_count(rows):
+    return int(_lib.lib().bf8_rmsnorm_partials(int(rows)))
+
+
+def rmsnorm(x, weight, eps, *, zero_centered=True, want_rstd=False, partials=None):
+    """RMSNorm of bf16 rows (HF T5Gemma2RMSNorm arithmetic) fused with the amax of its output.
+
+    Returns ``(y bf16 [rows, cols], rstd fp32 [rows] or None, partials int32)``; pass the
+    partials to :func:`cast_partials` (current scaling) to quantize y without an amax pass.
+    ``partials``: an optional caller-owned buffer of at least ``rmsnorm_partials_count``
+    entries (e.g. a delayed scaler's producer buffer).
+    """
+    _require_gpu(x, weight)
+    x = _bf16_2d(x)
+    rows, cols = x.shape
+    if weight.dtype != torch.bfloat16 or weight.numel() != cols:
+        raise ValueError(f"rmsnorm: weight must be bf16 [{cols}]")
+    weight = weight.contiguous()
+    L = _lib.lib()
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, dtype=torch.float32, device=x.device) if want_rstd else None
+    count = int(L.bf8_rmsnorm_partials(rows))
+    if partials is None:
+        parts = torch.empty(count, dtype=torch.int32, device=x.device)
+    else:
+        if partials.numel() < count or partials.dtype != torch.int32:
+            raise ValueError(f"rmsnorm: partials must be int32 with >= {count} entries")
+        parts = partials[:count]
+    _lib.check(L.bf8_rmsnorm_bf16(_ptr(x), rows, cols, _ptr(weight), float(eps),
+                                  int(bool(zero_centered)), _ptr(y), _ptr(rstd), _ptr(parts),
+                                  _stream(x.device)), "bf8_rmsnorm_bf16")
+    return y, rstd, parts
+
+
 def new_delayed_state(length, device):
     """Delayed-scaling state: float32 [length + 4] = history, {amax, scale, scale_inv, pos}."""
     st = torch.zeros(length + 4, dtype=torch.float32, device=device)

@@ -179,6 +179,21 @@ int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* stat
                           float* meta_out, uint8_t* out, uint8_t* out_t, uint32_t* partials_out,
                           void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * RMSNorm fused with the amax pass of the quantization that follows it.
+ * Replaces the RMSNorm (zero-centred gamma) of TE LayerNormMLP built at
+ * bongard/fused_mlp.py:25-30 (HF T5Gemma2RMSNorm in evaluation, bongard/fused_mlp.py:64-65):
+ *   r = 1 / sqrt(mean(f32(x)^2) + eps),  y = bf16((f32(x) * r) * (1 + f32(gamma)))
+ * (gamma unchanged when zero_centered == 0). x, y: bf16 [rows, cols] row-major, cols % 8
+ * == 0, cols <= 4096; gamma: bf16 [cols]; rstd: fp32 [rows] (r per row) or NULL.
+ * partials: uint32 [bf8_rmsnorm_partials(rows)] amax keys of |y| per block, to pass to
+ * bf8_cast_partials_bf16 (the cast then needs no amax pass over y).
+ * ------------------------------------------------------------------------------- */
+int64_t bf8_rmsnorm_partials(int64_t rows);
+int bf8_rmsnorm_bf16(const void* x, int64_t rows, int64_t cols, const void* gamma, float eps,
+                     int zero_centered, void* y, float* rstd, uint32_t* partials,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -212,3 +212,47 @@ def test_temlp_delayed_train_steps(gpu):
         t.down.weight.grad = None
     assert t.gate_up.scaling.input.recorded == 2    # amaxes of steps 0, 1 folded in
     assert t.state_dict()["down._extra_state"].numel() == 3 * (3 + 16 + 4)
+
+
+def test_fused_mlp_delayed_train_steps(gpu):
+    """'fp8_delayed' FusedMLP: the fused norm writes the amax partials of its output into
+    the fc1 input role's producer buffer, and three training steps follow the oracle chain
+    (norm -> delayed-scaled MLP; backward through the norm under CPU autograd).
+
+    Step 0 quantizes with the initial scale 1, so its dGU (~1e-5) mostly flushes to zero in
+    e5m2; step 1 is the first with a live backward. A single legitimate e5m2 flip of an
+    outlier dGU element moves a whole row of dW_gu by up to ~4 RMS(dGU) RMS(X), i.e. about
+    4/sqrt(rows) of RMS(dW_gu): 512 rows keep that under the 0.2 bar."""
+    hidden, inter, rows = 256, 512, 512
+    g = torch.Generator().manual_seed(78)
+    mlp = _mlp(hidden, inter, 78, "cpu")
+    norm = T5Gemma2RMSNorm(hidden, eps=1e-6).to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.normal_(std=0.1)
+    wg, wu, wd = (m.weight.detach().clone() for m in (mlp.gate_proj, mlp.up_proj, mlp.down_proj))
+    nw = norm.weight.detach().clone()
+    f = fused_mlp.FusedMLP(mlp, norm, "fp8_delayed").to(gpu).train()
+    quant = orc.DelayedQuantizer(16)
+    for step in range(3):
+        with torch.no_grad():
+            f.fc1_weight.mul_(1.0)
+            f.fc2_weight.mul_(1.0)
+        x = (torch.randn(rows, hidden, generator=g) * (1 + step)).to(torch.bfloat16)
+        dy = (torch.randn(rows, hidden, generator=g) * 1e-3).to(torch.bfloat16)
+        xg = x.to(gpu).requires_grad_(True)
+        y = f(xg)
+        y.backward(dy.to(gpu))
+        torch.cuda.synchronize()
+        xr = x.clone().requires_grad_(True)
+        normed = orc.rmsnorm(xr, nw, 1e-6)
+        fwd = orc.mlp_forward(normed.detach(), wg, wu, wd, quant=quant)
+        rdn, rdwgu, rdwd, _ = orc.mlp_backward(fwd, normed.detach(), wg, wu, wd, dy, quant=quant)
+        normed.backward(rdn.to(torch.bfloat16))
+        _close_requant(y, fwd["y"], f"fused delayed y step {step}", max_tol=0.10)
+        _close_requant(xg.grad, xr.grad, f"fused delayed dx step {step}", max_tol=0.2)
+        _close_requant(f.fc1_weight.grad, rdwgu, f"fused delayed dWgu step {step}", max_tol=0.2)
+        _close_requant(f.fc2_weight.grad, rdwd, f"fused delayed dWd step {step}", max_tol=0.2)
+        f.fc1_weight.grad = None
+        f.fc2_weight.grad = None
+    fc1, _ = f.scaling
+    assert fc1.input.recorded == 2

@@ -1,0 +1,91 @@
+"""GPU tests of the fused RMSNorm (bf8_rmsnorm_bf16) that feeds FusedMLP's fc1.
+
+Bar: the norm output y against the oracle's RMSNorm (HF T5Gemma2RMSNorm arithmetic, torch
+on the CPU): the kernel sums the squares in fp64 and rounds once, torch sums in fp32, so
+the mean (and with it the row's rstd) may differ by an fp32 ulp; where that straddles a
+bf16 rounding boundary y moves by one bf16 ulp. So: every element within 1 bf16 ulp, and
+at most 1 in 1000 elements not bit-identical. The amax partials are exact: their max is
+the bit pattern of max|y| of the kernel's own y, and the cast from them gives the same
+bytes and meta as the two-pass quantize of that y.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from bongard_amd import ops
+from oracle import fp8_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(rows, cols, seed, gamma_std=0.1):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, cols, generator=g)
+    if cols >= 16:
+        x[:, torch.randperm(cols, generator=g)[:4]] *= 20.0   # outlier columns
+    if rows > 2:
+        x[1] = 0.0                                               # an all-zero (padding) row
+    w = torch.randn(cols, generator=g) * gamma_std
+    return x.to(torch.bfloat16), w.to(torch.bfloat16)
+
+
+def _ulp_diff(a_bf16, b_bf16):
+    a = a_bf16.view(torch.int16).numpy().astype(np.int32)
+    b = b_bf16.view(torch.int16).numpy().astype(np.int32)
+    # order-preserving integer keys of bf16 bit patterns
+    ka = np.where(a < 0, -(a & 0x7FFF), a)
+    kb = np.where(b < 0, -(b & 0x7FFF), b)
+    return np.abs(ka - kb)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 8), (7, 520), (160, 256), (333, 2560), (64, 4096),
+                                       (1000, 1024), (4099, 2560)])
+def test_rmsnorm_matches_oracle(gpu, rows, cols):
+    x, w = _inputs(rows, cols, rows * 31 + cols)
+    y, rstd, parts = ops.rmsnorm(x.to(gpu), w.to(gpu), 1e-6, want_rstd=True)
+    torch.cuda.synchronize()
+    ref = orc.rmsnorm(x, w, 1e-6)
+    d = _ulp_diff(y.cpu(), ref)
+    frac = float((d != 0).mean())
+    print(f"[rmsnorm {rows}x{cols}] max ulp diff {d.max()}, non-identical {frac:.2e}", flush=True)
+    assert d.max() <= 1 and frac <= 1e-3
+    xf = x.double()
+    ref_r = 1.0 / torch.sqrt(xf.pow(2).mean(-1) + 1e-6)
+    torch.testing.assert_close(rstd.cpu().double(), ref_r, rtol=3e-7, atol=0)
+    assert parts.numel() == ops.rmsnorm_partials_count(rows)
+    amax_bits = int(parts.max().item())
+    yabs = y.float().abs().max()
+    assert amax_bits == int(yabs.view(torch.int32).item())
+
+
+@pytest.mark.parametrize("rows,cols", [(160, 256), (333, 2560), (2048, 2560)])
+def test_cast_from_norm_partials_equals_quantize(gpu, rows, cols):
+    x, w = _inputs(rows, cols, 5 + rows)
+    y, _, parts = ops.rmsnorm(x.to(gpu), w.to(gpu), 1e-6)
+    for transpose in (False, True):
+        fused = ops.cast_partials(y, parts, ops.E4M3, rowwise=True, transpose=transpose)
+        plain = ops.quantize(y, ops.E4M3, rowwise=True, transpose=transpose)
+        torch.cuda.synchronize()
+        assert torch.equal(fused.meta.cpu(), plain.meta.cpu())
+        assert torch.equal(fused.data.cpu(), plain.data.cpu())
+        if transpose:
+            assert torch.equal(fused.data_t.cpu(), plain.data_t.cpu())
+
+
+def test_rmsnorm_plain_gamma_and_errors(gpu):
+    x, w = _inputs(96, 512, 11, gamma_std=1.0)
+    y, _, _ = ops.rmsnorm(x.to(gpu), w.to(gpu), 1e-5, zero_centered=False)
+    torch.cuda.synchronize()
+    xf = x.float()
+    ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * w.float()).to(torch.bfloat16)
+    d = _ulp_diff(y.cpu(), ref)
+    assert d.max() <= 1 and float((d != 0).mean()) <= 1e-3
+    y0, _, p0 = ops.rmsnorm(torch.empty(0, 512, dtype=torch.bfloat16, device=gpu), w.to(gpu), 1e-6)
+    assert y0.shape == (0, 512)
+    with pytest.raises(Exception, match="cols"):
+        ops.rmsnorm(torch.zeros(4, 12, dtype=torch.bfloat16, device=gpu),
+                    torch.zeros(12, dtype=torch.bfloat16, device=gpu), 1e-6)
+    with pytest.raises(Exception, match="cols"):
+        ops.rmsnorm(torch.zeros(4, 8192, dtype=torch.bfloat16, device=gpu),
+                    torch.zeros(8192, dtype=torch.bfloat16, device=gpu), 1e-6)
