@@ -27,6 +27,10 @@ the same for the H cast against HBM bandwidth.
       (weights + activations + outputs) against peak as well as TFLOP/s
   c5  FP8 training step of the c2 MLP at M = 8192 (forward + backward, grad_out e5m2),
       delayed scaling with an amax history of 16 on every tensor role
+and two entries beyond the BASELINE configurations:
+  fused_norm  FusedMLP's RMSNorm -> e4m3 fc1 input at [8192, 2560], fused kernel vs torch
+  c1_rowwise  c1 under torchao's 'rowwise' recipe (per-row power-of-2 scales), and the
+              per-row + per-column quantization of [8192, 2560]
 
 ``cpu_baseline`` times the CPU oracle (torch CPU: amax, clamp, .to(float8), fp32 matmul,
 bf16 gelu chain -- torchao's emulate path) on the same c2 step, on this host's cores.
@@ -216,6 +220,7 @@ def main():
             "c4": _bench_c4(torch, ops, workloads, dev),
             "c5": _bench_c5(torch, workloads, dev),
             "fused_norm": _bench_norm(torch, ops, workloads, dev),
+            "c1_rowwise": _bench_c1_rowwise(torch, ops, workloads, dev),
         }
 
     cpu = None
@@ -409,6 +414,38 @@ def _bench_c5(torch, workloads, dev, steps=10):
                         "weights re-quantized every step",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
             "frac_of_fp8_peak": round(flop / s / 1e12 / FP8_PEAK_TFLOPS, 4)}
+
+
+def _bench_c1_rowwise(torch, ops, workloads, dev, steps=50):
+    """c1 under torchao's 'rowwise' recipe: per-row power-of-2 scales for X and W, the GEMM
+    with a scale vector on each side; plus the per-column (transposed) quantization of the
+    c5 activation [8192, 2560] that the recipe's wgrad needs."""
+    c = workloads.config1()
+    x, w = c["x"].to(dev), c["w"].to(dev)
+    M, K = x.shape
+    N = w.shape[0]
+
+    def step():
+        xq = ops.quantize_axiswise(x, ops.E4M3)
+        wq = ops.quantize_axiswise(w, ops.E4M3)
+        return ops.gemm_axiswise(xq.data, 0, xq.row_sinv, wq.data, 0, wq.row_sinv)
+
+    s = _timed(torch, step, steps, 5)
+    xq, wq = ops.quantize_axiswise(x, ops.E4M3), ops.quantize_axiswise(w, ops.E4M3)
+    gs = _ev_time(torch, lambda: ops.gemm_axiswise(xq.data, 0, xq.row_sinv, wq.data, 0,
+                                                   wq.row_sinv), steps)
+    flop = 2.0 * M * N * K
+    a = workloads.config5()["x"].to(dev)
+    R, C = a.shape
+    both = _ev_time(torch, lambda: ops.quantize_axiswise(a, ops.E4M3, colwise=True), steps)
+    rows_only = _ev_time(torch, lambda: ops.quantize_axiswise(a, ops.E4M3), steps)
+    return {"workload": f"linear [{M},{K}] x [{N},{K}]^T, axiswise (rowwise recipe) per call",
+            "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
+            "gemm_us": round(gs * 1e6, 2), "gemm_tflops": round(flop / gs / 1e12, 1),
+            "quantize_rows_8192x2560_us": round(rows_only * 1e6, 2),
+            "quantize_rows_gbps": round(3.0 * R * C / rows_only / 1e9, 1),
+            "quantize_rows_and_cols_8192x2560_us": round(both * 1e6, 2),
+            "quantize_rows_and_cols_gbps": round(4.0 * R * C / both / 1e9, 1)}
 
 
 def _bench_norm(torch, ops, workloads, dev, steps=50):

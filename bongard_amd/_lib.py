@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -41,6 +41,12 @@ SIGNATURES = {
     "bf8_cast_delayed_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int, c_int,
                                       c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p]),
+    "bf8_axiswise_workspace": (c_size_t, [c_int64, c_int64]),
+    "bf8_quantize_axiswise_bf16": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
+                                           c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "bf8_gemm_axiswise": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_int, c_int64, c_int64,
+                                  c_int64, c_int64, c_void_p, c_int, c_void_p, c_int, c_void_p,
+                                  c_void_p, c_int, c_int64, c_void_p, c_size_t, c_void_p]),
     "bf8_rmsnorm_partials": (c_int64, [c_int64]),
     "bf8_rmsnorm_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_float, c_int,
                                  c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -185,23 +185,34 @@ __device__ __forceinline__ void gelu_tanh_fwd_bwd(float x, float& y, float& dydx
   dydx = s + 2.0f * x * (s * s * e) * du;
 }
 
-// ---- per-tensor scale from block partials, finished by the last block ---------------
-// meta = {amax, scale, scale_inv, 0}: scale = fp32(fp8_max / max(f64(amax), 1e-12))
-// (f64 division, correctly rounded, then one rounding to fp32: equal to the correctly
-// rounded fp32 quotient since 53 >= 2 * 24 + 2); a NaN amax gives its quietened NaN.
-__device__ inline void write_meta_from_amax(uint32_t key, float fp8_max, float* meta) {
+// ---- scale from an amax key --------------------------------------------------------
+// scale = fp32(fp8_max / max(f64(amax), 1e-12)) (f64 division, correctly rounded, then one
+// rounding to fp32: equal to the correctly rounded fp32 quotient since 53 >= 2 * 24 + 2);
+// a NaN amax gives its quietened NaN. pow2 rounds the scale down to a power of two by
+// clearing its mantissa (torchao round_scales_to_power_of_2; 0 and inf stay as they are).
+// scale_inv = fp32(1 / scale), correctly rounded (exact for a power of two).
+__device__ inline void scale_from_amax_key(uint32_t key, float fp8_max, bool pow2, float& scale,
+                                           float& scale_inv) {
   const float amax = __uint_as_float(key);
-  float scale, scale_inv;
   if (amax != amax) {
     scale = __uint_as_float(key | 0x00400000u);
     scale_inv = scale;
-  } else {
-    double a = (double)amax;
-    if (a < 1e-12) a = 1e-12;
-    scale = (float)((double)fp8_max / a);
-    scale_inv = (float)(1.0 / (double)scale);
+    return;
   }
-  meta[0] = amax;
+  double a = (double)amax;
+  if (a < 1e-12) a = 1e-12;
+  scale = (float)((double)fp8_max / a);
+  if (pow2) scale = __uint_as_float(__float_as_uint(scale) & 0xFF800000u);
+  scale_inv = (float)(1.0 / (double)scale);
+}
+
+// ---- per-tensor scale from block partials, finished by the last block ---------------
+// meta = {amax, scale, scale_inv, 0} (scale_from_amax_key).
+__device__ inline void write_meta_from_amax(uint32_t key, float fp8_max, float* meta,
+                                            bool pow2 = false) {
+  float scale, scale_inv;
+  scale_from_amax_key(key, fp8_max, pow2, scale, scale_inv);
+  meta[0] = __uint_as_float(key);
   meta[1] = scale;
   meta[2] = scale_inv;
   meta[3] = 0.0f;
@@ -213,14 +224,15 @@ __device__ inline void write_meta_from_amax(uint32_t key, float fp8_max, float* 
 template <int NT>
 __device__ inline float scale_from_partials_block(const uint32_t* __restrict__ partials,
                                                   int64_t np, float fp8_max,
-                                                  float* __restrict__ meta_out) {
+                                                  float* __restrict__ meta_out,
+                                                  bool pow2 = false) {
   __shared__ float s_scale;
   uint32_t m = 0;
   for (int64_t i = threadIdx.x; i < np; i += NT) m = max(m, partials[i]);
   m = block_max_u32<NT>(m);
   if (threadIdx.x == 0) {
     float meta[4];
-    write_meta_from_amax(m, fp8_max, meta);
+    write_meta_from_amax(m, fp8_max, meta, pow2);
     s_scale = meta[1];
     if (meta_out && blockIdx.x == 0 && blockIdx.y == 0) {
       meta_out[0] = meta[0];

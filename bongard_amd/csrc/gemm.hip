@@ -183,10 +183,10 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(
     const float* __restrict__ P, int splits, int64_t stride, int M, int N,
     const float* __restrict__ a_sinv, const float* __restrict__ b_sinv, int b_stride,
     int n_seg, SegEnds seg_end, const uint16_t* __restrict__ bias, void* __restrict__ C,
-    int64_t ldc) {
+    int64_t ldc, int a_vec, int b_vec) {
   const int n8 = N >> 3;
   const int64_t total = (int64_t)M * n8;
-  const float sa = *a_sinv;
+  const float sa = a_vec ? 0.0f : *a_sinv;
   for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < total;
        g += (int64_t)gridDim.x * 256) {
     const int m = (int)(g / n8), n = (int)(g % n8) * 8;
@@ -210,12 +210,25 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(
       int seg = 0;
 #pragma unroll
       for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < n_seg && nh >= seg_end.e[s2]) ? 1 : 0;
-      const float alpha = sa * b_sinv[seg * b_stride];
       float b4[4] = {0.f, 0.f, 0.f, 0.f};
       if (bias) {
         const uint2 bb = *reinterpret_cast<const uint2*>(bias + nh);
         b4[0] = bf16_lo(bb.x); b4[1] = bf16_hi(bb.x); b4[2] = bf16_lo(bb.y); b4[3] = bf16_hi(bb.y);
       }
+      if (a_vec | b_vec) {  // axiswise: (a_sinv[m] or a_sinv[0]) * (b_sinv[n] or b_sinv[0])
+        const float ra = a_vec ? a_sinv[m] : *a_sinv;
+        float cf[4];
+        if (b_vec) {
+          const float4 f = *reinterpret_cast<const float4*>(b_sinv + nh);
+          cf[0] = f.x; cf[1] = f.y; cf[2] = f.z; cf[3] = f.w;
+        } else {
+          cf[0] = cf[1] = cf[2] = cf[3] = *b_sinv;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] * (ra * cf[e]) + b4[e];
+        continue;
+      }
+      const float alpha = sa * b_sinv[seg * b_stride];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] * alpha + b4[e];
     }
@@ -263,31 +276,19 @@ int launch_plan(const Plan& pl, GemmParams p, int epi, int out_dtype, int fa, in
   if (out_dtype == BF8_OUT_BF16)
     hipLaunchKernelGGL(split_reduce_kernel<BF8_OUT_BF16>, dim3(blocks), dim3(256), 0, s,
                        (const float*)ws, pl.splits, q.split_stride, p.M, p.N, p.a_sinv, p.b_sinv,
-                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc);
+                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc, p.a_vec, p.b_vec);
   else
     hipLaunchKernelGGL(split_reduce_kernel<BF8_OUT_F32>, dim3(blocks), dim3(256), 0, s,
                        (const float*)ws, pl.splits, q.split_stride, p.M, p.N, p.a_sinv, p.b_sinv,
-                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc);
+                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc, p.a_vec, p.b_vec);
   return launch_status("split_reduce_kernel");
 }
 
-}  // namespace
-}  // namespace bf8
-
-using namespace bf8;
-
-extern "C" {
-
-size_t bf8_gemm_workspace(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return choose_plan(M, N, K, false, (size_t)-1).ws_bytes;
-}
-
-int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt_b, int64_t ldb,
-             int64_t M, int64_t N, int64_t K, const float* a_scale_inv,
-             const float* b_scale_inv, int b_scale_stride, const int64_t* seg_ends, int n_seg,
-             const void* bias, void* C, int out_dtype, int64_t ldc, void* ws, size_t ws_bytes,
-             void* stream) {
+int gemm_entry(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt_b, int64_t ldb,
+               int64_t M, int64_t N, int64_t K, const float* a_scale_inv, int a_vec,
+               const float* b_scale_inv, int b_vec, int b_scale_stride, const int64_t* seg_ends,
+               int n_seg, const void* bias, void* C, int out_dtype, int64_t ldc, void* ws,
+               size_t ws_bytes, void* stream) {
   BF8_CHECK((fmt_a == BF8_E4M3 || fmt_a == BF8_E5M2) && (fmt_b == BF8_E4M3 || fmt_b == BF8_E5M2),
             "bf8_gemm: bad formats %d/%d", fmt_a, fmt_b);
   BF8_CHECK(out_dtype == BF8_OUT_BF16 || out_dtype == BF8_OUT_F32, "bf8_gemm: bad out_dtype");
@@ -311,6 +312,7 @@ int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt
   p.A = A; p.B = B; p.lda = lda; p.ldb = ldb;
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.I = 0;
   p.a_sinv = a_scale_inv; p.b_sinv = b_scale_inv; p.b_stride = b_scale_stride;
+  p.a_vec = a_vec; p.b_vec = b_vec;
   p.n_seg = n_seg;
   for (int s = 0; s < 4; ++s) p.seg_end[s] = (int)N;
   if (n_seg > 1) {
@@ -325,6 +327,40 @@ int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt
   const Plan pl = choose_plan(M, N, K, false, ws ? ws_bytes : 0);
   return launch_plan(pl, p, EPI_LINEAR, out_dtype, fmt_a, fmt_b, ws, as_stream(stream));
 }
+
+}  // namespace
+}  // namespace bf8
+
+using namespace bf8;
+
+extern "C" {
+
+size_t bf8_gemm_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return choose_plan(M, N, K, false, (size_t)-1).ws_bytes;
+}
+
+int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt_b, int64_t ldb,
+             int64_t M, int64_t N, int64_t K, const float* a_scale_inv,
+             const float* b_scale_inv, int b_scale_stride, const int64_t* seg_ends, int n_seg,
+             const void* bias, void* C, int out_dtype, int64_t ldc, void* ws, size_t ws_bytes,
+             void* stream) {
+  return gemm_entry(A, fmt_a, lda, B, fmt_b, ldb, M, N, K, a_scale_inv, 0, b_scale_inv, 0,
+                    b_scale_stride, seg_ends, n_seg, bias, C, out_dtype, ldc, ws, ws_bytes, stream);
+}
+
+int bf8_gemm_axiswise(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt_b,
+                      int64_t ldb, int64_t M, int64_t N, int64_t K, const float* a_scale_inv,
+                      int a_vec, const float* b_scale_inv, int b_vec, const void* bias, void* C,
+                      int out_dtype, int64_t ldc, void* ws, size_t ws_bytes, void* stream) {
+  BF8_CHECK((a_vec == 0 || a_vec == 1) && (b_vec == 0 || b_vec == 1),
+            "bf8_gemm_axiswise: a_vec and b_vec must be 0 or 1");
+  BF8_CHECK(!b_vec || ((uintptr_t)b_scale_inv & 15) == 0,
+            "bf8_gemm_axiswise: a per-column b_scale_inv must be 16-byte aligned");
+  return gemm_entry(A, fmt_a, lda, B, fmt_b, ldb, M, N, K, a_scale_inv, a_vec, b_scale_inv,
+                    b_vec, 0, nullptr, 1, bias, C, out_dtype, ldc, ws, ws_bytes, stream);
+}
+
 
 int64_t bf8_geglu_partials(int64_t M, int64_t I) {
   if (M <= 0 || I <= 0) return 0;

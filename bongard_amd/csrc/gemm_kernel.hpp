@@ -18,8 +18,9 @@ struct GemmParams {
   int tiles_m, tiles_n;  // output tiles
   int splits;            // K splits per output tile (LINEAR only; 1 = none)
   int ksteps_per_split;  // 128-byte K steps per split
-  const float* a_sinv;
-  const float* b_sinv;
+  const float* a_sinv;    // a_vec: one per row of A (M), else a single value
+  const float* b_sinv;    // b_vec: one per row of B (N), else n_seg values b_stride apart
+  int a_vec, b_vec;       // LINEAR only
   int b_stride;
   int n_seg;
   int seg_end[4];

@@ -365,6 +365,24 @@ gemm_kernel(GemmParams p) {
   constexpr int ROWS = FM * 32;  // rows of the wave's output tile
   const int lrow_m = lane & 31;
   const int lcol = (lane >> 5) * 4;
+  // Axiswise scales (a_vec / b_vec): the factor of element (m, n) is a_sinv[m] * b_sinv[n]
+  // (either side a single value when its flag is 0), read here from global memory.
+  const bool vec = EPI == EPI_LINEAR && (p.a_vec | p.b_vec);
+  float rsa[FM];
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int m = m0 + wave_m0 + j * 32 + lrow_m;
+    rsa[j] = (vec && p.a_vec) ? p.a_sinv[m < p.M ? m : p.M - 1] : sa;
+  }
+  auto col_factors = [&](int n, float alpha, float* cf) __attribute__((always_inline)) {
+    if (vec && p.b_vec && n < p.N) {
+      const float4 f = *reinterpret_cast<const float4*>(p.b_sinv + n);
+      cf[0] = f.x; cf[1] = f.y; cf[2] = f.z; cf[3] = f.w;
+    } else {
+      const float b = vec ? (p.b_vec ? 0.0f : sb[0]) : alpha;
+      cf[0] = b; cf[1] = b; cf[2] = b; cf[3] = b;
+    }
+  };
   if constexpr (EPI == EPI_LINEAR && OUT == BF8_OUT_BF16) {
     constexpr int CH = FN * 4;  // 16-byte chunks per staged row (FN*32 bf16)
     uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
@@ -384,6 +402,20 @@ gemm_kernel(GemmParams p) {
           const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
           bias[0] = bf16_lo(bb.x); bias[1] = bf16_hi(bb.x);
           bias[2] = bf16_lo(bb.y); bias[3] = bf16_hi(bb.y);
+        }
+        if (vec) {
+          float cf[4];
+          col_factors(n, alpha, cf);
+#pragma unroll
+          for (int j = 0; j < FM; ++j) {
+            uint2 w;
+            w.x = pack_bf16x2(acc[i][j][4 * q + 0] * (rsa[j] * cf[0]) + bias[0],
+                              acc[i][j][4 * q + 1] * (rsa[j] * cf[1]) + bias[1]);
+            w.y = pack_bf16x2(acc[i][j][4 * q + 2] * (rsa[j] * cf[2]) + bias[2],
+                              acc[i][j][4 * q + 3] * (rsa[j] * cf[3]) + bias[3]);
+            stage_put<CH>(wbuf, j * 32 + lrow_m, col, w);
+          }
+          continue;
         }
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
@@ -424,6 +456,22 @@ gemm_kernel(GemmParams p) {
           const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
           bias[0] = bf16_lo(bb.x); bias[1] = bf16_hi(bb.x);
           bias[2] = bf16_lo(bb.y); bias[3] = bf16_hi(bb.y);
+        }
+        if (vec && !raw) {
+          float cf[4];
+          col_factors(n, alpha, cf);
+#pragma unroll
+          for (int j = 0; j < FM; ++j) {
+            const int m = m0 + wave_m0 + j * 32 + lrow_m;
+            if (m >= p.M) continue;
+            float* c = cbase + (int64_t)m * p.ldc + n;
+            *reinterpret_cast<float4*>(c) = make_float4(
+                acc[i][j][4 * q + 0] * (rsa[j] * cf[0]) + bias[0],
+                acc[i][j][4 * q + 1] * (rsa[j] * cf[1]) + bias[1],
+                acc[i][j][4 * q + 2] * (rsa[j] * cf[2]) + bias[2],
+                acc[i][j][4 * q + 3] * (rsa[j] * cf[3]) + bias[3]);
+          }
+          continue;
         }
 #pragma unroll
         for (int j = 0; j < FM; ++j) {

@@ -99,17 +99,19 @@ __global__ __launch_bounds__(kNT) void amax_partials_kernel(const uint16_t* __re
 }
 
 __global__ __launch_bounds__(kNT) void scale_from_partials_kernel(
-    const uint32_t* __restrict__ partials, int64_t np, float fp8_max, float* __restrict__ meta) {
+    const uint32_t* __restrict__ partials, int64_t np, float fp8_max, int pow2,
+    float* __restrict__ meta) {
   uint32_t m = 0;
   for (int64_t i = threadIdx.x; i < np; i += kNT) m = max(m, partials[i]);
   m = block_max_u32<kNT>(m);
-  if (threadIdx.x == 0) write_meta_from_amax(m, fp8_max, meta);
+  if (threadIdx.x == 0) write_meta_from_amax(m, fp8_max, meta, pow2 != 0);
 }
 
 // Where a cast kernel takes its scale from (exactly one source):
 //  - `scale`: a device fp32 scalar;
 //  - current scaling: `partials` (np amax partials of x or of its producer), reduced in
-//    every block; block 0 publishes meta_out = {amax, scale, scale_inv, 0};
+//    every block; block 0 publishes meta_out = {amax, scale, scale_inv, 0}; `pow2` rounds
+//    that scale down to a power of two;
 //  - delayed scaling: `state` (amax history [len] + meta), which first absorbs the
 //    previous step's amax (`prev`, n_prev partials; none on the first step) at slot pos;
 //    block 0 copies this step's meta to meta_out (if not NULL).
@@ -122,6 +124,7 @@ struct ScaleSrc {
   int len, pos;
   const uint32_t* prev;
   int64_t n_prev;
+  int pow2;
 };
 
 template <int FMT>
@@ -130,7 +133,8 @@ __device__ __forceinline__ float resolve_scale(const ScaleSrc& s) {
   if (s.state)
     return delayed_scale_block<kNT>(s.state, s.len, s.pos, s.prev, s.n_prev, Fp8Max<FMT>::value,
                                     s.meta_out);
-  return scale_from_partials_block<kNT>(s.partials, s.np, Fp8Max<FMT>::value, s.meta_out);
+  return scale_from_partials_block<kNT>(s.partials, s.np, Fp8Max<FMT>::value, s.meta_out,
+                                        s.pow2 != 0);
 }
 
 // Block max of the lanes' amax keys, stored as this block's partial (amax_out != NULL).
@@ -321,6 +325,8 @@ __global__ __launch_bounds__(kNT) void fold_amax_kernel(float* state, int len, i
 int launch_cast(const void* x, int64_t rows, int64_t cols, ScaleSrc src, int fmt,
                 uint8_t* out, uint8_t* out_t, uint32_t* amax_out, void* stream, const char* who) {
   BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "%s: bad fmt %d", who, fmt);
+  BF8_CHECK(!src.pow2 || (src.partials && !src.state), "%s: BF8_SCALE_POW2 needs current scaling",
+            who);
   BF8_CHECK(rows >= 0 && cols >= 0, "%s: negative shape", who);
   BF8_CHECK(out || out_t, "%s: out and out_t are both NULL", who);
   BF8_CHECK(((uintptr_t)x & 15) == 0 && (!out || ((uintptr_t)out & 15) == 0),
@@ -333,7 +339,7 @@ int launch_cast(const void* x, int64_t rows, int64_t cols, ScaleSrc src, int fmt
     // current scaling from many partials: meta first, then a cast with its scale
     float* meta = src.meta_out;
     hipLaunchKernelGGL(scale_from_partials_kernel, dim3(1), dim3(kNT), 0, s, src.partials,
-                       src.np, fp8_max_host(fmt), meta);
+                       src.np, fp8_max_host(fmt), src.pow2, meta);
     const int rc = launch_status("scale_from_partials_kernel");
     if (rc != BF8_OK) return rc;
     src = ScaleSrc{};
@@ -393,7 +399,7 @@ using namespace bf8;
 extern "C" {
 
 const char* bf8_last_error(void) { return bf8::g_err; }
-int bf8_abi_version(void) { return 5; }
+int bf8_abi_version(void) { return 6; }
 
 int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
 
@@ -410,11 +416,13 @@ int bf8_amax_bf16(const void* x, int64_t n, uint32_t* partials, void* stream) {
 
 int bf8_scale_from_partials(const uint32_t* partials, int64_t n_partials, int fmt, float* meta,
                             void* stream) {
+  const int pow2 = (fmt & BF8_SCALE_POW2) ? 1 : 0;
+  fmt &= ~BF8_SCALE_POW2;
   BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "bf8_scale_from_partials: bad fmt %d", fmt);
   BF8_CHECK(partials && meta, "bf8_scale_from_partials: NULL pointer");
   BF8_CHECK(n_partials >= 1, "bf8_scale_from_partials: n_partials < 1");
   hipLaunchKernelGGL(scale_from_partials_kernel, dim3(1), dim3(kNT), 0, as_stream(stream),
-                     partials, n_partials, fp8_max_host(fmt), meta);
+                     partials, n_partials, fp8_max_host(fmt), pow2, meta);
   return launch_status("scale_from_partials_kernel");
 }
 
@@ -429,8 +437,10 @@ int bf8_cast_partials_bf16(const void* x, int64_t rows, int64_t cols, const uint
                            int64_t n_partials, int fmt, float* meta, uint8_t* out,
                            uint8_t* out_t, void* stream) {
   BF8_CHECK(partials && meta && n_partials >= 1, "bf8_cast_partials_bf16: bad partials or meta");
-  return launch_cast(x, rows, cols, current_scale(partials, n_partials, meta), fmt, out, out_t,
-                     nullptr, stream, "bf8_cast_partials_bf16");
+  ScaleSrc src = current_scale(partials, n_partials, meta);
+  src.pow2 = (fmt & BF8_SCALE_POW2) ? 1 : 0;
+  return launch_cast(x, rows, cols, src, fmt & ~BF8_SCALE_POW2, out, out_t, nullptr, stream,
+                     "bf8_cast_partials_bf16");
 }
 
 int64_t bf8_cast_amax_partials(int64_t rows, int64_t cols, int transpose) {
@@ -460,6 +470,8 @@ int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* stat
 int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
                       uint8_t* out_t, float* meta, uint32_t* partials, void* stream) {
   BF8_CHECK(rows >= 0 && cols >= 0, "bf8_quantize_bf16: negative shape");
+  BF8_CHECK((fmt & ~BF8_SCALE_POW2) == BF8_E4M3 || (fmt & ~BF8_SCALE_POW2) == BF8_E5M2,
+            "bf8_quantize_bf16: bad fmt %d", fmt);
   const int64_t n = rows * cols;
   int rc = bf8_amax_bf16(x, n, partials, stream);
   if (rc) return rc;

@@ -3,15 +3,16 @@
 Drop-in for bongard/float8_training.py (torchao Float8Linear path): same ``RECIPES``,
 ``enable_float8(model, recipe, *, emulate=False) -> int`` with the same module filter and
 errors, and ``TrainingLinear`` with BF16 ``F.linear`` in eval. In training the linear runs
-on the gfx950 FP8 kernels (bongard_amd.linear.Fp8LinearFunction) with torchao's
-tensorwise semantics: dynamic per-tensor e4m3 for X and W, e5m2 for grad_out.
+on the gfx950 FP8 kernels with torchao 0.17.0's recipe semantics:
+  * ``tensorwise`` (bongard_amd.linear.Fp8LinearFunction): dynamic per-tensor e4m3 for X
+    and W, e5m2 for grad_out;
+  * ``rowwise`` / ``rowwise_with_gw_hp`` (bongard_amd.linear.Fp8LinearAxiswiseFunction):
+    axiswise e4m3 casts of X, W and grad_out with power-of-2 scales; the second keeps the
+    weight gradient in bf16 and quantizes W tensorwise for the input gradient.
 
-Differences from the reference, by design:
-  * ``rowwise`` / ``rowwise_with_gw_hp`` (axiswise scales) are accepted by name but raise
-    NotImplementedError on conversion; only ``tensorwise`` has kernels.
-  * ``emulate=True`` skips the device check so modules can be converted (and their state
-    dicts inspected) on a CPU, but a training forward still needs the gfx950 device: the
-    product path has no CPU emulation.
+Difference from the reference, by design: ``emulate=True`` skips the device check so
+modules can be converted (and their state dicts inspected) on a CPU, but a training
+forward still needs the gfx950 device: the product path has no CPU emulation.
 """
 
 from dataclasses import dataclass, replace
@@ -79,7 +80,10 @@ class Float8Linear(torch.nn.Linear):
             flat = F.pad(flat, (0, 0, 0, aligned - length))
         weight = self.weight if self.weight.dtype == torch.bfloat16 else self.weight.to(torch.bfloat16)
         bias = None if self.bias is None else self.bias.to(torch.bfloat16)
-        out = _linear.Fp8LinearFunction.apply(flat, weight, bias, None)
+        if self.config.recipe == "tensorwise":
+            out = _linear.Fp8LinearFunction.apply(flat, weight, bias, None)
+        else:
+            out = _linear.Fp8LinearAxiswiseFunction.apply(flat, weight, bias, self.config.recipe)
         if aligned != length:
             out = out[:length]
         return out.reshape(*shape[:-1], out.shape[-1])
@@ -122,9 +126,6 @@ def enable_float8(model, recipe, *, emulate=False):
     device = next(model.parameters()).device if not hasattr(model, "device") else model.device
     if not emulate and not _is_gfx950(device):
         raise ValueError("FP8 training requires an MI355X (gfx950) GPU")
-    if recipe != "tensorwise":
-        raise NotImplementedError(
-            f"fp8 recipe {recipe!r} (axiswise scaling) has no gfx950 kernels yet; use 'tensorwise'")
     # Token counts vary per request, so the wgrad GEMM's reduction dim gets padded.
     config = replace(Float8LinearConfig.from_recipe_name(recipe), emulate=emulate,
                      pad_inner_dim=True)

@@ -97,6 +97,70 @@ class Fp8LinearFunction(torch.autograd.Function):
         return dx, dw, db, None, None
 
 
+AXISWISE_RECIPES = ("rowwise", "rowwise_with_gw_hp")
+
+
+class Fp8LinearAxiswiseFunction(torch.autograd.Function):
+    """y = x @ W^T (+ b) under torchao's axiswise recipes; x: bf16 [M, K], M % 16 == 0 when
+    grads are needed. Every cast is e4m3 with power-of-2 scales (torchao 0.17.0
+    Float8LinearConfig.from_recipe_name, round_scales_to_power_of_2=True):
+
+      forward              y  = X8[per row] . W8[per row]^T
+      rowwise              dX = dY8[per row] . W8[per column of W]
+                           dW = dY8[per column]^T . X8[per column]
+      rowwise_with_gw_hp   dX = dY8[per row] . W8[tensorwise]
+                           dW = dY^T . X in bf16 (torch.mm, the high-precision wgrad)
+
+    "per column" quantizations are stored transposed (the reduction dim contiguous), so
+    every FP8 GEMM is the same TN kernel with a scale vector on either side.
+    Reference: torchao matmul_with_hp_or_float8_args.forward/backward under
+    TrainingLinear.forward (bongard/float8_training.py:16-22) for the recipes at :9.
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, recipe):
+        if recipe not in AXISWISE_RECIPES:
+            raise ValueError(f"axiswise recipe must be one of {AXISWISE_RECIPES}")
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        hp_wgrad = recipe == "rowwise_with_gw_hp"
+        xq = ops.quantize_axiswise(x, E4M3, rowwise=True, colwise=need_dw and not hp_wgrad)
+        wq = ops.quantize_axiswise(weight.detach(), E4M3, rowwise=True,
+                                   colwise=need_dx and not hp_wgrad)
+        y = ops.gemm_axiswise(xq.data, E4M3, xq.row_sinv, wq.data, E4M3, wq.row_sinv, bias=bias)
+        ctx.recipe = recipe
+        ctx.has_bias = bias is not None
+        if hp_wgrad:
+            ctx.save_for_backward(x if need_dw else None, weight.detach() if need_dx else None)
+        else:
+            ctx.save_for_backward(xq.data_t, xq.col_sinv, wq.data_t, wq.col_sinv)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dy = dy.contiguous()
+        dx = dw = db = None
+        if ctx.recipe == "rowwise":
+            x8t, x_cs, w8t, w_cs = ctx.saved_tensors
+            dyq = ops.quantize_axiswise(dy, E4M3, rowwise=need_dx, colwise=need_dw)
+            if need_dx:
+                dx = ops.gemm_axiswise(dyq.data, E4M3, dyq.row_sinv, w8t, E4M3, w_cs)
+            if need_dw:
+                dw = ops.gemm_axiswise(dyq.data_t, E4M3, dyq.col_sinv, x8t, E4M3, x_cs)
+        else:
+            x, weight = ctx.saved_tensors
+            if need_dx:
+                dyq = ops.quantize_axiswise(dy, E4M3, rowwise=True)
+                wt = ops.quantize(weight, E4M3, rowwise=False, transpose=True, pow2=True)
+                dx = ops.gemm_axiswise(dyq.data, E4M3, dyq.row_sinv, wt.data_t, E4M3,
+                                       wt.meta[2:3])
+            if need_dw:
+                dw = torch.mm(dy.t().contiguous(), x)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = dy.sum(0)
+        return dx, dw, db, None
+
+
 class Fp8GegluMlpFunction(torch.autograd.Function):
     """y = down(gelu_tanh(x Wg^T) * (x Wu^T)) with every GEMM in FP8.
 

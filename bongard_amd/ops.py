@@ -26,6 +26,7 @@ FP8_MAX = {E4M3: 448.0, E5M2: 57344.0}
 TORCH_FP8 = {E4M3: torch.float8_e4m3fn, E5M2: torch.float8_e5m2}
 OUT_BF16 = 0
 OUT_F32 = 1
+SCALE_POW2 = 0x10  # OR'ed into fmt: round the scale down to a power of two
 
 
 @dataclass
@@ -115,11 +116,13 @@ def gemm_workspace(nbytes, device):
     return buf
 
 
-def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None, out_t=None):
+def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None, out_t=None,
+             pow2=False):
     """Current-scaling quantization of a bf16 tensor (flattened to 2-D [rows, cols]).
 
     Returns an :class:`Fp8Tensor` whose ``data`` is [rows, cols] (if ``rowwise``) and
-    ``data_t`` [cols, rows] (if ``transpose``), both as torch float8 tensors.
+    ``data_t`` [cols, rows] (if ``transpose``), both as torch float8 tensors. ``pow2``
+    rounds the scale down to a power of two (torchao round_scales_to_power_of_2).
     """
     _require_gpu(x)
     x = _bf16_2d(x)
@@ -133,7 +136,8 @@ def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None,
         out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=dev)
     L = _lib.lib()
     parts = partials_buffer(L.bf8_amax_partials(rows * cols), dev)
-    _lib.check(L.bf8_quantize_bf16(_ptr(x), rows, cols, fmt, _ptr(out if rowwise else None),
+    _lib.check(L.bf8_quantize_bf16(_ptr(x), rows, cols, fmt | (SCALE_POW2 if pow2 else 0),
+                                   _ptr(out if rowwise else None),
                                    _ptr(out_t if transpose else None), _ptr(meta),
                                    _ptr(parts), _stream(dev)), "bf8_quantize_bf16")
     return Fp8Tensor(out if rowwise else None, out_t if transpose else None, meta, fmt, rows, cols)
@@ -229,6 +233,99 @@ def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=N
                           _sinv_ptr(a_meta), _sinv_ptr(b_meta), b_meta_stride, seg, n_seg,
                           _ptr(bias), _ptr(out), OUT_BF16 if out_dtype == torch.bfloat16 else OUT_F32,
                           out.stride(0), _ptr(ws), ws_bytes, _stream(a.device)), "bf8_gemm")
+    return out
+
+
+@dataclass
+class AxisFp8Tensor:
+    """An axiswise-scaled FP8 tensor (torchao AXISWISE granularity) of x [rows, cols]:
+    ``data`` [rows, cols] with one scale per row (``row_sinv`` fp32 [rows], the inverse
+    scales) and/or ``data_t`` [cols, rows] with one scale per column of x (``col_sinv``
+    fp32 [cols])."""
+
+    data: Optional[torch.Tensor]
+    row_sinv: Optional[torch.Tensor]
+    data_t: Optional[torch.Tensor]
+    col_sinv: Optional[torch.Tensor]
+    fmt: int
+    rows: int
+    cols: int
+
+
+_AXIS_WS = {}
+
+
+def quantize_axiswise(x, fmt=E4M3, *, rowwise=True, colwise=False, pow2=True):
+    """Per-row (``rowwise``, torchao axiswise_dim=-1) and/or per-column (``colwise``,
+    axiswise_dim=0, stored transposed) quantization of a bf16 tensor; ``pow2`` rounds the
+    scales down to powers of two as torchao's rowwise recipes do."""
+    _require_gpu(x)
+    x = _bf16_2d(x)
+    rows, cols = x.shape
+    dev = x.device
+    if not (rowwise or colwise):
+        raise ValueError("quantize_axiswise: nothing requested")
+    out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=dev) if rowwise else None
+    rs = torch.empty(rows, dtype=torch.float32, device=dev) if rowwise else None
+    out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=dev) if colwise else None
+    cs = torch.empty(cols, dtype=torch.float32, device=dev) if colwise else None
+    L = _lib.lib()
+    ws, nbytes = None, 0
+    if colwise:
+        nbytes = int(L.bf8_axiswise_workspace(rows, cols))
+        key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+        ws = _AXIS_WS.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+            _AXIS_WS[key] = ws
+        nbytes = ws.numel()
+    _lib.check(L.bf8_quantize_axiswise_bf16(_ptr(x), rows, cols, fmt | (SCALE_POW2 if pow2 else 0),
+                                            _ptr(out), _ptr(rs), _ptr(out_t), _ptr(cs), _ptr(ws),
+                                            nbytes, _stream(dev)), "bf8_quantize_axiswise_bf16")
+    return AxisFp8Tensor(out, rs, out_t, cs, fmt, rows, cols)
+
+
+def gemm_axiswise(a, a_fmt, a_sinv, b, b_fmt, b_sinv, *, out_dtype=torch.bfloat16, bias=None,
+                  out=None):
+    """``C[m, n] = (a @ b.T)[m, n] * a_sinv[m] * b_sinv[n] (+ bias[n])`` on fp8 operands.
+
+    a: fp8 [M, K], b: fp8 [N, K]. ``a_sinv`` is fp32 [M] (one inverse scale per row of a)
+    or a single value (1-element tensor, e.g. a meta's ``scale_inv``); likewise ``b_sinv``
+    with [N]."""
+    _require_gpu(a, b, a_sinv, b_sinv)
+    M, K = a.shape
+    N, Kb = b.shape
+    if K != Kb:
+        raise ValueError(f"gemm_axiswise: inner dims differ ({K} vs {Kb})")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("gemm_axiswise: out_dtype must be bfloat16 or float32")
+
+    def vec_flag(sv, n, what):
+        if sv.dtype != torch.float32 or not sv.is_contiguous():
+            raise TypeError(f"gemm_axiswise: {what} must be contiguous float32")
+        if sv.numel() == n and n != 1:
+            return 1
+        if sv.numel() == 1:
+            return 0
+        raise ValueError(f"gemm_axiswise: {what} must have 1 or {n} elements")
+
+    a_vec = vec_flag(a_sinv, M, "a_sinv")
+    b_vec = vec_flag(b_sinv, N, "b_sinv")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    if bias is not None:
+        if bias.dtype != torch.bfloat16:
+            raise TypeError("gemm_axiswise: bias must be bfloat16")
+        bias = bias.contiguous()
+    L = _lib.lib()
+    ws_bytes = int(L.bf8_gemm_workspace(M, N, K))
+    ws = gemm_workspace(ws_bytes, a.device) if ws_bytes else None
+    ws_bytes = ws.numel() if ws is not None else 0
+    _lib.check(L.bf8_gemm_axiswise(_ptr(a), a_fmt, a.stride(0), _ptr(b), b_fmt, b.stride(0), M, N,
+                                   K, _ptr(a_sinv), a_vec, _ptr(b_sinv), b_vec, _ptr(bias),
+                                   _ptr(out), OUT_BF16 if out_dtype == torch.bfloat16 else OUT_F32,
+                                   out.stride(0), _ptr(ws), ws_bytes, _stream(a.device)),
+               "bf8_gemm_axiswise")
     return out
 
 

@@ -33,6 +33,11 @@ extern "C" {
 #endif
 
 enum { BF8_E4M3 = 0, BF8_E5M2 = 1 };
+/* Flag OR'ed into the fmt of a current-scaling entry point (bf8_scale_from_partials,
+ * bf8_cast_partials_bf16, bf8_quantize_bf16, bf8_quantize_axiswise_bf16): the scale is
+ * rounded down to a power of two by clearing its mantissa (torchao
+ * round_scales_to_power_of_2, set by its rowwise recipes). */
+enum { BF8_SCALE_POW2 = 0x10 };
 enum { BF8_OUT_BF16 = 0, BF8_OUT_F32 = 1 };
 enum {
   BF8_OK = 0,
@@ -178,6 +183,37 @@ int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* stat
                           int pos, const uint32_t* prev_partials, int64_t n_prev, int fmt,
                           float* meta_out, uint8_t* out, uint8_t* out_t, uint32_t* partials_out,
                           void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Axiswise (per-row / per-column) quantization, torchao AXISWISE scaling granularity.
+ * Replaces torchao hp_tensor_to_float8_dynamic(x, ..., scaling_granularity=AXISWISE,
+ * axiswise_dim=-1 or 0, round_scales_to_power_of_2) under TrainingLinear.forward
+ * (bongard/float8_training.py:22) for the rowwise recipes (bongard/float8_training.py:9).
+ * x: bf16 [rows, cols] row-major, cols % 16 == 0, cols <= 16384. fmt may carry
+ * BF8_SCALE_POW2 (the rowwise recipes set it).
+ *   out [rows, cols], row_scale_inv [rows]: one scale per row (axiswise_dim -1);
+ *   out_t [cols, rows], col_scale_inv [cols]: one scale per column (axiswise_dim 0),
+ *   stored transposed (row c of out_t = column c of x).
+ * Either pair may be NULL (not both). scale = fp32(fp8_max / max(f64(amax), 1e-12))
+ * (then rounded down to a power of two), scale_inv = fp32(1 / scale).
+ * ws: bf8_axiswise_workspace(rows, cols) bytes, 256-byte aligned, when out_t is given.
+ * ------------------------------------------------------------------------------- */
+size_t bf8_axiswise_workspace(int64_t rows, int64_t cols);
+int bf8_quantize_axiswise_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
+                               float* row_scale_inv, uint8_t* out_t, float* col_scale_inv,
+                               void* ws, size_t ws_bytes, void* stream);
+
+/* FP8 GEMM with axiswise dequant scales, TN like bf8_gemm:
+ *   C[m, n] = (sum_k A[m, k] * B[n, k]) * (a_scale_inv[a_vec ? m : 0] *
+ *             b_scale_inv[b_vec ? n : 0]) (+ bias[n]).
+ * Replaces torch._scaled_mm with row-wise scales (scale_a [M, 1], scale_b [1, N]) as
+ * torchao's addmm_float8_unwrapped issues it for the rowwise recipes (a tensorwise
+ * operand's scale is broadcast along its axis). Shapes, alignment and the split-K
+ * workspace as bf8_gemm; a per-column b_scale_inv is 16-byte aligned. */
+int bf8_gemm_axiswise(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt_b,
+                      int64_t ldb, int64_t M, int64_t N, int64_t K, const float* a_scale_inv,
+                      int a_vec, const float* b_scale_inv, int b_vec, const void* bias, void* C,
+                      int out_dtype, int64_t ldc, void* ws, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * RMSNorm fused with the amax pass of the quantization that follows it.

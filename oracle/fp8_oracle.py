@@ -209,6 +209,79 @@ def scaled_mm(aq, a_scale, a_fmt, bq, b_scale, b_fmt, *, bias=None, precise=True
 
 
 # ---------------------------------------------------------------------------------------
+# axiswise scaling  (torchao AXISWISE granularity: the rowwise recipes,
+# bongard/float8_training.py:9; torchao 0.17.0 float8 config / float8_utils)
+# ---------------------------------------------------------------------------------------
+def round_scale_down_to_power_of_2(scale: torch.Tensor) -> torch.Tensor:
+    """torchao _round_scale_down_to_power_of_2: exp2(floor(log2(scale))) on fp32."""
+    return torch.exp2(torch.floor(torch.log2(scale)))
+
+
+def amax_to_scale_axiswise(amax_f32: torch.Tensor, fmt: int, pow2: bool = True):
+    """torchao amax_to_scale(..., round_scales_to_power_of_2): fp32 scale tensor."""
+    a = amax_f32.to(torch.float64)
+    scale = (FP8_MAX[fmt] / torch.clamp(a, min=EPS)).to(torch.float32)
+    return round_scale_down_to_power_of_2(scale) if pow2 else scale
+
+
+def cast_bcast(x: torch.Tensor, scale: torch.Tensor, fmt: int) -> torch.Tensor:
+    """``cast`` with a scale tensor broadcast against x (same NaN byte conventions)."""
+    xf = x.to(torch.float32)
+    sc = scale.to(torch.float32).expand_as(xf)
+    prod = xf * sc
+    m = FP8_MAX[fmt]
+    q = torch.clamp(prod, -m, m).to(TORCH_FP8[fmt]).view(torch.uint8)
+    nan = torch.isnan(prod)
+    if bool(nan.any()):
+        xsign = xf.view(torch.int32) < 0
+        ssign = sc.view(torch.int32) < 0
+        sign = torch.where(torch.isnan(sc), ssign,
+                           torch.where(torch.isnan(xf), xsign, torch.ones_like(xsign)))
+        q = torch.where(nan, torch.where(sign, 0xFF, 0x7F).to(torch.uint8), q)
+    return q
+
+
+def quantize_axiswise(x: torch.Tensor, fmt: int, dim: int, pow2: bool = True):
+    """torchao hp_tensor_to_float8_dynamic with AXISWISE granularity along ``dim``:
+    amax = max |x| over ``dim`` (keepdim, NaN-propagating), scale per the remaining axis.
+    Returns (q uint8 like x, scale fp32 with a size-1 ``dim``)."""
+    a = x.abs().amax(dim=dim, keepdim=True).to(torch.float32)
+    scale = amax_to_scale_axiswise(a, fmt, pow2)
+    return cast_bcast(x, scale, fmt), scale
+
+
+def linear_fwd_bwd_axiswise(x, w, dy, recipe, *, precise=True):
+    """FP8 linear forward and backward under torchao's ``rowwise`` or ``rowwise_with_gw_hp``
+    recipe (every cast e4m3, power-of-2 axiswise scales):
+
+      y  = X8[dim -1] @ W8[dim -1]^T                      (both recipes)
+      rowwise:            dX = dY8[dim -1] @ W8[dim 0];  dW = dY8[dim 0]^T @ X8[dim 0]
+      rowwise_with_gw_hp: dX = dY8[dim -1] @ W8[tensorwise, pow2];  dW = dY^T @ X in
+                          high precision (bf16 operands, exact sum here)
+    Returns fp32 (y, dx, dw)."""
+    xq, xs = quantize_axiswise(x, E4M3, -1)
+    wq, ws = quantize_axiswise(w, E4M3, -1)
+    y = scaled_mm(xq, xs, E4M3, wq, ws, E4M3, precise=precise)
+    dq, dsc = quantize_axiswise(dy, E4M3, -1)
+    if recipe == "rowwise":
+        wcq, wcs = quantize_axiswise(w, E4M3, 0)            # scale per column k: [1, K]
+        dx = scaled_mm(dq, dsc, E4M3, wcq.t().contiguous(), wcs.t(), E4M3, precise=precise)
+        dcq, dcs = quantize_axiswise(dy, E4M3, 0)            # [1, N]
+        xcq, xcs = quantize_axiswise(x, E4M3, 0)             # [1, K]
+        dw = scaled_mm(dcq.t().contiguous(), dcs.t(), E4M3, xcq.t().contiguous(), xcs.t(),
+                       E4M3, precise=precise)
+    elif recipe == "rowwise_with_gw_hp":
+        a = amax(w)
+        wts = round_scale_down_to_power_of_2(amax_to_scale(a, E4M3)[0])
+        wtq = cast(w, wts, E4M3)
+        dx = scaled_mm(dq, dsc, E4M3, wtq.t().contiguous(), wts, E4M3, precise=precise)
+        dw = (dy.double().t() @ x.double()).to(torch.float32)
+    else:
+        raise ValueError(recipe)
+    return y, dx, dw
+
+
+# ---------------------------------------------------------------------------------------
 # gated GELU chain and its backward  (bongard/te_linear.py:98-103, HF T5Gemma2MLP)
 # ---------------------------------------------------------------------------------------
 def geglu(g_bf16: torch.Tensor, u_bf16: torch.Tensor) -> torch.Tensor:

@@ -226,8 +226,6 @@ def test_enable_float8_errors():
         float8_training.enable_float8(_Model("cpu"), "bogus", emulate=True)
     with pytest.raises(ValueError, match="MI355X"):
         float8_training.enable_float8(_Model("cpu"), "tensorwise")
-    with pytest.raises(NotImplementedError):
-        float8_training.enable_float8(_Model("cpu"), "rowwise", emulate=True)
     model = _Model("cpu")
     for p in model.parameters():
         p.requires_grad_(False)
@@ -239,6 +237,18 @@ def test_enable_float8_errors():
         recipe="tensorwise")
     with pytest.raises(ValueError, match="retain its FP8 recipe"):
         float8_training.enable_float8(model, "tensorwise", emulate=True)
+    # a model converted under one recipe cannot be converted again under another
+    with pytest.raises(ValueError, match="retain its FP8 recipe"):
+        float8_training.enable_float8(model, "rowwise", emulate=True)
+
+
+@pytest.mark.parametrize("recipe", ["rowwise", "rowwise_with_gw_hp"])
+def test_enable_float8_axiswise_recipes_convert(recipe):
+    model = _Model("cpu")
+    assert float8_training.enable_float8(model, recipe, emulate=True) == 3 * 7
+    lin = model.backbone.encoder.text_model.layers[0].self_attn.q_proj
+    assert isinstance(lin, float8_training.TrainingLinear) and lin.config.recipe == recipe
+    assert float8_training.enable_float8(model, recipe, emulate=True) == 3 * 7
 
 
 # ---- delayed scaling recipe ('fp8_delayed') ---------------------------------------------

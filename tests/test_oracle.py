@@ -237,3 +237,108 @@ def test_delayed_quantizer_uses_previous_amaxes():
     assert float(s3) == float(np.float32(448.0 / m))
     _, sw = q("w", xs[2], E5M2)                # roles keep separate histories
     assert float(sw) == 1.0
+
+
+# ---- axiswise scaling (torchao rowwise recipes) -------------------------------------------
+def _pow2_floor(v):
+    """Largest power of two <= v (> 0, finite) from frexp: independent of log2 rounding."""
+    m, e = math.frexp(v)
+    return math.ldexp(0.5, e)
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_pow2_rounding_equals_mantissa_clear_on_all_bf16_amaxes(fmt):
+    """torchao's exp2(floor(log2(scale))) is, on every scale a bf16 amax can produce
+    (incl. the 1e-12 clamp), the scale with its mantissa cleared (the kernels' method).
+    fp32 log2 rounds up to the next integer only within ~11 ulp below a power of two,
+    which fp8_max / bf16 never reaches (fp8_max is 1.75 * 2^k, bf16 has 8 mantissa bits)."""
+    bits = torch.arange(0, 0x7F80, dtype=torch.int32).to(torch.int16)
+    amax = bits.view(torch.bfloat16).float()
+    raw = orc.amax_to_scale_axiswise(amax, fmt, pow2=False)
+    got = orc.amax_to_scale_axiswise(amax, fmt, pow2=True)
+    cleared = (raw.view(torch.int32) & 0xFF800000).view(torch.float32)
+    assert torch.equal(got, cleared)
+    assert bool((got <= raw).all()) and bool((got * 2 > raw).all())
+    for a in (3.0, 0.1, 448.0, 1e-3):
+        s = orc.amax_to_scale_axiswise(torch.tensor([a]).to(torch.bfloat16).float(), fmt)
+        want = _pow2_floor(float(np.float32(orc.FP8_MAX[fmt] / float(torch.tensor(a).to(torch.bfloat16)))))
+        assert s.item() == want
+    assert orc.amax_to_scale_axiswise(torch.tensor([0.0]), fmt).item() == _pow2_floor(
+        float(np.float32(orc.FP8_MAX[fmt] / 1e-12)))
+
+
+def test_pow2_known_answers():
+    assert orc.amax_to_scale_axiswise(torch.tensor([3.0]), E4M3).item() == 128.0   # 149.3
+    assert orc.amax_to_scale_axiswise(torch.tensor([448.0]), E4M3).item() == 1.0
+    assert orc.amax_to_scale_axiswise(torch.tensor([449.0]), E4M3).item() == 0.5   # 0.998
+    assert orc.amax_to_scale_axiswise(torch.tensor([1.0]), E5M2).item() == 32768.0  # 57344
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+@pytest.mark.parametrize("dim", [-1, 0])
+def test_axiswise_equals_per_slice_tensorwise(fmt, dim):
+    """Brute force: each row (dim -1) / column (dim 0) quantized on its own with the
+    pinned tensorwise amax, scale and cast, the scale floored to a power of two via frexp."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(37, 48, generator=g)
+    x[3] *= 300.0
+    x[:, 5] *= 1e-3
+    x[7] = 0.0
+    x[:, 11] = 0.0
+    x = x.to(torch.bfloat16)
+    q, s = orc.quantize_axiswise(x, fmt, dim)
+    n = x.shape[0] if dim == -1 else x.shape[1]
+    for i in range(n):
+        sl = x[i] if dim == -1 else x[:, i]
+        sc = _pow2_floor(float(orc.amax_to_scale(orc.amax(sl), fmt)[0]))
+        want = orc.cast(sl, torch.tensor(sc, dtype=torch.float32), fmt)
+        got_q = q[i] if dim == -1 else q[:, i]
+        got_s = s[i, 0] if dim == -1 else s[0, i]
+        assert got_s.item() == sc
+        assert torch.equal(got_q, want)
+
+
+def test_axiswise_nan_and_inf_rows():
+    x = torch.randn(4, 16).to(torch.bfloat16)
+    x[1, 3] = float("nan")
+    x[2, 5] = float("inf")
+    q, s = orc.quantize_axiswise(x, E4M3, -1)
+    assert math.isnan(s[1, 0].item()) and bool((q[1] == 0x7F).all())   # NaN scale: +NaN bytes
+    assert s[2, 0].item() == 0.0                                         # 448 / inf
+    assert q[2, 5].item() == 0xFF and bool((q[2, :5] & 0x7F == 0).all())  # inf * 0 = -NaN
+
+
+def test_scaled_mm_with_axis_scales_brute_force():
+    g = torch.Generator().manual_seed(22)
+    a = torch.randn(5, 32, generator=g).to(torch.bfloat16)
+    b = (torch.randn(7, 32, generator=g) * 0.02).to(torch.bfloat16)
+    aq, sa = orc.quantize_axiswise(a, E4M3, -1)
+    bq, sb = orc.quantize_axiswise(b, E4M3, -1)
+    y = orc.scaled_mm(aq, sa, E4M3, bq, sb, E4M3)
+    da = aq.view(torch.float8_e4m3fn).double()
+    db = bq.view(torch.float8_e4m3fn).double()
+    for i in range(5):
+        for j in range(7):
+            want = sum(da[i, k] * db[j, k] for k in range(32)) / (float(sa[i, 0]) * float(sb[j, 0]))
+            assert abs(y[i, j].item() - want) <= 1e-6 * max(1e-30, abs(want))
+
+
+@pytest.mark.parametrize("recipe", ["rowwise", "rowwise_with_gw_hp"])
+def test_linear_axiswise_recipes_track_the_bf16_linear(recipe):
+    """Shapes, and every output within e4m3 error of the unquantized products (a
+    transposed operand or a scale on the wrong axis would be far off)."""
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(64, 48, generator=g).to(torch.bfloat16)
+    w = (torch.randn(32, 48, generator=g) * 0.05).to(torch.bfloat16)
+    w[:, 3] *= 40.0   # an outlier input feature: per-column W scales matter for dX
+    dy = (torch.randn(64, 32, generator=g) * 1e-3).to(torch.bfloat16)
+    y, dx, dw = orc.linear_fwd_bwd_axiswise(x, w, dy, recipe)
+    ref_y = x.double() @ w.double().t()
+    ref_dx = dy.double() @ w.double()
+    ref_dw = dy.double().t() @ x.double()
+    for got, ref in ((y, ref_y), (dx, ref_dx), (dw, ref_dw)):
+        assert got.shape == ref.shape
+        rel = (got.double() - ref).norm() / ref.norm()
+        assert rel < 0.08, rel
+    if recipe == "rowwise_with_gw_hp":
+        assert torch.equal(dw, ref_dw.float())
