@@ -47,6 +47,16 @@ SIGNATURES = {
     "bf8_gemm_axiswise": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_int, c_int64, c_int64,
                                   c_int64, c_int64, c_void_p, c_int, c_void_p, c_int, c_void_p,
                                   c_void_p, c_int, c_int64, c_void_p, c_size_t, c_void_p]),
+    "bf8_mx_scale_ld": (c_int64, [c_int64]),
+    "bf8_quantize_mx_bf16": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
+                                     c_void_p, c_void_p, c_void_p]),
+    "bf8_gemm_mx_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
+    "bf8_gemm_mx": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                            c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int,
+                            c_int64, c_void_p, c_size_t, c_void_p]),
+    "bf8_gemm_geglu_mx": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                  c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p,
+                                  c_int64, c_void_p, c_void_p]),
     "bf8_rmsnorm_partials": (c_int64, [c_int64]),
     "bf8_rmsnorm_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_float, c_int,
                                  c_void_p, c_void_p, c_void_p, c_void_p]),

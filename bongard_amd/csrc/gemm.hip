@@ -41,18 +41,19 @@ struct TileInfo {
   double geglu_rate;  // the same with the gated-GELU epilogue; 0: no such variant (the
                       // gated GELU pairs gate and up sub-tiles, so FN must be even)
   const char* name;
+  bool mx;            // has an MX (block-scaled) variant: its stages fit the scale dwords
 };
 
 // Rates are per-CU throughputs measured on MI355X (time per K step of one workgroup, with
 // every CU busy, over the tile's FLOP per step).
 constexpr TileInfo kTiles[NUM_TILES] = {
-    {256, 256, 1, 9.6, 8.8, "256x256"},
-    {256, 160, 1, 9.2, 0.0, "256x160"},
-    {160, 256, 1, 9.0, 7.6, "160x256"},
-    {128, 128, 1, 8.0, 6.2, "128x128"},
-    {192, 256, 1, 9.0, 8.0, "192x256"},
-    {128, 64, 2, 6.5, 0.0, "128x64"},
-    {64, 128, 2, 6.5, 4.0, "64x128"},
+    {256, 256, 1, 9.6, 8.8, "256x256", true},
+    {256, 160, 1, 9.2, 0.0, "256x160", false},
+    {160, 256, 1, 9.0, 7.6, "160x256", false},
+    {128, 128, 1, 8.0, 6.2, "128x128", true},
+    {192, 256, 1, 9.0, 8.0, "192x256", true},
+    {128, 64, 2, 6.5, 0.0, "128x64", true},
+    {64, 128, 2, 6.5, 4.0, "64x128", true},
 };
 // Gated-GELU plans may not depend on K (the amax partial count is sized from M and I
 // alone); they are costed at a typical 20 K steps (hidden size 2560).
@@ -125,10 +126,11 @@ bool env_override(int& tile, int& splits) {
 
 // Chooses the tile and K split for C[M, N] = A[M, K] . B[N, K]^T. GEGLU plans never split
 // and depend on (M, N) only, so the per-tile amax partial count is known without K.
-Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail) {
+Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, bool mx = false) {
   const int64_t ksteps = std::max<int64_t>(cdiv(K, kStepBytes), 1);
   int otile, osplits;
-  if (env_override(otile, osplits) && (!geglu || kTiles[otile].geglu_rate > 0)) {
+  if (env_override(otile, osplits) && (!geglu || kTiles[otile].geglu_rate > 0) &&
+      (!mx || kTiles[otile].mx)) {
     Plan p = make_plan(otile, M, N, ksteps, geglu ? 1 : osplits);
     if (p.ws_bytes > ws_avail) p = make_plan(otile, M, N, ksteps, 1);
     return p;
@@ -137,7 +139,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail) {
   double best_cost = 0;
   bool have = false;
   for (int tile = 0; tile < NUM_TILES; ++tile) {
-    if (geglu && kTiles[tile].geglu_rate <= 0) continue;
+    if ((geglu && kTiles[tile].geglu_rate <= 0) || (mx && !kTiles[tile].mx)) continue;
     for (int s = 1; s <= (geglu ? 1 : kMaxSplits); ++s) {
       const Plan p = make_plan(tile, M, N, geglu ? kGegluNominalSteps : ksteps, s);
       if (p.splits != s || (s > 1 && p.kps < kMinStepsPerSplit) || p.ws_bytes > ws_avail)
@@ -152,22 +154,22 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail) {
   }
   if (geglu) best.kps = (int)ksteps;
   if (const char* d = std::getenv("BONGARD_FP8_GEMM_DEBUG"); d && d[0] == '1')
-    std::fprintf(stderr, "bf8 plan %s M=%lld N=%lld K=%lld: tile %s splits %d (%d x %d tiles)\n",
-                 geglu ? "geglu" : "gemm", (long long)M, (long long)N, (long long)K,
+    std::fprintf(stderr, "bf8 plan %s%s M=%lld N=%lld K=%lld: tile %s splits %d (%d x %d tiles)\n",
+                 geglu ? "geglu" : "gemm", mx ? " mx" : "", (long long)M, (long long)N, (long long)K,
                  kTiles[best.tile].name, best.splits, best.tiles_m, best.tiles_n);
   return best;
 }
 
 int launch_tile(const Plan& pl, const GemmParams& p, int epi, int out_dtype, int fa, int fb,
-                hipStream_t s) {
+                hipStream_t s, bool mx) {
   switch (pl.tile) {
-    case TILE_256x256: return launch_gemm_tile<Tile256x256>(p, epi, out_dtype, fa, fb, s);
-    case TILE_256x160: return launch_gemm_tile<Tile256x160>(p, epi, out_dtype, fa, fb, s);
-    case TILE_160x256: return launch_gemm_tile<Tile160x256>(p, epi, out_dtype, fa, fb, s);
-    case TILE_192x256: return launch_gemm_tile<Tile192x256>(p, epi, out_dtype, fa, fb, s);
-    case TILE_128x64: return launch_gemm_tile<Tile128x64>(p, epi, out_dtype, fa, fb, s);
-    case TILE_64x128: return launch_gemm_tile<Tile64x128>(p, epi, out_dtype, fa, fb, s);
-    default: return launch_gemm_tile<Tile128x128>(p, epi, out_dtype, fa, fb, s);
+    case TILE_256x256: return launch_gemm_tile<Tile256x256>(p, epi, out_dtype, fa, fb, s, mx);
+    case TILE_256x160: return launch_gemm_tile<Tile256x160>(p, epi, out_dtype, fa, fb, s, mx);
+    case TILE_160x256: return launch_gemm_tile<Tile160x256>(p, epi, out_dtype, fa, fb, s, mx);
+    case TILE_192x256: return launch_gemm_tile<Tile192x256>(p, epi, out_dtype, fa, fb, s, mx);
+    case TILE_128x64: return launch_gemm_tile<Tile128x64>(p, epi, out_dtype, fa, fb, s, mx);
+    case TILE_64x128: return launch_gemm_tile<Tile64x128>(p, epi, out_dtype, fa, fb, s, mx);
+    default: return launch_gemm_tile<Tile128x128>(p, epi, out_dtype, fa, fb, s, mx);
   }
 }
 
@@ -183,10 +185,10 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(
     const float* __restrict__ P, int splits, int64_t stride, int M, int N,
     const float* __restrict__ a_sinv, const float* __restrict__ b_sinv, int b_stride,
     int n_seg, SegEnds seg_end, const uint16_t* __restrict__ bias, void* __restrict__ C,
-    int64_t ldc, int a_vec, int b_vec) {
+    int64_t ldc, int a_vec, int b_vec, int unit) {
   const int n8 = N >> 3;
   const int64_t total = (int64_t)M * n8;
-  const float sa = a_vec ? 0.0f : *a_sinv;
+  const float sa = (a_vec || unit) ? 0.0f : *a_sinv;
   for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < total;
        g += (int64_t)gridDim.x * 256) {
     const int m = (int)(g / n8), n = (int)(g % n8) * 8;
@@ -214,6 +216,11 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(
       if (bias) {
         const uint2 bb = *reinterpret_cast<const uint2*>(bias + nh);
         b4[0] = bf16_lo(bb.x); b4[1] = bf16_hi(bb.x); b4[2] = bf16_lo(bb.y); b4[3] = bf16_hi(bb.y);
+      }
+      if (unit) {  // MX: the block scales were applied inside the MFMA
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] + b4[e];
+        continue;
       }
       if (a_vec | b_vec) {  // axiswise: (a_sinv[m] or a_sinv[0]) * (b_sinv[n] or b_sinv[0])
         const float ra = a_vec ? a_sinv[m] : *a_sinv;
@@ -255,19 +262,19 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(
 }
 
 int launch_plan(const Plan& pl, GemmParams p, int epi, int out_dtype, int fa, int fb, void* ws,
-                hipStream_t s) {
+                hipStream_t s, bool mx = false) {
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
   p.splits = pl.splits;
   p.ksteps_per_split = pl.kps;
-  if (pl.splits == 1) return launch_tile(pl, p, epi, out_dtype, fa, fb, s);
+  if (pl.splits == 1) return launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
   // K split: raw fp32 partials into the workspace, then the ordered reduction
   GemmParams q = p;
   q.C = ws;
   q.ldc = p.N;
   q.split_stride = (int64_t)p.M * p.N;
   q.bias = nullptr;
-  const int rc = launch_tile(pl, q, EPI_LINEAR, BF8_OUT_F32, fa, fb, s);
+  const int rc = launch_tile(pl, q, EPI_LINEAR, BF8_OUT_F32, fa, fb, s, mx);
   if (rc != BF8_OK) return rc;
   const int64_t items = (int64_t)p.M * (p.N / 8);
   const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(items, 256), 4096);
@@ -276,11 +283,13 @@ int launch_plan(const Plan& pl, GemmParams p, int epi, int out_dtype, int fa, in
   if (out_dtype == BF8_OUT_BF16)
     hipLaunchKernelGGL(split_reduce_kernel<BF8_OUT_BF16>, dim3(blocks), dim3(256), 0, s,
                        (const float*)ws, pl.splits, q.split_stride, p.M, p.N, p.a_sinv, p.b_sinv,
-                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc, p.a_vec, p.b_vec);
+                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc, p.a_vec, p.b_vec,
+                       mx ? 1 : 0);
   else
     hipLaunchKernelGGL(split_reduce_kernel<BF8_OUT_F32>, dim3(blocks), dim3(256), 0, s,
                        (const float*)ws, pl.splits, q.split_stride, p.M, p.N, p.a_sinv, p.b_sinv,
-                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc, p.a_vec, p.b_vec);
+                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc, p.a_vec, p.b_vec,
+                       mx ? 1 : 0);
   return launch_status("split_reduce_kernel");
 }
 
@@ -391,6 +400,85 @@ int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw,
   Plan pl = choose_plan(M, 2 * I, K, true, 0);
   return launch_plan(pl, p, EPI_GEGLU, BF8_OUT_BF16, BF8_E4M3, BF8_E4M3, nullptr,
                      as_stream(stream));
+}
+
+// ---- MX (block-scaled) GEMMs ----------------------------------------------------------
+size_t bf8_gemm_mx_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return choose_plan(M, N, K, false, (size_t)-1, true).ws_bytes;
+}
+
+int64_t bf8_mx_scale_ld(int64_t K) { return (K + 127) / 128 * 4; }
+
+static int check_mx_operand(const char* who, const char* what, const uint8_t* q, int64_t ld,
+                            const uint8_t* sc, int64_t ld_sc, int64_t rows, int64_t K) {
+  BF8_CHECK(q && sc, "%s: %s or its scales are NULL", who, what);
+  BF8_CHECK(ld % 16 == 0 && ld >= K && ((uintptr_t)q & 15) == 0,
+            "%s: %s needs a 16-byte aligned base and row stride >= K", who, what);
+  BF8_CHECK(ld_sc % 4 == 0 && ld_sc >= bf8_mx_scale_ld(K) && ((uintptr_t)sc & 3) == 0,
+            "%s: %s scales need a 4-byte aligned base and row stride >= %lld", who, what,
+            (long long)bf8_mx_scale_ld(K));
+  BF8_CHECK(rows * ld < (1LL << 31) && rows * ld_sc < (1LL << 31), "%s: %s larger than 2 GiB",
+            who, what);
+  return BF8_OK;
+}
+
+int bf8_gemm_mx(const uint8_t* A, int64_t lda, const uint8_t* A_scales, int64_t lda_sc,
+                const uint8_t* B, int64_t ldb, const uint8_t* B_scales, int64_t ldb_sc,
+                int64_t M, int64_t N, int64_t K, const void* bias, void* C, int out_dtype,
+                int64_t ldc, void* ws, size_t ws_bytes, void* stream) {
+  BF8_CHECK(out_dtype == BF8_OUT_BF16 || out_dtype == BF8_OUT_F32, "bf8_gemm_mx: bad out_dtype");
+  BF8_CHECK(M >= 0 && N >= 0 && K >= 0, "bf8_gemm_mx: negative shape");
+  BF8_CHECK(K % 32 == 0, "bf8_gemm_mx: K must be a multiple of the 32-element block (got %lld)",
+            (long long)K);
+  BF8_CHECK(N % 8 == 0 && ldc >= N && ldc % 4 == 0,
+            "bf8_gemm_mx: need N %% 8 == 0, ldc >= N, ldc %% 4 == 0");
+  BF8_CHECK(((uintptr_t)C & 15) == 0 && ((uintptr_t)bias & 7) == 0,
+            "bf8_gemm_mx: C must be 16-byte, bias 8-byte aligned");
+  BF8_CHECK(ws_bytes == 0 || (ws && ((uintptr_t)ws & 255) == 0),
+            "bf8_gemm_mx: workspace must be 256-byte aligned");
+  if (M == 0 || N == 0) return BF8_OK;
+  BF8_CHECK(K > 0, "bf8_gemm_mx: K == 0 is not supported");
+  int rc = check_mx_operand("bf8_gemm_mx", "A", A, lda, A_scales, lda_sc, M, K);
+  if (rc) return rc;
+  rc = check_mx_operand("bf8_gemm_mx", "B", B, ldb, B_scales, ldb_sc, N, K);
+  if (rc) return rc;
+  GemmParams p{};
+  p.A = A; p.B = B; p.lda = lda; p.ldb = ldb;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.I = 0;
+  p.a_sc = A_scales; p.b_sc = B_scales; p.a_sc_ld = lda_sc; p.b_sc_ld = ldb_sc;
+  p.n_seg = 1;
+  for (int s = 0; s < 4; ++s) p.seg_end[s] = (int)N;
+  p.bias = (const uint16_t*)bias; p.C = C; p.ldc = ldc;
+  const Plan pl = choose_plan(M, N, K, false, ws ? ws_bytes : 0, true);
+  return launch_plan(pl, p, EPI_LINEAR, out_dtype, BF8_E4M3, BF8_E4M3, ws, as_stream(stream),
+                     true);
+}
+
+int bf8_gemm_geglu_mx(const uint8_t* X, int64_t ldx, const uint8_t* X_scales, int64_t ldx_sc,
+                      const uint8_t* W, int64_t ldw, const uint8_t* W_scales, int64_t ldw_sc,
+                      int64_t M, int64_t I, int64_t K, void* H, int64_t ldh, void* GU,
+                      void* stream) {
+  BF8_CHECK(M >= 1 && I >= 1 && K >= 32, "bf8_gemm_geglu_mx: bad shape");
+  BF8_CHECK(I % 128 == 0, "bf8_gemm_geglu_mx: I must be a multiple of 128 (got %lld)",
+            (long long)I);
+  BF8_CHECK(K % 32 == 0, "bf8_gemm_geglu_mx: K must be a multiple of 32");
+  BF8_CHECK(ldh >= I && ldh % 4 == 0, "bf8_gemm_geglu_mx: bad ldh");
+  BF8_CHECK(((uintptr_t)H & 15) == 0 && ((uintptr_t)GU & 15) == 0,
+            "bf8_gemm_geglu_mx: H, GU must be 16-byte aligned");
+  int rc = check_mx_operand("bf8_gemm_geglu_mx", "X", X, ldx, X_scales, ldx_sc, M, K);
+  if (rc) return rc;
+  rc = check_mx_operand("bf8_gemm_geglu_mx", "W", W, ldw, W_scales, ldw_sc, 2 * I, K);
+  if (rc) return rc;
+  GemmParams p{};
+  p.A = X; p.B = W; p.lda = ldx; p.ldb = ldw;
+  p.M = (int)M; p.N = (int)(2 * I); p.K = (int)K; p.I = (int)I;
+  p.a_sc = X_scales; p.b_sc = W_scales; p.a_sc_ld = ldx_sc; p.b_sc_ld = ldw_sc;
+  p.n_seg = 1;
+  p.C = H; p.ldc = ldh; p.GU = (uint16_t*)GU; p.partials = nullptr;
+  Plan pl = choose_plan(M, 2 * I, K, true, 0, true);
+  return launch_plan(pl, p, EPI_GEGLU, BF8_OUT_BF16, BF8_E4M3, BF8_E4M3, nullptr,
+                     as_stream(stream), true);
 }
 
 }  // extern "C"

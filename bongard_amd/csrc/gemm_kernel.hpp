@@ -21,6 +21,9 @@ struct GemmParams {
   const float* a_sinv;    // a_vec: one per row of A (M), else a single value
   const float* b_sinv;    // b_vec: one per row of B (N), else n_seg values b_stride apart
   int a_vec, b_vec;       // LINEAR only
+  const uint8_t* a_sc;    // MX: E8M0 block scales [M, a_sc_ld] (byte k/32 of row m)
+  const uint8_t* b_sc;    // MX: [N, b_sc_ld]
+  int64_t a_sc_ld, b_sc_ld;
   int b_stride;
   int n_seg;
   int seg_end[4];
@@ -57,6 +60,6 @@ using Tile64x128 = GemmTile<2, 2, 1, 2, 3, 2>;
 // status; the host entry points have validated p.
 template <class T>
 int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
-                     hipStream_t stream);
+                     hipStream_t stream, bool mx);
 
 }  // namespace bf8

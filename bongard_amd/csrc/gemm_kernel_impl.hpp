@@ -66,6 +66,17 @@ __device__ __forceinline__ void dma16(i32x4 srd, uint32_t lds_addr, uint32_t vof
                : "memory");
 }
 
+// 4-byte-per-lane variant (MX block scales): lane l's dword lands at lds_addr + 4 l.
+__device__ __forceinline__ void dma4(i32x4 srd, uint32_t lds_addr, uint32_t voff,
+                                     uint32_t soff) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(m0v), "v"(voff), "s"(srd), "s"(so)
+               : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(
       (__attribute__((address_space(3))) const uint8_t*)(p));
@@ -99,16 +110,30 @@ __device__ __forceinline__ v16f mfma(v8i a, v8i b, v16f c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
 }
 
+// Block-scaled (MX) form: each lane supplies the E8M0 scale of the 32 K-values it holds
+// (its row of the operand, K block lane >> 5 of the 64-byte sub-step), as byte OPSEL of
+// its scale register; the product of the two scales multiplies that block's products.
+template <int FA, int FB, int OPSEL>
+__device__ __forceinline__ v16f mfma_mx(v8i a, v8i b, v16f c, uint32_t sa, uint32_t sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, OPSEL, (int)sa, OPSEL,
+                                                         (int)sb);
+}
+
 // Swizzled position of logical 16-byte chunk c in tile row r (128-byte rows).
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
 // Reads 16 bytes of an MFMA operand fragment: 32 rows starting at `row0` of an LDS tile,
-// K bytes [kk*64, kk*64+64); lane l holds row row0 + (l & 31), bytes (l >> 5)*32 + 16*half
-// .. +15 (two halves make the lane's 32 bytes).
+// K bytes [kk*64, kk*64+64); lane l holds row row0 + (l & 31) (two halves make the lane's
+// 32 bytes). The f8f6f4 MFMA takes register bytes 0-15 of lane half h as K = 16 h + 0..15
+// and bytes 16-31 as K = 32 + 16 h + 0..15 (measured on gfx950). A plain MFMA does not
+// care which K the bytes are (A and B are permuted alike), so it reads the lane's 32
+// contiguous bytes (l >> 5)*32 + 16*half; the block-scaled MFMA needs K blocks [0, 32)
+// and [32, 64) of the sub-step to be the ones its scales describe, so `mx` reads
+// 32*half + 16*(l >> 5).
 __device__ __forceinline__ v4u read_half(const uint8_t* tile, int row0, int kk, int half,
-                                         int lane) {
+                                         int lane, bool mx = false) {
   const int row = row0 + (lane & 31);
-  const int c = kk * 4 + (lane >> 5) * 2 + half;
+  const int c = mx ? kk * 4 + half * 2 + (lane >> 5) : kk * 4 + (lane >> 5) * 2 + half;
   return *reinterpret_cast<const v4u*>(tile + row * kBK + (swz(row, c) << 4));
 }
 
@@ -165,29 +190,34 @@ struct Frags {
   v4u h[NH];
 };
 
-template <class T, int FA, int FB, int EPI, int OUT>
+template <class T, int FA, int FB, int EPI, int OUT, bool MX = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(T::OCC, T::OCC))) void
 gemm_kernel(GemmParams p) {
   constexpr int BM = T::BM, BN = T::BN, FM = T::FM, FN = T::FN, WM = T::WM, NS = T::NS;
   constexpr int kA = BM * kBK;               // A tile bytes per stage
-  constexpr int kStage = (BM + BN) * kBK;    // [A tile | B tile]
+  // MX: each stage also holds the E8M0 block scales of its K step: one dword (4 blocks of
+  // 32) per tile row, A rows at kData + 4 r, B rows at kData + 1024 + 4 r (r < 256).
+  constexpr int kData = (BM + BN) * kBK;
+  constexpr int kStage = kData + (MX ? 2048 : 0);  // [A tile | B tile | scales]
   constexpr int DA = BM / 32, DB = BN / 32;  // 1 KB DMA blocks per wave per stage
-  constexpr int ND = DA + DB;
+  constexpr int ND = DA + DB + (MX ? 2 : 0);  // loads per wave per stage
   constexpr int NM = FM * FN;                // MFMAs per sub-step
   constexpr int NH = 2 * (FM + FN);          // 16-byte fragment halves per sub-step
   static_assert(EPI != EPI_GEGLU || FN % 2 == 0, "GEGLU pairs gate and up sub-tiles");
+  static_assert(!MX || (BM <= 256 && BN <= 256), "MX scale rows: one dword per lane");
+  static_assert(NS * kStage * T::OCC <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage];
 
   // Dequant scales: read at the start, so their latency hides behind the first loads.
-  const float sa = *p.a_sinv;
+  const float sa = MX ? 1.0f : *p.a_sinv;
   float sb[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) sb[s] = s < p.n_seg ? p.b_sinv[s * p.b_stride] : 0.0f;
+  for (int s = 0; s < 4; ++s) sb[s] = MX ? 1.0f : s < p.n_seg ? p.b_sinv[s * p.b_stride] : 0.0f;
   float ag = 0.0f, au = 0.0f;
   if constexpr (EPI == EPI_GEGLU) {
-    ag = sa * p.b_sinv[0];
-    au = sa * p.b_sinv[p.b_stride];
+    ag = MX ? 1.0f : sa * p.b_sinv[0];
+    au = MX ? 1.0f : sa * p.b_sinv[p.b_stride];
   }
 
   int tm, tn, split;
@@ -235,16 +265,45 @@ gemm_kernel(GemmParams p) {
     }
     b_off[j] = bvalid ? (uint32_t)((int64_t)bn * p.ldb + lchunk * 16) : kOob;
   }
+  // MX: lane l of wave w loads the scale dword of tile row w * 64 + l (A and B), from
+  // the [rows, ld] E8M0 arrays; rows outside the tile or the tensor read as zero.
+  i32x4 srd_sa = {0, 0, 0, 0}, srd_sb = {0, 0, 0, 0};
+  uint32_t sa_off = kOob, sb_off = kOob;
+  if constexpr (MX) {
+    srd_sa = make_srd(p.a_sc, (uint32_t)((int64_t)p.M * p.a_sc_ld));
+    srd_sb = make_srd(p.b_sc, (uint32_t)((int64_t)p.N * p.b_sc_ld));
+    const int r = wid * 64 + lane;
+    if (r < BM && m0 + r < p.M) sa_off = (uint32_t)((int64_t)(m0 + r) * p.a_sc_ld);
+    if (r < BN) {
+      int bn;
+      bool bvalid;
+      if (EPI == EPI_GEGLU) {
+        const int rr = r < BN / 2 ? r : r - BN / 2;
+        bn = (r < BN / 2 ? 0 : p.I) + n0 + rr;
+        bvalid = n0 + rr < p.I;
+      } else {
+        bn = n0 + r;
+        bvalid = bn < p.N;
+      }
+      if (bvalid) sb_off = (uint32_t)((int64_t)bn * p.b_sc_ld);
+    }
+  }
   // A partial last K step (K % 128 != 0) must read its chunks at or beyond K as zero.
   const bool lane_ktail_dead = (p.K % kBK) != 0 && (ksteps - 1) * kBK + lchunk * 16 >= p.K;
 
-  // Load x of a stage (x < DA: A block x, else B block x - DA). `kill` zero-fills.
-  auto dma_load = [&](int x, uint8_t* stage, uint32_t k0, bool kill) {
+  // Load x of a stage (x < DA: A block x, DA <= x < DA + DB: B block x - DA, then (MX)
+  // the A and B scale dwords). `kill` zero-fills data, `kill_sc` the scales (a partial
+  // last K step keeps the scales of its blocks within K).
+  auto dma_load = [&](int x, uint8_t* stage, uint32_t k0, bool kill, bool kill_sc) {
     const uint32_t base = lds_addr(stage);
     if (x < DA)
       dma16(ra, base + (x * 4 + wid) * 1024, kill ? kOob : a_off[x], k0);
-    else
+    else if (x < DA + DB)
       dma16(rb, base + kA + ((x - DA) * 4 + wid) * 1024, kill ? kOob : b_off[x - DA], k0);
+    else if (x == DA + DB)
+      dma4(srd_sa, base + kData + wid * 256, kill_sc ? kOob : sa_off, k0 >> 5);
+    else
+      dma4(srd_sb, base + kData + 1024 + wid * 256, kill_sc ? kOob : sb_off, k0 >> 5);
   };
   // Stages past this split's last step are filled with zeros (never read); the partial
   // last K step of the tensor masks lanes beyond K.
@@ -266,11 +325,11 @@ gemm_kernel(GemmParams p) {
   auto read_one = [&](Frags<NH>& f, const uint8_t* stage, int kk, int h) {
     const int fr = h >> 1;  // 0: b0, 1..FM: a0.., FM+1..: b1..
     if (fr == 0)
-      f.h[h] = read_half(stage + kA, brow[0], kk, h & 1, lane);
+      f.h[h] = read_half(stage + kA, brow[0], kk, h & 1, lane, MX);
     else if (fr <= FM)
-      f.h[h] = read_half(stage, wave_m0 + (fr - 1) * 32, kk, h & 1, lane);
+      f.h[h] = read_half(stage, wave_m0 + (fr - 1) * 32, kk, h & 1, lane, MX);
     else
-      f.h[h] = read_half(stage + kA, brow[fr - FM], kk, h & 1, lane);
+      f.h[h] = read_half(stage + kA, brow[fr - FM], kk, h & 1, lane, MX);
   };
 
   v16f acc[FN][FM];
@@ -282,11 +341,32 @@ gemm_kernel(GemmParams p) {
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   // MFMA x of a sub-step: n-subtile x / FM, m-subtile x % FM.
-  auto mma_one = [&](const Frags<NH>& f, int x) {
+  // MX scales of the current stage (per fragment: the row's four block scales, shifted
+  // so that byte 2 kk holds block 2 kk + (lane >> 5)) and of the next one.
+  uint32_t scA[MX ? FM : 1], scB[MX ? FN : 1], scA_n[MX ? FM : 1], scB_n[MX ? FN : 1];
+  auto read_scales = [&](const uint8_t* stage, uint32_t* sa_, uint32_t* sb_)
+      __attribute__((always_inline)) {
+    if constexpr (MX) {
+      const uint8_t* sc = stage + kData;
+      const int sh = (lane >> 5) * 8;
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        sa_[j] = *reinterpret_cast<const uint32_t*>(sc + (wave_m0 + j * 32 + (lane & 31)) * 4) >> sh;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+        sb_[i] = *reinterpret_cast<const uint32_t*>(sc + 1024 + (brow[i] + (lane & 31)) * 4) >> sh;
+    }
+  };
+  auto mma_one = [&](const Frags<NH>& f, int x, auto kk_tag) __attribute__((always_inline)) {
+    constexpr int kk = decltype(kk_tag)::value;
     const int i = x / FM, j = x % FM;
     const int hb = i == 0 ? 0 : 2 * (FM + i);
     const int ha = 2 * (1 + j);
-    acc[i][j] = mfma<FB, FA>(join(f.h[hb], f.h[hb + 1]), join(f.h[ha], f.h[ha + 1]), acc[i][j]);
+    if constexpr (MX)
+      acc[i][j] = mfma_mx<FB, FA, 2 * kk>(join(f.h[hb], f.h[hb + 1]), join(f.h[ha], f.h[ha + 1]),
+                                         acc[i][j], scB[i], scA[j]);
+    else
+      acc[i][j] = mfma<FB, FA>(join(f.h[hb], f.h[hb + 1]), join(f.h[ha], f.h[ha + 1]), acc[i][j]);
   };
 
   // Pipeline (NS LDS stages, 2 MFMA sub-steps of 64 K-bytes per stage). Step ls:
@@ -304,7 +384,7 @@ gemm_kernel(GemmParams p) {
   for (int ls = 0; ls < NS; ++ls) {
 #pragma unroll
     for (int x = 0; x < ND; ++x)
-      dma_load(x, smem + ls * kStage, (uint32_t)(kbeg + ls) * kBK, stage_kill(ls));
+      dma_load(x, smem + ls * kStage, (uint32_t)(kbeg + ls) * kBK, stage_kill(ls), ls >= nsteps);
   }
   // stage 0 landed: the NS-1 later stages (ND loads each) may still be in flight
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 1)) : "memory");
@@ -317,6 +397,7 @@ gemm_kernel(GemmParams p) {
     read_one(f0, smem, 0, h);
     __builtin_amdgcn_sched_barrier(0);
   }
+  read_scales(smem, scA, scB);
   auto step = [&](auto with_dma, int ls) __attribute__((always_inline)) {
     constexpr bool kDma = decltype(with_dma)::value;
     uint8_t* cur = stage_ptr(ls);
@@ -324,7 +405,7 @@ gemm_kernel(GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int x = 0; x < NM; ++x) {
-      mma_one(f0, x);
+      mma_one(f0, x, std::integral_constant<int, 0>{});
 #pragma unroll
       for (int h = x * NH / NM; h < (x + 1) * NH / NM; ++h) read_one(f1, cur, 1, h);
       __builtin_amdgcn_sched_barrier(0);
@@ -338,16 +419,25 @@ gemm_kernel(GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t kn = (uint32_t)(kbeg + ls + NS) * kBK;
     const bool killn = stage_kill(ls + NS);
+    const bool killn_sc = ls + NS >= nsteps;
+    read_scales(nxt, scA_n, scB_n);
 #pragma unroll
     for (int x = 0; x < NM; ++x) {
-      mma_one(f1, x);
+      mma_one(f1, x, std::integral_constant<int, 1>{});
 #pragma unroll
       for (int h = x * NH / NM; h < (x + 1) * NH / NM; ++h) read_one(f0, nxt, 0, h);
       if constexpr (kDma) {
 #pragma unroll
-        for (int d = x * ND / NM; d < (x + 1) * ND / NM; ++d) dma_load(d, cur, kn, killn);
+        for (int d = x * ND / NM; d < (x + 1) * ND / NM; ++d)
+          dma_load(d, cur, kn, killn, killn_sc);
       }
       __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (MX) {
+#pragma unroll
+      for (int j = 0; j < FM; ++j) scA[j] = scA_n[j];
+#pragma unroll
+      for (int i = 0; i < FN; ++i) scB[i] = scB_n[i];
     }
   };
   int ls = 0;
@@ -548,7 +638,7 @@ gemm_kernel(GemmParams p) {
       run_pass(std::integral_constant<int, 2>{});
     }
     hmax = block_max_u32<kThreads>(hmax);
-    if (t == 0) p.partials[blockIdx.x] = hmax;
+    if (t == 0 && p.partials) p.partials[blockIdx.x] = hmax;
   }
 }
 
@@ -570,7 +660,30 @@ int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
 
 template <class T>
 int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
-                     hipStream_t stream) {
+                     hipStream_t stream, bool mx) {
+  if (mx) {
+    // MX block scales: e4m3 operands; the tile's stages must fit the scale dwords too
+    if constexpr (T::NS * ((T::BM + T::BN) * kBK + 2048) * T::OCC <= 160 * 1024) {
+      const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads);
+      if (epi == EPI_GEGLU) {
+        if constexpr (T::FN % 2 == 0) {
+          hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI_GEGLU, BF8_OUT_BF16, true>), grid, block,
+                             0, stream, p);
+          return launch_status("gemm_kernel(geglu, mx)");
+        }
+      } else if (out_dtype == BF8_OUT_BF16) {
+        hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI_LINEAR, BF8_OUT_BF16, true>), grid, block, 0,
+                           stream, p);
+        return launch_status("gemm_kernel(mx)");
+      } else {
+        hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI_LINEAR, BF8_OUT_F32, true>), grid, block, 0,
+                           stream, p);
+        return launch_status("gemm_kernel(mx)");
+      }
+    }
+    set_error("gemm: tile %dx%d has no MX variant for this epilogue", T::BM, T::BN);
+    return BF8_EINVAL;
+  }
   if (epi == EPI_GEGLU) {
     if constexpr (T::FN % 2 == 0) {
       const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(kThreads);

@@ -2,5 +2,6 @@
 #include "gemm_kernel_impl.hpp"
 
 namespace bf8 {
-template int launch_gemm_tile<Tile256x160>(const GemmParams&, int, int, int, int, hipStream_t);
+template int launch_gemm_tile<Tile256x160>(const GemmParams&, int, int, int, int, hipStream_t,
+                                              bool);
 }  // namespace bf8

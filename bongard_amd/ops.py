@@ -329,6 +329,91 @@ def gemm_axiswise(a, a_fmt, a_sinv, b, b_fmt, b_sinv, *, out_dtype=torch.bfloat1
     return out
 
 
+@dataclass
+class MxFp8Tensor:
+    """An MXFP8 tensor of x [rows, cols] (32-element blocks, one E8M0 byte each):
+    ``data`` [rows, cols] with ``scales`` [rows, mx_scale_ld(cols)] (blocks along rows)
+    and/or ``data_t`` [cols, rows] with ``scales_t`` [cols, mx_scale_ld(rows)] (blocks along
+    columns of x, stored transposed)."""
+
+    data: Optional[torch.Tensor]
+    scales: Optional[torch.Tensor]
+    data_t: Optional[torch.Tensor]
+    scales_t: Optional[torch.Tensor]
+    fmt: int
+    rows: int
+    cols: int
+
+
+def mx_scale_ld(K):
+    return int(_lib.lib().bf8_mx_scale_ld(int(K)))
+
+
+def quantize_mx(x, fmt=E4M3, *, rowwise=True, colwise=False):
+    """MXFP8 quantization of a bf16 tensor (TE MXFP8BlockScaling arithmetic)."""
+    _require_gpu(x)
+    x = _bf16_2d(x)
+    rows, cols = x.shape
+    dev = x.device
+    if not (rowwise or colwise):
+        raise ValueError("quantize_mx: nothing requested")
+    out = sc = out_t = sc_t = None
+    if rowwise:
+        out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=dev)
+        sc = torch.empty((rows, mx_scale_ld(cols)), dtype=torch.uint8, device=dev)
+    if colwise:
+        out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=dev)
+        sc_t = torch.empty((cols, mx_scale_ld(rows)), dtype=torch.uint8, device=dev)
+    _lib.check(_lib.lib().bf8_quantize_mx_bf16(_ptr(x), rows, cols, fmt, _ptr(out), _ptr(sc),
+                                               _ptr(out_t), _ptr(sc_t), _stream(dev)),
+               "bf8_quantize_mx_bf16")
+    return MxFp8Tensor(out, sc, out_t, sc_t, fmt, rows, cols)
+
+
+def gemm_mx(a, a_scales, b, b_scales, *, out_dtype=torch.bfloat16, bias=None, out=None):
+    """``C = a @ b.T`` on MXFP8 (e4m3) operands a [M, K], b [N, K] with their E8M0 block
+    scales [M, >= mx_scale_ld(K)], [N, ...]."""
+    _require_gpu(a, b, a_scales, b_scales)
+    M, K = a.shape
+    N, Kb = b.shape
+    if K != Kb:
+        raise ValueError(f"gemm_mx: inner dims differ ({K} vs {Kb})")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("gemm_mx: out_dtype must be bfloat16 or float32")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    if bias is not None:
+        if bias.dtype != torch.bfloat16:
+            raise TypeError("gemm_mx: bias must be bfloat16")
+        bias = bias.contiguous()
+    L = _lib.lib()
+    ws_bytes = int(L.bf8_gemm_mx_workspace(M, N, K))
+    ws = gemm_workspace(ws_bytes, a.device) if ws_bytes else None
+    ws_bytes = ws.numel() if ws is not None else 0
+    _lib.check(L.bf8_gemm_mx(_ptr(a), a.stride(0), _ptr(a_scales), a_scales.stride(0), _ptr(b),
+                             b.stride(0), _ptr(b_scales), b_scales.stride(0), M, N, K, _ptr(bias),
+                             _ptr(out), OUT_BF16 if out_dtype == torch.bfloat16 else OUT_F32,
+                             out.stride(0), _ptr(ws), ws_bytes, _stream(a.device)), "bf8_gemm_mx")
+    return out
+
+
+def gemm_geglu_mx(x8, x_scales, w8, w_scales, intermediate, *, keep_gu=False):
+    """Gate/up GEMM + gated GELU on MXFP8 operands; returns ``(H bf16 [M, I], GU or None)``."""
+    _require_gpu(x8, x_scales, w8, w_scales)
+    M, K = x8.shape
+    I = int(intermediate)
+    if w8.shape != (2 * I, K):
+        raise ValueError(f"gemm_geglu_mx: W must be [{2 * I}, {K}]")
+    H = torch.empty((M, I), dtype=torch.bfloat16, device=x8.device)
+    GU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=x8.device) if keep_gu else None
+    _lib.check(_lib.lib().bf8_gemm_geglu_mx(_ptr(x8), x8.stride(0), _ptr(x_scales),
+                                            x_scales.stride(0), _ptr(w8), w8.stride(0),
+                                            _ptr(w_scales), w_scales.stride(0), M, I, K, _ptr(H),
+                                            H.stride(0), _ptr(GU), _stream(x8.device)),
+               "bf8_gemm_geglu_mx")
+    return H, GU
+
+
 def geglu_partials_count(M, intermediate):
     return int(_lib.lib().bf8_geglu_partials(int(M), int(intermediate)))
 

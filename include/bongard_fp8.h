@@ -216,6 +216,43 @@ int bf8_gemm_axiswise(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B
                       int out_dtype, int64_t ldc, void* ws, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * MXFP8 (OCP microscaling: 32-element blocks, one E8M0 scale byte each).
+ * Replaces TE's MXFP8BlockScaling recipe (bongard/te_linear.py:17,38-39;
+ * bongard/fused_mlp.py:9,31-33): its quantizer and its block-scaled FP8 GEMM.
+ * Per block: amax = max |x|, e = E8M0 of fp32(amax * fp32(1 / fp8_max)) rounded up to a
+ * power of two (NaN amax -> 0xFF, capped at 0xFE), q = fp8(clamp(x * 2^(127 - e))).
+ * Scale arrays are [rows, bf8_mx_scale_ld(K)] bytes: byte b of a row is block b (K
+ * elements b*32 .. b*32+31); bytes past the last block are 127 (= 1.0).
+ * ------------------------------------------------------------------------------- */
+int64_t bf8_mx_scale_ld(int64_t K);
+
+/* x: bf16 [rows, cols]. out [rows, cols] + out_scales [rows, bf8_mx_scale_ld(cols)]:
+ * blocks along rows (cols % 32 == 0). out_t [cols, rows] + out_t_scales
+ * [cols, bf8_mx_scale_ld(rows)]: blocks along columns, stored transposed (rows % 32 == 0).
+ * Either pair may be NULL (not both). */
+int bf8_quantize_mx_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
+                         uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
+                         void* stream);
+
+/* C[m, n] = sum_b 2^(ea[m,b] + eb[n,b] - 254) * sum_{k in block b} A[m, k] * B[n, k]
+ * (+ bias[n]), e4m3 operands, fp32 accumulation; TN like bf8_gemm, K % 32 == 0. Scale
+ * arrays 4-byte aligned with row strides >= bf8_mx_scale_ld(K), multiples of 4.
+ * ws: bf8_gemm_mx_workspace(M, N, K) bytes (split-K partials) or 0. */
+size_t bf8_gemm_mx_workspace(int64_t M, int64_t N, int64_t K);
+int bf8_gemm_mx(const uint8_t* A, int64_t lda, const uint8_t* A_scales, int64_t lda_sc,
+                const uint8_t* B, int64_t ldb, const uint8_t* B_scales, int64_t ldb_sc,
+                int64_t M, int64_t N, int64_t K, const void* bias, void* C, int out_dtype,
+                int64_t ldc, void* ws, size_t ws_bytes, void* stream);
+
+/* The gate/up GEMM with the gated-GELU epilogue (as bf8_gemm_geglu) on MXFP8 operands:
+ * X [M, K] + scales, W [2I, K] = [W_gate; W_up] + scales. H, GU as bf8_gemm_geglu; no
+ * amax partials (H's own MX quantization needs none). */
+int bf8_gemm_geglu_mx(const uint8_t* X, int64_t ldx, const uint8_t* X_scales, int64_t ldx_sc,
+                      const uint8_t* W, int64_t ldw, const uint8_t* W_scales, int64_t ldw_sc,
+                      int64_t M, int64_t I, int64_t K, void* H, int64_t ldh, void* GU,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------------
  * RMSNorm fused with the amax pass of the quantization that follows it.
  * Replaces the RMSNorm (zero-centred gamma) of TE LayerNormMLP built at
  * bongard/fused_mlp.py:25-30 (HF T5Gemma2RMSNorm in evaluation, bongard/fused_mlp.py:64-65):

@@ -282,6 +282,70 @@ def linear_fwd_bwd_axiswise(x, w, dy, recipe, *, precise=True):
 
 
 # ---------------------------------------------------------------------------------------
+# MXFP8  (TE 2.19.0 MXFP8BlockScaling: bongard/te_linear.py:17,38-39,
+# bongard/fused_mlp.py:9,31-33; OCP MX: 32-element blocks, E8M0 scales)
+# ---------------------------------------------------------------------------------------
+MX_BLOCK = 32
+
+
+def mx_exponent(amax_f32: torch.Tensor, fmt: int) -> torch.Tensor:
+    """E8M0 byte (int32) of fp32(amax * fp32(1 / fp8_max)) rounded up to a power of two
+    (TE float_to_e8m0): NaN -> 0xFF, inf -> 0xFE, the carry never passes 0xFE, values at
+    or below 2^-127 -> 0."""
+    rcp = torch.tensor(1.0 / FP8_MAX[fmt], dtype=torch.float64).to(torch.float32)
+    val = (amax_f32.to(torch.float32) * rcp).to(torch.float32)
+    bits = val.view(torch.int32)
+    exp = (bits >> 23) & 0xFF
+    man = bits & 0x7FFFFF
+    inc = (man > 0) & (exp != 0xFE) & ~((exp == 0) & (man <= 0x400000))
+    e = exp + inc.to(torch.int32)
+    e = torch.where(torch.isinf(val), torch.full_like(e, 0xFE), e)
+    return torch.where(torch.isnan(val), torch.full_like(e, 0xFF), e)
+
+
+def mx_multiplier(e: torch.Tensor) -> torch.Tensor:
+    """2^(127 - e) as fp32 (NaN for 0xFF): the factor a block's values are scaled by."""
+    m = torch.pow(2.0, (127 - e).to(torch.float64)).to(torch.float32)
+    return torch.where(e == 0xFF, torch.full_like(m, float("nan")), m)
+
+
+def quantize_mx(x: torch.Tensor, fmt: int, axis: int = -1):
+    """MXFP8 of bf16 x [R, C] with blocks along ``axis`` (-1: along rows, returns q [R, C]
+    and e [R, C/32]; 0: along columns, returned transposed, q [C, R] and e [C, R/32])."""
+    xt = x if axis == -1 else x.t().contiguous()
+    R, C = xt.shape
+    blocks = xt.reshape(R, C // MX_BLOCK, MX_BLOCK)
+    amax = blocks.abs().amax(dim=-1).to(torch.float32)
+    e = mx_exponent(amax, fmt)
+    q = cast_bcast(blocks, mx_multiplier(e)[..., None], fmt).reshape(R, C)
+    return q, e
+
+
+def dequant_mx(q: torch.Tensor, e: torch.Tensor, fmt: int) -> torch.Tensor:
+    """q * 2^(e - 127) per block, in fp64 (exact)."""
+    R, C = q.shape
+    v = q.view(TORCH_FP8[fmt]).to(torch.float64).reshape(R, C // MX_BLOCK, MX_BLOCK)
+    return (v * torch.pow(2.0, (e - 127).to(torch.float64))[..., None]).reshape(R, C)
+
+
+def scaled_mm_mx(aq, ae, bq, be, fmt=E4M3, *, bias=None):
+    """fp32 result of dequant_mx(A) @ dequant_mx(B).T (+ bias), accumulated in fp64."""
+    y = dequant_mx(aq, ae, fmt) @ dequant_mx(bq, be, fmt).T
+    if bias is not None:
+        y = y + bias.double()
+    return y.to(torch.float32)
+
+
+def mx_scale_rows(e: torch.Tensor) -> torch.Tensor:
+    """E8M0 bytes as the kernels store them: rows padded to a multiple of 4 bytes with 127."""
+    R, nb = e.shape
+    ld = (nb + 3) // 4 * 4
+    out = torch.full((R, ld), 127, dtype=torch.uint8)
+    out[:, :nb] = e.to(torch.uint8)
+    return out
+
+
+# ---------------------------------------------------------------------------------------
 # gated GELU chain and its backward  (bongard/te_linear.py:98-103, HF T5Gemma2MLP)
 # ---------------------------------------------------------------------------------------
 def geglu(g_bf16: torch.Tensor, u_bf16: torch.Tensor) -> torch.Tensor:

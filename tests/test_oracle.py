@@ -342,3 +342,78 @@ def test_linear_axiswise_recipes_track_the_bf16_linear(recipe):
         assert rel < 0.08, rel
     if recipe == "rowwise_with_gw_hp":
         assert torch.equal(dw, ref_dw.float())
+
+
+# ---- MXFP8 (TE MXFP8BlockScaling) ----------------------------------------------------------
+def _ceil_log2(v):
+    m, e = math.frexp(v)          # v = m * 2^e, 0.5 <= m < 1
+    return e - 1 if m == 0.5 else e
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_mx_exponent_is_ceil_log2_on_all_bf16_amaxes(fmt):
+    bits = torch.arange(0, 0x7F81, dtype=torch.int32).to(torch.int16)   # 0 .. +inf
+    amax = bits.view(torch.bfloat16).float()
+    got = orc.mx_exponent(amax, fmt)
+    rcp = float(np.float32(1.0 / orc.FP8_MAX[fmt]))
+    for a, e in zip(amax.tolist(), got.tolist()):
+        val = float(np.float32(np.float32(a) * np.float32(rcp)))
+        if math.isinf(val):
+            want = 0xFE
+        elif val == 0.0:
+            want = 0
+        else:
+            want = min(max(127 + _ceil_log2(val), 0), 0xFE)
+        assert e == want, (a, e, want)
+    assert orc.mx_exponent(torch.tensor([float("nan")]), fmt).item() == 0xFF
+
+
+def test_mx_known_answers():
+    x = torch.zeros(2, 32)
+    x[0, 3] = 448.0        # amax 448: val exactly 1.0 -> e = 127, q(448) = 0x7E
+    x[1, 0] = 1.0          # amax 1: val = 1/448 -> 2^-8 -> e = 119, x * 256 = 256 -> 0x78
+    x[1, 1] = -0.5
+    q, e = orc.quantize_mx(x.to(torch.bfloat16), E4M3)
+    assert e.tolist() == [[127], [119]]
+    assert q[0, 3].item() == 0x7E and q[1, 0].item() == 0x78 and q[1, 1].item() == 0xF0
+
+
+@pytest.mark.parametrize("fmt", [E4M3, E5M2])
+def test_mx_block_max_lands_in_top_binade(fmt):
+    g = torch.Generator().manual_seed(31)
+    x = (torch.randn(64, 256, generator=g) * torch.logspace(-20, 20, 64)[:, None]).to(torch.bfloat16)
+    q, e = orc.quantize_mx(x, fmt)
+    blocks = x.float().abs().reshape(64, 8, 32).amax(-1)
+    scaled = blocks.double() * torch.pow(2.0, (127 - e).double())
+    m = orc.FP8_MAX[fmt]
+    assert bool((scaled > m / 2).all()) and bool((scaled <= m * (1 + 2 ** -20)).all())
+    deq = orc.dequant_mx(q, e, fmt)
+    step = 2.0 ** -3 if fmt == E4M3 else 2.0 ** -2          # half the top-binade spacing
+    err = (deq - x.double()).abs().reshape(64, 8, 32).amax(-1)
+    assert bool((err <= step * blocks.double() + 1e-300).all())
+
+
+def test_mx_columnwise_is_rowwise_of_transpose_and_padding():
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(96, 64, generator=g).to(torch.bfloat16)
+    qc, ec = orc.quantize_mx(x, E4M3, 0)
+    qr, er = orc.quantize_mx(x.t().contiguous(), E4M3, -1)
+    assert torch.equal(qc, qr) and torch.equal(ec, er) and qc.shape == (64, 96)
+    rows = orc.mx_scale_rows(ec)          # 3 blocks -> 4 bytes, the last one 127
+    assert rows.shape == (64, 4) and bool((rows[:, 3] == 127).all())
+
+
+def test_scaled_mm_mx_brute_force():
+    g = torch.Generator().manual_seed(33)
+    a = (torch.randn(5, 64, generator=g) * torch.tensor([1e-3, 1.0, 30.0, 0.2, 5.0])[:, None]).to(torch.bfloat16)
+    b = (torch.randn(7, 64, generator=g) * 0.02).to(torch.bfloat16)
+    aq, ae = orc.quantize_mx(a, E4M3)
+    bq, be = orc.quantize_mx(b, E4M3)
+    y = orc.scaled_mm_mx(aq, ae, bq, be)
+    da = aq.view(torch.float8_e4m3fn).double()
+    db = bq.view(torch.float8_e4m3fn).double()
+    for i in range(5):
+        for j in range(7):
+            want = sum(da[i, k] * db[j, k] * 2.0 ** (int(ae[i, k // 32]) - 127)
+                       * 2.0 ** (int(be[j, k // 32]) - 127) for k in range(64))
+            assert abs(y[i, j].item() - want) <= 1e-6 * max(abs(want), 1e-30)
