@@ -25,7 +25,8 @@ import torch
 
 from . import linear as _linear
 from . import ops as _ops
-from .te_linear import RECIPES, _ScalingExtraState, _make_recipe, _new_scaling, _pad_rows, present
+from .te_linear import (RECIPES, _is_mx, _make_recipe, _new_scaling, _pad_rows, _ScalingExtraState,
+                        present)
 
 __all__ = ["RECIPES", "FusedMLP", "enable_fused_mlp", "hf_state_dict"]
 
@@ -133,14 +134,30 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
         self.counts['real_tokens'] += length
         self.counts['kernel_tokens'] += aligned
         fc1, fc2 = self.scaling if self.scaling is not None else (None, None)
+        mx = _is_mx(self.recipe)
         if first:
-            self._fp8_weights = (
-                _linear.quantize_gate_up(self.fc1_weight, self.intermediate_size,
-                                         split_scales=False, scaler=fc1 and fc1.weight),
-                _linear.quantize_weight(self.fc2_weight, transpose=True,
-                                        scaler=fc2 and fc2.weight))
+            if mx:
+                self._fp8_weights = (_linear.quantize_weight_mx(self.fc1_weight),
+                                     _linear.quantize_weight_mx(self.fc2_weight))
+            else:
+                self._fp8_weights = (
+                    _linear.quantize_gate_up(self.fc1_weight, self.intermediate_size,
+                                             split_scales=False, scaler=fc1 and fc1.weight),
+                    _linear.quantize_weight(self.fc2_weight, transpose=True,
+                                            scaler=fc2 and fc2.weight))
         gu_q, down_q = self._fp8_weights
         flat = flat.to(torch.bfloat16).contiguous()
+        if mx:
+            # block scales need no tensor-wide amax: the norm's partials go unused
+            if _ops.rmsnorm_supported(flat.shape[1]):
+                parts = torch.empty(_ops.rmsnorm_partials_count(flat.shape[0]),
+                                    dtype=torch.int32, device=flat.device)
+                normed = _FusedRMSNorm.apply(flat, self.layer_norm_weight, self.eps, parts)
+            else:
+                normed = _rms_norm(flat, self.layer_norm_weight, self.eps)
+            out = _linear.Fp8GegluMlpMxFunction.apply(normed, self.fc1_weight, self.fc2_weight,
+                                                      gu_q, down_q, self.intermediate_size)
+            return out[:length].reshape_as(x)
         count = _ops.rmsnorm_partials_count(flat.shape[0])
         if not _ops.rmsnorm_supported(flat.shape[1]):
             # rows wider than the fused kernel holds in registers: norm in torch ops on the

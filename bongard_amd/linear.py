@@ -161,6 +161,93 @@ class Fp8LinearAxiswiseFunction(torch.autograd.Function):
         return dx, dw, db, None
 
 
+def quantize_weight_mx(weight, *, transpose=True):
+    """MXFP8 copy of a weight [N, K]: blocks along K (forward), and with ``transpose`` the
+    [K, N] copy with blocks along N (the input-gradient GEMM's operand)."""
+    return ops.quantize_mx(weight.detach(), E4M3, rowwise=True, colwise=transpose)
+
+
+class Fp8LinearMxFunction(torch.autograd.Function):
+    """y = x @ W^T under TE's MXFP8BlockScaling (every tensor e4m3 in 32-element blocks
+    with E8M0 scales); x: bf16 [M, K] with M % 32 == 0 when grads are needed.
+
+      forward  y  = X8 . W8^T         blocks along K on both
+      dgrad    dX = dY8 . (W^T)8      dY blocks along N, W's columnwise copy
+      wgrad    dW = (dY^T)8 . (X^T)8  columnwise copies of dY and X (blocks along M)
+
+    Reference: te.Linear under the 'mxfp8' recipe (bongard/te_linear.py:17,38-39,73-74).
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, wq):
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        xq = ops.quantize_mx(x, E4M3, rowwise=True, colwise=need_dw)
+        if wq is None:
+            wq = quantize_weight_mx(weight, transpose=need_dx)
+        y = ops.gemm_mx(xq.data, xq.scales, wq.data, wq.scales)
+        ctx.save_for_backward(xq.data_t, xq.scales_t, wq.data_t if need_dx else None,
+                              wq.scales_t if need_dx else None)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x8t, xst, w8t, wst = ctx.saved_tensors
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dyq = ops.quantize_mx(dy.contiguous(), E4M3, rowwise=need_dx, colwise=need_dw)
+        dx = dw = None
+        if need_dx:
+            dx = ops.gemm_mx(dyq.data, dyq.scales, w8t, wst)
+        if need_dw:
+            dw = ops.gemm_mx(dyq.data_t, dyq.scales_t, x8t, xst)
+        return dx, dw, None
+
+
+class Fp8GegluMlpMxFunction(torch.autograd.Function):
+    """The gated MLP of :class:`Fp8GegluMlpFunction` under MXFP8 (e4m3 blocks of 32, E8M0
+    scales, gradients e4m3 too): gate/up GEMM with the gated-GELU epilogue, H quantized in
+    blocks (no tensor-wide amax), down GEMM; backward through dH, the gelu chain's dGU and
+    the dgrad/wgrad GEMMs on the columnwise copies. ``gu_q`` / ``down_q``: optional cached
+    MX weights (with their columnwise copies). Reference: TEMLP / FusedMLP (te.LayerNormMLP)
+    under 'mxfp8' (bongard/te_linear.py:98-103, bongard/fused_mlp.py:25-33)."""
+
+    @staticmethod
+    def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate):
+        I = int(intermediate)
+        need_dx, need_dgu, need_dd = ctx.needs_input_grad[:3]
+        train = need_dx or need_dgu or need_dd
+        xq = ops.quantize_mx(x, E4M3, rowwise=True, colwise=need_dgu)
+        if gu_q is None:
+            gu_q = quantize_weight_mx(w_gu, transpose=need_dx)
+        H, GU = ops.gemm_geglu_mx(xq.data, xq.scales, gu_q.data, gu_q.scales, I, keep_gu=train)
+        hq = ops.quantize_mx(H, E4M3, rowwise=True, colwise=need_dd)
+        if down_q is None:
+            down_q = quantize_weight_mx(w_down, transpose=need_dx or need_dgu)
+        y = ops.gemm_mx(hq.data, hq.scales, down_q.data, down_q.scales)
+        ctx.intermediate = I
+        ctx.save_for_backward(GU, xq.data_t, xq.scales_t, hq.data_t, hq.scales_t, gu_q.data_t,
+                              gu_q.scales_t, down_q.data_t, down_q.scales_t)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        GU, x8t, xst, h8t, hst, gu8t, gust, d8t, dst = ctx.saved_tensors
+        need_dx, need_dgu, need_dd = ctx.needs_input_grad[:3]
+        dyq = ops.quantize_mx(dy.contiguous(), E4M3, rowwise=need_dx or need_dgu,
+                              colwise=need_dd)
+        dx = dgu = dd = None
+        if need_dd:
+            dd = ops.gemm_mx(dyq.data_t, dyq.scales_t, h8t, hst)
+        if need_dx or need_dgu:
+            dH = ops.gemm_mx(dyq.data, dyq.scales, d8t, dst)
+            dGU, _ = ops.geglu_bwd(dH, GU)
+            dq = ops.quantize_mx(dGU, E4M3, rowwise=need_dx, colwise=need_dgu)
+            if need_dx:
+                dx = ops.gemm_mx(dq.data, dq.scales, gu8t, gust)
+            if need_dgu:
+                dgu = ops.gemm_mx(dq.data_t, dq.scales_t, x8t, xst)
+        return dx, dgu, dd, None, None, None
+
+
 class Fp8GegluMlpFunction(torch.autograd.Function):
     """y = down(gelu_tanh(x Wg^T) * (x Wu^T)) with every GEMM in FP8.
 

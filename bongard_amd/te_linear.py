@@ -18,8 +18,11 @@ gated-GELU fused into its epilogue and feeds H's FP8 copy to the down projection
 history of 16 and HYBRID formats: each projection keeps the histories of its input,
 weight and output gradient in ``_extra_state``, which is then non-empty, so export raises
 as the reference does for stateful scaling.
-'mxfp8' and 'nvfp4' are accepted by name but raise NotImplementedError when a module is
-built: their block-scaled kernels do not exist yet.
+'mxfp8' is TE's MXFP8BlockScaling: every tensor (gradients included) in e4m3 blocks of 32
+values sharing an E8M0 scale, on the gfx950 block-scaled MFMA
+(bongard_amd.linear.Fp8LinearMxFunction / Fp8GegluMlpMxFunction); stateless, so export
+works as for 'fp8'. 'nvfp4' is accepted by name but raises NotImplementedError when a
+module is built: NVFP4 (e4m3 scales per 16 values) has no bit-compatible gfx950 format.
 """
 
 import os
@@ -53,13 +56,27 @@ class DelayedScaling:
     amax_compute_algo: str = "max"
 
 
+@dataclass(frozen=True)
+class MXFP8BlockScaling:
+    """OCP MXFP8: 32-element blocks with E8M0 scales, e4m3 for every tensor (TE default)."""
+
+    fp8_format: str = "E4M3"
+
+
 def _make_recipe(name):
     if name == 'fp8':
         return Float8CurrentScaling()
     if name == 'fp8_delayed':
         return DelayedScaling()
+    if name == 'mxfp8':
+        return MXFP8BlockScaling()
     raise NotImplementedError(
-        f"TE recipe {name!r} (block scaling) has no gfx950 kernels yet; use 'fp8'")
+        f"TE recipe {name!r} has no gfx950 kernels (NVFP4's e4m3 block scales have no "
+        "gfx950 counterpart); use 'mxfp8' or 'fp8'")
+
+
+def _is_mx(recipe):
+    return isinstance(recipe, MXFP8BlockScaling)
 
 
 def _new_scaling(recipe):
@@ -154,8 +171,11 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
     def fp8_weight(self, is_first_microbatch):
         """Quantized weight (+ transposed copy); cached across microbatches like TE."""
         if is_first_microbatch or self._fp8_weight is None:
-            q = _linear.quantize_weight(self.weight, transpose=True,
-                                        scaler=self.scaling and self.scaling.weight)
+            if _is_mx(self.recipe):
+                q = _linear.quantize_weight_mx(self.weight, transpose=True)
+            else:
+                q = _linear.quantize_weight(self.weight, transpose=True,
+                                            scaler=self.scaling and self.scaling.weight)
             if is_first_microbatch is not None:
                 self._fp8_weight = q
             return q
@@ -178,8 +198,12 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
         flat, length, aligned = _pad_rows(flat)
         if flat.dtype != torch.bfloat16:
             flat = flat.to(torch.bfloat16)
-        out = _linear.Fp8LinearFunction.apply(flat, self.weight, None,
-                                              self.fp8_weight(first_microbatch), self.scaling)
+        if _is_mx(self.recipe):
+            out = _linear.Fp8LinearMxFunction.apply(flat, self.weight,
+                                                    self.fp8_weight(first_microbatch))
+        else:
+            out = _linear.Fp8LinearFunction.apply(flat, self.weight, None,
+                                                  self.fp8_weight(first_microbatch), self.scaling)
         if aligned != length:
             out = out[:length]
         return out.reshape(*x.shape[:-1], out.shape[-1])
@@ -230,6 +254,8 @@ class TEMLP(torch.nn.Module):
             flat = flat.to(torch.bfloat16)
         down_first = self.down._note_microbatch()
         down_q = self.down.fp8_weight(down_first)
+        if _is_mx(self.down.recipe):
+            return self._mx_forward(x, flat, length, aligned, down_q)
         if self.fused_gate_up:
             first = self.gate_up._note_microbatch()
             if first or self.gate_up._fp8_weight is None:
@@ -252,6 +278,30 @@ class TEMLP(torch.nn.Module):
             scaling = (self.gate_up.scaling, self.down.scaling)
         out = _linear.Fp8GegluMlpFunction.apply(flat, w_gu, self.down.weight, gu_q, down_q, I,
                                                 not self.fused_gate_up, scaling)
+        if aligned != length:
+            out = out[:length]
+        return out.reshape(*x.shape[:-1], out.shape[-1])
+
+
+    def _mx_forward(self, x, flat, length, aligned, down_q):
+        """MXFP8: blocks along K never straddle gate and up rows, so the stacked weight's
+        MX copy is the two projections' copies side by side (fused or split alike)."""
+        I = self.intermediate_size
+        if self.fused_gate_up:
+            first = self.gate_up._note_microbatch()
+            if first or self.gate_up._fp8_weight is None:
+                self.gate_up._fp8_weight = _linear.quantize_weight_mx(self.gate_up.weight)
+            gu_q = self.gate_up._fp8_weight
+            w_gu = self.gate_up.weight
+        else:
+            first_g = self.gate_proj._note_microbatch()
+            first_u = self.up_proj._note_microbatch()
+            if first_g or first_u or self._split_cache is None:
+                self._split_cache = _linear.quantize_weight_mx(
+                    torch.cat([self.gate_proj.weight, self.up_proj.weight], 0))
+            gu_q = self._split_cache
+            w_gu = _SplitGateUp.apply(self.gate_proj.weight, self.up_proj.weight)
+        out = _linear.Fp8GegluMlpMxFunction.apply(flat, w_gu, self.down.weight, gu_q, down_q, I)
         if aligned != length:
             out = out[:length]
         return out.reshape(*x.shape[:-1], out.shape[-1])

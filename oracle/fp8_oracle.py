@@ -345,6 +345,52 @@ def mx_scale_rows(e: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def linear_fwd_bwd_mx(x, w, dy):
+    """te.Linear under MXFP8 (every tensor e4m3 blocks): y = X8 W8^T; dX = dY8 (W^T)8 with
+    W's columnwise blocks; dW = (dY^T)8 (X^T)8 with columnwise blocks along M. fp32 out."""
+    xq, xe = quantize_mx(x, E4M3, -1)
+    wq, we = quantize_mx(w, E4M3, -1)
+    y = scaled_mm_mx(xq, xe, wq, we)
+    dq, de = quantize_mx(dy, E4M3, -1)
+    wtq, wte = quantize_mx(w, E4M3, 0)
+    dx = scaled_mm_mx(dq, de, wtq, wte)
+    dtq, dte = quantize_mx(dy, E4M3, 0)
+    xtq, xte = quantize_mx(x, E4M3, 0)
+    dw = scaled_mm_mx(dtq, dte, xtq, xte)
+    return y, dx, dw
+
+
+def mlp_fwd_bwd_mx(x, w_gate, w_up, w_down, dy):
+    """The gated MLP (te_linear TEMLP / te.LayerNormMLP) under MXFP8, forward and backward
+    through the same chain as the tensorwise ``mlp_forward`` / ``mlp_backward``.
+    Returns fp32 y, dx, dW_gate_up [2I, K], dW_down and the bf16 H."""
+    I = w_gate.shape[0]
+    wgu = torch.cat([w_gate, w_up], 0)
+    xq, xe = quantize_mx(x, E4M3, -1)
+    wq, we = quantize_mx(wgu, E4M3, -1)
+    g = scaled_mm_mx(xq, xe, wq[:I], we[:I]).to(torch.bfloat16)
+    u = scaled_mm_mx(xq, xe, wq[I:], we[I:]).to(torch.bfloat16)
+    h = geglu(g, u)
+    hq, he = quantize_mx(h, E4M3, -1)
+    dq_, de_ = quantize_mx(w_down, E4M3, -1)
+    y = scaled_mm_mx(hq, he, dq_, de_)
+    yq, ye = quantize_mx(dy, E4M3, -1)
+    wdt, wdte = quantize_mx(w_down, E4M3, 0)
+    dh = scaled_mm_mx(yq, ye, wdt, wdte)
+    yt, yte = quantize_mx(dy, E4M3, 0)
+    ht, hte = quantize_mx(h, E4M3, 0)
+    dwd = scaled_mm_mx(yt, yte, ht, hte)
+    dg, du = geglu_bwd(g, u, dh.to(torch.bfloat16))
+    dgu = torch.cat([dg, du], 1)
+    gq, ge = quantize_mx(dgu, E4M3, -1)
+    wgt, wgte = quantize_mx(wgu, E4M3, 0)
+    dx = scaled_mm_mx(gq, ge, wgt, wgte)
+    gt, gte = quantize_mx(dgu, E4M3, 0)
+    xt, xte = quantize_mx(x, E4M3, 0)
+    dwgu = scaled_mm_mx(gt, gte, xt, xte)
+    return dict(y=y, dx=dx, dwgu=dwgu, dwd=dwd, h=h)
+
+
 # ---------------------------------------------------------------------------------------
 # gated GELU chain and its backward  (bongard/te_linear.py:98-103, HF T5Gemma2MLP)
 # ---------------------------------------------------------------------------------------

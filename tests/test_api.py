@@ -87,9 +87,10 @@ def test_telinear_state_dict_and_eval():
 def test_telinear_rejects_bias_and_block_recipes():
     with pytest.raises(ValueError, match="bias-free"):
         te_linear.TELinear([nn.Linear(H, 16)], "fp8")
-    for r in ("mxfp8", "nvfp4"):
-        with pytest.raises(NotImplementedError):
-            te_linear.TELinear([nn.Linear(H, 16, bias=False)], r)
+    with pytest.raises(NotImplementedError, match="NVFP4"):
+        te_linear.TELinear([nn.Linear(H, 16, bias=False)], "nvfp4")
+    t = te_linear.TELinear([nn.Linear(H, 16, bias=False)], "mxfp8")
+    assert t.recipe.fp8_format == "E4M3" and t.state_dict()["_extra_state"].numel() == 0
 
 
 def test_temlp_eval_matches_hf_mlp():

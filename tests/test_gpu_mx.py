@@ -121,3 +121,131 @@ def test_gemm_geglu_mx(gpu, M, I, K):
     slack = 2.0 ** -20 * H_ref.float().abs().max()
     assert bool((diff <= 2 * ulp + slack).all()), "H beyond 2 bf16 ulps of the gelu chain"
     assert (diff > 0).float().mean().item() <= 0.05
+
+
+# ---- the TE modules under 'mxfp8' ------------------------------------------------------
+import types  # noqa: E402
+
+from torch import nn  # noqa: E402
+from transformers.models.t5gemma2.modeling_t5gemma2 import T5Gemma2MLP, T5Gemma2RMSNorm  # noqa: E402
+
+from bongard_amd import fused_mlp, te_linear  # noqa: E402
+
+
+def _close(got, ref, what, tol=0.01):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    excess = ((got - ref).abs() - 0.5 * orc.bf16_ulp(ref)).clamp(min=0).max().item()
+    rel = excess / max(_rms(ref), 1e-30)
+    print(f"[{what}] max(|err| - ulp/2)/RMS = {rel:.3e}", flush=True)
+    assert rel <= tol, what
+
+
+def _close_requant(got, ref, what, max_tol=0.05, rms_tol=0.005):
+    """H (and dGU) are requantized inside the chain: sparse legitimate fp8 flips where
+    GPU and oracle round a value to neighbouring bf16s; statistical bar as for 'fp8'."""
+    got, ref = got.float().cpu(), ref.float().cpu()
+    rms = max(_rms(ref), 1e-30)
+    max_rel = (got - ref).abs().max().item() / rms
+    rms_rel = _rms(got - ref) / rms
+    print(f"[{what}] max|err|/RMS = {max_rel:.3e}, RMS(err)/RMS = {rms_rel:.3e}", flush=True)
+    assert max_rel <= max_tol and rms_rel <= rms_tol, what
+
+
+def _mlp(hidden, inter, seed):
+    cfg = types.SimpleNamespace(hidden_size=hidden, intermediate_size=inter,
+                                hidden_activation="gelu_pytorch_tanh", dropout_rate=0.0)
+    torch.manual_seed(seed)
+    m = T5Gemma2MLP(cfg)
+    with torch.no_grad():
+        m.gate_proj.weight.normal_(std=0.02)
+        m.up_proj.weight.normal_(std=0.02)
+        m.down_proj.weight.normal_(std=0.014)
+    return m.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows", [256, 200])
+def test_telinear_mxfp8_fwd_bwd(gpu, rows):
+    g = torch.Generator().manual_seed(rows + 1)
+    x = torch.randn(rows, 512, generator=g).to(torch.bfloat16)
+    w = (torch.randn(384, 512, generator=g) * 0.02).to(torch.bfloat16)
+    dy = (torch.randn(rows, 384, generator=g) * 1e-3).to(torch.bfloat16)
+    lin = nn.Linear(512, 384, bias=False)
+    lin.weight.data = w.clone().float()
+    t = te_linear.TELinear([lin], "mxfp8").to(gpu).train()
+    xg = x.to(gpu).requires_grad_(True)
+    y = t(xg)
+    y.backward(dy.to(gpu))
+    torch.cuda.synchronize()
+    pad = (rows + 31) // 32 * 32 - rows
+    ry, rdx, rdw = orc.linear_fwd_bwd_mx(torch.nn.functional.pad(x, (0, 0, 0, pad)), w,
+                                         torch.nn.functional.pad(dy, (0, 0, 0, pad)))
+    _close(y, ry[:rows], "mx telinear y")
+    _close(xg.grad, rdx[:rows], "mx telinear dx")
+    _close(t.weight.grad, rdw, "mx telinear dw")
+    t(xg)
+    assert t.counts == {"weight_quantizations": 1, "cached_weights": 1}
+
+
+def _temlp_mx_step(gpu, mlp, x, dy, split, monkeypatch):
+    monkeypatch.setenv("BONGARD_TE_SPLIT_GATE_UP", "1" if split else "0")
+    t = te_linear.TEMLP(mlp, "mxfp8").to(gpu).train()
+    assert t.fused_gate_up != split
+    xg = x.to(gpu).requires_grad_(True)
+    y = t(xg)
+    y.backward(dy.to(gpu))
+    torch.cuda.synchronize()
+    dwgu = (t.gate_up.weight.grad if not split
+            else torch.cat([t.gate_proj.weight.grad, t.up_proj.weight.grad]))
+    return y, xg.grad, dwgu, t.down.weight.grad
+
+
+def test_temlp_mxfp8_fwd_bwd(gpu, monkeypatch):
+    """TEMLP under 'mxfp8' against the oracle chain (statistical bar: H and dGU are
+    requantized in blocks; where GPU and oracle round a block's largest element to
+    neighbouring bf16s across a power of two, the whole block's E8M0 scale moves and its 32
+    values requantize on a grid twice as coarse or fine, so single outputs can move by up to
+    ~0.1 RMS). The split gate/up layout (BONGARD_TE_SPLIT_GATE_UP=1) quantizes the same
+    blocks, so it must reproduce the fused layout bit for bit."""
+    hidden, inter, rows = 256, 512, 512
+    g = torch.Generator().manual_seed(61)
+    mlp = _mlp(hidden, inter, 61)
+    wg, wu, wd = (m.weight.detach().clone() for m in (mlp.gate_proj, mlp.up_proj, mlp.down_proj))
+    x = torch.randn(rows, hidden, generator=g).to(torch.bfloat16)
+    dy = (torch.randn(rows, hidden, generator=g) * 1e-3).to(torch.bfloat16)
+    fused = _temlp_mx_step(gpu, mlp, x, dy, False, monkeypatch)
+    split = _temlp_mx_step(gpu, mlp, x, dy, True, monkeypatch)
+    for a, b in zip(fused, split):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    ref = orc.mlp_fwd_bwd_mx(x, wg, wu, wd, dy)
+    y, dx, dwgu, dwd = fused
+    _close_requant(y, ref["y"], "mx temlp y", max_tol=0.10)
+    _close_requant(dx, ref["dx"], "mx temlp dx", max_tol=0.2)
+    _close_requant(dwgu, ref["dwgu"], "mx temlp dWgu", max_tol=0.2)
+    _close_requant(dwd, ref["dwd"], "mx temlp dWd", max_tol=0.2)
+
+
+def test_fused_mlp_mxfp8_fwd_bwd(gpu):
+    hidden, inter, rows = 256, 512, 480
+    g = torch.Generator().manual_seed(62)
+    mlp = _mlp(hidden, inter, 62)
+    norm = T5Gemma2RMSNorm(hidden, eps=1e-6).to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.normal_(std=0.1)
+    wg, wu, wd = (m.weight.detach().clone() for m in (mlp.gate_proj, mlp.up_proj, mlp.down_proj))
+    nw = norm.weight.detach().clone()
+    x = torch.randn(rows, hidden, generator=g).to(torch.bfloat16)
+    dy = (torch.randn(rows, hidden, generator=g) * 1e-3).to(torch.bfloat16)
+    f = fused_mlp.FusedMLP(mlp, norm, "mxfp8").to(gpu).train()
+    xg = x.to(gpu).requires_grad_(True)
+    y = f(xg)
+    y.backward(dy.to(gpu))
+    torch.cuda.synchronize()
+    xr = x.clone().requires_grad_(True)
+    normed = orc.rmsnorm(xr, nw, 1e-6)
+    ref = orc.mlp_fwd_bwd_mx(normed.detach(), wg, wu, wd, dy)
+    normed.backward(ref["dx"].to(torch.bfloat16))
+    _close_requant(y, ref["y"], "mx fused y", max_tol=0.10)
+    _close_requant(xg.grad, xr.grad, "mx fused dx", max_tol=0.2)
+    _close_requant(f.fc1_weight.grad, ref["dwgu"], "mx fused dWgu", max_tol=0.2)
+    _close_requant(f.fc2_weight.grad, ref["dwd"], "mx fused dWd", max_tol=0.2)
+    assert f.state_dict()["_extra_state"].numel() == 0

@@ -417,3 +417,30 @@ def test_scaled_mm_mx_brute_force():
             want = sum(da[i, k] * db[j, k] * 2.0 ** (int(ae[i, k // 32]) - 127)
                        * 2.0 ** (int(be[j, k // 32]) - 127) for k in range(64))
             assert abs(y[i, j].item() - want) <= 1e-6 * max(abs(want), 1e-30)
+
+
+def test_mx_chains_track_the_bf16_products():
+    """The MXFP8 linear and MLP chains: shapes, and every output within MX e4m3 error of
+    the unquantized products (a transposed operand or misplaced block would be far off)."""
+    g = torch.Generator().manual_seed(34)
+    x = torch.randn(64, 96, generator=g).to(torch.bfloat16)
+    w = (torch.randn(32, 96, generator=g) * 0.05).to(torch.bfloat16)
+    dy = (torch.randn(64, 32, generator=g) * 1e-3).to(torch.bfloat16)
+    y, dx, dw = orc.linear_fwd_bwd_mx(x, w, dy)
+    for got, ref in ((y, x.double() @ w.double().t()), (dx, dy.double() @ w.double()),
+                     (dw, dy.double().t() @ x.double())):
+        assert got.shape == ref.shape
+        assert (got.double() - ref).norm() / ref.norm() < 0.08
+    wg = (torch.randn(64, 96, generator=g) * 0.05).to(torch.bfloat16)
+    wu = (torch.randn(64, 96, generator=g) * 0.05).to(torch.bfloat16)
+    wd = (torch.randn(96, 64, generator=g) * 0.05).to(torch.bfloat16)
+    dyo = (torch.randn(64, 96, generator=g) * 1e-3).to(torch.bfloat16)
+    out = orc.mlp_fwd_bwd_mx(x, wg, wu, wd, dyo)
+    xr = x.double().requires_grad_(True)
+    gu = [t.double().requires_grad_(True) for t in (wg, wu, wd)]
+    yr = (F.gelu(xr @ gu[0].t(), approximate="tanh") * (xr @ gu[1].t())) @ gu[2].t()
+    yr.backward(dyo.double())
+    for got, ref in ((out["y"], yr.detach()), (out["dx"], xr.grad),
+                     (out["dwgu"], torch.cat([gu[0].grad, gu[1].grad])), (out["dwd"], gu[2].grad)):
+        assert got.shape == ref.shape
+        assert (got.double() - ref).norm() / ref.norm() < 0.12
