@@ -31,6 +31,7 @@ and two entries beyond the BASELINE configurations:
   fused_norm  FusedMLP's RMSNorm -> e4m3 fc1 input at [8192, 2560], fused kernel vs torch
   c1_rowwise  c1 under torchao's 'rowwise' recipe (per-row power-of-2 scales), and the
               per-row + per-column quantization of [8192, 2560]
+  c2_mxfp8    the c2 MLP forward under TE's 'mxfp8' recipe (block-scaled MFMA)
 
 ``cpu_baseline`` times the CPU oracle (torch CPU: amax, clamp, .to(float8), fp32 matmul,
 bf16 gelu chain -- torchao's emulate path) on the same c2 step, on this host's cores.
@@ -221,6 +222,7 @@ def main():
             "c5": _bench_c5(torch, workloads, dev),
             "fused_norm": _bench_norm(torch, ops, workloads, dev),
             "c1_rowwise": _bench_c1_rowwise(torch, ops, workloads, dev),
+            "c2_mxfp8": _bench_c2_mx(torch, ops, workloads, dev),
         }
 
     cpu = None
@@ -414,6 +416,44 @@ def _bench_c5(torch, workloads, dev, steps=10):
                         "weights re-quantized every step",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
             "frac_of_fp8_peak": round(flop / s / 1e12 / FP8_PEAK_TFLOPS, 4)}
+
+
+def _bench_c2_mx(torch, ops, workloads, dev, steps=30):
+    """The c2 MLP forward under TE's 'mxfp8' recipe: X, [W_gate; W_up], W_down quantized in
+    32-element blocks (E8M0 scales), gated-GELU GEMM on the block-scaled MFMA, H quantized
+    in blocks, down GEMM."""
+    c = workloads.config2()
+    x = c["x"].to(dev)
+    w_gu = torch.cat([c["w_gate"], c["w_up"]]).to(dev)
+    w_d = c["w_down"].to(dev)
+    M, K = x.shape
+    I = c["w_gate"].shape[0]
+
+    def step():
+        xq = ops.quantize_mx(x)
+        gq = ops.quantize_mx(w_gu)
+        dq = ops.quantize_mx(w_d)
+        H, _ = ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I)
+        hq = ops.quantize_mx(H)
+        return ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales)
+
+    s = _timed(torch, step, steps, 3)
+    xq, gq, dq = ops.quantize_mx(x), ops.quantize_mx(w_gu), ops.quantize_mx(w_d)
+    H, _ = ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I)
+    hq = ops.quantize_mx(H)
+    g_s = _ev_time(torch, lambda: ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I),
+                   steps)
+    d_s = _ev_time(torch, lambda: ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales), steps)
+    h_s = _ev_time(torch, lambda: ops.quantize_mx(H), steps)
+    flop = 2.0 * M * (2 * I * K + K * I)
+    return {"workload": f"c2 MLP forward [{M},{K}] x [2*{I},{K}] -> [{M},{I}] x [{K},{I}], MXFP8",
+            "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
+            "gemm_geglu_us": round(g_s * 1e6, 2),
+            "gemm_geglu_tflops": round(2.0 * M * 2 * I * K / g_s / 1e12, 1),
+            "gemm_down_us": round(d_s * 1e6, 2),
+            "gemm_down_tflops": round(2.0 * M * K * I / d_s / 1e12, 1),
+            "quantize_h_us": round(h_s * 1e6, 2),
+            "quantize_h_gbps": round((3.0 * M * I + M * I / 32) / h_s / 1e9, 1)}
 
 
 def _bench_c1_rowwise(torch, ops, workloads, dev, steps=50):

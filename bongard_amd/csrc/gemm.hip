@@ -41,15 +41,16 @@ struct TileInfo {
   double geglu_rate;  // the same with the gated-GELU epilogue; 0: no such variant (the
                       // gated GELU pairs gate and up sub-tiles, so FN must be even)
   const char* name;
-  bool mx;            // has an MX (block-scaled) variant: its stages fit the scale dwords
+  bool mx;            // has an MX (block-scaled) variant (tiles whose stages would overflow
+                      // the LDS with the scale dwords run it with one stage fewer)
 };
 
 // Rates are per-CU throughputs measured on MI355X (time per K step of one workgroup, with
 // every CU busy, over the tile's FLOP per step).
 constexpr TileInfo kTiles[NUM_TILES] = {
     {256, 256, 1, 9.6, 8.8, "256x256", true},
-    {256, 160, 1, 9.2, 0.0, "256x160", false},
-    {160, 256, 1, 9.0, 7.6, "160x256", false},
+    {256, 160, 1, 9.2, 0.0, "256x160", true},
+    {160, 256, 1, 9.0, 7.6, "160x256", true},
     {128, 128, 1, 8.0, 6.2, "128x128", true},
     {192, 256, 1, 9.0, 8.0, "192x256", true},
     {128, 64, 2, 6.5, 0.0, "128x64", true},

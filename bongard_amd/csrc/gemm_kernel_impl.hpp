@@ -662,27 +662,31 @@ template <class T>
 int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
                      hipStream_t stream, bool mx) {
   if (mx) {
-    // MX block scales: e4m3 operands; the tile's stages must fit the scale dwords too
-    if constexpr (T::NS * ((T::BM + T::BN) * kBK + 2048) * T::OCC <= 160 * 1024) {
-      const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads);
-      if (epi == EPI_GEGLU) {
-        if constexpr (T::FN % 2 == 0) {
-          hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI_GEGLU, BF8_OUT_BF16, true>), grid, block,
-                             0, stream, p);
-          return launch_status("gemm_kernel(geglu, mx)");
-        }
-      } else if (out_dtype == BF8_OUT_BF16) {
-        hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI_LINEAR, BF8_OUT_BF16, true>), grid, block, 0,
+    // MX block scales (e4m3 operands): each stage also holds 2 KB of scale dwords; a tile
+    // whose stages would then overflow the LDS runs with one stage fewer.
+    constexpr bool kFits = T::NS * ((T::BM + T::BN) * kBK + 2048) * T::OCC <= 160 * 1024;
+    using TM = std::conditional_t<kFits, T,
+                                  GemmTile<T::WM, T::WN, T::FM, T::FN, T::NS - 1, T::OCC>>;
+    static_assert(TM::NS * ((TM::BM + TM::BN) * kBK + 2048) * TM::OCC <= 160 * 1024,
+                  "MX stages do not fit the LDS");
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads);
+    if (epi == EPI_GEGLU) {
+      if constexpr (TM::FN % 2 == 0) {
+        hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_GEGLU, BF8_OUT_BF16, true>), grid, block, 0,
                            stream, p);
-        return launch_status("gemm_kernel(mx)");
+        return launch_status("gemm_kernel(geglu, mx)");
       } else {
-        hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI_LINEAR, BF8_OUT_F32, true>), grid, block, 0,
-                           stream, p);
-        return launch_status("gemm_kernel(mx)");
+        set_error("gemm: tile %dx%d has no gated-GELU variant", T::BM, T::BN);
+        return BF8_EINVAL;
       }
+    } else if (out_dtype == BF8_OUT_BF16) {
+      hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_BF16, true>), grid, block, 0,
+                         stream, p);
+    } else {
+      hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_F32, true>), grid, block, 0,
+                         stream, p);
     }
-    set_error("gemm: tile %dx%d has no MX variant for this epilogue", T::BM, T::BN);
-    return BF8_EINVAL;
+    return launch_status("gemm_kernel(mx)");
   }
   if (epi == EPI_GEGLU) {
     if constexpr (T::FN % 2 == 0) {

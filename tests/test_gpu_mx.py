@@ -249,3 +249,12 @@ def test_fused_mlp_mxfp8_fwd_bwd(gpu):
     _close_requant(f.fc1_weight.grad, ref["dwgu"], "mx fused dWgu", max_tol=0.2)
     _close_requant(f.fc2_weight.grad, ref["dwd"], "mx fused dWd", max_tol=0.2)
     assert f.state_dict()["_extra_state"].numel() == 0
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x160", "160x256", "128x128", "192x256",
+                                  "128x64", "64x128"])
+def test_gemm_mx_every_tile(gpu, monkeypatch, tile):
+    """Every block tile's MX variant (those whose stages would overflow the LDS with the
+    scale dwords run with one stage fewer), forced through the tuning override."""
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", tile)
+    _mx_gemm_case(gpu, 300, 392, 544, seed=17)
