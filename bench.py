@@ -32,6 +32,7 @@ and two entries beyond the BASELINE configurations:
   c1_rowwise  c1 under torchao's 'rowwise' recipe (per-row power-of-2 scales), and the
               per-row + per-column quantization of [8192, 2560]
   c2_mxfp8    the c2 MLP forward under TE's 'mxfp8' recipe (block-scaled MFMA)
+  state_kv    the decoder's state-bank K/V projection of the c3 packed state
 
 ``cpu_baseline`` times the CPU oracle (torch CPU: amax, clamp, .to(float8), fp32 matmul,
 bf16 gelu chain -- torchao's emulate path) on the same c2 step, on this host's cores.
@@ -42,6 +43,7 @@ import json
 import os
 import sys
 import time
+import types
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -223,6 +225,7 @@ def main():
             "fused_norm": _bench_norm(torch, ops, workloads, dev),
             "c1_rowwise": _bench_c1_rowwise(torch, ops, workloads, dev),
             "c2_mxfp8": _bench_c2_mx(torch, ops, workloads, dev),
+            "state_kv": _bench_state_kv(torch, workloads, dev),
         }
 
     cpu = None
@@ -416,6 +419,44 @@ def _bench_c5(torch, workloads, dev, steps=10):
                         "weights re-quantized every step",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
             "frac_of_fp8_peak": round(flop / s / 1e12 / FP8_PEAK_TFLOPS, 4)}
+
+
+def _bench_state_kv(torch, workloads, dev, steps=20):
+    """The decoder's state-bank K/V projection (once per decoder layer) on the c3 packed
+    state [M, 2560] with cached FP8 k/v weights: the shared-input form (state quantized
+    once) against the two separate projection calls of the reference form."""
+    from torch import nn
+
+    from bongard_amd import state_kv, te_linear
+
+    c = workloads.config3()
+    x = c["x"].to(dev)
+    M, K = x.shape
+    head_dim = 256
+
+    def proj(w):
+        lin = nn.Linear(K, w.shape[0], bias=False)
+        lin.weight.data = w.float()
+        return te_linear.TELinear([lin], "fp8").to(dev).train()
+
+    att = types.SimpleNamespace(k_proj=proj(c["w_k"]), v_proj=proj(c["w_v"]),
+                                k_norm=nn.Identity(), head_dim=head_dim)
+    state = x.reshape(1, M, K)
+
+    def shared():
+        with torch.no_grad():
+            return state_kv.project_state_kv(att, state)
+
+    def separate():
+        with torch.no_grad():
+            return att.k_proj(state), att.v_proj(state)
+
+    s_sh = _timed(torch, shared, steps, 3)
+    s_sep = _timed(torch, separate, steps, 3)
+    flop = 2.0 * M * K * (c["w_k"].shape[0] + c["w_v"].shape[0])
+    return {"workload": f"k/v projections of a packed state [{M},{K}] on cached FP8 weights",
+            "shared_input_us": round(s_sh * 1e6, 2), "separate_calls_us": round(s_sep * 1e6, 2),
+            "shared_input_tflops": round(flop / s_sh / 1e12, 1)}
 
 
 def _bench_c2_mx(torch, ops, workloads, dev, steps=30):

@@ -256,3 +256,82 @@ def test_fused_mlp_delayed_train_steps(gpu):
         f.fc2_weight.grad = None
     fc1, _ = f.scaling
     assert fc1.input.recorded == 2
+
+
+def test_telinear_second_call_per_step_reuses_cached_weight(gpu):
+    """The decoder's state-bank K/V projection (bongard/model.py:342-347, 349-359) calls a
+    layer's k_proj / v_proj a second time in the same step, on the encoded state: the
+    second call reuses the step's FP8 weight (no re-quantization), and the weight gradient
+    is the sum of both calls' wgrad GEMMs."""
+    g = torch.Generator().manual_seed(91)
+    hidden, out = 512, 256
+    x = torch.randn(160, hidden, generator=g).to(torch.bfloat16)       # decoder tokens
+    state = torch.randn(2, 96, hidden, generator=g).to(torch.bfloat16)  # encoded state bank
+    w = (torch.randn(out, hidden, generator=g) * 0.02).to(torch.bfloat16)
+    dy1 = (torch.randn(160, out, generator=g) * 1e-3).to(torch.bfloat16)
+    dy2 = (torch.randn(2, 96, out, generator=g) * 1e-3).to(torch.bfloat16)
+    lin = nn.Linear(hidden, out, bias=False)
+    lin.weight.data = w.clone().float()
+    t = te_linear.TELinear([lin], "fp8").to(gpu).train()
+    xg = x.to(gpu).requires_grad_(True)
+    sg = state.to(gpu).requires_grad_(True)
+    y1 = t(xg)
+    y2 = t(sg)
+    assert t.counts == {"weight_quantizations": 1, "cached_weights": 1}
+    (y1.float() * dy1.to(gpu).float()).sum().add_((y2.float() * dy2.to(gpu).float()).sum()).backward()
+    torch.cuda.synchronize()
+    s_flat = state.reshape(-1, hidden)
+    r1 = orc.linear_fwd_bwd(x, w, dy1)
+    r2 = orc.linear_fwd_bwd(s_flat, w, dy2.reshape(-1, out))
+    _close(y1, r1[0], "state pass 1 y")
+    _close(y2.reshape(-1, out), r2[0], "state pass 2 y")
+    _close(xg.grad, r1[1], "state pass 1 dx")
+    _close(sg.grad.reshape(-1, hidden), r2[1], "state pass 2 dx")
+    # two bf16-rounded wgrads summed in bf16: half an ulp of each term and of the sum
+    got, ref = t.weight.grad.float().cpu(), r1[2] + r2[2]
+    slack = 0.5 * (orc.bf16_ulp(r1[2]) + orc.bf16_ulp(r2[2]) + orc.bf16_ulp(ref))
+    rel = ((got - ref).abs() - slack).clamp(min=0).max().item() / _rms(ref)
+    print(f"[summed dW] max(|err| - rounding)/RMS = {rel:.3e}", flush=True)
+    assert rel <= 0.01
+
+
+def test_state_kv_shared_input_matches_separate_calls(gpu):
+    """bongard_amd.state_kv.project_state_kv (one quantization of the state for k and v)
+    against the reference form (k_proj(state), v_proj(state)) on copies of the same
+    projections: outputs and all gradients bit-identical; counters as two calls."""
+    from bongard_amd import state_kv
+
+    g = torch.Generator().manual_seed(92)
+    hidden, nk, head_dim = 512, 256, 64
+    state = torch.randn(3, 64, hidden, generator=g).to(torch.bfloat16)
+    wk = (torch.randn(nk, hidden, generator=g) * 0.02).to(torch.bfloat16)
+    wv = (torch.randn(nk, hidden, generator=g) * 0.02).to(torch.bfloat16)
+    dk = (torch.randn(3, nk // head_dim, 64, head_dim, generator=g) * 1e-3).to(torch.bfloat16)
+    dv = (torch.randn(3, nk // head_dim, 64, head_dim, generator=g) * 1e-3).to(torch.bfloat16)
+
+    def attention():
+        lk, lv = nn.Linear(hidden, nk, bias=False), nn.Linear(hidden, nk, bias=False)
+        lk.weight.data, lv.weight.data = wk.clone().float(), wv.clone().float()
+        norm = T5Gemma2RMSNorm(head_dim, eps=1e-6).to(torch.bfloat16).to(gpu)
+        return types.SimpleNamespace(
+            k_proj=te_linear.TELinear([lk], "fp8").to(gpu).train(),
+            v_proj=te_linear.TELinear([lv], "fp8").to(gpu).train(),
+            k_norm=norm, head_dim=head_dim)
+
+    results = []
+    for fused in (True, False):
+        att = attention()
+        sg = state.to(gpu).requires_grad_(True)
+        if fused:
+            keys, values = state_kv.project_state_kv(att, sg)
+        else:
+            shape = (*sg.shape[:-1], -1, head_dim)
+            keys = att.k_norm(att.k_proj(sg).view(shape).transpose(1, 2))
+            values = att.v_proj(sg).view(shape).transpose(1, 2)
+        ((keys.float() * dk.to(gpu).float()).sum()
+         + (values.float() * dv.to(gpu).float()).sum()).backward()
+        torch.cuda.synchronize()
+        assert att.k_proj.counts == {"weight_quantizations": 1}
+        results.append((keys, values, sg.grad, att.k_proj.weight.grad, att.v_proj.weight.grad))
+    for a, b in zip(*results):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
