@@ -194,12 +194,28 @@ __global__ __launch_bounds__(kColNT) void axis_col_scale_kernel(
   const int v = blockIdx.x * 8 + cg;
   uint4 k = make_uint4(0u, 0u, 0u, 0u);
   if (v < nvec) {
+    // four independent loads in flight per thread (the partial rows are a latency-bound
+    // gather of ~nblk / 32 loads each)
     const uint4* src = reinterpret_cast<const uint4*>(colpart);
-    for (int b = rg; b < nblk; b += 32) {
-      const uint4 o = src[(int64_t)b * nvec + v];
-      k = make_uint4(pk_max_u16(k.x, o.x), pk_max_u16(k.y, o.y), pk_max_u16(k.z, o.z),
-                     pk_max_u16(k.w, o.w));
+    uint4 k4[4] = {k, k, k, k};
+    int b = rg;
+    for (; b + 96 < nblk; b += 128) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint4 o = src[(int64_t)(b + 32 * u) * nvec + v];
+        k4[u] = make_uint4(pk_max_u16(k4[u].x, o.x), pk_max_u16(k4[u].y, o.y),
+                           pk_max_u16(k4[u].z, o.z), pk_max_u16(k4[u].w, o.w));
+      }
     }
+    for (; b < nblk; b += 32) {
+      const uint4 o = src[(int64_t)b * nvec + v];
+      k4[0] = make_uint4(pk_max_u16(k4[0].x, o.x), pk_max_u16(k4[0].y, o.y),
+                         pk_max_u16(k4[0].z, o.z), pk_max_u16(k4[0].w, o.w));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      k = make_uint4(pk_max_u16(k.x, k4[u].x), pk_max_u16(k.y, k4[u].y), pk_max_u16(k.z, k4[u].z),
+                     pk_max_u16(k.w, k4[u].w));
   }
   red[rg][cg] = k;
   __syncthreads();

@@ -18,7 +18,7 @@ namespace bf8 {
 namespace {
 
 constexpr int kNormNT = 256;            // four waves, one row per wave at a time
-constexpr int kMaxNormBlocks = 1024;    // amax partials stay below the cast's inline limit
+constexpr int kMaxNormBlocks = 1024;    // amax partials stay within the cast's inline limit
 constexpr int kMaxVecPerLane = 8;       // 16-byte vectors of a row per lane (cols <= 4096)
 
 int64_t norm_blocks(int64_t rows) {
@@ -33,8 +33,21 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return v;
 }
 
-// One wave per row (grid-stride over rows). Lane l holds the row's 16-byte vectors
-// l, l + 64, ... (V of them, cols = 8 * 64 * V at most).
+// One wave per row (grid-stride over rows), the next row's loads issued before the current
+// row is reduced and written. Lane l holds the row's 16-byte vectors l, l + 64, ... (V of
+// them, cols = 8 * 64 * V at most).
+template <int V>
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ x, int64_t row,
+                                         int64_t rows, int cols, int lane, uint4* xv) {
+  const int nvec = cols >> 3;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int v = lane + 64 * j;
+    xv[j] = (row < rows && v < nvec) ? xr[v] : make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
 template <int V>
 __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(
     const uint16_t* __restrict__ x, int64_t rows, int cols, const uint16_t* __restrict__ gamma,
@@ -43,30 +56,23 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int nvec = cols >> 3;
-  // the lane's gamma factors, the same for every row
-  float gf[V][8];
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  int64_t row = (int64_t)blockIdx.x * 4 + wid;
+  uint4 xv[V];
+  load_row<V>(x, row, rows, cols, lane, xv);
+  // the lane's gamma vectors (bf16, the same for every row; the factor 1 + gamma is formed
+  // per use, which keeps half the registers of holding it in fp32)
+  uint4 gv[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
     const int v = lane + 64 * j;
-    uint4 g = make_uint4(0u, 0u, 0u, 0u);
-    if (v < nvec) g = reinterpret_cast<const uint4*>(gamma)[v];
-    const uint32_t w[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = bf16_lo(w[e]), hi = bf16_hi(w[e]);
-      gf[j][2 * e] = zero_centered ? 1.0f + lo : lo;
-      gf[j][2 * e + 1] = zero_centered ? 1.0f + hi : hi;
-    }
+    gv[j] = v < nvec ? reinterpret_cast<const uint4*>(gamma)[v] : make_uint4(0u, 0u, 0u, 0u);
   }
+  const float g0 = zero_centered ? 1.0f : 0.0f;
   uint32_t m = 0;
-  for (int64_t row = (int64_t)blockIdx.x * 4 + wid; row < rows; row += (int64_t)gridDim.x * 4) {
-    const uint4* xr = reinterpret_cast<const uint4*>(x + row * cols);
-    uint4 xv[V];
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const int v = lane + 64 * j;
-      xv[j] = v < nvec ? xr[v] : make_uint4(0u, 0u, 0u, 0u);
-    }
+  for (; row < rows; row += stride) {
+    uint4 nx[V];
+    load_row<V>(x, row + stride, rows, cols, lane, nx);
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
@@ -88,11 +94,12 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(
       const int v = lane + 64 * j;
       if (v < nvec) {
         const uint32_t w[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        const uint32_t gw[4] = {gv[j].x, gv[j].y, gv[j].z, gv[j].w};
         uint32_t o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float a = (bf16_lo(w[e]) * r) * gf[j][2 * e];
-          const float b = (bf16_hi(w[e]) * r) * gf[j][2 * e + 1];
+          const float a = (bf16_lo(w[e]) * r) * (g0 + bf16_lo(gw[e]));
+          const float b = (bf16_hi(w[e]) * r) * (g0 + bf16_hi(gw[e]));
           o[e] = f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
         }
         const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
@@ -100,6 +107,8 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(
         yr[v] = ov;
       }
     }
+#pragma unroll
+    for (int j = 0; j < V; ++j) xv[j] = nx[j];
   }
   m = block_max_u32<kNormNT>(m);
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
@@ -131,18 +140,19 @@ int bf8_rmsnorm_bf16(const void* x, int64_t rows, int64_t cols, const void* gamm
   const uint16_t* xs = (const uint16_t*)x;
   const uint16_t* gs = (const uint16_t*)gamma;
   uint16_t* ys = (uint16_t*)y;
-  if (nvec_lane <= 1)
-    hipLaunchKernelGGL(rmsnorm_kernel<1>, grid, block, 0, s, xs, rows, (int)cols, gs, eps,
-                       zero_centered, ys, rstd, partials);
-  else if (nvec_lane <= 2)
-    hipLaunchKernelGGL(rmsnorm_kernel<2>, grid, block, 0, s, xs, rows, (int)cols, gs, eps,
-                       zero_centered, ys, rstd, partials);
-  else if (nvec_lane <= 4)
-    hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, block, 0, s, xs, rows, (int)cols, gs, eps,
-                       zero_centered, ys, rstd, partials);
-  else
-    hipLaunchKernelGGL(rmsnorm_kernel<8>, grid, block, 0, s, xs, rows, (int)cols, gs, eps,
-                       zero_centered, ys, rstd, partials);
+#define BF8_NORM(VV)                                                                      \
+  hipLaunchKernelGGL(rmsnorm_kernel<VV>, grid, block, 0, s, xs, rows, (int)cols, gs, eps, \
+                     zero_centered, ys, rstd, partials)
+  switch (nvec_lane) {
+    case 1: BF8_NORM(1); break;
+    case 2: BF8_NORM(2); break;
+    case 3: BF8_NORM(3); break;
+    case 4: BF8_NORM(4); break;
+    case 5: BF8_NORM(5); break;
+    case 6: BF8_NORM(6); break;
+    default: BF8_NORM(8); break;
+  }
+#undef BF8_NORM
   return launch_status("rmsnorm_kernel");
 }
 

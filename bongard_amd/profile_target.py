@@ -8,7 +8,10 @@ FETCH_SIZE / WRITE_SIZE counters into bytes.
 
 ``c2``: the whole config-2 MLP forward (quantize X and weights, gate/up GEMM + gated-GELU
 epilogue, H scale + cast, down GEMM). ``square``: one 8192^3 e4m3 GEMM, the steady-state
-main loop with no epilogue-heavy work.
+main loop with no epilogue-heavy work. ``recipes``: the kernels of the other recipes and
+the fused norm: the config-2 MLP forward under MXFP8 (block quantize, MX gated-GELU GEMM,
+MX down GEMM), the axiswise (torchao rowwise) quantization of a [8192, 2560] activation
+per row and per column, and the fused RMSNorm of the same activation.
 """
 
 import argparse
@@ -24,7 +27,7 @@ def main():
     p = argparse.ArgumentParser()
     p.add_argument("--iters", type=int, default=5)
     p.add_argument("--rows", type=int, default=4096)
-    p.add_argument("--case", choices=("c2", "square"), default="c2")
+    p.add_argument("--case", choices=("c2", "square", "recipes"), default="c2")
     args = p.parse_args()
     dev = torch.device("cuda:0")
     if args.case == "square":
@@ -36,6 +39,9 @@ def main():
             ops.gemm(aq.data, ops.E4M3, aq.meta, bq.data, ops.E4M3, bq.meta)
         torch.cuda.synchronize()
         print(f"profile_target done: {args.iters} x 8192^3 GEMM", flush=True)
+        return
+    if args.case == "recipes":
+        _recipes(dev, args.iters)
         return
     c = workloads.config2(rows=args.rows)
     I = workloads.INTERMEDIATE
@@ -55,6 +61,28 @@ def main():
         ops.gemm(hq.data, ops.E4M3, hm, dq.data, ops.E4M3, dq.meta)
     torch.cuda.synchronize()
     print(f"profile_target done: {args.iters} iterations, copy {COPY_BYTES} bytes", flush=True)
+
+
+def _recipes(dev, iters):
+    c = workloads.config2()
+    I = workloads.INTERMEDIATE
+    x = c["x"].to(dev)
+    w_gu = torch.cat([c["w_gate"], c["w_up"]], 0).to(dev)
+    w_d = c["w_down"].to(dev)
+    a = workloads.config5()["x"].to(dev)
+    gamma = torch.zeros(a.shape[1], dtype=torch.bfloat16, device=dev)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        dst.copy_(src)
+        xq, gq, dq = ops.quantize_mx(x), ops.quantize_mx(w_gu), ops.quantize_mx(w_d)
+        H, _ = ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I)
+        hq = ops.quantize_mx(H)
+        ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales)
+        ops.quantize_axiswise(a, ops.E4M3, rowwise=True, colwise=True)
+        ops.rmsnorm(a, gamma, 1e-6)
+    torch.cuda.synchronize()
+    print(f"profile_target done: {iters} iterations (recipes), copy {COPY_BYTES} bytes", flush=True)
 
 
 if __name__ == "__main__":
