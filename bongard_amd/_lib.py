@@ -41,6 +41,10 @@ SIGNATURES = {
     "bf8_cast_delayed_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int, c_int,
                                       c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p]),
+    "bf8_geglu_bwd_delayed_partials": (c_int64, [c_int64, c_int64]),
+    "bf8_geglu_bwd_delayed": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int,
+                                      c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,
+                                      c_void_p, c_void_p, c_void_p]),
     "bf8_axiswise_workspace": (c_size_t, [c_int64, c_int64]),
     "bf8_quantize_axiswise_bf16": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
                                            c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

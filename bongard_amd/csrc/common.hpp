@@ -171,7 +171,8 @@ __device__ __forceinline__ float gelu_tanh_f32(float x) {
 
 // gelu_tanh and its derivative, both from s = 1 / (1 + exp(-2u)) = 0.5 (1 + tanh(u)):
 //   y = x s,   dy/dx = s + 2 x s (1 - s) u',  u' = sqrt(2/pi) (1 + 3 * 0.044715 x^2),
-// with 1 - s = e s (e = exp(-2u)) to avoid cancellation. y is bit-identical to
+// with 1 - s = e s (e = exp(-2u)) to avoid cancellation (and 1 - s = 1 where e
+// overflows, so the derivative stays finite for large negative x). y is bit-identical to
 // gelu_tanh_f32(x), so the backward sees the forward's activation.
 __device__ __forceinline__ void gelu_tanh_fwd_bwd(float x, float& y, float& dydx) {
   const float kBeta = 0.7978845608028654f;
@@ -182,7 +183,9 @@ __device__ __forceinline__ void gelu_tanh_fwd_bwd(float x, float& y, float& dydx
   const float s = __builtin_amdgcn_rcpf(1.0f + e);
   y = x * s;
   const float du = kBeta * (1.0f + 3.0f * kKappa * (x * x));
-  dydx = s + 2.0f * x * (s * s * e) * du;
+  // 1 - s = e s; where exp(-2u) overflows (x below about -10) s is 0 and 1 - s is 1
+  const float oms = e > 1e30f ? 1.0f : s * e;
+  dydx = s + 2.0f * x * (s * oms) * du;
 }
 
 // ---- scale from an amax key --------------------------------------------------------

@@ -314,12 +314,15 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
             return dx, dgu, dd, None, None, None, None, None, None
         dH = ops.gemm(dyq.data, E5M2, dyq.meta, d8t, E4M3, d_meta)
         if gs is not None:
+            # delayed scaling: dGU's scale is known already, so the gelu backward writes
+            # fp8 dGU (and its transpose) in the same pass
             M = dH.shape[0]
-            count = ops.geglu_bwd_partials_count(M, I)
-            dGU, _ = ops.geglu_bwd(
-                dH, GU, partials=gs.grad_output.partials_for_producer(count, dH.device))
-            dq = gs.grad_output.quantize(dGU, rowwise=need_dx, transpose=need_dgu,
-                                         producer_count=count)
+            count = ops.geglu_bwd_delayed_partials_count(M, I)
+            scaler = gs.grad_output
+            dq = scaler.produce(count, dH.device, lambda st, L, pos, prev, parts:
+                                ops.geglu_bwd_delayed(dH, GU, st, L, pos, prev, scaler.fmt,
+                                                      rowwise=need_dx, transpose=need_dgu,
+                                                      partials_out=parts))
             if need_dx:
                 dx = ops.gemm(dq.data, E5M2, dq.meta, gu8t, E4M3, gu_meta[0])
             if need_dgu:

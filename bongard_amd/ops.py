@@ -516,6 +516,32 @@ def rmsnorm(x, weight, eps, *, zero_centered=True, want_rstd=False, partials=Non
     return y, rstd, parts
 
 
+def geglu_bwd_delayed_partials_count(M, intermediate):
+    return int(_lib.lib().bf8_geglu_bwd_delayed_partials(int(M), int(intermediate)))
+
+
+def geglu_bwd_delayed(dH, GU, state, length, pos, prev_partials, fmt=E5M2, *, rowwise=True,
+                      transpose=False, partials_out, meta_out=None):
+    """dGU of the gated GELU quantized at once with a delayed scale (``cast_delayed``
+    semantics for state / pos / prev_partials / meta_out); returns the :class:`Fp8Tensor`
+    of dGU [M, 2I] (``data`` and/or ``data_t``). ``partials_out`` receives this step's
+    amax partials (``geglu_bwd_delayed_partials_count`` entries)."""
+    _require_gpu(dH, GU, state)
+    dH = dH.contiguous()
+    M, I = dH.shape
+    dev = dH.device
+    if meta_out is None:
+        meta_out = new_meta(dev)
+    out = torch.empty((M, 2 * I), dtype=TORCH_FP8[fmt], device=dev) if rowwise else None
+    out_t = torch.empty((2 * I, M), dtype=TORCH_FP8[fmt], device=dev) if transpose else None
+    n_prev = 0 if prev_partials is None else prev_partials.numel()
+    _lib.check(_lib.lib().bf8_geglu_bwd_delayed(
+        _ptr(dH), _ptr(GU), M, I, _ptr(state), int(length), int(pos), _ptr(prev_partials),
+        n_prev, fmt, _ptr(meta_out), _ptr(out), _ptr(out_t), _ptr(partials_out), _stream(dev)),
+        "bf8_geglu_bwd_delayed")
+    return Fp8Tensor(out, out_t, meta_out, fmt, M, 2 * I)
+
+
 def new_delayed_state(length, device):
     """Delayed-scaling state: float32 [length + 4] = history, {amax, scale, scale_inv, pos}."""
     st = torch.zeros(length + 4, dtype=torch.float32, device=device)

@@ -80,6 +80,21 @@ class DelayedScaler:
         self._slot ^= 1
         return q
 
+    def produce(self, count, device, launch):
+        """Runs a kernel that produces this role's tensor and casts it with the role's
+        delayed scale in the same pass: ``launch(state, length, pos, prev_partials,
+        partials_out)`` (the arguments of ``cast_delayed``) returns the FP8 tensor and
+        writes ``count`` amax partials of the new tensor into ``partials_out``."""
+        self._ensure(device)
+        out_parts = self._buffer(self._slot, count, device)
+        prev = self._bufs[self._slot ^ 1][:self._pending] if self._pending else None
+        q = launch(self.state, self.length, self.recorded % self.length, prev, out_parts)
+        if prev is not None:
+            self.recorded += 1
+        self._pending = int(count)
+        self._slot ^= 1
+        return q
+
     # -- persistence (``_extra_state``) -------------------------------------------------
     def to_tensor(self):
         """float32 [3 + length + 4] on the CPU: length, amaxes recorded, format, state."""

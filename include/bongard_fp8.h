@@ -184,6 +184,20 @@ int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* stat
                           float* meta_out, uint8_t* out, uint8_t* out_t, uint32_t* partials_out,
                           void* stream);
 
+/* bf8_geglu_bwd fused with the delayed-scaling cast of its output (bf8_cast_delayed_bf16
+ * semantics for state / len / pos / prev_partials / meta_out): for the 'fp8_delayed'
+ * recipe, whose dGU scale is known before dGU exists. Writes dGU in fp8 directly, as
+ * out [M, 2I] and/or out_t [2I, M], and this step's amax partials of |dGU| into
+ * partials_out [bf8_geglu_bwd_delayed_partials(M, I)]; no bf16 dGU round trip. Bytes
+ * equal bf8_geglu_bwd followed by bf8_cast_delayed_bf16. I % 64 == 0, M % 16 == 0,
+ * n_prev <= 4096. Replaces the dGU cast of TE's delayed-scaling backward under TEMLP /
+ * FusedMLP (bongard/te_linear.py:98-103; bongard/fused_mlp.py:25-30). */
+int64_t bf8_geglu_bwd_delayed_partials(int64_t M, int64_t I);
+int bf8_geglu_bwd_delayed(const void* dH, const void* GU, int64_t M, int64_t I, float* state,
+                          int len, int pos, const uint32_t* prev_partials, int64_t n_prev, int fmt,
+                          float* meta_out, uint8_t* out, uint8_t* out_t, uint32_t* partials_out,
+                          void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Axiswise (per-row / per-column) quantization, torchao AXISWISE scaling granularity.
  * Replaces torchao hp_tensor_to_float8_dynamic(x, ..., scaling_granularity=AXISWISE,

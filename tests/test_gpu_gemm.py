@@ -315,3 +315,26 @@ def test_skinny_down_projection_auto_plan(gpu):
     """c4's down projection (M=512, K=10240): the automatic plan splits K."""
     assert ops._lib.lib().bf8_gemm_workspace(512, 2560, 10240) > 0
     _gemm_case(gpu, 512, 2560, 10240, seed=23, b_std=0.014)
+
+
+def test_geglu_bwd_extreme_preactivations(gpu):
+    """Gate pre-activations far in both tails (exp(-2u) overflows below about -10): the
+    backward stays finite and matches torch's bf16 chain there (d_g ~ 0 for g << 0,
+    d_g ~ dh * u for g >> 0)."""
+    M, I = 64, 128
+    g = torch.Generator().manual_seed(32)
+    gate = torch.randn(M, I, generator=g) * 2
+    tails = torch.tensor([-300.0, -60.0, -20.0, -11.0, -10.5, -10.0, -9.0, -8.0, 8.0, 20.0,
+                          60.0, 300.0])
+    gate[:, :tails.numel()] = tails
+    up = torch.randn(M, I, generator=g)
+    GU = torch.cat([gate, up], 1).to(torch.bfloat16)
+    dH = torch.randn(M, I, generator=g).to(torch.bfloat16)
+    dGU, _ = ops.geglu_bwd(dH.to(gpu), GU.to(gpu))
+    torch.cuda.synchronize()
+    got = dGU.cpu().float()
+    assert bool(torch.isfinite(got).all())
+    dg, du = orc.geglu_bwd(GU[:, :I], GU[:, I:], dH)
+    for part, ref in ((got[:, :I], dg.float()), (got[:, I:], du.float())):
+        diff = (part - ref).abs()
+        assert bool((diff <= 2 * orc.bf16_ulp(ref) + 2.0 ** -20 * ref.abs().max()).all())
