@@ -66,6 +66,10 @@ class Float8Linear(torch.nn.Linear):
         new.config = config
         return new
 
+    # The FP8 kernels are opaque to torch.compile (ctypes calls into the HIP library):
+    # under the reference's regional compile (bongard/model.py:249-281) a compiled layer
+    # runs this forward eagerly, between its compiled pieces, as it does TE's modules.
+    @torch.compiler.disable
     def forward(self, inputs):
         if inputs.device.type != "cuda":
             raise RuntimeError("FP8 training forward needs the MI355X device (no CPU emulation)")

@@ -67,8 +67,11 @@ def _shared_input_ok(projections):
                and isinstance(p.recipe, Float8CurrentScaling) for p in projections)
 
 
+@torch.compiler.disable
 def shared_input_projections(x, projections):
-    """Outputs of several TELinear projections of one input (see module doc)."""
+    """Outputs of several TELinear projections of one input (see module doc). Opaque to
+    torch.compile, like the projections themselves: the reference compiles
+    project_state_kv (bongard/model.py:279), which then runs this part eagerly."""
     flat = x.reshape(-1, x.shape[-1])
     flat, length, aligned = _pad_rows(flat)
     if flat.dtype != torch.bfloat16:

@@ -319,10 +319,14 @@ def test_state_kv_shared_input_matches_separate_calls(gpu):
             k_norm=norm, head_dim=head_dim)
 
     results = []
-    for fused in (True, False):
+    compiled_kv = torch.compile(state_kv.project_state_kv, dynamic=True, backend="aot_eager")
+    for mode in ("shared", "separate", "shared_compiled"):
+        fused = mode != "separate"
         att = attention()
         sg = state.to(gpu).requires_grad_(True)
-        if fused:
+        if mode == "shared_compiled":
+            keys, values = compiled_kv(att, sg)
+        elif fused:
             keys, values = state_kv.project_state_kv(att, sg)
         else:
             shape = (*sg.shape[:-1], -1, head_dim)
@@ -333,5 +337,55 @@ def test_state_kv_shared_input_matches_separate_calls(gpu):
         torch.cuda.synchronize()
         assert att.k_proj.counts == {"weight_quantizations": 1}
         results.append((keys, values, sg.grad, att.k_proj.weight.grad, att.v_proj.weight.grad))
+    for other in results[1:]:
+        for a, b in zip(results[0], other):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+class _Block(nn.Module):
+    """A text block in miniature: norm -> FP8 linear -> gelu -> FP8 linear, residual."""
+
+    def __init__(self, make_linear, hidden, inter):
+        super().__init__()
+        self.norm = T5Gemma2RMSNorm(hidden, eps=1e-6).to(torch.bfloat16)
+        self.up = make_linear(hidden, inter)
+        self.down = make_linear(inter, hidden)
+
+    def forward(self, x):
+        h = self.up(self.norm(x))
+        return x + self.down(torch.nn.functional.gelu(h, approximate="tanh"))
+
+
+@pytest.mark.parametrize("kind", ["tensorwise", "rowwise", "te_fp8", "te_mxfp8"])
+def test_fp8_linears_inside_a_compiled_region(gpu, kind):
+    """The reference compiles each text layer (bongard/model.py:249-281, module.compile(
+    dynamic=True)); the FP8 linears inside must run there and give the eager results."""
+    hidden, inter, rows = 256, 512, 96
+
+    def make_linear(i, o):
+        torch.manual_seed(i * 7 + o)
+        lin = nn.Linear(i, o, bias=False).to(torch.bfloat16)
+        with torch.no_grad():
+            lin.weight.normal_(std=0.02)
+        if kind in ("tensorwise", "rowwise"):
+            cfg = float8_training.Float8LinearConfig(recipe=kind, pad_inner_dim=True)
+            f8 = float8_training.Float8Linear.from_float(lin, cfg)
+            f8.__class__ = float8_training.TrainingLinear
+            return f8
+        return te_linear.TELinear([lin], "fp8" if kind == "te_fp8" else "mxfp8")
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, rows // 2, hidden, generator=g).to(torch.bfloat16).to(gpu)
+    dy = (torch.randn(2, rows // 2, hidden, generator=g) * 1e-2).to(torch.bfloat16).to(gpu)
+    results = []
+    for compiled in (False, True):
+        block = _Block(make_linear, hidden, inter).to(gpu).train()
+        if compiled:
+            block.compile(dynamic=True, backend="aot_eager")
+        xg = x.clone().requires_grad_(True)
+        y = block(xg)
+        y.backward(dy)
+        torch.cuda.synchronize()
+        results.append((y.detach(), xg.grad, block.up.weight.grad, block.down.weight.grad))
     for a, b in zip(*results):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
