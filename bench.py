@@ -477,8 +477,9 @@ def _bench_state_kv(torch, workloads, dev, steps=20):
 
 def _bench_c2_mx(torch, ops, workloads, dev, steps=30):
     """The c2 MLP forward under TE's 'mxfp8' recipe: X, [W_gate; W_up], W_down quantized in
-    32-element blocks (E8M0 scales), gated-GELU GEMM on the block-scaled MFMA, H quantized
-    in blocks, down GEMM."""
+    32-element blocks (E8M0 scales), gated-GELU GEMM on the block-scaled MFMA with H
+    quantized in blocks in its epilogue, down GEMM (and, for comparison, the same step with
+    a separate bf16 H and quantize pass)."""
     c = workloads.config2()
     x = c["x"].to(dev)
     w_gu = torch.cat([c["w_gate"], c["w_up"]]).to(dev)
@@ -486,25 +487,35 @@ def _bench_c2_mx(torch, ops, workloads, dev, steps=30):
     M, K = x.shape
     I = c["w_gate"].shape[0]
 
-    def step():
+    def step(fused=True):
         xq = ops.quantize_mx(x)
         gq = ops.quantize_mx(w_gu)
         dq = ops.quantize_mx(w_d)
-        H, _ = ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I)
-        hq = ops.quantize_mx(H)
+        if fused:  # H quantized in the gate/up GEMM's epilogue (the product path)
+            hq, _, _ = ops.gemm_geglu_mx_quant(xq.data, xq.scales, gq.data, gq.scales, I)
+        else:
+            H, _ = ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I)
+            hq = ops.quantize_mx(H)
         return ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales)
 
     s = _timed(torch, step, steps, 3)
+    s_unfused = _timed(torch, lambda: step(False), steps, 3)
+    s_graph, graph_ok = _graph_timed(torch, step, steps, 3)
     xq, gq, dq = ops.quantize_mx(x), ops.quantize_mx(w_gu), ops.quantize_mx(w_d)
     H, _ = ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I)
     hq = ops.quantize_mx(H)
     g_s = _ev_time(torch, lambda: ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I),
                    steps)
+    gq_s = _ev_time(torch, lambda: ops.gemm_geglu_mx_quant(xq.data, xq.scales, gq.data,
+                                                           gq.scales, I), steps)
     d_s = _ev_time(torch, lambda: ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales), steps)
     h_s = _ev_time(torch, lambda: ops.quantize_mx(H), steps)
     flop = 2.0 * M * (2 * I * K + K * I)
     return {"workload": f"c2 MLP forward [{M},{K}] x [2*{I},{K}] -> [{M},{I}] x [{K},{I}], MXFP8",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
+            "us_per_step_graph": round(s_graph * 1e6, 2) if graph_ok else None,
+            "us_per_step_unfused_h": round(s_unfused * 1e6, 2),
+            "gemm_geglu_quant_h_us": round(gq_s * 1e6, 2),
             "gemm_geglu_us": round(g_s * 1e6, 2),
             "gemm_geglu_tflops": round(2.0 * M * 2 * I * K / g_s / 1e12, 1),
             "gemm_down_us": round(d_s * 1e6, 2),

@@ -135,6 +135,32 @@ __device__ __forceinline__ uint32_t absmax_key8(uint4 v) {
   return max(m0, m1) << 16;
 }
 
+// ---- MXFP8 block scales (TE MXFP8BlockScaling, 32-element blocks, E8M0 bytes) -------
+constexpr uint32_t kMxPadScale = 127u;  // E8M0 1.0, the padding past a row's last block
+
+// E8M0 exponent of amax / fp8_max rounded up to a power of two (TE float_to_e8m0 on
+// fp32(amax * fp32(1 / fp8_max))). key: fp32 bits of amax (>= 0 or NaN).
+template <int FMT>
+__device__ __forceinline__ uint32_t mx_exponent(uint32_t key) {
+  constexpr float kRcp = (float)(1.0 / (double)Fp8Max<FMT>::value);
+  const float amax = __uint_as_float(key);
+  if (amax != amax) return 0xFFu;
+  const float val = amax * kRcp;
+  const uint32_t b = __float_as_uint(val);
+  if (b >= 0x7F800000u) return 0xFEu;  // inf: saturate
+  uint32_t e = b >> 23;
+  const uint32_t man = b & 0x7FFFFFu;
+  if (man != 0 && e != 0xFEu && !(e == 0 && man <= 0x400000u)) ++e;
+  return e;
+}
+
+// 2^(127 - e), the factor applied to the block's values (NaN for e = 0xFF).
+__device__ __forceinline__ float mx_multiplier(uint32_t e) {
+  if (e == 0xFFu) return __uint_as_float(0x7FC00000u);
+  if (e == 254u) return __uint_as_float(0x00400000u);  // 2^-127, subnormal
+  return __uint_as_float((254u - e) << 23);
+}
+
 // Wavefront (64-lane) max reduction.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll

@@ -456,20 +456,35 @@ int bf8_gemm_mx(const uint8_t* A, int64_t lda, const uint8_t* A_scales, int64_t 
                      true);
 }
 
-int bf8_gemm_geglu_mx(const uint8_t* X, int64_t ldx, const uint8_t* X_scales, int64_t ldx_sc,
-                      const uint8_t* W, int64_t ldw, const uint8_t* W_scales, int64_t ldw_sc,
-                      int64_t M, int64_t I, int64_t K, void* H, int64_t ldh, void* GU,
-                      void* stream) {
-  BF8_CHECK(M >= 1 && I >= 1 && K >= 32, "bf8_gemm_geglu_mx: bad shape");
-  BF8_CHECK(I % 128 == 0, "bf8_gemm_geglu_mx: I must be a multiple of 128 (got %lld)",
-            (long long)I);
-  BF8_CHECK(K % 32 == 0, "bf8_gemm_geglu_mx: K must be a multiple of 32");
-  BF8_CHECK(ldh >= I && ldh % 4 == 0, "bf8_gemm_geglu_mx: bad ldh");
+// The MX gate/up GEMM + gated GELU; H8 (with H8t) set: H quantized in the epilogue.
+static int geglu_mx_entry(const char* who, const uint8_t* X, int64_t ldx, const uint8_t* X_scales,
+                          int64_t ldx_sc, const uint8_t* W, int64_t ldw, const uint8_t* W_scales,
+                          int64_t ldw_sc, int64_t M, int64_t I, int64_t K, void* H, int64_t ldh,
+                          uint8_t* H8, uint8_t* H8_scales, int64_t ldh8_sc, uint8_t* H8t,
+                          uint8_t* H8t_scales, int64_t ldh8t_sc, void* GU, void* stream) {
+  BF8_CHECK(M >= 1 && I >= 1 && K >= 32, "%s: bad shape", who);
+  BF8_CHECK(I % 128 == 0, "%s: I must be a multiple of 128 (got %lld)", who, (long long)I);
+  BF8_CHECK(K % 32 == 0, "%s: K must be a multiple of 32", who);
+  BF8_CHECK(H || H8, "%s: H is NULL", who);
+  BF8_CHECK(!H || (ldh >= I && ldh % 4 == 0), "%s: bad ldh", who);
   BF8_CHECK(((uintptr_t)H & 15) == 0 && ((uintptr_t)GU & 15) == 0,
-            "bf8_gemm_geglu_mx: H, GU must be 16-byte aligned");
-  int rc = check_mx_operand("bf8_gemm_geglu_mx", "X", X, ldx, X_scales, ldx_sc, M, K);
+            "%s: H, GU must be 16-byte aligned", who);
+  if (H8) {
+    BF8_CHECK(H8_scales && ldh8_sc >= I / 32 && ((uintptr_t)H8 & 7) == 0,
+              "%s: H8 needs 8-byte alignment and scales with row stride >= I / 32", who);
+    BF8_CHECK(M * I < (1LL << 31), "%s: H8 larger than 2 GiB", who);
+  }
+  BF8_CHECK(!H8t || H8, "%s: H8t needs H8", who);
+  if (H8t) {
+    BF8_CHECK(M % 32 == 0, "%s: H8t blocks along M need M %% 32 == 0 (got %lld)", who,
+              (long long)M);
+    BF8_CHECK(H8t_scales && ldh8t_sc >= bf8_mx_scale_ld(M) && ((uintptr_t)H8t & 15) == 0,
+              "%s: H8t needs 16-byte alignment and scales with row stride >= %lld", who,
+              (long long)bf8_mx_scale_ld(M));
+  }
+  int rc = check_mx_operand(who, "X", X, ldx, X_scales, ldx_sc, M, K);
   if (rc) return rc;
-  rc = check_mx_operand("bf8_gemm_geglu_mx", "W", W, ldw, W_scales, ldw_sc, 2 * I, K);
+  rc = check_mx_operand(who, "W", W, ldw, W_scales, ldw_sc, 2 * I, K);
   if (rc) return rc;
   GemmParams p{};
   p.A = X; p.B = W; p.lda = ldx; p.ldb = ldw;
@@ -477,9 +492,31 @@ int bf8_gemm_geglu_mx(const uint8_t* X, int64_t ldx, const uint8_t* X_scales, in
   p.a_sc = X_scales; p.b_sc = W_scales; p.a_sc_ld = ldx_sc; p.b_sc_ld = ldw_sc;
   p.n_seg = 1;
   p.C = H; p.ldc = ldh; p.GU = (uint16_t*)GU; p.partials = nullptr;
+  p.h8 = H8; p.h8_sc = H8_scales; p.h8_sc_ld = ldh8_sc;
+  p.h8t = H8t; p.h8t_sc = H8t_scales; p.h8t_sc_ld = ldh8t_sc;
   Plan pl = choose_plan(M, 2 * I, K, true, 0, true);
   return launch_plan(pl, p, EPI_GEGLU, BF8_OUT_BF16, BF8_E4M3, BF8_E4M3, nullptr,
                      as_stream(stream), true);
+}
+
+int bf8_gemm_geglu_mx(const uint8_t* X, int64_t ldx, const uint8_t* X_scales, int64_t ldx_sc,
+                      const uint8_t* W, int64_t ldw, const uint8_t* W_scales, int64_t ldw_sc,
+                      int64_t M, int64_t I, int64_t K, void* H, int64_t ldh, void* GU,
+                      void* stream) {
+  return geglu_mx_entry("bf8_gemm_geglu_mx", X, ldx, X_scales, ldx_sc, W, ldw, W_scales, ldw_sc,
+                        M, I, K, H, ldh, nullptr, nullptr, 0, nullptr, nullptr, 0, GU, stream);
+}
+
+int bf8_gemm_geglu_mx_quant(const uint8_t* X, int64_t ldx, const uint8_t* X_scales,
+                            int64_t ldx_sc, const uint8_t* W, int64_t ldw,
+                            const uint8_t* W_scales, int64_t ldw_sc, int64_t M, int64_t I,
+                            int64_t K, void* H, int64_t ldh, uint8_t* H8, uint8_t* H8_scales,
+                            int64_t ldh8_sc, uint8_t* H8t, uint8_t* H8t_scales,
+                            int64_t ldh8t_sc, void* GU, void* stream) {
+  BF8_CHECK(H8 != nullptr, "bf8_gemm_geglu_mx_quant: H8 is NULL");
+  return geglu_mx_entry("bf8_gemm_geglu_mx_quant", X, ldx, X_scales, ldx_sc, W, ldw, W_scales,
+                        ldw_sc, M, I, K, H, ldh, H8, H8_scales, ldh8_sc, H8t, H8t_scales,
+                        ldh8t_sc, GU, stream);
 }
 
 }  // extern "C"

@@ -32,6 +32,14 @@ struct GemmParams {
   int64_t ldc;
   uint16_t* GU;
   uint32_t* partials;     // GEGLU: one amax key of |H| per tile
+  // MX GEGLU: H quantized in the epilogue (C, the bf16 H, may then be NULL). h8: e4m3
+  // [M, I] with E8M0 scales h8_sc [M, h8_sc_ld] (blocks along I); h8t (optional, needs
+  // M % 32 == 0): e4m3 H^T [I, M] with scales h8t_sc [I, h8t_sc_ld] (blocks along M).
+  uint8_t* h8;
+  uint8_t* h8_sc;
+  uint8_t* h8t;
+  uint8_t* h8t_sc;
+  int64_t h8_sc_ld, h8t_sc_ld;
   int64_t split_stride;   // splits > 1: C is fp32 [splits][M][ldc], raw sums, this many
                           // elements apart (a reduce kernel applies scales and bias)
 };

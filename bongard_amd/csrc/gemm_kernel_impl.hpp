@@ -173,6 +173,12 @@ template <int CH>
 __device__ __forceinline__ uint4 stage_get(const uint8_t* buf, int row, int c) {
   return *reinterpret_cast<const uint4*>(buf + row * (CH * 16) + (stage_pos<CH>(row, c) << 4));
 }
+// The bf16 pair at columns col, col + 1 (col even) of a staged row.
+template <int CH>
+__device__ __forceinline__ uint32_t stage_get_pair(const uint8_t* buf, int row, int col) {
+  return *reinterpret_cast<const uint32_t*>(buf + row * (CH * 16) +
+                                            (stage_pos<CH>(row, col >> 3) << 4) + (col & 7) * 2);
+}
 // 8 bf16 to global: one 16-byte store when the row stride keeps it aligned.
 __device__ __forceinline__ void store_bf16x8(uint16_t* dst, uint4 d, int64_t ld) {
   if ((ld & 7) == 0) {
@@ -180,6 +186,83 @@ __device__ __forceinline__ void store_bf16x8(uint16_t* dst, uint4 d, int64_t ld)
   } else {
     reinterpret_cast<uint2*>(dst)[0] = make_uint2(d.x, d.y);
     reinterpret_cast<uint2*>(dst)[1] = make_uint2(d.z, d.w);
+  }
+}
+
+// MX gated-GELU epilogue: the wave's staged H (ROWS rows x CH*8 bf16 columns in LDS, first
+// global row gm0, first H column h0) quantized to e4m3 in blocks of 32 with the standalone
+// MX quantizer's arithmetic: along rows into h8 / h8_sc (a 4-lane group per block, 8
+// values a lane), and, when h8t is set, along columns into h8t / h8t_sc (a lane per
+// column pair and 32-row block). C, when set, also receives the bf16 H.
+template <int ROWS, int CH>
+__device__ __forceinline__ void mx_h_epilogue(const GemmParams& p, const uint8_t* wbuf, int lane,
+                                              int gm0, int h0) {
+#pragma unroll 4
+  for (int it = 0; it < ROWS * CH / 64; ++it) {
+    const int idx = it * 64 + lane;
+    const int row = idx / CH, c = idx % CH;  // lanes 4j .. 4j+3: one block of one row
+    const uint4 d = stage_get<CH>(wbuf, row, c);
+    uint32_t k = absmax_key8(d);
+    k = max(k, (uint32_t)__shfl_xor((int)k, 1, 64));
+    k = max(k, (uint32_t)__shfl_xor((int)k, 2, 64));
+    const int gm = gm0 + row;
+    if (gm < p.M) {
+      const int n = h0 + c * 8;
+      if (p.C) store_bf16x8(reinterpret_cast<uint16_t*>(p.C) + (int64_t)gm * p.ldc + n, d, p.ldc);
+      const uint32_t e = mx_exponent<BF8_E4M3>(k);
+      *reinterpret_cast<uint2*>(p.h8 + (int64_t)gm * p.I + n) =
+          quant8_bf16<BF8_E4M3>(d, mx_multiplier(e));
+      if ((c & 3) == 0) p.h8_sc[(int64_t)gm * p.h8_sc_ld + (n >> 5)] = (uint8_t)e;
+    }
+  }
+  if (p.h8t == nullptr) return;
+  constexpr int CP = CH * 4;                 // column pairs per staged row
+  constexpr int ITEMS = (ROWS / 32) * CP;    // (32-row block, column pair) items
+  const int nblk = p.M >> 5;                 // M % 32 == 0 here
+  const int sc_pad_end = ((p.M + 127) >> 7) << 2;
+#pragma unroll 1
+  for (int item = lane; item < ITEMS; item += 64) {
+    const int blk = item / CP, cp = item % CP;
+    const int gm = gm0 + blk * 32;
+    if (gm >= p.M) continue;
+    uint32_t v[32];
+    uint32_t k0 = 0, k1 = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      v[i] = stage_get_pair<CH>(wbuf, blk * 32 + i, 2 * cp);
+      k0 = max(k0, v[i] & 0x7FFFu);
+      k1 = max(k1, (v[i] >> 16) & 0x7FFFu);
+    }
+    const uint32_t e0 = mx_exponent<BF8_E4M3>(k0 << 16), e1 = mx_exponent<BF8_E4M3>(k1 << 16);
+    const float s0 = mx_multiplier(e0), s1 = mx_multiplier(e1);
+    uint32_t q0[8], q1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a0 = bf16_lo(v[4 * j]), a1 = bf16_lo(v[4 * j + 1]);
+      const float a2 = bf16_lo(v[4 * j + 2]), a3 = bf16_lo(v[4 * j + 3]);
+      const float b0 = bf16_hi(v[4 * j]), b1 = bf16_hi(v[4 * j + 1]);
+      const float b2 = bf16_hi(v[4 * j + 2]), b3 = bf16_hi(v[4 * j + 3]);
+      q0[j] = quant4<BF8_E4M3>(a0 * s0, a1 * s0, a2 * s0, a3 * s0, a0, a1, a2, a3, s0);
+      q1[j] = quant4<BF8_E4M3>(b0 * s1, b1 * s1, b2 * s1, b3 * s1, b0, b1, b2, b3, s1);
+    }
+    const int n = h0 + 2 * cp;
+    uint4* d0 = reinterpret_cast<uint4*>(p.h8t + (int64_t)n * p.M + gm);
+    uint4* d1 = reinterpret_cast<uint4*>(p.h8t + (int64_t)(n + 1) * p.M + gm);
+    d0[0] = make_uint4(q0[0], q0[1], q0[2], q0[3]);
+    d0[1] = make_uint4(q0[4], q0[5], q0[6], q0[7]);
+    d1[0] = make_uint4(q1[0], q1[1], q1[2], q1[3]);
+    d1[1] = make_uint4(q1[4], q1[5], q1[6], q1[7]);
+    uint8_t* r0 = p.h8t_sc + (int64_t)n * p.h8t_sc_ld;
+    uint8_t* r1 = r0 + p.h8t_sc_ld;
+    r0[gm >> 5] = (uint8_t)e0;
+    r1[gm >> 5] = (uint8_t)e1;
+    if ((gm >> 5) == nblk - 1) {
+      // the column's last block also pads its scale row to whole dwords
+      for (int pb = nblk; pb < sc_pad_end; ++pb) {
+        r0[pb] = (uint8_t)kMxPadScale;
+        r1[pb] = (uint8_t)kMxPadScale;
+      }
+    }
   }
 }
 
@@ -618,6 +701,12 @@ gemm_kernel(GemmParams p) {
             }
             stage_put<CH>(wbuf, j * 32 + lrow_m, col, make_uint2(w0, w1));
           }
+        }
+      }
+      if constexpr (MX && pass == 0) {
+        if (p.h8) {
+          mx_h_epilogue<ROWS, CH>(p, wbuf, lane, m0 + wave_m0, wave_h0);
+          return;
         }
       }
       uint16_t* dst = pass == 0 ? reinterpret_cast<uint16_t*>(p.C) : p.GU;

@@ -26,31 +26,6 @@ constexpr int kMxMaxRowBlocks = 8192;
 constexpr int kMT = 64;                // columnwise tile (rows x cols)
 constexpr int kMPitch = kMT + 4;
 constexpr int kMaxMxTileBlocks = 2048;
-constexpr uint32_t kPadScale = 127u;   // E8M0 1.0
-
-// E8M0 exponent of amax / fp8_max rounded up to a power of two (TE float_to_e8m0 on
-// fp32(amax * fp32(1 / fp8_max))). key: fp32 bits of amax (>= 0 or NaN).
-template <int FMT>
-__device__ __forceinline__ uint32_t mx_exponent(uint32_t key) {
-  constexpr float kRcp = (float)(1.0 / (double)Fp8Max<FMT>::value);
-  const float amax = __uint_as_float(key);
-  if (amax != amax) return 0xFFu;
-  const float val = amax * kRcp;
-  const uint32_t b = __float_as_uint(val);
-  if (b >= 0x7F800000u) return 0xFEu;  // inf: saturate
-  uint32_t e = b >> 23;
-  const uint32_t man = b & 0x7FFFFFu;
-  if (man != 0 && e != 0xFEu && !(e == 0 && man <= 0x400000u)) ++e;
-  return e;
-}
-
-// 2^(127 - e), the factor applied to the block's values (NaN for e = 0xFF).
-__device__ __forceinline__ float mx_multiplier(uint32_t e) {
-  if (e == 0xFFu) return __uint_as_float(0x7FC00000u);
-  if (e == 254u) return __uint_as_float(0x00400000u);  // 2^-127, subnormal
-  return __uint_as_float((254u - e) << 23);
-}
-
 // Rowwise: a 16-lane group handles 128 consecutive elements of a row (4 blocks, 4 lanes
 // each, 8 elements per lane) and writes the dword of their 4 scale bytes. Grid-stride over
 // (row, 128-element group) pairs; groups past the row's last block write padding scales.
@@ -75,7 +50,7 @@ __global__ __launch_bounds__(kMxNT) void mx_row_kernel(const uint16_t* __restric
     m = max(m, (uint32_t)__shfl_xor((int)m, 1, 64));
     m = max(m, (uint32_t)__shfl_xor((int)m, 2, 64));
     const bool block_valid = valid;  // cols % 32 == 0: a block is valid iff its lanes are
-    const uint32_t e = block_valid ? mx_exponent<FMT>(m) : kPadScale;
+    const uint32_t e = block_valid ? mx_exponent<FMT>(m) : kMxPadScale;
     if (valid) {
       const float mult = mx_multiplier(e);
       *reinterpret_cast<uint2*>(out + r * cols + c) = quant8_bf16<FMT>(v, mult);
@@ -140,7 +115,7 @@ __global__ __launch_bounds__(kMxNT) void mx_col_kernel(const uint16_t* __restric
         if (gb < nblk_rows) srow[gb] = (uint8_t)e;
         // the last tile row also pads the column's scale row to whole dwords
         if (blk == 1 && r0 + kMT >= rows)
-          for (int64_t pb = nblk_rows; pb < ld_sc_t; ++pb) srow[pb] = (uint8_t)kPadScale;
+          for (int64_t pb = nblk_rows; pb < ld_sc_t; ++pb) srow[pb] = (uint8_t)kMxPadScale;
       }
     }
     __syncthreads();

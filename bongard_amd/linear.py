@@ -204,8 +204,8 @@ class Fp8LinearMxFunction(torch.autograd.Function):
 
 class Fp8GegluMlpMxFunction(torch.autograd.Function):
     """The gated MLP of :class:`Fp8GegluMlpFunction` under MXFP8 (e4m3 blocks of 32, E8M0
-    scales, gradients e4m3 too): gate/up GEMM with the gated-GELU epilogue, H quantized in
-    blocks (no tensor-wide amax), down GEMM; backward through dH, the gelu chain's dGU and
+    scales, gradients e4m3 too): gate/up GEMM whose epilogue applies the gated GELU and
+    quantizes H in blocks (no tensor-wide amax, no bf16 H in memory), down GEMM; backward through dH, the gelu chain's dGU and
     the dgrad/wgrad GEMMs on the columnwise copies. ``gu_q`` / ``down_q``: optional cached
     MX weights (with their columnwise copies). Reference: TEMLP / FusedMLP (te.LayerNormMLP)
     under 'mxfp8' (bongard/te_linear.py:98-103, bongard/fused_mlp.py:25-33)."""
@@ -218,8 +218,10 @@ class Fp8GegluMlpMxFunction(torch.autograd.Function):
         xq = ops.quantize_mx(x, E4M3, rowwise=True, colwise=need_dgu)
         if gu_q is None:
             gu_q = quantize_weight_mx(w_gu, transpose=need_dx)
-        H, GU = ops.gemm_geglu_mx(xq.data, xq.scales, gu_q.data, gu_q.scales, I, keep_gu=train)
-        hq = ops.quantize_mx(H, E4M3, rowwise=True, colwise=need_dd)
+        # H is quantized (rowwise, plus the columnwise copy for the down wgrad) in the
+        # GEMM's epilogue; the bf16 H itself is never written
+        hq, GU, _ = ops.gemm_geglu_mx_quant(xq.data, xq.scales, gu_q.data, gu_q.scales, I,
+                                            colwise=need_dd, keep_gu=train)
         if down_q is None:
             down_q = quantize_weight_mx(w_down, transpose=need_dx or need_dgu)
         y = ops.gemm_mx(hq.data, hq.scales, down_q.data, down_q.scales)

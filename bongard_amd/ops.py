@@ -414,6 +414,36 @@ def gemm_geglu_mx(x8, x_scales, w8, w_scales, intermediate, *, keep_gu=False):
     return H, GU
 
 
+def gemm_geglu_mx_quant(x8, x_scales, w8, w_scales, intermediate, *, colwise=False,
+                        keep_gu=False, keep_h=False):
+    """:func:`gemm_geglu_mx` with H's MXFP8 (e4m3) quantization done in the GEMM epilogue.
+
+    Returns ``(hq, GU or None, H or None)``: ``hq`` an :class:`MxFp8Tensor` of H with the
+    rowwise copy and, if ``colwise`` (needs M % 32 == 0), the columnwise one, byte for byte
+    what :func:`quantize_mx` gives for the bf16 H; ``H`` the bf16 H when ``keep_h``."""
+    _require_gpu(x8, x_scales, w8, w_scales)
+    M, K = x8.shape
+    I = int(intermediate)
+    if w8.shape != (2 * I, K):
+        raise ValueError(f"gemm_geglu_mx_quant: W must be [{2 * I}, {K}]")
+    dev = x8.device
+    fp8 = TORCH_FP8[E4M3]
+    h8 = torch.empty((M, I), dtype=fp8, device=dev)
+    h8_sc = torch.empty((M, mx_scale_ld(I)), dtype=torch.uint8, device=dev)
+    h8t = h8t_sc = None
+    if colwise:
+        h8t = torch.empty((I, M), dtype=fp8, device=dev)
+        h8t_sc = torch.empty((I, mx_scale_ld(M)), dtype=torch.uint8, device=dev)
+    H = torch.empty((M, I), dtype=torch.bfloat16, device=dev) if keep_h else None
+    GU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=dev) if keep_gu else None
+    _lib.check(_lib.lib().bf8_gemm_geglu_mx_quant(
+        _ptr(x8), x8.stride(0), _ptr(x_scales), x_scales.stride(0), _ptr(w8), w8.stride(0),
+        _ptr(w_scales), w_scales.stride(0), M, I, K, _ptr(H), I, _ptr(h8), _ptr(h8_sc),
+        h8_sc.stride(0), _ptr(h8t), _ptr(h8t_sc), h8t_sc.stride(0) if colwise else 0, _ptr(GU),
+        _stream(dev)), "bf8_gemm_geglu_mx_quant")
+    return MxFp8Tensor(h8, h8_sc, h8t, h8t_sc, E4M3, M, I), GU, H
+
+
 def geglu_partials_count(M, intermediate):
     return int(_lib.lib().bf8_geglu_partials(int(M), int(intermediate)))
 

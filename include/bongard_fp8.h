@@ -266,6 +266,22 @@ int bf8_gemm_geglu_mx(const uint8_t* X, int64_t ldx, const uint8_t* X_scales, in
                       int64_t M, int64_t I, int64_t K, void* H, int64_t ldh, void* GU,
                       void* stream);
 
+/* bf8_gemm_geglu_mx with H's MXFP8 (e4m3) quantization fused into the epilogue: the
+ * activation-and-cast step ahead of fc2 in TE LayerNormMLP / te.Linear under
+ * MXFP8BlockScaling (bongard/fused_mlp.py:25-33, bongard/te_linear.py:98-103), with
+ * bytes and scales identical to bf8_quantize_mx_bf16 of the bf16 H.
+ * H8 [M, I] (8-byte aligned) + H8_scales [M, ldh8_sc >= I / 32]: blocks along I (bytes
+ * past I / 32 untouched). H8t [I, M] (16-byte aligned, M % 32 == 0) + H8t_scales
+ * [I, ldh8t_sc >= bf8_mx_scale_ld(M)]: blocks along M, padded with 127 to
+ * bf8_mx_scale_ld(M); NULL for none. H (bf16, ldh) and GU are optional (NULL = not
+ * written). I % 128 == 0. */
+int bf8_gemm_geglu_mx_quant(const uint8_t* X, int64_t ldx, const uint8_t* X_scales,
+                            int64_t ldx_sc, const uint8_t* W, int64_t ldw,
+                            const uint8_t* W_scales, int64_t ldw_sc, int64_t M, int64_t I,
+                            int64_t K, void* H, int64_t ldh, uint8_t* H8, uint8_t* H8_scales,
+                            int64_t ldh8_sc, uint8_t* H8t, uint8_t* H8t_scales,
+                            int64_t ldh8t_sc, void* GU, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * RMSNorm fused with the amax pass of the quantization that follows it.
  * Replaces the RMSNorm (zero-centred gamma) of TE LayerNormMLP built at

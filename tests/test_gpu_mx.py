@@ -123,6 +123,60 @@ def test_gemm_geglu_mx(gpu, M, I, K):
     assert (diff > 0).float().mean().item() <= 0.05
 
 
+GEGLU_TILES = ["256x256", "160x256", "192x256", "128x128", "64x128"]
+
+
+@pytest.mark.parametrize("tile", ["auto"] + GEGLU_TILES)
+@pytest.mark.parametrize("M,I,K", [(320, 384, 256), (100, 256, 128)])
+def test_gemm_geglu_mx_quant(gpu, monkeypatch, tile, M, I, K):
+    """H quantized in the GEGLU epilogue == bf8_quantize_mx_bf16 of the bf16 H of the
+    unfused kernel, byte for byte (fp8 payloads, E8M0 scales, the transposed copy and its
+    padding), on every tile with a gated-GELU variant, with inf / NaN blocks in H."""
+    if tile != "auto":
+        monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(M + I + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    x[7] *= 1e-4                      # a row of small activations
+    w = (torch.randn(2 * I, K, generator=g) * 0.02).to(torch.bfloat16)
+    qx = ops.quantize_mx(x.to(gpu))
+    qw = ops.quantize_mx(w.to(gpu))
+    qx.scales[5, 0] = 254             # row 5: 2^127 on its first block -> +-inf gate/up, NaN H
+    qx.data.view(torch.uint8)[9, 3] = 0x7F  # row 9: an e4m3 NaN operand -> NaN row of H
+    colwise = M % 32 == 0
+    args = (qx.data, qx.scales, qw.data, qw.scales, I)
+    hq, GU, H = ops.gemm_geglu_mx_quant(*args, colwise=colwise, keep_gu=True, keep_h=True)
+    hq2, GU2, H2 = ops.gemm_geglu_mx_quant(*args, colwise=colwise)
+    H_ref, GU_ref = ops.gemm_geglu_mx(*args, keep_gu=True)
+    ref = ops.quantize_mx(H_ref, rowwise=True, colwise=colwise)
+    torch.cuda.synchronize()
+    assert GU2 is None and H2 is None and (hq2.data_t is None) == (not colwise)
+    assert torch.equal(H.view(torch.int16), H_ref.view(torch.int16))
+    assert torch.equal(GU.view(torch.int16), GU_ref.view(torch.int16))
+    hc = H_ref.cpu()
+    assert bool(hc[9].isnan().any()) and bool(hc[5].isinf().any() or hc[5].isnan().any())
+    for q, what in ((hq, "with H"), (hq2, "without H")):
+        same = [torch.equal(q.data.view(torch.uint8), ref.data.view(torch.uint8)),
+                torch.equal(q.scales, ref.scales)]
+        if colwise:
+            same += [torch.equal(q.data_t.view(torch.uint8), ref.data_t.view(torch.uint8)),
+                     torch.equal(q.scales_t, ref.scales_t)]
+        print(f"[mx geglu quant {tile} {M}x{I}x{K} {what}] rows, scales, cols, scales_t: "
+              f"{same}", flush=True)
+        assert all(same)
+    # and the oracle on the finite rows (the kernel's own H as input)
+    finite = hc.isfinite().all(dim=1)
+    rq, re_ = orc.quantize_mx(hc[finite], ops.E4M3)
+    assert torch.equal(hq.data.view(torch.uint8).cpu()[finite], rq)
+    assert torch.equal(hq.scales.cpu()[finite][:, :I // 32], re_.to(torch.uint8))
+
+
+def test_gemm_geglu_mx_quant_errors(gpu):
+    qx = ops.quantize_mx(torch.randn(100, 128, device=gpu).to(torch.bfloat16))
+    qw = ops.quantize_mx(torch.randn(512, 128, device=gpu).to(torch.bfloat16))
+    with pytest.raises(RuntimeError, match="M % 32"):
+        ops.gemm_geglu_mx_quant(qx.data, qx.scales, qw.data, qw.scales, 256, colwise=True)
+
+
 # ---- the TE modules under 'mxfp8' ------------------------------------------------------
 import types  # noqa: E402
 
