@@ -161,6 +161,37 @@ __device__ __forceinline__ float mx_multiplier(uint32_t e) {
   return __uint_as_float((254u - e) << 23);
 }
 
+// ---- wave-level 64 x 64 byte transpose ------------------------------------------------
+constexpr int kWaveTilePitch = 17;  // dwords per staged row (odd: conflict-free row writes)
+constexpr int kWaveTileDwords = 64 * kWaveTilePitch;
+
+// Transpose of a 64 x 64 byte tile that one wave has staged in its own LDS region (row r
+// at lds + r * kWaveTilePitch dwords, kWaveTileDwords in all): lane l gets columns
+// 4 (l & 15) + c, c < 4, over rows 16 (l >> 4) .. +15 as t[c] (byte i of t[c] = row
+// 16 (l >> 4) + i). No barrier is needed between the wave's staging stores and these
+// reads: a wave's LDS accesses complete in order.
+__device__ __forceinline__ void wave_transpose64_staged(const uint32_t* lds, int lane,
+                                                        uint4 (&t)[4]) {
+  const int row0 = (lane >> 4) * 16, cg = lane & 15;
+  uint32_t d[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) d[i] = lds[(row0 + i) * kWaveTilePitch + cg];
+  uint32_t c[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // 4 x 4 byte transpose of rows 4k .. 4k+3
+    const uint32_t t0 = __byte_perm(d[4 * k], d[4 * k + 1], 0x5140);
+    const uint32_t t1 = __byte_perm(d[4 * k], d[4 * k + 1], 0x7362);
+    const uint32_t t2 = __byte_perm(d[4 * k + 2], d[4 * k + 3], 0x5140);
+    const uint32_t t3 = __byte_perm(d[4 * k + 2], d[4 * k + 3], 0x7362);
+    c[0][k] = __byte_perm(t0, t2, 0x5410);
+    c[1][k] = __byte_perm(t0, t2, 0x7632);
+    c[2][k] = __byte_perm(t1, t3, 0x5410);
+    c[3][k] = __byte_perm(t1, t3, 0x7632);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) t[k] = make_uint4(c[k][0], c[k][1], c[k][2], c[k][3]);
+}
+
 // Wavefront (64-lane) max reduction.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll

@@ -189,76 +189,84 @@ __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ 
   store_block_amax(m, amax_out, blockIdx.x);
 }
 
-// Cast with a transposed copy, over 64 x 64 tiles of x (grid-stride, so the grid and the
-// number of amax partials stay bounded). Per tile:
-//  - each lane loads 16 bf16 of one row (4 lanes cover a 128-byte row segment),
-//    quantizes, stores 16 bytes of `out` (if requested) and stages the bytes in LDS;
-//  - after a barrier each lane gathers 16 bytes of one tile column and stores them as a
-//    16-byte row segment of out_t.
-// rows and cols need not be multiples of 64; cols % 16 == 0.
-constexpr int kTT = 64;
-constexpr int kTPitch = kTT + 4;  // LDS row pitch (bytes), staggers banks for the gather
-constexpr int kMaxTransposeBlocks = 1024;
+// Cast with a transposed copy, over kTR x 64 tiles of x, one tile per wave (grid-stride,
+// so the grid and the number of amax partials stay bounded). Per tile:
+//  - the wave loads the tile as 8-row x 128-byte pieces (kTR / 8 16-byte loads in flight
+//    per lane), quantizes, stores `out` (if requested) and stages the bytes in its own LDS
+//    region;
+//  - per 64-row half, each lane reads back 4 columns x 16 rows (wave_transpose64_staged)
+//    and stores them as four 16-byte row segments of out_t.
+// rows and cols need not be multiples of the tile; cols % 16 == 0.
+constexpr int kTR = 64;   // tile rows
+constexpr int kTT = 64;   // tile columns
+constexpr int kWavesPerBlock = kNT / 64;
+constexpr int kMaxTransposeBlocks = 2048;
 
 template <int FMT>
 __global__ __launch_bounds__(kNT) void cast_transpose_kernel(
     const uint16_t* __restrict__ x, int64_t rows, int64_t cols, ScaleSrc src,
     uint8_t* __restrict__ out, uint8_t* __restrict__ out_t, uint32_t* __restrict__ amax_out) {
-  __shared__ uint32_t tile[kTT * kTPitch / 4];
-  uint8_t* tb = reinterpret_cast<uint8_t*>(tile);
+  constexpr int NL = kTR / 8;  // 16-byte loads per lane
+  __shared__ uint32_t stage[kWavesPerBlock][(kTR / 64) * kWaveTileDwords];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const float scale = resolve_scale<FMT>(src);
   const int64_t tiles_c = (cols + kTT - 1) / kTT;
-  const int64_t ntiles = tiles_c * ((rows + kTT - 1) / kTT);
-  const int t = threadIdx.x;
+  const int64_t ntiles = tiles_c * ((rows + kTR - 1) / kTR);
+  const bool t16 = (rows & 15) == 0;  // out_t rows 16-byte aligned
   uint32_t m = 0;
-  for (int64_t tile_id = blockIdx.x; tile_id < ntiles; tile_id += gridDim.x) {
-    const int64_t r0 = (tile_id / tiles_c) * kTT, c0 = (tile_id % tiles_c) * kTT;
-    {
-      const int lr = t >> 2, lc = (t & 3) * 16;
-      const int64_t r = r0 + lr, c = c0 + lc;
-      uint32_t q[4] = {0u, 0u, 0u, 0u};
-      if (r < rows && c < cols) {
-        const uint4* src4 = reinterpret_cast<const uint4*>(x + r * cols + c);
-        uint4 a0 = src4[0];
-        uint4 a1 = src4[1];
-        if (amax_out) m = max(m, max(absmax_key8(a0), absmax_key8(a1)));
-        uint2 q0 = quant8_bf16<FMT>(a0, scale), q1 = quant8_bf16<FMT>(a1, scale);
-        q[0] = q0.x; q[1] = q0.y; q[2] = q1.x; q[3] = q1.y;
-        if (out) *reinterpret_cast<uint4*>(out + r * cols + c) = make_uint4(q[0], q[1], q[2], q[3]);
-      }
-      uint32_t* dst = reinterpret_cast<uint32_t*>(tb + lr * kTPitch + lc);
-      dst[0] = q[0]; dst[1] = q[1]; dst[2] = q[2]; dst[3] = q[3];
-    }
-    __syncthreads();
-    {
-      const int oc = t >> 2, orow = (t & 3) * 16;  // out_t row = tile column oc
-      const int64_t tr = c0 + oc, tc = r0 + orow;  // position in out_t [cols, rows]
-      if (tr < cols && tc < rows) {
-        uint32_t w[4];
+  for (int64_t tile_id = (int64_t)blockIdx.x * kWavesPerBlock + wid; tile_id < ntiles;
+       tile_id += (int64_t)gridDim.x * kWavesPerBlock) {
+    const int64_t r0 = (tile_id / tiles_c) * kTR, c0 = (tile_id % tiles_c) * kTT;
+    // load k: rows 8k + (lane >> 3), 16-byte chunk lane & 7 (8 rows x 128 bytes each)
+    const int ch = lane & 7;
+    const int64_t c = c0 + 8 * ch;
+    uint4 v[NL];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint32_t b0 = tb[(orow + 4 * j + 0) * kTPitch + oc];
-          uint32_t b1 = tb[(orow + 4 * j + 1) * kTPitch + oc];
-          uint32_t b2 = tb[(orow + 4 * j + 2) * kTPitch + oc];
-          uint32_t b3 = tb[(orow + 4 * j + 3) * kTPitch + oc];
-          w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        }
-        uint8_t* dst = out_t + tr * rows + tc;
-        if (tc + 16 <= rows && (rows & 15) == 0) {
-          *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-        } else {
-          for (int j = 0; j < 16 && tc + j < rows; ++j) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+    for (int k = 0; k < NL; ++k) {
+      const int64_t r = r0 + 8 * k + (lane >> 3);
+      v[k] = make_uint4(0u, 0u, 0u, 0u);
+      if (r < rows && c < cols) v[k] = *reinterpret_cast<const uint4*>(x + r * cols + c);
+    }
+    uint32_t* lds = stage[wid];
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      const int lr = 8 * k + (lane >> 3);
+      const int64_t r = r0 + lr;
+      if (amax_out) m = max(m, absmax_key8(v[k]));
+      const uint2 qq = quant8_bf16<FMT>(v[k], scale);
+      if (out && r < rows && c < cols) *reinterpret_cast<uint2*>(out + r * cols + c) = qq;
+      lds[lr * kWaveTilePitch + 2 * ch] = qq.x;
+      lds[lr * kWaveTilePitch + 2 * ch + 1] = qq.y;
+    }
+#pragma unroll
+    for (int h = 0; h < kTR / 64; ++h) {
+      uint4 tq[4];
+      wave_transpose64_staged(lds + h * kWaveTileDwords, lane, tq);
+      const int64_t tc = r0 + 64 * h + (lane >> 4) * 16;  // out_t column (a row of x)
+      if (tc < rows) {
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const int64_t tr = c0 + 4 * (lane & 15) + cc;  // out_t row (a column of x)
+          if (tr >= cols) continue;
+          uint8_t* dst = out_t + tr * rows + tc;
+          if (t16 && tc + 16 <= rows) {
+            *reinterpret_cast<uint4*>(dst) = tq[cc];
+          } else {
+            const uint32_t w[4] = {tq[cc].x, tq[cc].y, tq[cc].z, tq[cc].w};
+            for (int j = 0; j < 16 && tc + j < rows; ++j)
+              dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+          }
         }
       }
     }
-    __syncthreads();  // the next tile reuses the LDS staging
   }
   store_block_amax(m, amax_out, blockIdx.x);
 }
 
 int64_t transpose_blocks(int64_t rows, int64_t cols) {
-  const int64_t tiles = ((rows + kTT - 1) / kTT) * ((cols + kTT - 1) / kTT);
-  return tiles < kMaxTransposeBlocks ? (tiles > 0 ? tiles : 1) : kMaxTransposeBlocks;
+  const int64_t tiles = ((rows + kTR - 1) / kTR) * ((cols + kTT - 1) / kTT);
+  const int64_t blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+  return blocks < kMaxTransposeBlocks ? (blocks > 0 ? blocks : 1) : kMaxTransposeBlocks;
 }
 
 // Blocks of the row-major cast: up to kMaxCastBlocks, but no more than the consumers of

@@ -9,9 +9,11 @@ FETCH_SIZE / WRITE_SIZE counters into bytes.
 ``c2``: the whole config-2 MLP forward (quantize X and weights, gate/up GEMM + gated-GELU
 epilogue, H scale + cast, down GEMM). ``square``: one 8192^3 e4m3 GEMM, the steady-state
 main loop with no epilogue-heavy work. ``recipes``: the kernels of the other recipes and
-the fused norm: the config-2 MLP forward under MXFP8 (block quantize, MX gated-GELU GEMM,
-MX down GEMM), the axiswise (torchao rowwise) quantization of a [8192, 2560] activation
-per row and per column, and the fused RMSNorm of the same activation.
+the fused norm: the config-2 MLP forward under MXFP8 (block quantize, MX gated-GELU GEMM with H
+quantized in its epilogue, MX down GEMM), the axiswise (torchao rowwise) quantization of a [8192, 2560] activation
+per row and per column, and the fused RMSNorm of the same activation. ``c5``: the
+config-5 training step (the c2 MLP at M = 8192, forward and backward, delayed scaling with
+an amax history of 16).
 """
 
 import argparse
@@ -27,7 +29,7 @@ def main():
     p = argparse.ArgumentParser()
     p.add_argument("--iters", type=int, default=5)
     p.add_argument("--rows", type=int, default=4096)
-    p.add_argument("--case", choices=("c2", "square", "recipes"), default="c2")
+    p.add_argument("--case", choices=("c2", "square", "recipes", "c5"), default="c2")
     args = p.parse_args()
     dev = torch.device("cuda:0")
     if args.case == "square":
@@ -42,6 +44,9 @@ def main():
         return
     if args.case == "recipes":
         _recipes(dev, args.iters)
+        return
+    if args.case == "c5":
+        _c5(dev, args.iters)
         return
     c = workloads.config2(rows=args.rows)
     I = workloads.INTERMEDIATE
@@ -63,6 +68,24 @@ def main():
     print(f"profile_target done: {args.iters} iterations, copy {COPY_BYTES} bytes", flush=True)
 
 
+def _c5(dev, iters):
+    from . import linear, scaling
+
+    c = workloads.config5()
+    x = c["x"].to(dev).requires_grad_(True)
+    dy = c["dy"].to(dev)
+    I = c["w_gate"].shape[0]
+    w_gu = torch.cat([c["w_gate"], c["w_up"]]).to(dev).requires_grad_(True)
+    w_d = c["w_down"].to(dev).requires_grad_(True)
+    sc = (scaling.LinearScaling(c["history"]), scaling.LinearScaling(c["history"]))
+    for _ in range(iters):
+        x.grad = w_gu.grad = w_d.grad = None
+        y = linear.Fp8GegluMlpFunction.apply(x, w_gu, w_d, None, None, I, False, sc)
+        y.backward(dy)
+    torch.cuda.synchronize()
+    print(f"profile_target done: {iters} c5 training steps", flush=True)
+
+
 def _recipes(dev, iters):
     c = workloads.config2()
     I = workloads.INTERMEDIATE
@@ -76,8 +99,7 @@ def _recipes(dev, iters):
     for _ in range(iters):
         dst.copy_(src)
         xq, gq, dq = ops.quantize_mx(x), ops.quantize_mx(w_gu), ops.quantize_mx(w_d)
-        H, _ = ops.gemm_geglu_mx(xq.data, xq.scales, gq.data, gq.scales, I)
-        hq = ops.quantize_mx(H)
+        hq, _, _ = ops.gemm_geglu_mx_quant(xq.data, xq.scales, gq.data, gq.scales, I)
         ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales)
         ops.quantize_axiswise(a, ops.E4M3, rowwise=True, colwise=True)
         ops.rmsnorm(a, gamma, 1e-6)
