@@ -70,6 +70,28 @@ __device__ __forceinline__ float bf16_round(float f) {
   return __uint_as_float(f32_to_bf16_bits(f) << 16);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16x2 with round-to-nearest-even (gfx950 v_cvt_pk_bf16_f32); equal
+// to f32_to_bf16_bits on each value except that a NaN keeps its sign and payload bits.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// A packed bf16 pair with each NaN replaced by 0x7FC0 (torch's canonical bf16 NaN), so
+// that pack_bf16x2 then gives f32_to_bf16_bits bit for bit. A half h is NaN iff
+// (h & 0x7FFF) + 0x7F carries into bit 15; the low half's sum cannot reach bit 16.
+__device__ __forceinline__ uint32_t canon_nan_bf16x2(uint32_t w) {
+  const uint32_t nan = ((w & 0x7FFF7FFFu) + 0x007F007Fu) & 0x80008000u;
+  if (__builtin_expect(nan != 0, 0)) {
+    if (nan & 0x8000u) w = (w & 0xFFFF0000u) | 0x7FC0u;
+    if (nan & 0x80000000u) w = (w & 0x0000FFFFu) | 0x7FC00000u;
+  }
+  return w;
+}
+
 // Byte for an fp32 product p = f32(x) * scale that is NaN. It follows torch's CPU
 // result for clamp(x.float() * scale).to(float8): the NaN carries the scale's sign if
 // the scale is NaN, else x's sign if x is NaN, else (inf * 0) the x86 default NaN, which

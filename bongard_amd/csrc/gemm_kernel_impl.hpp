@@ -144,15 +144,6 @@ __device__ __forceinline__ v8i join(v4u lo, v4u hi) {
   return r;
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// Two fp32 -> packed bf16x2 with round-to-nearest-even (gfx950 v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  const f32x2_t v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-}
-
 // Epilogue staging in LDS: rows of CH 16-byte chunks; chunk c of row r lives at
 // c ^ (r & (CH - 1)) for power-of-two CH, else at (c + r) % CH, so that the 32 rows a
 // wave writes at once spread over the banks. Lanes put 8-byte runs (4 bf16) and get

@@ -29,6 +29,25 @@ int64_t bwd_blocks(int64_t M, int64_t I) {
 }
 
 
+// The chain for the two elements of one packed bf16 pair (g, u, dh words): d_g, d_u as
+// packed bf16 pairs (NaNs canonical, as torch's bf16 rounding gives them), and the running
+// amax key of |d_g|, |d_u|. Intermediate roundings use the packed RNE conversion.
+__device__ __forceinline__ void geglu_bwd_pair(uint32_t dhw, uint32_t gw, uint32_t uw,
+                                               uint32_t& dg, uint32_t& du, uint32_t& m) {
+  const float x0 = bf16_lo(gw), x1 = bf16_hi(gw);
+  const float u0 = bf16_lo(uw), u1 = bf16_hi(uw);
+  const float d0 = bf16_lo(dhw), d1 = bf16_hi(dhw);
+  float y0, y1, s0, s1;
+  gelu_tanh_fwd_bwd(x0, y0, s0);
+  gelu_tanh_fwd_bwd(x1, y1, s1);
+  const uint32_t a = pack_bf16x2(y0, y1);             // bf16(gelu(g))
+  const uint32_t da = pack_bf16x2(d0 * u0, d1 * u1);   // bf16(dh * u)
+  du = canon_nan_bf16x2(pack_bf16x2(d0 * bf16_lo(a), d1 * bf16_hi(a)));
+  dg = canon_nan_bf16x2(pack_bf16x2(bf16_lo(da) * s0, bf16_hi(da) * s1));
+  const uint32_t kg = dg & 0x7FFF7FFFu, ku = du & 0x7FFF7FFFu;
+  m = max(m, max(max(kg << 16, kg & 0xFFFF0000u), max(ku << 16, ku & 0xFFFF0000u)));
+}
+
 __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restrict__ dH,
                                                         const uint16_t* __restrict__ GU,
                                                         int64_t M, int64_t I,
@@ -49,26 +68,7 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restri
     const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
     uint32_t dg[4], du[4];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      uint32_t og = 0, ou = 0;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float x = h ? bf16_hi(gw[w]) : bf16_lo(gw[w]);
-        const float uu = h ? bf16_hi(uw[w]) : bf16_lo(uw[w]);
-        const float d = h ? bf16_hi(dhw[w]) : bf16_lo(dhw[w]);
-        float y, dydx;
-        gelu_tanh_fwd_bwd(x, y, dydx);
-        const float a = bf16_round(y);
-        const float da = bf16_round(d * uu);
-        const uint32_t bu = f32_to_bf16_bits(d * a);
-        const uint32_t bg = f32_to_bf16_bits(da * dydx);
-        og |= bg << (16 * h);
-        ou |= bu << (16 * h);
-        m = max(m, max((bg & 0x7FFFu) << 16, (bu & 0x7FFFu) << 16));
-      }
-      dg[w] = og;
-      du[w] = ou;
-    }
+    for (int w = 0; w < 4; ++w) geglu_bwd_pair(dhw[w], gw[w], uw[w], dg[w], du[w], m);
     *reinterpret_cast<uint4*>(dGU + row * 2 * I + col) = make_uint4(dg[0], dg[1], dg[2], dg[3]);
     *reinterpret_cast<uint4*>(dGU + row * 2 * I + I + col) = make_uint4(du[0], du[1], du[2], du[3]);
   }
@@ -79,39 +79,19 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restri
 // The geglu backward fused with its delayed-scaling cast (for 'fp8_delayed', where dGU's
 // scale is known before dGU exists): the same per-element chain as geglu_bwd_kernel, the
 // bf16 d_g, d_u quantized at once with the role's delayed scale, written as fp8 rows
-// [M, 2I] and/or through an LDS transpose as fp8 [2I, M] (the wgrad layout), plus this
-// step's amax partials of |dGU|. Tiles of 64 rows x 64 columns of I; thread t handles 16
-// consecutive columns of one row for d_g and the same for d_u. Identical bytes to
-// geglu_bwd_kernel followed by the delayed cast of its output.
+// [M, 2I] and/or transposed as fp8 [2I, M] (the wgrad layout), plus this step's amax
+// partials of |dGU|. One 64-row x 64-column tile of I per wave: the wave streams it in
+// 8-row pieces (dH, g, u: 16-byte loads, four pieces in flight), stages the fp8 d_g and
+// d_u bytes in its own LDS regions and reads them back transposed (wave_transpose64_staged).
+// Identical bytes to geglu_bwd_kernel followed by the delayed cast of its output.
 constexpr int kTT = 64;
-constexpr int kTPitch = kTT + 4;
+constexpr int kFusedWaves = kNT / 64;
 constexpr int64_t kMaxFusedBlocks = 1024;
 
 int64_t fused_blocks(int64_t M, int64_t I) {
   const int64_t tiles = ((M + kTT - 1) / kTT) * (I / kTT);
-  return tiles < 1 ? 1 : (tiles < kMaxFusedBlocks ? tiles : kMaxFusedBlocks);
-}
-
-__device__ __forceinline__ void geglu_bwd_pair(uint32_t dhw, uint32_t gw, uint32_t uw,
-                                               uint32_t& dg, uint32_t& du, uint32_t& m) {
-  uint32_t og = 0, ou = 0;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const float x = h ? bf16_hi(gw) : bf16_lo(gw);
-    const float uu = h ? bf16_hi(uw) : bf16_lo(uw);
-    const float d = h ? bf16_hi(dhw) : bf16_lo(dhw);
-    float y, dydx;
-    gelu_tanh_fwd_bwd(x, y, dydx);
-    const float a = bf16_round(y);
-    const float da = bf16_round(d * uu);
-    const uint32_t bu = f32_to_bf16_bits(d * a);
-    const uint32_t bg = f32_to_bf16_bits(da * dydx);
-    og |= bg << (16 * h);
-    ou |= bu << (16 * h);
-    m = max(m, max((bg & 0x7FFFu) << 16, (bu & 0x7FFFu) << 16));
-  }
-  dg = og;
-  du = ou;
+  const int64_t blocks = (tiles + kFusedWaves - 1) / kFusedWaves;
+  return blocks < 1 ? 1 : (blocks < kMaxFusedBlocks ? blocks : kMaxFusedBlocks);
 }
 
 template <int FMT>
@@ -120,73 +100,69 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_delayed_kernel(
     float* __restrict__ state, int len, int pos, const uint32_t* __restrict__ prev,
     int64_t n_prev, float* __restrict__ meta_out, uint8_t* __restrict__ out,
     uint8_t* __restrict__ out_t, uint32_t* __restrict__ partials) {
-  __shared__ uint32_t tiles[2][kTT * kTPitch / 4];
+  __shared__ uint32_t stage[kFusedWaves][2][kWaveTileDwords];
   const float scale =
       delayed_scale_block<kNT>(state, len, pos, prev, n_prev, Fp8Max<FMT>::value, meta_out);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t tiles_c = I / kTT;
   const int64_t ntiles = tiles_c * ((M + kTT - 1) / kTT);
-  const int t = threadIdx.x;
-  const int lr = t >> 2, lc = (t & 3) * 16;
+  const int ch = lane & 7;  // 16-byte chunk of the piece's rows
+  uint32_t* lg = stage[wid][0];
+  uint32_t* lu = stage[wid][1];
   uint32_t m = 0;
-  for (int64_t tile_id = blockIdx.x; tile_id < ntiles; tile_id += gridDim.x) {
+  for (int64_t tile_id = (int64_t)blockIdx.x * kFusedWaves + wid; tile_id < ntiles;
+       tile_id += (int64_t)gridDim.x * kFusedWaves) {
     const int64_t r0 = (tile_id / tiles_c) * kTT, c0 = (tile_id % tiles_c) * kTT;
-    const int64_t r = r0 + lr, c = c0 + lc;
-    uint32_t qg[4] = {0u, 0u, 0u, 0u}, qu[4] = {0u, 0u, 0u, 0u};
-    if (r < M) {
-      const uint4* dh4 = reinterpret_cast<const uint4*>(dH + r * I + c);
-      const uint4* g4 = reinterpret_cast<const uint4*>(GU + r * 2 * I + c);
-      const uint4* u4 = reinterpret_cast<const uint4*>(GU + r * 2 * I + I + c);
+    const int64_t c = c0 + 8 * ch;
 #pragma unroll
-      for (int hv = 0; hv < 2; ++hv) {
-        const uint4 dh = dh4[hv], g = g4[hv], u = u4[hv];
-        const uint32_t dhw[4] = {dh.x, dh.y, dh.z, dh.w};
-        const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
-        const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+    for (int half = 0; half < 2; ++half) {
+      uint4 dh[4], g[4], u[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t r = r0 + 32 * half + 8 * k + (lane >> 3);
+        dh[k] = g[k] = u[k] = make_uint4(0u, 0u, 0u, 0u);
+        if (r < M) {
+          dh[k] = *reinterpret_cast<const uint4*>(dH + r * I + c);
+          g[k] = *reinterpret_cast<const uint4*>(GU + r * 2 * I + c);
+          u[k] = *reinterpret_cast<const uint4*>(GU + r * 2 * I + I + c);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int lr = 32 * half + 8 * k + (lane >> 3);
+        const int64_t r = r0 + lr;
+        const uint32_t dhw[4] = {dh[k].x, dh[k].y, dh[k].z, dh[k].w};
+        const uint32_t gw[4] = {g[k].x, g[k].y, g[k].z, g[k].w};
+        const uint32_t uw[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
         uint32_t dg[4], du[4];
 #pragma unroll
         for (int w = 0; w < 4; ++w) geglu_bwd_pair(dhw[w], gw[w], uw[w], dg[w], du[w], m);
-        const uint2 a = quant8_bf16<FMT>(make_uint4(dg[0], dg[1], dg[2], dg[3]), scale);
-        const uint2 b = quant8_bf16<FMT>(make_uint4(du[0], du[1], du[2], du[3]), scale);
-        qg[2 * hv] = a.x; qg[2 * hv + 1] = a.y;
-        qu[2 * hv] = b.x; qu[2 * hv + 1] = b.y;
-      }
-      if (out) {
-        *reinterpret_cast<uint4*>(out + r * 2 * I + c) = make_uint4(qg[0], qg[1], qg[2], qg[3]);
-        *reinterpret_cast<uint4*>(out + r * 2 * I + I + c) =
-            make_uint4(qu[0], qu[1], qu[2], qu[3]);
+        const uint2 qg = quant8_bf16<FMT>(make_uint4(dg[0], dg[1], dg[2], dg[3]), scale);
+        const uint2 qu = quant8_bf16<FMT>(make_uint4(du[0], du[1], du[2], du[3]), scale);
+        if (out && r < M) {
+          *reinterpret_cast<uint2*>(out + r * 2 * I + c) = qg;
+          *reinterpret_cast<uint2*>(out + r * 2 * I + I + c) = qu;
+        }
+        lg[lr * kWaveTilePitch + 2 * ch] = qg.x;
+        lg[lr * kWaveTilePitch + 2 * ch + 1] = qg.y;
+        lu[lr * kWaveTilePitch + 2 * ch] = qu.x;
+        lu[lr * kWaveTilePitch + 2 * ch + 1] = qu.y;
       }
     }
     if (out_t) {
-      uint8_t* tg = reinterpret_cast<uint8_t*>(tiles[0]);
-      uint8_t* tu = reinterpret_cast<uint8_t*>(tiles[1]);
-      uint32_t* dg_l = reinterpret_cast<uint32_t*>(tg + lr * kTPitch + lc);
-      uint32_t* du_l = reinterpret_cast<uint32_t*>(tu + lr * kTPitch + lc);
+      const int64_t tc = r0 + (lane >> 4) * 16;  // column of out_t (a row of dGU)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        dg_l[k] = qg[k];
-        du_l[k] = qu[k];
-      }
-      __syncthreads();
-      const int oc = t >> 2, orow = (t & 3) * 16;
-      const int64_t tc = r0 + orow;  // column of out_t (a row of dGU)
-      if (tc < M) {
+      for (int which = 0; which < 2; ++which) {
+        uint4 tq[4];
+        wave_transpose64_staged(which ? lu : lg, lane, tq);
+        if (tc < M) {  // M % 16 == 0: whole 16-byte segments
 #pragma unroll
-        for (int which = 0; which < 2; ++which) {
-          const uint8_t* tb = which ? tu : tg;
-          uint32_t w[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t b0 = tb[(orow + 4 * j + 0) * kTPitch + oc];
-            const uint32_t b1 = tb[(orow + 4 * j + 1) * kTPitch + oc];
-            const uint32_t b2 = tb[(orow + 4 * j + 2) * kTPitch + oc];
-            const uint32_t b3 = tb[(orow + 4 * j + 3) * kTPitch + oc];
-            w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+          for (int cc = 0; cc < 4; ++cc) {
+            const int64_t tr = (which ? I : 0) + c0 + 4 * (lane & 15) + cc;  // row of out_t
+            *reinterpret_cast<uint4*>(out_t + tr * M + tc) = tq[cc];
           }
-          const int64_t tr = (which ? I : 0) + c0 + oc;  // row of out_t
-          *reinterpret_cast<uint4*>(out_t + tr * M + tc) = make_uint4(w[0], w[1], w[2], w[3]);
         }
       }
-      __syncthreads();  // the next tile reuses the LDS tiles
     }
   }
   m = block_max_u32<kNT>(m);
