@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -65,6 +65,12 @@ SIGNATURES = {
                                         c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                         c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                         c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "bf8_delayed_scale_fold": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int64, c_int,
+                                       c_void_p, c_void_p]),
+    "bf8_gemm_geglu_quant": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64,
+                                     c_int64, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                                     c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                     c_void_p]),
     "bf8_rmsnorm_partials": (c_int64, [c_int64]),
     "bf8_rmsnorm_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_float, c_int,
                                  c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -146,6 +146,37 @@ __device__ __forceinline__ uint2 quant8_bf16(uint4 v, float scale) {
   return r;
 }
 
+// quant4 / quant8_bf16 for inputs known to be finite with a finite scale (no product can
+// be NaN): the same bytes without the NaN patch. CLAMP = false further drops the clamp,
+// for callers whose products are known to lie within +-fp8_max (MX blocks of finite
+// values).
+template <int FMT, bool CLAMP>
+__device__ __forceinline__ uint32_t quant4_finite(float p0, float p1, float p2, float p3) {
+  constexpr float M = Fp8Max<FMT>::value;
+  if constexpr (CLAMP) {
+    p0 = __builtin_amdgcn_fmed3f(p0, -M, M);
+    p1 = __builtin_amdgcn_fmed3f(p1, -M, M);
+    p2 = __builtin_amdgcn_fmed3f(p2, -M, M);
+    p3 = __builtin_amdgcn_fmed3f(p3, -M, M);
+  }
+  uint32_t w;
+  if constexpr (FMT == BF8_E4M3) {
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(p0, p1, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(p2, p3, w, true);
+  } else {
+    w = __builtin_amdgcn_cvt_pk_bf8_f32(p0, p1, 0, false);
+    w = __builtin_amdgcn_cvt_pk_bf8_f32(p2, p3, w, true);
+  }
+  return w;
+}
+template <int FMT, bool CLAMP>
+__device__ __forceinline__ uint2 quant8_bf16_finite(uint4 v, float scale) {
+  return make_uint2(quant4_finite<FMT, CLAMP>(bf16_lo(v.x) * scale, bf16_hi(v.x) * scale,
+                                              bf16_lo(v.y) * scale, bf16_hi(v.y) * scale),
+                    quant4_finite<FMT, CLAMP>(bf16_lo(v.z) * scale, bf16_hi(v.z) * scale,
+                                              bf16_lo(v.w) * scale, bf16_hi(v.w) * scale));
+}
+
 // Max of |bf16| over the 8 values of v, as an fp32 bit pattern key: for non-negative
 // floats the unsigned order of the bits is the numeric order, and NaN keys sort above
 // +inf (as torch's NaN-propagating max does).

@@ -378,29 +378,59 @@ int64_t bf8_geglu_partials(int64_t M, int64_t I) {
   return (int64_t)pl.tiles_m * pl.tiles_n;
 }
 
-int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw, int64_t M,
-                   int64_t I, int64_t K, const float* x_scale_inv, const float* w_scale_inv,
-                   int w_scale_stride, void* H, int64_t ldh, void* GU, uint32_t* h_partials,
-                   void* stream) {
-  BF8_CHECK(M >= 1 && I >= 1 && K >= 16, "bf8_gemm_geglu: bad shape");
-  BF8_CHECK(I % 128 == 0, "bf8_gemm_geglu: I must be a multiple of 128 (got %lld)", (long long)I);
+// The gate/up GEMM + gated GELU; h_scale set: H quantized in the epilogue (H8, H8t).
+static int geglu_entry(const char* who, const uint8_t* X, int64_t ldx, const uint8_t* W,
+                       int64_t ldw, int64_t M, int64_t I, int64_t K, const float* x_scale_inv,
+                       const float* w_scale_inv, int w_scale_stride, void* H, int64_t ldh,
+                       const float* h_scale, uint8_t* H8, uint8_t* H8t, void* GU,
+                       uint32_t* h_partials, void* stream) {
+  BF8_CHECK(M >= 1 && I >= 1 && K >= 16, "%s: bad shape", who);
+  BF8_CHECK(I % 128 == 0, "%s: I must be a multiple of 128 (got %lld)", who, (long long)I);
   BF8_CHECK(K % 16 == 0 && ldx % 16 == 0 && ldw % 16 == 0 && ldx >= K && ldw >= K,
-            "bf8_gemm_geglu: need K, ldx, ldw multiples of 16 and >= K");
-  BF8_CHECK(ldh >= I && ldh % 4 == 0, "bf8_gemm_geglu: bad ldh");
+            "%s: need K, ldx, ldw multiples of 16 and >= K", who);
+  BF8_CHECK(H || H8, "%s: H is NULL", who);
+  BF8_CHECK(!H || (ldh >= I && ldh % 4 == 0), "%s: bad ldh", who);
   BF8_CHECK(((uintptr_t)X & 15) == 0 && ((uintptr_t)W & 15) == 0 && ((uintptr_t)H & 15) == 0 &&
                 ((uintptr_t)GU & 15) == 0,
-            "bf8_gemm_geglu: X, W, H, GU must be 16-byte aligned");
-  BF8_CHECK(M * ldx < (1LL << 31) && 2 * I * ldw < (1LL << 31), "bf8_gemm_geglu: operand > 2 GiB");
-  BF8_CHECK(x_scale_inv && w_scale_inv && h_partials, "bf8_gemm_geglu: NULL pointer");
+            "%s: X, W, H, GU must be 16-byte aligned", who);
+  BF8_CHECK(M * ldx < (1LL << 31) && 2 * I * ldw < (1LL << 31), "%s: operand > 2 GiB", who);
+  BF8_CHECK(x_scale_inv && w_scale_inv && h_partials, "%s: NULL pointer", who);
+  if (H8) {
+    BF8_CHECK(h_scale && ((uintptr_t)H8 & 7) == 0, "%s: H8 needs h_scale and 8-byte alignment",
+              who);
+    BF8_CHECK(M * I < (1LL << 31), "%s: H8 larger than 2 GiB", who);
+  }
+  BF8_CHECK(!H8t || H8, "%s: H8t needs H8", who);
+  BF8_CHECK(!H8t || (M % 32 == 0 && ((uintptr_t)H8t & 15) == 0),
+            "%s: H8t needs M %% 32 == 0 (got %lld) and 16-byte alignment", who, (long long)M);
   GemmParams p{};
   p.A = X; p.B = W; p.lda = ldx; p.ldb = ldw;
   p.M = (int)M; p.N = (int)(2 * I); p.K = (int)K; p.I = (int)I;
   p.a_sinv = x_scale_inv; p.b_sinv = w_scale_inv; p.b_stride = w_scale_stride;
   p.n_seg = 1;
   p.C = H; p.ldc = ldh; p.GU = (uint16_t*)GU; p.partials = h_partials;
+  p.h8_scale = h_scale; p.h8 = H8; p.h8t = H8t;
   Plan pl = choose_plan(M, 2 * I, K, true, 0);
   return launch_plan(pl, p, EPI_GEGLU, BF8_OUT_BF16, BF8_E4M3, BF8_E4M3, nullptr,
                      as_stream(stream));
+}
+
+int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw, int64_t M,
+                   int64_t I, int64_t K, const float* x_scale_inv, const float* w_scale_inv,
+                   int w_scale_stride, void* H, int64_t ldh, void* GU, uint32_t* h_partials,
+                   void* stream) {
+  return geglu_entry("bf8_gemm_geglu", X, ldx, W, ldw, M, I, K, x_scale_inv, w_scale_inv,
+                     w_scale_stride, H, ldh, nullptr, nullptr, nullptr, GU, h_partials, stream);
+}
+
+int bf8_gemm_geglu_quant(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw,
+                         int64_t M, int64_t I, int64_t K, const float* x_scale_inv,
+                         const float* w_scale_inv, int w_scale_stride, const float* h_scale,
+                         void* H, int64_t ldh, uint8_t* H8, uint8_t* H8t, void* GU,
+                         uint32_t* h_partials, void* stream) {
+  BF8_CHECK(H8 != nullptr, "bf8_gemm_geglu_quant: H8 is NULL");
+  return geglu_entry("bf8_gemm_geglu_quant", X, ldx, W, ldw, M, I, K, x_scale_inv, w_scale_inv,
+                     w_scale_stride, H, ldh, h_scale, H8, H8t, GU, h_partials, stream);
 }
 
 // ---- MX (block-scaled) GEMMs ----------------------------------------------------------

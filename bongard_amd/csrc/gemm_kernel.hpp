@@ -32,9 +32,11 @@ struct GemmParams {
   int64_t ldc;
   uint16_t* GU;
   uint32_t* partials;     // GEGLU: one amax key of |H| per tile
-  // MX GEGLU: H quantized in the epilogue (C, the bf16 H, may then be NULL). h8: e4m3
-  // [M, I] with E8M0 scales h8_sc [M, h8_sc_ld] (blocks along I); h8t (optional, needs
-  // M % 32 == 0): e4m3 H^T [I, M] with scales h8t_sc [I, h8t_sc_ld] (blocks along M).
+  // GEGLU with H quantized in the epilogue (C, the bf16 H, may then be NULL). h8: e4m3
+  // [M, I]; h8t (optional, needs M % 32 == 0): e4m3 H^T [I, M]. MX: E8M0 block scales
+  // h8_sc [M, h8_sc_ld] (blocks along I) and h8t_sc [I, h8t_sc_ld] (blocks along M);
+  // otherwise one scale, read from the device word h8_scale.
+  const float* h8_scale;
   uint8_t* h8;
   uint8_t* h8_sc;
   uint8_t* h8t;

@@ -185,7 +185,7 @@ __device__ __forceinline__ void store_bf16x8(uint16_t* dst, uint4 d, int64_t ld)
 // MX quantizer's arithmetic: along rows into h8 / h8_sc (a 4-lane group per block, 8
 // values a lane), and, when h8t is set, along columns into h8t / h8t_sc (a lane per
 // column pair and 32-row block). C, when set, also receives the bf16 H.
-template <int ROWS, int CH>
+template <int ROWS, int CH, bool FAST>
 __device__ __forceinline__ void mx_h_epilogue(const GemmParams& p, const uint8_t* wbuf, int lane,
                                               int gm0, int h0) {
 #pragma unroll 4
@@ -201,8 +201,9 @@ __device__ __forceinline__ void mx_h_epilogue(const GemmParams& p, const uint8_t
       const int n = h0 + c * 8;
       if (p.C) store_bf16x8(reinterpret_cast<uint16_t*>(p.C) + (int64_t)gm * p.ldc + n, d, p.ldc);
       const uint32_t e = mx_exponent<BF8_E4M3>(k);
+      const float mult = mx_multiplier(e);
       *reinterpret_cast<uint2*>(p.h8 + (int64_t)gm * p.I + n) =
-          quant8_bf16<BF8_E4M3>(d, mx_multiplier(e));
+          FAST ? quant8_bf16_finite<BF8_E4M3, false>(d, mult) : quant8_bf16<BF8_E4M3>(d, mult);
       if ((c & 3) == 0) p.h8_sc[(int64_t)gm * p.h8_sc_ld + (n >> 5)] = (uint8_t)e;
     }
   }
@@ -233,8 +234,13 @@ __device__ __forceinline__ void mx_h_epilogue(const GemmParams& p, const uint8_t
       const float a2 = bf16_lo(v[4 * j + 2]), a3 = bf16_lo(v[4 * j + 3]);
       const float b0 = bf16_hi(v[4 * j]), b1 = bf16_hi(v[4 * j + 1]);
       const float b2 = bf16_hi(v[4 * j + 2]), b3 = bf16_hi(v[4 * j + 3]);
-      q0[j] = quant4<BF8_E4M3>(a0 * s0, a1 * s0, a2 * s0, a3 * s0, a0, a1, a2, a3, s0);
-      q1[j] = quant4<BF8_E4M3>(b0 * s1, b1 * s1, b2 * s1, b3 * s1, b0, b1, b2, b3, s1);
+      if constexpr (FAST) {
+        q0[j] = quant4_finite<BF8_E4M3, false>(a0 * s0, a1 * s0, a2 * s0, a3 * s0);
+        q1[j] = quant4_finite<BF8_E4M3, false>(b0 * s1, b1 * s1, b2 * s1, b3 * s1);
+      } else {
+        q0[j] = quant4<BF8_E4M3>(a0 * s0, a1 * s0, a2 * s0, a3 * s0, a0, a1, a2, a3, s0);
+        q1[j] = quant4<BF8_E4M3>(b0 * s1, b1 * s1, b2 * s1, b3 * s1, b0, b1, b2, b3, s1);
+      }
     }
     const int n = h0 + 2 * cp;
     uint4* d0 = reinterpret_cast<uint4*>(p.h8t + (int64_t)n * p.M + gm);
@@ -254,6 +260,62 @@ __device__ __forceinline__ void mx_h_epilogue(const GemmParams& p, const uint8_t
         r1[pb] = (uint8_t)kMxPadScale;
       }
     }
+  }
+}
+
+// Tensor-scaled gated-GELU epilogue (a scale known before the GEMM, as delayed scaling
+// has): the wave's staged H quantized to e4m3 with `scale` exactly as the standalone cast
+// does (quant8_bf16), into h8 [M, I] and, when h8t is set, h8t = H^T [I, M] (a lane per
+// column pair and 32-row block; M % 32 == 0). C, when set, also receives the bf16 H.
+template <int ROWS, int CH, bool FAST>
+__device__ __forceinline__ void scaled_h_epilogue(const GemmParams& p, const uint8_t* wbuf,
+                                                  int lane, int gm0, int h0, float scale) {
+#pragma unroll 4
+  for (int it = 0; it < ROWS * CH / 64; ++it) {
+    const int idx = it * 64 + lane;
+    const int row = idx / CH, c = idx % CH;
+    const uint4 d = stage_get<CH>(wbuf, row, c);
+    const int gm = gm0 + row;
+    if (gm < p.M) {
+      const int n = h0 + c * 8;
+      if (p.C) store_bf16x8(reinterpret_cast<uint16_t*>(p.C) + (int64_t)gm * p.ldc + n, d, p.ldc);
+      *reinterpret_cast<uint2*>(p.h8 + (int64_t)gm * p.I + n) =
+          FAST ? quant8_bf16_finite<BF8_E4M3, true>(d, scale) : quant8_bf16<BF8_E4M3>(d, scale);
+    }
+  }
+  if (p.h8t == nullptr) return;
+  constexpr int CP = CH * 4;
+  constexpr int ITEMS = (ROWS / 32) * CP;
+#pragma unroll 1
+  for (int item = lane; item < ITEMS; item += 64) {
+    const int blk = item / CP, cp = item % CP;
+    const int gm = gm0 + blk * 32;
+    if (gm >= p.M) continue;
+    uint32_t q0[8], q1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = stage_get_pair<CH>(wbuf, blk * 32 + 4 * j + e, 2 * cp);
+      const float a0 = bf16_lo(v[0]), a1 = bf16_lo(v[1]), a2 = bf16_lo(v[2]), a3 = bf16_lo(v[3]);
+      const float b0 = bf16_hi(v[0]), b1 = bf16_hi(v[1]), b2 = bf16_hi(v[2]), b3 = bf16_hi(v[3]);
+      if constexpr (FAST) {
+        q0[j] = quant4_finite<BF8_E4M3, true>(a0 * scale, a1 * scale, a2 * scale, a3 * scale);
+        q1[j] = quant4_finite<BF8_E4M3, true>(b0 * scale, b1 * scale, b2 * scale, b3 * scale);
+      } else {
+        q0[j] = quant4<BF8_E4M3>(a0 * scale, a1 * scale, a2 * scale, a3 * scale, a0, a1, a2, a3,
+                                 scale);
+        q1[j] = quant4<BF8_E4M3>(b0 * scale, b1 * scale, b2 * scale, b3 * scale, b0, b1, b2, b3,
+                                 scale);
+      }
+    }
+    const int n = h0 + 2 * cp;
+    uint4* d0 = reinterpret_cast<uint4*>(p.h8t + (int64_t)n * p.M + gm);
+    uint4* d1 = reinterpret_cast<uint4*>(p.h8t + (int64_t)(n + 1) * p.M + gm);
+    d0[0] = make_uint4(q0[0], q0[1], q0[2], q0[3]);
+    d0[1] = make_uint4(q0[4], q0[5], q0[6], q0[7]);
+    d1[0] = make_uint4(q1[0], q1[1], q1[2], q1[3]);
+    d1[1] = make_uint4(q1[4], q1[5], q1[6], q1[7]);
   }
 }
 
@@ -288,10 +350,11 @@ gemm_kernel(GemmParams p) {
   float sb[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) sb[s] = MX ? 1.0f : s < p.n_seg ? p.b_sinv[s * p.b_stride] : 0.0f;
-  float ag = 0.0f, au = 0.0f;
+  float ag = 0.0f, au = 0.0f, hs = 0.0f;
   if constexpr (EPI == EPI_GEGLU) {
     ag = MX ? 1.0f : sa * p.b_sinv[0];
     au = MX ? 1.0f : sa * p.b_sinv[p.b_stride];
+    if (!MX && p.h8) hs = *p.h8_scale;  // the quantization scale of H
   }
 
   int tm, tn, split;
@@ -694,9 +757,22 @@ gemm_kernel(GemmParams p) {
           }
         }
       }
-      if constexpr (MX && pass == 0) {
+      if constexpr (pass == 0) {
         if (p.h8) {
-          mx_h_epilogue<ROWS, CH>(p, wbuf, lane, m0 + wave_m0, wave_h0);
+          // every value this wave quantizes is one it staged: with none of them inf or NaN
+          // (and a finite scale) no product can be NaN, so the NaN patch is skipped
+          const bool finite = !__any(hmax >= 0x7F800000u) && (MX || hs < INFINITY);
+          if constexpr (MX) {
+            if (finite)
+              mx_h_epilogue<ROWS, CH, true>(p, wbuf, lane, m0 + wave_m0, wave_h0);
+            else
+              mx_h_epilogue<ROWS, CH, false>(p, wbuf, lane, m0 + wave_m0, wave_h0);
+          } else {
+            if (finite)
+              scaled_h_epilogue<ROWS, CH, true>(p, wbuf, lane, m0 + wave_m0, wave_h0, hs);
+            else
+              scaled_h_epilogue<ROWS, CH, false>(p, wbuf, lane, m0 + wave_m0, wave_h0, hs);
+          }
           return;
         }
       }

@@ -297,6 +297,16 @@ __global__ void delayed_begin_kernel(float* state, int len, float fp8_max) {
   }
 }
 
+// Only the scale step of a delayed cast (for a producer that quantizes its own output with
+// the scale, as the gated-GELU GEMM does for H): push the previous step's amax, derive
+// this step's scale and publish it at state + len and meta_out.
+__global__ __launch_bounds__(kNT) void delayed_fold_kernel(float* state, int len, int pos,
+                                                           const uint32_t* __restrict__ prev,
+                                                           int64_t n_prev, float fp8_max,
+                                                           float* meta_out) {
+  delayed_scale_block<kNT>(state, len, pos, prev, n_prev, fp8_max, meta_out);
+}
+
 __global__ __launch_bounds__(kNT) void delayed_end_kernel(float* state, int len,
                                                           const uint32_t* __restrict__ partials,
                                                           int64_t np) {
@@ -407,7 +417,7 @@ using namespace bf8;
 extern "C" {
 
 const char* bf8_last_error(void) { return bf8::g_err; }
-int bf8_abi_version(void) { return 7; }
+int bf8_abi_version(void) { return 8; }
 
 int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
 
@@ -493,6 +503,18 @@ int bf8_delayed_scale_begin(float* state, int len, int fmt, void* stream) {
   hipLaunchKernelGGL(delayed_begin_kernel, dim3(1), dim3(64), 0, as_stream(stream), state, len,
                      fp8_max_host(fmt));
   return launch_status("delayed_begin_kernel");
+}
+
+int bf8_delayed_scale_fold(float* state, int len, int pos, const uint32_t* prev_partials,
+                           int64_t n_prev, int fmt, float* meta_out, void* stream) {
+  BF8_CHECK(state && len >= 1 && len <= 1024, "bf8_delayed_scale_fold: bad state/len");
+  BF8_CHECK(pos >= 0 && pos < len, "bf8_delayed_scale_fold: pos %d outside [0, %d)", pos, len);
+  BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "bf8_delayed_scale_fold: bad fmt %d", fmt);
+  BF8_CHECK(n_prev >= 0 && (n_prev == 0 || prev_partials),
+            "bf8_delayed_scale_fold: bad previous partials");
+  hipLaunchKernelGGL(delayed_fold_kernel, dim3(1), dim3(kNT), 0, as_stream(stream), state, len,
+                     pos, prev_partials, n_prev, fp8_max_host(fmt), meta_out);
+  return launch_status("delayed_fold_kernel");
 }
 
 int bf8_delayed_scale_end(float* state, int len, const uint32_t* partials, int64_t n_partials,

@@ -283,11 +283,24 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
                                    transpose=ctx.needs_input_grad[2])
         else:
             count = ops.geglu_partials_count(M, I)
-            H, GU, _ = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
-                                      keep_gu=train,
-                                      partials=ds.input.partials_for_producer(count, x.device))
-            hq = ds.input.quantize(H, rowwise=True, transpose=ctx.needs_input_grad[2],
-                                   producer_count=count)
+            transpose = ctx.needs_input_grad[2]
+            if M % 32 == 0 or not transpose:
+                # H's scale is known before the GEMM: the epilogue casts H (and its
+                # transpose for the down wgrad) itself; no bf16 H round trip
+                def launch(st, length, pos, prev, parts):
+                    meta = ops.delayed_scale_fold(st, length, pos, prev, E4M3)
+                    q, gu, _, _ = ops.gemm_geglu_quant(xq.data, xq.meta, gu_q.data, gu_q.meta,
+                                                       I, meta, transpose=transpose,
+                                                       keep_gu=train, partials=parts)
+                    return q, gu
+
+                hq, GU = ds.input.produce(count, x.device, launch)
+            else:
+                H, GU, _ = ops.gemm_geglu(
+                    xq.data, xq.meta, gu_q.data, gu_q.meta, I, keep_gu=train,
+                    partials=ds.input.partials_for_producer(count, x.device))
+                hq = ds.input.quantize(H, rowwise=True, transpose=transpose,
+                                       producer_count=count)
         h_meta = hq.meta
         if down_q is None:
             down_q = quantize_weight(

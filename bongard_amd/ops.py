@@ -479,6 +479,53 @@ def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu
     return H, GU, parts
 
 
+def gemm_geglu_quant(x8, x_meta, w8, w_meta, intermediate, h_meta, *, w_meta_stride=0,
+                     transpose=False, keep_gu=False, keep_h=False, partials=None):
+    """:func:`gemm_geglu` with H cast to e4m3 in the epilogue with the scale ``h_meta[1]``
+    (a device meta record, e.g. from :func:`delayed_scale_fold`), byte for byte what
+    :func:`cast` gives for the bf16 H. Returns ``(hq, GU or None, H or None, h_partials)``:
+    ``hq`` the :class:`Fp8Tensor` of H (``data`` [M, I], ``data_t`` [I, M] when
+    ``transpose``, which needs M % 32 == 0) with meta ``h_meta``."""
+    _require_gpu(x8, w8, x_meta, w_meta, h_meta)
+    M, K = x8.shape
+    I = int(intermediate)
+    if w8.shape != (2 * I, K):
+        raise ValueError(f"gemm_geglu_quant: weight must be [{2 * I}, {K}], got {tuple(w8.shape)}")
+    dev = x8.device
+    L = _lib.lib()
+    h8 = torch.empty((M, I), dtype=TORCH_FP8[E4M3], device=dev)
+    h8t = torch.empty((I, M), dtype=TORCH_FP8[E4M3], device=dev) if transpose else None
+    H = torch.empty((M, I), dtype=torch.bfloat16, device=dev) if keep_h else None
+    GU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=dev) if keep_gu else None
+    count = int(L.bf8_geglu_partials(M, I))
+    if partials is None:
+        parts = torch.empty(count, dtype=torch.int32, device=dev)
+    else:
+        if partials.numel() < count or partials.dtype != torch.int32:
+            raise ValueError(f"gemm_geglu_quant: partials must be int32 with >= {count} entries")
+        parts = partials[:count]
+    _lib.check(L.bf8_gemm_geglu_quant(
+        _ptr(x8), x8.stride(0), _ptr(w8), w8.stride(0), M, I, K, _sinv_ptr(x_meta),
+        _sinv_ptr(w_meta), w_meta_stride, ctypes.c_void_p(h_meta.data_ptr() + 4), _ptr(H), I,
+        _ptr(h8), _ptr(h8t), _ptr(GU), _ptr(parts), _stream(dev)), "bf8_gemm_geglu_quant")
+    return Fp8Tensor(h8, h8t, h_meta, E4M3, M, I), GU, H, parts
+
+
+def delayed_scale_fold(state, length, pos, prev_partials, fmt=E4M3, meta_out=None):
+    """The scale step of :func:`cast_delayed` alone: pushes ``prev_partials`` (the previous
+    step's amax partials, or None) into history slot ``pos``, derives this step's scale and
+    returns it as a meta record (``meta_out``, allocated when None)."""
+    _require_gpu(state)
+    if meta_out is None:
+        meta_out = new_meta(state.device)
+    n_prev = 0 if prev_partials is None else prev_partials.numel()
+    _lib.check(_lib.lib().bf8_delayed_scale_fold(_ptr(state), int(length), int(pos),
+                                                 _ptr(prev_partials), n_prev, fmt,
+                                                 _ptr(meta_out), _stream(state.device)),
+               "bf8_delayed_scale_fold")
+    return meta_out
+
+
 def geglu_bwd_partials_count(M, intermediate):
     return int(_lib.lib().bf8_geglu_bwd_partials(int(M), int(intermediate)))
 

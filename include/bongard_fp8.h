@@ -168,6 +168,14 @@ int bf8_delayed_scale_begin(float* state, int len, int fmt, void* stream);
 int bf8_delayed_scale_end(float* state, int len, const uint32_t* partials,
                           int64_t n_partials, void* stream);
 
+/* The scale step of bf8_cast_delayed_bf16 alone (same state / len / pos / prev_partials /
+ * meta_out semantics, meta_out nullable): for a producer that then quantizes its own
+ * output with the published scale (bf8_gemm_geglu_quant reading meta_out + 1) and writes
+ * the new amax partials itself. Replaces the scale update of TE's DelayedScaling cast of
+ * the fc2 input (bongard/te_linear.py:98-103; bongard/fused_mlp.py:25-30). */
+int bf8_delayed_scale_fold(float* state, int len, int pos, const uint32_t* prev_partials,
+                           int64_t n_prev, int fmt, float* meta_out, void* stream);
+
 /* Delayed-scaling cast in one pass (the begin / cast / amax / end sequence above fused):
  * the kernel first pushes the previous step's amax (max of prev_partials, n_prev of them,
  * n_prev = 0 on the first step) into slot pos (0 <= pos < len) of the history, derives
@@ -228,6 +236,19 @@ int bf8_gemm_axiswise(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B
                       int64_t ldb, int64_t M, int64_t N, int64_t K, const float* a_scale_inv,
                       int a_vec, const float* b_scale_inv, int b_vec, const void* bias, void* C,
                       int out_dtype, int64_t ldc, void* ws, size_t ws_bytes, void* stream);
+
+/* bf8_gemm_geglu with H quantized in the epilogue: H8 = e4m3(clamp(H * h_scale)) [M, I]
+ * (8-byte aligned) and optionally H8t = its transpose [I, M] (16-byte aligned, M % 32 ==
+ * 0), bytes identical to bf8_cast_bf16 of the bf16 H with the scale at h_scale (a device
+ * fp32, e.g. meta_out + 1 of bf8_delayed_scale_fold). H (bf16) and GU are optional; the
+ * amax partials of |H| are written as by bf8_gemm_geglu. The activation-and-cast ahead of
+ * fc2 in TE LayerNormMLP / te.Linear under delayed scaling (bongard/te_linear.py:98-103,
+ * bongard/fused_mlp.py:25-30). */
+int bf8_gemm_geglu_quant(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw,
+                         int64_t M, int64_t I, int64_t K, const float* x_scale_inv,
+                         const float* w_scale_inv, int w_scale_stride, const float* h_scale,
+                         void* H, int64_t ldh, uint8_t* H8, uint8_t* H8t, void* GU,
+                         uint32_t* h_partials, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * MXFP8 (OCP microscaling: 32-element blocks, one E8M0 scale byte each).

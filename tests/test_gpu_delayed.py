@@ -182,3 +182,80 @@ def test_geglu_bwd_delayed_fused_equals_two_pass(gpu, M, I):
                   flush=True)
         assert same
     assert a.recorded == b.recorded == 3
+
+
+GEGLU_TILES = ["auto", "256x256", "160x256", "192x256", "128x128", "64x128"]
+
+
+@pytest.mark.parametrize("tile", GEGLU_TILES)
+@pytest.mark.parametrize("M", [320, 100])
+def test_gemm_geglu_quant_equals_cast(gpu, monkeypatch, tile, M):
+    """H cast in the gated-GELU epilogue with a given scale == bf8_cast_bf16 of the bf16 H
+    of the unfused kernel (rows and, for M % 32 == 0, the transposed copy), with clamped
+    values and a NaN row; H, GU and the amax partials unchanged."""
+    if tile != "auto":
+        monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", tile)
+    I, K = 384, 256
+    g = torch.Generator().manual_seed(M + 7)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(2 * I, K, generator=g) * 0.05).to(torch.bfloat16)
+    xq = ops.quantize(x.to(gpu), ops.E4M3)
+    wq = ops.quantize(w.to(gpu), ops.E4M3)
+    xq.data.view(torch.uint8)[9, 3] = 0x7F          # a NaN operand: row 9 of H is NaN
+    h_meta = torch.tensor([0.0, 300.0, 1.0 / 300.0, 0.0], device=gpu)  # saturates the tail
+    transpose = M % 32 == 0
+    args = (xq.data, xq.meta, wq.data, wq.meta, I)
+    H_ref, GU_ref, p_ref = ops.gemm_geglu(*args, keep_gu=True)
+    ref = ops.cast(H_ref, h_meta, ops.E4M3, rowwise=True, transpose=transpose)
+    hq, GU, H, parts = ops.gemm_geglu_quant(*args, h_meta, transpose=transpose, keep_gu=True,
+                                            keep_h=True)
+    hq2, GU2, H2, _ = ops.gemm_geglu_quant(*args, h_meta, transpose=transpose)
+    torch.cuda.synchronize()
+    assert GU2 is None and H2 is None
+    assert torch.equal(H.view(torch.int16), H_ref.view(torch.int16))
+    assert torch.equal(GU.view(torch.int16), GU_ref.view(torch.int16))
+    assert torch.equal(parts, p_ref)
+    hb = H_ref.float().cpu()
+    assert bool(hb[9].isnan().all()) and bool((hb.nan_to_num().abs() * 300 > 448).any())
+    for q, what in ((hq, "with H"), (hq2, "without H")):
+        same = [torch.equal(q.data.view(torch.uint8), ref.data.view(torch.uint8))]
+        if transpose:
+            same.append(torch.equal(q.data_t.view(torch.uint8), ref.data_t.view(torch.uint8)))
+        print(f"[geglu quant {tile} M={M} {what}] rows, cols identical: {same}", flush=True)
+        assert all(same)
+
+
+@pytest.mark.parametrize("M,transpose", [(256, True), (200, False)])
+def test_geglu_delayed_fused_h_equals_two_pass(gpu, M, transpose):
+    """Delayed scaling of H produced by the GEGLU GEMM itself (scale fold, then the GEMM
+    casting H in its epilogue) against the two-pass form (bf16 H with producer partials,
+    then the delayed cast), over four steps of one scaler each: H bytes, per-step meta and
+    history state identical."""
+    I, K = 256, 320
+    a = scaling.DelayedScaler(ops.E4M3, 16)
+    b = scaling.DelayedScaler(ops.E4M3, 16)
+    g = torch.Generator(device=gpu).manual_seed(M + I + K)
+    for step in range(4):
+        x = (torch.randn(M, K, device=gpu, generator=g) * (1 + step)).to(torch.bfloat16)
+        w = (torch.randn(2 * I, K, device=gpu, generator=g) * 0.05).to(torch.bfloat16)
+        xq, wq = ops.quantize(x, ops.E4M3), ops.quantize(w, ops.E4M3)
+        count = ops.geglu_partials_count(M, I)
+        H, _, _ = ops.gemm_geglu(xq.data, xq.meta, wq.data, wq.meta, I,
+                                 partials=a.partials_for_producer(count, gpu))
+        qa = a.quantize(H, rowwise=True, transpose=transpose, producer_count=count)
+
+        def launch(st, L, pos, prev, parts):
+            meta = ops.delayed_scale_fold(st, L, pos, prev, ops.E4M3)
+            return ops.gemm_geglu_quant(xq.data, xq.meta, wq.data, wq.meta, I, meta,
+                                        transpose=transpose, partials=parts)[0]
+
+        qb = b.produce(count, gpu, launch)
+        torch.cuda.synchronize()
+        parts = [torch.equal(qa.data.view(torch.uint8), qb.data.view(torch.uint8)),
+                 torch.equal(qa.meta, qb.meta), torch.equal(a.state, b.state)]
+        if transpose:
+            parts.append(torch.equal(qa.data_t.view(torch.uint8), qb.data_t.view(torch.uint8)))
+        print(f"[delayed H M={M} step {step}] identical: {parts} meta {qb.meta.tolist()}",
+              flush=True)
+        assert all(parts)
+    assert a.recorded == b.recorded == 3
