@@ -17,7 +17,8 @@
 //   axis_row_kernel      one pass over x: per-row amax -> scale -> cast (row output), and
 //                        per-block column amax partials (bf16 keys) for the column scales;
 //   axis_col_scale_kernel the column partials -> per-column scale and scale_inv;
-//   axis_col_cast_kernel  second pass over x: per-column cast through an LDS transpose.
+//   axis_col_cast_kernel  second pass over x: per-column cast through a wave-level LDS
+//                        transpose.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -33,8 +34,7 @@ constexpr int kAxBlocksPartials = 512;  // row-kernel blocks when it writes colu
 constexpr int kAxBlocksPlain = 2048;    // ... when it does not
 constexpr int kColNT = 256;
 constexpr int kCT = 64;                 // column-cast tile (rows x cols)
-constexpr int kCPitch = kCT + 4;
-constexpr int kMaxColCastBlocks = 1024;
+constexpr int kMaxColCastBlocks = 2048;
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
@@ -237,63 +237,66 @@ __global__ __launch_bounds__(kColNT) void axis_col_scale_kernel(
   }
 }
 
-// q_t [cols, rows] = per-column cast of x, through 64 x 64 LDS tiles (as the tensorwise
-// cast-transpose, with one scale per column).
+// q_t [cols, rows] = per-column cast of x: one 64 x 64 tile per wave (grid-stride), loaded
+// as eight 8-row x 128-byte pieces, cast with the lane's 8 column scales, staged in the
+// wave's own LDS region and stored transposed (wave_transpose64_staged), as the tensorwise
+// cast-transpose does with one scale per column.
 template <int FMT>
 __global__ __launch_bounds__(kColNT) void axis_col_cast_kernel(
     const uint16_t* __restrict__ x, int64_t rows, int64_t cols,
     const float* __restrict__ col_scale, uint8_t* __restrict__ out_t) {
-  __shared__ uint32_t tile[kCT * kCPitch / 4];
-  uint8_t* tb = reinterpret_cast<uint8_t*>(tile);
+  constexpr int kWaves = kColNT / 64;
+  __shared__ uint32_t stage[kWaves][kWaveTileDwords];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t tiles_c = (cols + kCT - 1) / kCT;
   const int64_t ntiles = tiles_c * ((rows + kCT - 1) / kCT);
-  const int t = threadIdx.x;
-  for (int64_t tile_id = blockIdx.x; tile_id < ntiles; tile_id += gridDim.x) {
+  const bool t16 = (rows & 15) == 0;
+  const int ch = lane & 7;
+  uint32_t* lds = stage[wid];
+  for (int64_t tile_id = (int64_t)blockIdx.x * kWaves + wid; tile_id < ntiles;
+       tile_id += (int64_t)gridDim.x * kWaves) {
     const int64_t r0 = (tile_id / tiles_c) * kCT, c0 = (tile_id % tiles_c) * kCT;
-    {
-      const int lr = t >> 2, lc = (t & 3) * 16;
-      const int64_t r = r0 + lr, c = c0 + lc;
-      uint32_t q[4] = {0u, 0u, 0u, 0u};
-      if (r < rows && c < cols) {
-        const uint4* src4 = reinterpret_cast<const uint4*>(x + r * cols + c);
-        const uint4 a0 = src4[0];
-        const uint4 a1 = src4[1];
-        float sc[16];
-        const float4* s4 = reinterpret_cast<const float4*>(col_scale + c);
+    const int64_t c = c0 + 8 * ch;
+    const bool cv = c < cols;
+    uint4 v[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float4 f = s4[i];
-          sc[4 * i] = f.x; sc[4 * i + 1] = f.y; sc[4 * i + 2] = f.z; sc[4 * i + 3] = f.w;
-        }
-        const uint2 q0 = quant8_bf16_vs<FMT>(a0, sc), q1 = quant8_bf16_vs<FMT>(a1, sc + 8);
-        q[0] = q0.x; q[1] = q0.y; q[2] = q1.x; q[3] = q1.y;
-      }
-      uint32_t* dst = reinterpret_cast<uint32_t*>(tb + lr * kCPitch + lc);
-      dst[0] = q[0]; dst[1] = q[1]; dst[2] = q[2]; dst[3] = q[3];
+    for (int k = 0; k < 8; ++k) {
+      const int64_t r = r0 + 8 * k + (lane >> 3);
+      v[k] = make_uint4(0u, 0u, 0u, 0u);
+      if (r < rows && cv) v[k] = *reinterpret_cast<const uint4*>(x + r * cols + c);
     }
-    __syncthreads();
-    {
-      const int oc = t >> 2, orow = (t & 3) * 16;
-      const int64_t tr = c0 + oc, tc = r0 + orow;
-      if (tr < cols && tc < rows) {
-        uint32_t w[4];
+    float sc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (cv) {
+      const float4 s0 = reinterpret_cast<const float4*>(col_scale + c)[0];
+      const float4 s1 = reinterpret_cast<const float4*>(col_scale + c)[1];
+      sc[0] = s0.x; sc[1] = s0.y; sc[2] = s0.z; sc[3] = s0.w;
+      sc[4] = s1.x; sc[5] = s1.y; sc[6] = s1.z; sc[7] = s1.w;
+    }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t b0 = tb[(orow + 4 * j + 0) * kCPitch + oc];
-          const uint32_t b1 = tb[(orow + 4 * j + 1) * kCPitch + oc];
-          const uint32_t b2 = tb[(orow + 4 * j + 2) * kCPitch + oc];
-          const uint32_t b3 = tb[(orow + 4 * j + 3) * kCPitch + oc];
-          w[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        }
+    for (int k = 0; k < 8; ++k) {
+      const int lr = 8 * k + (lane >> 3);
+      const uint2 q = quant8_bf16_vs<FMT>(v[k], sc);
+      lds[lr * kWaveTilePitch + 2 * ch] = q.x;
+      lds[lr * kWaveTilePitch + 2 * ch + 1] = q.y;
+    }
+    uint4 tq[4];
+    wave_transpose64_staged(lds, lane, tq);
+    const int64_t tc = r0 + (lane >> 4) * 16;  // column of out_t (a row of x)
+    if (tc < rows) {
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const int64_t tr = c0 + 4 * (lane & 15) + cc;  // row of out_t (a column of x)
+        if (tr >= cols) continue;
         uint8_t* dst = out_t + tr * rows + tc;
-        if (tc + 16 <= rows && (rows & 15) == 0) {
-          *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+        if (t16 && tc + 16 <= rows) {
+          *reinterpret_cast<uint4*>(dst) = tq[cc];
         } else {
-          for (int j = 0; j < 16 && tc + j < rows; ++j) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+          const uint32_t w[4] = {tq[cc].x, tq[cc].y, tq[cc].z, tq[cc].w};
+          for (int j = 0; j < 16 && tc + j < rows; ++j)
+            dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
         }
       }
     }
-    __syncthreads();
   }
 }
 
@@ -354,7 +357,8 @@ int run_axiswise(const uint16_t* x, int rows, int cols, int pow2, uint8_t* out, 
   rc = launch_status("axis_col_scale_kernel");
   if (rc != BF8_OK) return rc;
   const int64_t tiles = ((int64_t)(rows + kCT - 1) / kCT) * ((cols + kCT - 1) / kCT);
-  const unsigned grid = (unsigned)std::min<int64_t>(tiles, kMaxColCastBlocks);
+  const unsigned grid = (unsigned)std::min<int64_t>((tiles + kColNT / 64 - 1) / (kColNT / 64),
+                                                    kMaxColCastBlocks);
   hipLaunchKernelGGL(axis_col_cast_kernel<FMT>, dim3(grid), dim3(kColNT), 0, s, x,
                      (int64_t)rows, (int64_t)cols, col_scale, out_t);
   return launch_status("axis_col_cast_kernel");
