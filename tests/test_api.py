@@ -287,3 +287,17 @@ def test_delayed_recipe_needs_fused_gate_up(monkeypatch):
     monkeypatch.setenv("BONGARD_TE_SPLIT_GATE_UP", "1")
     with pytest.raises(ValueError, match="fused gate_up"):
         te_linear.TEMLP(_mlp(4), "fp8_delayed")
+
+
+def test_pack_to_32_rows_need_no_pad_copy():
+    """The pack-to-32 contract (bongard/packing.py:240-246): a packed batch whose row count
+    is already a multiple of 32 (filler segment included) reaches the projections as is,
+    with no alignment copy; other row counts are padded with zero rows, which leave every
+    amax unchanged."""
+    x = torch.randn(64, 16)
+    flat, length, aligned = te_linear._pad_rows(x)
+    assert flat is x and length == aligned == 64
+    y = torch.randn(70, 16)
+    flat, length, aligned = te_linear._pad_rows(y)
+    assert (length, aligned) == (70, 96) and torch.equal(flat[:70], y)
+    assert bool((flat[70:] == 0).all()) and flat.abs().max() == y.abs().max()
