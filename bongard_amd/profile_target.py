@@ -13,7 +13,9 @@ the fused norm: the config-2 MLP forward under MXFP8 (block quantize, MX gated-G
 quantized in its epilogue, MX down GEMM), the axiswise (torchao rowwise) quantization of a [8192, 2560] activation
 per row and per column, and the fused RMSNorm of the same activation. ``c5``: the
 config-5 training step (the c2 MLP at M = 8192, forward and backward, delayed scaling with
-an amax history of 16).
+an amax history of 16). ``vs_hipblaslt``: this library's FP8 GEMM and hipBLASLt's (through
+``torch._scaled_mm``) on the c2 / c4 / square shapes, each captured as a HIP graph of 20
+calls and timed from HIP events around its replay; prints one line per shape.
 """
 
 import argparse
@@ -29,7 +31,8 @@ def main():
     p = argparse.ArgumentParser()
     p.add_argument("--iters", type=int, default=5)
     p.add_argument("--rows", type=int, default=4096)
-    p.add_argument("--case", choices=("c2", "square", "recipes", "c5"), default="c2")
+    p.add_argument("--case", choices=("c2", "square", "recipes", "c5", "vs_hipblaslt"),
+                   default="c2")
     args = p.parse_args()
     dev = torch.device("cuda:0")
     if args.case == "square":
@@ -47,6 +50,9 @@ def main():
         return
     if args.case == "c5":
         _c5(dev, args.iters)
+        return
+    if args.case == "vs_hipblaslt":
+        _vs_hipblaslt(dev, args.iters)
         return
     c = workloads.config2(rows=args.rows)
     I = workloads.INTERMEDIATE
@@ -66,6 +72,62 @@ def main():
         ops.gemm(hq.data, ops.E4M3, hm, dq.data, ops.E4M3, dq.meta)
     torch.cuda.synchronize()
     print(f"profile_target done: {args.iters} iterations, copy {COPY_BYTES} bytes", flush=True)
+
+
+def _graph_time(fn, n=20, reps=5):
+    """Seconds per call of ``fn``: n calls captured in one HIP graph, median of reps replays."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(n):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) / 1e3 / n)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _vs_hipblaslt(dev, iters):
+    meta = torch.tensor([1.0, 1.0, 1.0, 0.0], device=dev)
+    one = torch.tensor(1.0, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def rnd(r, c):  # finite e4m3 bytes
+        v = torch.randint(0, 0x70, (r, c), dtype=torch.int16, device=dev, generator=gen)
+        return v.to(torch.uint8).view(torch.float8_e4m3fn)
+
+    for M, N, K in [(512, 4096, 2560), (512, 2560, 2048), (512, 2560, 10240),
+                    (512, 20480, 2560), (4096, 20480, 2560), (4096, 2560, 10240),
+                    (8192, 8192, 8192)]:
+        a, b = rnd(M, K), rnd(N, K)
+        bt = b.t()
+
+        def lt():
+            return torch._scaled_mm(a, bt, scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+
+        def ours():
+            return ops.gemm(a, ops.E4M3, meta, b, ops.E4M3, meta)
+
+        for _ in range(iters):
+            lt()
+            ours()
+        t_lt, t_ours = _graph_time(lt), _graph_time(ours)
+        f = 2.0 * M * N * K
+        print(f"{M}x{N}x{K}: hipBLASLt {t_lt * 1e6:8.2f} us {f / t_lt / 1e12:6.0f} TFLOP/s   "
+              f"bf8_gemm {t_ours * 1e6:8.2f} us {f / t_ours / 1e12:6.0f} TFLOP/s", flush=True)
 
 
 def _c5(dev, iters):
