@@ -67,6 +67,32 @@ def _require_gpu(*tensors):
             raise RuntimeError("bongard_amd FP8 ops need tensors on the HIP device (no CPU path)")
 
 
+def _byte_matrix(who, **tensors):
+    """FP8 payloads and E8M0 scale arrays reach the kernels as row-major byte matrices
+    (row stride = stride(0), elements contiguous within a row): reject anything else
+    rather than let the kernel read a transposed view's bytes in the wrong order."""
+    for name, t in tensors.items():
+        if t is None:
+            continue
+        if t.dim() != 2 or t.element_size() != 1 or (t.shape[1] > 1 and t.stride(1) != 1):
+            raise ValueError(f"{who}: {name} must be a 2-D one-byte tensor with contiguous rows "
+                             f"(got {t.dtype} {tuple(t.shape)} strides {t.stride()})")
+
+
+def _out_matrix(who, out, shape, dtype):
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype or (shape[1] > 1 and out.stride(1) != 1):
+        raise ValueError(f"{who}: out must be {dtype} {tuple(shape)} with contiguous rows")
+
+
+def _check_cast_outputs(who, out, out_t, rows, cols):
+    """Caller-supplied cast outputs: contiguous one-byte [rows, cols] / [cols, rows]."""
+    for name, t, shape in (("out", out, (rows, cols)), ("out_t", out_t, (cols, rows))):
+        if t is not None and (tuple(t.shape) != shape or t.element_size() != 1
+                              or not t.is_contiguous()):
+            raise ValueError(f"{who}: {name} must be a contiguous one-byte tensor of shape "
+                             f"{shape} (got {t.dtype} {tuple(t.shape)})")
+
+
 def _bf16_2d(x):
     if x.dtype != torch.bfloat16:
         raise TypeError(f"expected a bfloat16 tensor, got {x.dtype}")
@@ -134,6 +160,8 @@ def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None,
         out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=dev)
     if transpose and out_t is None:
         out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=dev)
+    _check_cast_outputs("quantize", out if rowwise else None, out_t if transpose else None,
+                        rows, cols)
     L = _lib.lib()
     parts = partials_buffer(L.bf8_amax_partials(rows * cols), dev)
     _lib.check(L.bf8_quantize_bf16(_ptr(x), rows, cols, fmt | (SCALE_POW2 if pow2 else 0),
@@ -187,6 +215,8 @@ def cast(x, meta, fmt=E4M3, *, rowwise=True, transpose=False, out=None, out_t=No
         out = torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=x.device)
     if transpose and out_t is None:
         out_t = torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=x.device)
+    _check_cast_outputs("cast", out if rowwise else None, out_t if transpose else None,
+                        rows, cols)
     scale_ptr = ctypes.c_void_p(meta.data_ptr() + 4)
     _lib.check(_lib.lib().bf8_cast_bf16(_ptr(x), rows, cols, scale_ptr, fmt,
                                         _ptr(out if rowwise else None),
@@ -208,6 +238,7 @@ def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=N
     ``b_meta_stride`` floats apart.
     """
     _require_gpu(a, b, a_meta, b_meta)
+    _byte_matrix("gemm", a=a, b=b)
     M, K = a.shape
     N, Kb = b.shape
     if K != Kb:
@@ -216,6 +247,7 @@ def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=N
         raise TypeError("gemm: out_dtype must be bfloat16 or float32")
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    _out_matrix("gemm", out, (M, N), out_dtype)
     n_seg = 1
     seg = None
     if seg_ends is not None:
@@ -293,6 +325,7 @@ def gemm_axiswise(a, a_fmt, a_sinv, b, b_fmt, b_sinv, *, out_dtype=torch.bfloat1
     or a single value (1-element tensor, e.g. a meta's ``scale_inv``); likewise ``b_sinv``
     with [N]."""
     _require_gpu(a, b, a_sinv, b_sinv)
+    _byte_matrix("gemm_axiswise", a=a, b=b)
     M, K = a.shape
     N, Kb = b.shape
     if K != Kb:
@@ -313,6 +346,7 @@ def gemm_axiswise(a, a_fmt, a_sinv, b, b_fmt, b_sinv, *, out_dtype=torch.bfloat1
     b_vec = vec_flag(b_sinv, N, "b_sinv")
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    _out_matrix("gemm_axiswise", out, (M, N), out_dtype)
     if bias is not None:
         if bias.dtype != torch.bfloat16:
             raise TypeError("gemm_axiswise: bias must be bfloat16")
@@ -374,6 +408,7 @@ def gemm_mx(a, a_scales, b, b_scales, *, out_dtype=torch.bfloat16, bias=None, ou
     """``C = a @ b.T`` on MXFP8 (e4m3) operands a [M, K], b [N, K] with their E8M0 block
     scales [M, >= mx_scale_ld(K)], [N, ...]."""
     _require_gpu(a, b, a_scales, b_scales)
+    _byte_matrix("gemm_mx", a=a, b=b, a_scales=a_scales, b_scales=b_scales)
     M, K = a.shape
     N, Kb = b.shape
     if K != Kb:
@@ -382,6 +417,7 @@ def gemm_mx(a, a_scales, b, b_scales, *, out_dtype=torch.bfloat16, bias=None, ou
         raise TypeError("gemm_mx: out_dtype must be bfloat16 or float32")
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    _out_matrix("gemm_mx", out, (M, N), out_dtype)
     if bias is not None:
         if bias.dtype != torch.bfloat16:
             raise TypeError("gemm_mx: bias must be bfloat16")
@@ -400,6 +436,7 @@ def gemm_mx(a, a_scales, b, b_scales, *, out_dtype=torch.bfloat16, bias=None, ou
 def gemm_geglu_mx(x8, x_scales, w8, w_scales, intermediate, *, keep_gu=False):
     """Gate/up GEMM + gated GELU on MXFP8 operands; returns ``(H bf16 [M, I], GU or None)``."""
     _require_gpu(x8, x_scales, w8, w_scales)
+    _byte_matrix("gemm_geglu_mx", x8=x8, w8=w8, x_scales=x_scales, w_scales=w_scales)
     M, K = x8.shape
     I = int(intermediate)
     if w8.shape != (2 * I, K):
@@ -422,6 +459,7 @@ def gemm_geglu_mx_quant(x8, x_scales, w8, w_scales, intermediate, *, colwise=Fal
     rowwise copy and, if ``colwise`` (needs M % 32 == 0), the columnwise one, byte for byte
     what :func:`quantize_mx` gives for the bf16 H; ``H`` the bf16 H when ``keep_h``."""
     _require_gpu(x8, x_scales, w8, w_scales)
+    _byte_matrix("gemm_geglu_mx_quant", x8=x8, w8=w8, x_scales=x_scales, w_scales=w_scales)
     M, K = x8.shape
     I = int(intermediate)
     if w8.shape != (2 * I, K):
@@ -458,6 +496,7 @@ def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu
     optional caller-owned buffer of at least ``geglu_partials_count(M, I)`` entries.
     """
     _require_gpu(x8, w8, x_meta, w_meta)
+    _byte_matrix("gemm_geglu", x8=x8, w8=w8)
     M, K = x8.shape
     I = int(intermediate)
     if w8.shape != (2 * I, K):
@@ -487,6 +526,7 @@ def gemm_geglu_quant(x8, x_meta, w8, w_meta, intermediate, h_meta, *, w_meta_str
     ``hq`` the :class:`Fp8Tensor` of H (``data`` [M, I], ``data_t`` [I, M] when
     ``transpose``, which needs M % 32 == 0) with meta ``h_meta``."""
     _require_gpu(x8, w8, x_meta, w_meta, h_meta)
+    _byte_matrix("gemm_geglu_quant", x8=x8, w8=w8)
     M, K = x8.shape
     I = int(intermediate)
     if w8.shape != (2 * I, K):

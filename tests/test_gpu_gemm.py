@@ -338,3 +338,23 @@ def test_geglu_bwd_extreme_preactivations(gpu):
     for part, ref in ((got[:, :I], dg.float()), (got[:, I:], du.float())):
         diff = (part - ref).abs()
         assert bool((diff <= 2 * orc.bf16_ulp(ref) + 2.0 ** -20 * ref.abs().max()).all())
+
+
+def test_operand_layout_is_checked(gpu):
+    """Operands reach the kernels as row-major byte matrices: a transposed view, a
+    non-byte tensor or a mis-shaped output is refused before any launch."""
+    a = ops.quantize(torch.randn(64, 128, device=gpu).to(torch.bfloat16))
+    b = ops.quantize(torch.randn(96, 128, device=gpu).to(torch.bfloat16))
+    with pytest.raises(ValueError, match="contiguous rows"):
+        ops.gemm(a.data.t().contiguous().t(), 0, a.meta, b.data, 0, b.meta)
+    with pytest.raises(ValueError, match="one-byte"):
+        ops.gemm(a.data.view(torch.uint8).to(torch.int16), 0, a.meta, b.data, 0, b.meta)
+    with pytest.raises(ValueError, match="out must be"):
+        ops.gemm(a.data, 0, a.meta, b.data, 0, b.meta,
+                 out=torch.empty(96, 64, dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(ValueError, match="out_t must be"):
+        ops.cast(torch.randn(64, 128, device=gpu).to(torch.bfloat16), a.meta, transpose=True,
+                 out_t=torch.empty(64, 128, dtype=torch.uint8, device=gpu))
+    y = ops.gemm(a.data, 0, a.meta, b.data, 0, b.meta)
+    torch.cuda.synchronize()
+    assert y.shape == (64, 96)
