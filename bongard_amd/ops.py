@@ -93,6 +93,13 @@ def _check_cast_outputs(who, out, out_t, rows, cols):
                              f"{shape} (got {t.dtype} {tuple(t.shape)})")
 
 
+def _gu_operand(who, GU, M, I):
+    """The forward's saved [gate | up] pre-activations: bf16 [M, 2I], contiguous."""
+    if GU.dtype != torch.bfloat16 or tuple(GU.shape) != (M, 2 * I):
+        raise ValueError(f"{who}: GU must be bf16 [{M}, {2 * I}] (got {GU.dtype} {tuple(GU.shape)})")
+    return GU.contiguous()
+
+
 def _bf16_2d(x):
     if x.dtype != torch.bfloat16:
         raise TypeError(f"expected a bfloat16 tensor, got {x.dtype}")
@@ -577,6 +584,7 @@ def geglu_bwd(dH, GU, *, partials=None):
     _require_gpu(dH, GU)
     dH = dH.contiguous()
     M, I = dH.shape
+    GU = _gu_operand("geglu_bwd", GU, M, I)
     L = _lib.lib()
     dGU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=dH.device)
     count = int(L.bf8_geglu_bwd_partials(M, I))
@@ -646,6 +654,7 @@ def geglu_bwd_delayed(dH, GU, state, length, pos, prev_partials, fmt=E5M2, *, ro
     _require_gpu(dH, GU, state)
     dH = dH.contiguous()
     M, I = dH.shape
+    GU = _gu_operand("geglu_bwd_delayed", GU, M, I)
     dev = dH.device
     if meta_out is None:
         meta_out = new_meta(dev)
