@@ -318,6 +318,7 @@ int gemm_entry(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int f
             "bf8_gemm: workspace must be 256-byte aligned");
   if (M == 0 || N == 0) return BF8_OK;
   BF8_CHECK(K > 0, "bf8_gemm: K == 0 is not supported");
+  BF8_CHECK(A && B && C, "bf8_gemm: A, B or C is NULL");
   GemmParams p{};
   p.A = A; p.B = B; p.lda = lda; p.ldb = ldb;
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.I = 0;
@@ -394,7 +395,7 @@ static int geglu_entry(const char* who, const uint8_t* X, int64_t ldx, const uin
                 ((uintptr_t)GU & 15) == 0,
             "%s: X, W, H, GU must be 16-byte aligned", who);
   BF8_CHECK(M * ldx < (1LL << 31) && 2 * I * ldw < (1LL << 31), "%s: operand > 2 GiB", who);
-  BF8_CHECK(x_scale_inv && w_scale_inv && h_partials, "%s: NULL pointer", who);
+  BF8_CHECK(X && W && x_scale_inv && w_scale_inv && h_partials, "%s: NULL pointer", who);
   if (H8) {
     BF8_CHECK(h_scale && ((uintptr_t)H8 & 7) == 0, "%s: H8 needs h_scale and 8-byte alignment",
               who);
@@ -470,6 +471,7 @@ int bf8_gemm_mx(const uint8_t* A, int64_t lda, const uint8_t* A_scales, int64_t 
             "bf8_gemm_mx: workspace must be 256-byte aligned");
   if (M == 0 || N == 0) return BF8_OK;
   BF8_CHECK(K > 0, "bf8_gemm_mx: K == 0 is not supported");
+  BF8_CHECK(C != nullptr, "bf8_gemm_mx: C is NULL");
   int rc = check_mx_operand("bf8_gemm_mx", "A", A, lda, A_scales, lda_sc, M, K);
   if (rc) return rc;
   rc = check_mx_operand("bf8_gemm_mx", "B", B, ldb, B_scales, ldb_sc, N, K);

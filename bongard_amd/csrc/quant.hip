@@ -351,6 +351,7 @@ int launch_cast(const void* x, int64_t rows, int64_t cols, ScaleSrc src, int fmt
             "%s: x and out must be 16-byte aligned", who);
   const int64_t n = rows * cols;
   if (n == 0) return BF8_OK;
+  BF8_CHECK(x != nullptr, "%s: x is NULL", who);
   hipStream_t s = as_stream(stream);
   const uint16_t* xs = (const uint16_t*)x;
   if (!src.scale && !src.state && src.np > kMaxInlinePartials) {
@@ -490,6 +491,12 @@ int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_
   BF8_CHECK(rows >= 0 && cols >= 0, "bf8_quantize_bf16: negative shape");
   BF8_CHECK((fmt & ~BF8_SCALE_POW2) == BF8_E4M3 || (fmt & ~BF8_SCALE_POW2) == BF8_E5M2,
             "bf8_quantize_bf16: bad fmt %d", fmt);
+  // everything the cast checks, checked before the amax pass is enqueued
+  BF8_CHECK(meta && (out || out_t), "bf8_quantize_bf16: meta is NULL or no output given");
+  BF8_CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)out_t & 15) == 0,
+            "bf8_quantize_bf16: x, out and out_t must be 16-byte aligned");
+  BF8_CHECK(!out_t || cols % 16 == 0,
+            "bf8_quantize_bf16: transposed cast needs cols %% 16 == 0 (got %lld)", (long long)cols);
   const int64_t n = rows * cols;
   int rc = bf8_amax_bf16(x, n, partials, stream);
   if (rc) return rc;
