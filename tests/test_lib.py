@@ -72,3 +72,33 @@ def test_plan_override_env(monkeypatch):
     assert L.bf8_gemm_workspace(512, 2560, 10240) == 4 * 512 * 2560 * 4
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x160")  # no gated-GELU variant
     assert L.bf8_geglu_partials(4096, 10240) >= 1
+
+
+def test_quantizing_geglu_and_scale_fold_reject_bad_arguments():
+    """The epilogue-quantizing gate/up entries and the delayed scale fold check their
+    arguments on the host (no launch): missing H8, a transposed copy with M % 32 != 0,
+    bad history slots."""
+    L = _lib.lib()
+    null = ctypes.c_void_p(0)
+    buf = ctypes.create_string_buffer(1 << 12)
+    ptr = ctypes.c_void_p((ctypes.addressof(buf) + 255) // 256 * 256)
+    # bf8_gemm_geglu_quant: H8 is required
+    rc = L.bf8_gemm_geglu_quant(ptr, 32, ptr, 32, 32, 128, 32, ptr, ptr, 0, ptr, null, 128,
+                                null, null, null, ptr, null)
+    assert rc == 1 and b"H8 is NULL" in L.bf8_last_error()
+    # ... and H8t needs M % 32 == 0
+    rc = L.bf8_gemm_geglu_quant(ptr, 32, ptr, 32, 40, 128, 32, ptr, ptr, 0, ptr, null, 128,
+                                ptr, ptr, null, ptr, null)
+    assert rc == 1 and b"M % 32" in L.bf8_last_error()
+    # MX variant: I must be a multiple of 128, H8 required
+    rc = L.bf8_gemm_geglu_mx_quant(ptr, 32, ptr, 4, ptr, 32, ptr, 4, 32, 100, 32, null, 128,
+                                   ptr, ptr, 4, null, null, 0, null, null)
+    assert rc == 1 and b"multiple of 128" in L.bf8_last_error()
+    rc = L.bf8_gemm_geglu_mx_quant(ptr, 32, ptr, 4, ptr, 32, ptr, 4, 32, 128, 32, null, 128,
+                                   null, null, 4, null, null, 0, null, null)
+    assert rc == 1 and b"H8 is NULL" in L.bf8_last_error()
+    # delayed scale fold: slot outside the history
+    rc = L.bf8_delayed_scale_fold(ptr, 16, 16, null, 0, 0, null, null)
+    assert rc == 1 and b"outside" in L.bf8_last_error()
+    rc = L.bf8_delayed_scale_fold(ptr, 16, 0, null, 5, 0, null, null)
+    assert rc == 1 and b"previous partials" in L.bf8_last_error()
