@@ -36,14 +36,6 @@ constexpr int kColNT = 256;
 constexpr int kCT = 64;                 // column-cast tile (rows x cols)
 constexpr int kMaxColCastBlocks = 2048;
 
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
-  const u16x2 r = __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
-                                            __builtin_bit_cast(u16x2, b));
-  return __builtin_bit_cast(uint32_t, r);
-}
-
 // |x| keys of two packed bf16: clearing the sign makes the unsigned order of each half the
 // order of |x| (NaN above inf).
 __device__ __forceinline__ uint4 abs_keys(uint4 v) {

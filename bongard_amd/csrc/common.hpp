@@ -177,6 +177,15 @@ __device__ __forceinline__ uint2 quant8_bf16_finite(uint4 v, float scale) {
                                               bf16_lo(v.w) * scale, bf16_hi(v.w) * scale));
 }
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Per-half unsigned max of two packed 16-bit pairs (v_pk_max_u16).
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  const u16x2 r = __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                            __builtin_bit_cast(u16x2, b));
+  return __builtin_bit_cast(uint32_t, r);
+}
+
 // Max of |bf16| over the 8 values of v, as an fp32 bit pattern key: for non-negative
 // floats the unsigned order of the bits is the numeric order, and NaN keys sort above
 // +inf (as torch's NaN-propagating max does).
@@ -270,13 +279,16 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v) {
 // gelu_tanh(x) = 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
 // the identical x / (1 + exp(-2u)): no cancellation of 1 + tanh(u) for negative x, and
 // two transcendental instructions (v_exp_f32, v_rcp_f32) instead of a libm tanh.
+// gelu_tanh_exp: exp(-2u) = 2^(x (c1 + c2 x^2)) with the constants folded,
+// c1 = -2 sqrt(2/pi) / ln 2, c2 = 0.044715 c1 (x2 = x * x; one FMA and two multiplies).
+__device__ __forceinline__ float gelu_tanh_exp(float x, float x2) {
+  constexpr float kC1 = -2.3022082f;
+  constexpr float kC2 = -0.10294324f;
+  return __builtin_amdgcn_exp2f(x * __builtin_fmaf(x2, kC2, kC1));
+}
+
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
-  const float kBeta = 0.7978845608028654f;
-  const float kKappa = 0.044715f;
-  const float kM2Log2e = -2.8853900817779268f;  // -2 / ln 2
-  const float u = kBeta * (x + kKappa * (x * x * x));
-  const float e = __builtin_amdgcn_exp2f(u * kM2Log2e);  // exp(-2u)
-  return x * __builtin_amdgcn_rcpf(1.0f + e);
+  return x * __builtin_amdgcn_rcpf(1.0f + gelu_tanh_exp(x, x * x));
 }
 
 // gelu_tanh and its derivative, both from s = 1 / (1 + exp(-2u)) = 0.5 (1 + tanh(u)):
@@ -287,12 +299,11 @@ __device__ __forceinline__ float gelu_tanh_f32(float x) {
 __device__ __forceinline__ void gelu_tanh_fwd_bwd(float x, float& y, float& dydx) {
   const float kBeta = 0.7978845608028654f;
   const float kKappa = 0.044715f;
-  const float kM2Log2e = -2.8853900817779268f;
-  const float u = kBeta * (x + kKappa * (x * x * x));
-  const float e = __builtin_amdgcn_exp2f(u * kM2Log2e);
+  const float x2 = x * x;
+  const float e = gelu_tanh_exp(x, x2);
   const float s = __builtin_amdgcn_rcpf(1.0f + e);
   y = x * s;
-  const float du = kBeta * (1.0f + 3.0f * kKappa * (x * x));
+  const float du = kBeta * (1.0f + 3.0f * kKappa * x2);
   // 1 - s = e s; where exp(-2u) overflows (x below about -10) s is 0 and 1 - s is 1
   const float oms = e > 1e30f ? 1.0f : s * e;
   dydx = s + 2.0f * x * (s * oms) * du;

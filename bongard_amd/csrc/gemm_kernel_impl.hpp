@@ -721,7 +721,8 @@ gemm_kernel(GemmParams p) {
     constexpr int CH = HF * 4;  // 16-byte chunks per staged H row
     uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
     const int wave_h0 = n0 + wn * HF * 32;
-    uint32_t hmax = 0;
+    uint32_t hkeys = 0;  // packed max of the |H| bf16 keys staged by this lane
+    uint32_t hmax = 0;   // the same as one fp32-bit amax key
     auto run_pass = [&](auto pass_tag) {
       constexpr int pass = decltype(pass_tag)::value;
 #pragma unroll
@@ -745,8 +746,8 @@ gemm_kernel(GemmParams p) {
               const uint32_t l23 = pack_bf16x2(gelu_tanh_f32(bf16_lo(g23)), gelu_tanh_f32(bf16_hi(g23)));
               w0 = pack_bf16x2(bf16_lo(l01) * bf16_lo(u01), bf16_hi(l01) * bf16_hi(u01));
               w1 = pack_bf16x2(bf16_lo(l23) * bf16_lo(u23), bf16_hi(l23) * bf16_hi(u23));
-              const uint32_t a0 = w0 & 0x7FFF7FFFu, a1 = w1 & 0x7FFF7FFFu;
-              hmax = max(hmax, max(max(a0 << 16, a0 & 0xFFFF0000u), max(a1 << 16, a1 & 0xFFFF0000u)));
+              // |h| keys, both halves of a pair in one packed max
+              hkeys = pk_max_u16(hkeys, pk_max_u16(w0 & 0x7FFF7FFFu, w1 & 0x7FFF7FFFu));
             } else if constexpr (pass == 1) {
               w0 = pack_bf16x2(ga[0] * ag, ga[1] * ag);
               w1 = pack_bf16x2(ga[2] * ag, ga[3] * ag);
@@ -758,6 +759,7 @@ gemm_kernel(GemmParams p) {
           }
         }
       }
+      if constexpr (pass == 0) hmax = max(hkeys << 16, hkeys & 0xFFFF0000u);
       if constexpr (pass == 0) {
         if (p.h8) {
           // every value this wave quantizes is one it staged: with none of them inf or NaN
