@@ -194,9 +194,13 @@ __device__ __forceinline__ void mx_h_epilogue(const GemmParams& p, const uint8_t
     const int idx = it * 64 + lane;
     const int row = idx / CH, c = idx % CH;  // lanes 4j .. 4j+3: one block of one row
     const uint4 d = stage_get<CH>(wbuf, row, c);
-    uint32_t k = absmax_key8(d);
-    k = max(k, (uint32_t)__shfl_xor((int)k, 1, 64));
-    k = max(k, (uint32_t)__shfl_xor((int)k, 2, 64));
+    // |x| keys of the 8 values as one packed 16-bit max, then the block's max over the
+    // 4-lane group with DPP quad permutes ([1,0,3,2], then [2,3,0,1])
+    const uint32_t k2 = pk_max_u16(pk_max_u16(d.x & 0x7FFF7FFFu, d.y & 0x7FFF7FFFu),
+                                   pk_max_u16(d.z & 0x7FFF7FFFu, d.w & 0x7FFF7FFFu));
+    uint32_t k = max(k2 << 16, k2 & 0xFFFF0000u);
+    k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, 0xB1, 0xF, 0xF, true));
+    k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, 0x4E, 0xF, 0xF, true));
     const int gm = gm0 + row;
     if (gm < p.M) {
       const int n = h0 + c * 8;
