@@ -343,13 +343,14 @@ __device__ inline void write_meta_from_amax(uint32_t key, float fp8_max, float* 
 }
 
 // Scale of a tensor from the per-block amax partials its producer wrote, computed by
-// every block of the consumer (each reads the <= 2048 partials once); block 0 also
-// publishes the meta record. Result valid in all threads.
+// every block of the consumer (each reads the <= 2048 partials once); the leader block
+// (the consumer's first block of this tensor) also publishes the meta record. Result
+// valid in all threads.
 template <int NT>
 __device__ inline float scale_from_partials_block(const uint32_t* __restrict__ partials,
                                                   int64_t np, float fp8_max,
                                                   float* __restrict__ meta_out,
-                                                  bool pow2 = false) {
+                                                  bool pow2, bool leader) {
   __shared__ float s_scale;
   uint32_t m = 0;
   for (int64_t i = threadIdx.x; i < np; i += NT) m = max(m, partials[i]);
@@ -358,7 +359,7 @@ __device__ inline float scale_from_partials_block(const uint32_t* __restrict__ p
     float meta[4];
     write_meta_from_amax(m, fp8_max, meta, pow2);
     s_scale = meta[1];
-    if (meta_out && blockIdx.x == 0 && blockIdx.y == 0) {
+    if (meta_out && leader) {
       meta_out[0] = meta[0];
       meta_out[1] = meta[1];
       meta_out[2] = meta[2];

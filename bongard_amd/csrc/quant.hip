@@ -70,32 +70,40 @@ int grid_for_stream(int64_t work_items, int64_t per_block, int64_t cap) {
   return (int)(b < cap ? b : cap);
 }
 
-// partials[b] = max over block b's grid-stride share of |x| keys.
-__global__ __launch_bounds__(kNT) void amax_partials_kernel(const uint16_t* __restrict__ x,
-                                                            int64_t n,
-                                                            uint32_t* __restrict__ partials) {
+// partials[blk] = max over the grid-stride share of |x| keys of block blk of the nblk
+// blocks that read x.
+__device__ __forceinline__ void amax_partials_body(const uint16_t* __restrict__ x, int64_t n,
+                                                   uint32_t* __restrict__ partials,
+                                                   int64_t blk, int64_t nblk) {
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   const int64_t nvec = n >> 3;
-  const int64_t stride = (int64_t)gridDim.x * kNT;
+  const int64_t stride = nblk * kNT;
   uint32_t m = 0;
-  int64_t i = (int64_t)blockIdx.x * kNT + threadIdx.x;
+  int64_t i = blk * kNT + threadIdx.x;
   // kVecPerThread independent 16-byte loads per lane in flight (HBM latency x bandwidth
-  // needs ~32 MB in flight chip-wide)
-  for (; i + (kVecPerThread - 1) * stride < nvec; i += kVecPerThread * stride) {
+  // needs ~32 MB in flight chip-wide), also in the last, partial round: its missing loads
+  // are zero vectors (key 0), so a tail never degrades to one load in flight at a time
+  for (; i < nvec; i += kVecPerThread * stride) {
     uint4 v[kVecPerThread];
 #pragma unroll
-    for (int j = 0; j < kVecPerThread; ++j) v[j] = xv[i + j * stride];
+    for (int j = 0; j < kVecPerThread; ++j)
+      v[j] = i + j * stride < nvec ? xv[i + j * stride] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int j = 0; j < kVecPerThread; ++j) m = max(m, absmax_key8(v[j]));
   }
-  for (; i < nvec; i += stride) m = max(m, absmax_key8(xv[i]));
-  // scalar tail (n % 8), handled by block 0
-  if (blockIdx.x == 0) {
+  // scalar tail (n % 8), handled by the first block
+  if (blk == 0) {
     for (int64_t j = (nvec << 3) + threadIdx.x; j < n; j += kNT)
       m = max(m, (uint32_t)(x[j] & 0x7FFFu) << 16);
   }
   m = block_max_u32<kNT>(m);
-  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+  if (threadIdx.x == 0) partials[blk] = m;
+}
+
+__global__ __launch_bounds__(kNT) void amax_partials_kernel(const uint16_t* __restrict__ x,
+                                                            int64_t n,
+                                                            uint32_t* __restrict__ partials) {
+  amax_partials_body(x, n, partials, blockIdx.x, gridDim.x);
 }
 
 __global__ __launch_bounds__(kNT) void scale_from_partials_kernel(
@@ -128,13 +136,13 @@ struct ScaleSrc {
 };
 
 template <int FMT>
-__device__ __forceinline__ float resolve_scale(const ScaleSrc& s) {
+__device__ __forceinline__ float resolve_scale(const ScaleSrc& s, bool leader) {
   if (s.scale) return *s.scale;
   if (s.state)
     return delayed_scale_block<kNT>(s.state, s.len, s.pos, s.prev, s.n_prev, Fp8Max<FMT>::value,
                                     s.meta_out);
   return scale_from_partials_block<kNT>(s.partials, s.np, Fp8Max<FMT>::value, s.meta_out,
-                                        s.pow2 != 0);
+                                        s.pow2 != 0, leader);
 }
 
 // Block max of the lanes' amax keys, stored as this block's partial (amax_out != NULL).
@@ -147,22 +155,24 @@ __device__ __forceinline__ void store_block_amax(uint32_t m, uint32_t* amax_out,
 // Row-major cast: each lane converts 16 consecutive bf16 (two 16-byte loads) into one
 // 16-byte store. n16 = number of 16-element groups; the n % 16 tail is done bytewise.
 // With amax_out, each block also writes the max |x| key of the elements it cast.
+// Block blk of the nblk blocks that cast x; blk == 0 leads (publishes the meta record).
 template <int FMT>
-__global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ x, int64_t n,
-                                                   ScaleSrc src, uint8_t* __restrict__ out,
-                                                   uint32_t* __restrict__ amax_out) {
+__device__ __forceinline__ void cast_body(const uint16_t* __restrict__ x, int64_t n,
+                                          const ScaleSrc& src, uint8_t* __restrict__ out,
+                                          uint32_t* __restrict__ amax_out, int64_t blk,
+                                          int64_t nblk) {
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint4* ov = reinterpret_cast<uint4*>(out);
   const int64_t n16 = n >> 4;
-  const int64_t stride = (int64_t)gridDim.x * kNT;
-  int64_t i = (int64_t)blockIdx.x * kNT + threadIdx.x;
+  const int64_t stride = nblk * kNT;
+  int64_t i = blk * kNT + threadIdx.x;
   // Two 16-element groups (i, i + stride) per lane and iteration; the next iteration's
   // four loads are issued before this one is converted, and the first iteration's before
   // the scale is resolved (whose partial-amax reduction then overlaps them).
   uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = a0, b0 = a0, b1 = a0;
   if (i < n16) { a0 = xv[2 * i]; a1 = xv[2 * i + 1]; }
   if (i + stride < n16) { b0 = xv[2 * (i + stride)]; b1 = xv[2 * (i + stride) + 1]; }
-  const float scale = resolve_scale<FMT>(src);
+  const float scale = resolve_scale<FMT>(src, blk == 0);
   uint32_t m = 0;
   for (; i < n16; i += 2 * stride) {
     const uint4 c0 = a0, c1 = a1, d0 = b0, d1 = b1;
@@ -178,7 +188,7 @@ __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ 
       ov[i + stride] = make_uint4(qd0.x, qd0.y, qd1.x, qd1.y);
     }
   }
-  if (blockIdx.x == 0) {
+  if (blk == 0) {
     for (int64_t j = (n16 << 4) + threadIdx.x; j < n; j += kNT) {
       float xf = __uint_as_float((uint32_t)x[j] << 16);
       float p = xf * scale;
@@ -186,7 +196,14 @@ __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ 
       m = max(m, (uint32_t)(x[j] & 0x7FFFu) << 16);
     }
   }
-  store_block_amax(m, amax_out, blockIdx.x);
+  store_block_amax(m, amax_out, blk);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ x, int64_t n,
+                                                   ScaleSrc src, uint8_t* __restrict__ out,
+                                                   uint32_t* __restrict__ amax_out) {
+  cast_body<FMT>(x, n, src, out, amax_out, blockIdx.x, gridDim.x);
 }
 
 // Cast with a transposed copy, over kTR x 64 tiles of x, one tile per wave (grid-stride,
@@ -209,7 +226,7 @@ __global__ __launch_bounds__(kNT) void cast_transpose_kernel(
   constexpr int NL = kTR / 8;  // 16-byte loads per lane
   __shared__ uint32_t stage[kWavesPerBlock][(kTR / 64) * kWaveTileDwords];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const float scale = resolve_scale<FMT>(src);
+  const float scale = resolve_scale<FMT>(src, blockIdx.x == 0);
   const int64_t tiles_c = (cols + kTT - 1) / kTT;
   const int64_t ntiles = tiles_c * ((rows + kTR - 1) / kTR);
   const bool t16 = (rows & 15) == 0;  // out_t rows 16-byte aligned
@@ -410,6 +427,64 @@ ScaleSrc current_scale(const uint32_t* partials, int64_t np, float* meta) {
   return s;
 }
 
+// ---- several tensors in two launches ------------------------------------------------
+// Current-scaling quantization of up to kMaxMany bf16 tensors: one launch computes every
+// tensor's amax partials, one launch casts them all. Each tensor keeps the block count,
+// grid-stride order, partials and scale it has in amax_partials_kernel + cast_kernel, so
+// its bytes and meta are those of its own quantization; sharing the launches fills the
+// chip when a tensor alone would not, and saves two launches per extra tensor.
+constexpr int kMaxMany = 8;
+static_assert(kMaxAmaxBlocks <= kMaxInlinePartials, "the cast reduces a tensor's partials inline");
+
+struct ManySeg {
+  const uint16_t* x;
+  int64_t n;
+  uint8_t* out;
+  float* meta;
+  int64_t part_off;    // this tensor's partials: [part_off, part_off + amax_blocks)
+  int64_t amax_first;  // first block of this tensor in the amax launch
+  int64_t amax_blocks;
+  int64_t cast_first;  // first block of this tensor in the cast launch
+  int64_t cast_blocks;
+  int fmt, pow2;
+};
+
+struct ManyArgs {
+  ManySeg seg[kMaxMany];
+  int count;
+  uint32_t* partials;
+};
+
+// The tensor whose blocks include block b (segments in launch order).
+__device__ __forceinline__ int many_segment(const ManyArgs& a, int64_t b, bool cast) {
+  int t = 0;
+  for (int k = 1; k < a.count; ++k)
+    if (b >= (cast ? a.seg[k].cast_first : a.seg[k].amax_first)) t = k;
+  return t;
+}
+
+__global__ __launch_bounds__(kNT) void amax_many_kernel(ManyArgs a) {
+  const int t = many_segment(a, blockIdx.x, false);
+  const ManySeg& g = a.seg[t];
+  amax_partials_body(g.x, g.n, a.partials + g.part_off, (int64_t)blockIdx.x - g.amax_first,
+                     g.amax_blocks);
+}
+
+__global__ __launch_bounds__(kNT) void cast_many_kernel(ManyArgs a) {
+  const int t = many_segment(a, blockIdx.x, true);
+  const ManySeg& g = a.seg[t];
+  ScaleSrc src{};
+  src.partials = a.partials + g.part_off;
+  src.np = g.amax_blocks;
+  src.meta_out = g.meta;
+  src.pow2 = g.pow2;
+  const int64_t blk = (int64_t)blockIdx.x - g.cast_first;
+  if (g.fmt == BF8_E4M3)
+    cast_body<BF8_E4M3>(g.x, g.n, src, g.out, nullptr, blk, g.cast_blocks);
+  else
+    cast_body<BF8_E5M2>(g.x, g.n, src, g.out, nullptr, blk, g.cast_blocks);
+}
+
 }  // namespace
 }  // namespace bf8
 
@@ -418,7 +493,7 @@ using namespace bf8;
 extern "C" {
 
 const char* bf8_last_error(void) { return bf8::g_err; }
-int bf8_abi_version(void) { return 8; }
+int bf8_abi_version(void) { return 9; }
 
 int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
 
@@ -502,6 +577,57 @@ int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_
   if (rc) return rc;
   return bf8_cast_partials_bf16(x, rows, cols, partials, amax_blocks(n), fmt, meta, out, out_t,
                                 stream);
+}
+
+int64_t bf8_quantize_many_partials(int count, const int64_t* n) {
+  if (count < 1 || count > kMaxMany || !n) return 0;
+  int64_t total = 0;
+  for (int t = 0; t < count; ++t) total += n[t] > 0 ? amax_blocks(n[t]) : 0;
+  return total;
+}
+
+int bf8_quantize_many_bf16(int count, const void* const* x, const int64_t* n, const int* fmt,
+                           uint8_t* const* out, float* const* meta, uint32_t* partials,
+                           void* stream) {
+  BF8_CHECK(count >= 1 && count <= kMaxMany, "bf8_quantize_many_bf16: count %d outside [1, %d]",
+            count, kMaxMany);
+  BF8_CHECK(x && n && fmt && out && meta, "bf8_quantize_many_bf16: NULL array");
+  ManyArgs a{};
+  a.partials = partials;
+  int64_t amax_total = 0, cast_total = 0;
+  for (int t = 0; t < count; ++t) {
+    const int f = fmt[t] & ~BF8_SCALE_POW2;
+    BF8_CHECK(f == BF8_E4M3 || f == BF8_E5M2, "bf8_quantize_many_bf16: tensor %d: bad fmt %d", t,
+              fmt[t]);
+    BF8_CHECK(n[t] >= 0, "bf8_quantize_many_bf16: tensor %d: n < 0", t);
+    BF8_CHECK(meta[t] != nullptr, "bf8_quantize_many_bf16: tensor %d: meta is NULL", t);
+    if (n[t] == 0) continue;  // as bf8_quantize_bf16: nothing cast, meta untouched
+    BF8_CHECK(x[t] && out[t], "bf8_quantize_many_bf16: tensor %d: x or out is NULL", t);
+    BF8_CHECK(((uintptr_t)x[t] & 15) == 0 && ((uintptr_t)out[t] & 15) == 0,
+              "bf8_quantize_many_bf16: tensor %d: x and out must be 16-byte aligned", t);
+    ManySeg& g = a.seg[a.count++];
+    g.x = (const uint16_t*)x[t];
+    g.n = n[t];
+    g.out = out[t];
+    g.meta = meta[t];
+    g.fmt = f;
+    g.pow2 = (fmt[t] & BF8_SCALE_POW2) ? 1 : 0;
+    g.part_off = amax_total;
+    g.amax_first = amax_total;
+    g.amax_blocks = amax_blocks(n[t]);
+    g.cast_first = cast_total;
+    g.cast_blocks = row_cast_blocks(n[t], false);
+    amax_total += g.amax_blocks;
+    cast_total += g.cast_blocks;
+  }
+  if (a.count == 0) return BF8_OK;
+  BF8_CHECK(partials != nullptr, "bf8_quantize_many_bf16: partials is NULL");
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(amax_many_kernel, dim3((unsigned)amax_total), dim3(kNT), 0, s, a);
+  const int rc = launch_status("amax_many_kernel");
+  if (rc != BF8_OK) return rc;
+  hipLaunchKernelGGL(cast_many_kernel, dim3((unsigned)cast_total), dim3(kNT), 0, s, a);
+  return launch_status("cast_many_kernel");
 }
 
 int bf8_delayed_scale_begin(float* state, int len, int fmt, void* stream) {

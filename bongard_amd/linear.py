@@ -68,7 +68,11 @@ class Fp8LinearFunction(torch.autograd.Function):
     def forward(ctx, x, weight, bias, wq, scaling=None):
         need_dx = ctx.needs_input_grad[0]
         need_dw = ctx.needs_input_grad[1]
-        xq = _quantize(x, E4M3, scaling and scaling.input, transpose=need_dw)
+        if scaling is None and wq is None and not (need_dx or need_dw):
+            # current scaling, no transposed copies: x and W in one amax + one cast launch
+            xq, wq = ops.quantize_many([x, weight.detach()])
+        else:
+            xq = _quantize(x, E4M3, scaling and scaling.input, transpose=need_dw)
         if wq is None:
             wq = quantize_weight(weight, transpose=need_dx,
                                  scaler=scaling and scaling.weight)
@@ -270,7 +274,19 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
         if scaling is not None and split_scales:
             raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
         gs, ds = scaling if scaling is not None else (None, None)
-        xq = _quantize_input(x, gs and gs.input, x_amax, ctx.needs_input_grad[1])
+        if (scaling is None and x_amax is None and not train and not split_scales
+                and (gu_q is None or down_q is None)):
+            # current-scaling inference: x and the uncached weights in one amax + one cast
+            # launch (the rowwise copies are all the forward needs)
+            ws = [w for w, q in ((w_gu, gu_q), (w_down, down_q)) if q is None]
+            qs = ops.quantize_many([x] + [w.detach() for w in ws])
+            xq = qs[0]
+            if gu_q is None:
+                gu_q = _GateUp(qs[1].data, None, qs[1].meta.view(1, 4))
+            if down_q is None:
+                down_q = qs[-1]
+        else:
+            xq = _quantize_input(x, gs and gs.input, x_amax, ctx.needs_input_grad[1])
         if gu_q is None:
             gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=ctx.needs_input_grad[0],
                                     scaler=gs and gs.weight)

@@ -178,6 +178,41 @@ def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None,
     return Fp8Tensor(out if rowwise else None, out_t if transpose else None, meta, fmt, rows, cols)
 
 
+def quantize_many(xs, fmts=None, *, pow2=False, metas=None):
+    """:func:`quantize` (rowwise output, current scaling) of up to 8 bf16 tensors in two
+    launches: one amax pass over all of them, one cast pass. Each result equals that
+    tensor's own ``quantize(x, fmt, pow2=pow2)``, bytes and meta. ``fmts``: one format
+    for all tensors or one per tensor (default e4m3); ``metas``: optional meta rows to
+    write (as ``quantize(meta=...)``)."""
+    xs = [_bf16_2d(x) for x in xs]
+    count = len(xs)
+    if not 1 <= count <= 8:
+        raise ValueError(f"quantize_many: {count} tensors (1 to 8 supported)")
+    _require_gpu(*xs)
+    dev = xs[0].device
+    if any(x.device != dev for x in xs):
+        raise ValueError("quantize_many: tensors on different devices")
+    if fmts is None or isinstance(fmts, int):
+        fmts = [E4M3 if fmts is None else fmts] * count
+    if len(fmts) != count:
+        raise ValueError("quantize_many: one format per tensor")
+    if metas is None:
+        metas = [new_meta(dev) for _ in range(count)]
+    outs = [torch.empty(x.shape, dtype=TORCH_FP8[f], device=dev) for x, f in zip(xs, fmts)]
+    L = _lib.lib()
+    n = (ctypes.c_int64 * count)(*[x.numel() for x in xs])
+    parts = partials_buffer(max(1, L.bf8_quantize_many_partials(count, n)), dev)
+    flag = SCALE_POW2 if pow2 else 0
+    _lib.check(L.bf8_quantize_many_bf16(
+        count, (ctypes.c_void_p * count)(*[x.data_ptr() for x in xs]), n,
+        (ctypes.c_int * count)(*[f | flag for f in fmts]),
+        (ctypes.c_void_p * count)(*[o.data_ptr() for o in outs]),
+        (ctypes.c_void_p * count)(*[m.data_ptr() for m in metas]), _ptr(parts), _stream(dev)),
+        "bf8_quantize_many_bf16")
+    return [Fp8Tensor(o, None, m, f, x.shape[0], x.shape[1])
+            for x, o, m, f in zip(xs, outs, metas, fmts)]
+
+
 def amax(x):
     """Per-block partial amax keys (int32 view of fp32 bits) of a bf16 tensor."""
     _require_gpu(x)

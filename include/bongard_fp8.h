@@ -94,6 +94,21 @@ int bf8_cast_partials_bf16(const void* x, int64_t rows, int64_t cols, const uint
 int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
                       uint8_t* out_t, float* meta, uint32_t* partials, void* stream);
 
+/* bf8_quantize_bf16 (rowwise output only) of 1-8 tensors in two launches: one amax pass
+ * over all of them, one cast pass. Tensor t (x[t]: bf16 [n[t]], out[t]: fp8 [n[t]], both
+ * 16-byte aligned; fmt[t] may carry BF8_SCALE_POW2) gets the bytes and meta[t] that its
+ * own bf8_quantize_bf16 call would give; tensors with n[t] == 0 are skipped (meta
+ * untouched). The arrays are host memory. partials: uint32
+ * [bf8_quantize_many_partials(count, n)].
+ * Replaces the back-to-back per-tensor casts of one forward: input and weight of
+ * Float8Linear (bongard/float8_training.py:22) and TELinear (bongard/te_linear.py:73-74),
+ * input, fc1 and fc2 weights of TEMLP / FusedMLP (bongard/te_linear.py:98-103,
+ * bongard/fused_mlp.py:76-78). */
+int64_t bf8_quantize_many_partials(int count, const int64_t* n);
+int bf8_quantize_many_bf16(int count, const void* const* x, const int64_t* n, const int* fmt,
+                           uint8_t* const* out, float* const* meta, uint32_t* partials,
+                           void* stream);
+
 /* ---------------------------------------------------------------------------------
  * FP8 GEMM, TN: C[m, n] = (sum_k A[m, k] * B[n, k]) * a_scale_inv * b_scale_inv(n)
  *                          (+ bias[n]), fp32 accumulation, bf16 or fp32 output.

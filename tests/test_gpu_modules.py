@@ -20,7 +20,7 @@ import torch
 from torch import nn
 from transformers.models.t5gemma2.modeling_t5gemma2 import T5Gemma2MLP, T5Gemma2RMSNorm
 
-from bongard_amd import float8_training, fused_mlp, te_linear
+from bongard_amd import float8_training, fused_mlp, ops, te_linear
 from oracle import fp8_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -389,3 +389,30 @@ def test_fp8_linears_inside_a_compiled_region(gpu, kind):
         results.append((y.detach(), xg.grad, block.up.weight.grad, block.down.weight.grad))
     for a, b in zip(*results):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_inference_forward_shares_quantize_launches(gpu):
+    """Under no_grad the FP8 linear and gated MLP quantize x and their weights in shared
+    launches (ops.quantize_many); the output is bit-identical to the training forward's,
+    which quantizes each tensor on its own."""
+    from bongard_amd import linear
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(300, 256, generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.randn(384, 256, generator=g) * 0.05).to(torch.bfloat16).to(gpu)
+    w_gu = (torch.randn(2 * 512, 256, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    w_d = (torch.randn(256, 512, generator=g) * 0.014).to(torch.bfloat16).to(gpu)
+    x16 = x[:288]
+    y_train = linear.Fp8LinearFunction.apply(x16, w.requires_grad_(), None, None)
+    with torch.no_grad():
+        y_inf = linear.Fp8LinearFunction.apply(x16, w, None, None)
+    assert torch.equal(y_train.detach(), y_inf)
+    with torch.no_grad():   # a row count the training path would reject (M % 16 != 0)
+        y_odd = linear.Fp8LinearFunction.apply(x, w, None, None)
+        xq, wq = ops.quantize(x), ops.quantize(w)
+        y_sep = ops.gemm(xq.data, ops.E4M3, xq.meta, wq.data, ops.E4M3, wq.meta)
+    assert torch.equal(y_odd, y_sep)
+    y_train = linear.Fp8GegluMlpFunction.apply(x16, w_gu.requires_grad_(), w_d, None, None,
+                                               512, False)
+    with torch.no_grad():
+        y_inf = linear.Fp8GegluMlpFunction.apply(x16, w_gu, w_d, None, None, 512, False)
+    assert torch.equal(y_train.detach(), y_inf)

@@ -111,3 +111,50 @@ def test_delayed_scaling_matches_closed_form(gpu):
         assert m[1].item() == float(s) and m[2].item() == float(si), (step, m, s, si)
         assert torch.equal(_bytes(q.data), ref_q), step
     assert np.array_equal(st[:L].cpu().numpy(), ref.history)
+
+
+def test_quantize_many_equals_quantize(gpu):
+    """Several tensors quantized in two shared launches give each tensor's own bytes and
+    meta: against the oracle for the small ones, against the single-tensor quantization
+    (itself pinned to the oracle above) for one large enough to hit the partials cap;
+    formats mixed, a ragged size, an empty tensor (its meta left untouched)."""
+    g = torch.Generator().manual_seed(11)
+    small = [torch.randn(512, 2560, generator=g).to(torch.bfloat16),
+             (torch.randn(1, 1007, generator=g) * 300).to(torch.bfloat16),
+             torch.randn(256, 4096, generator=g).to(torch.bfloat16)]
+    small[2][7, 9] = float("inf")
+    big = torch.randn(8192, 4608, generator=g).to(torch.bfloat16).to(gpu)
+    empty = torch.empty(0, 2560, dtype=torch.bfloat16, device=gpu)
+    fmts = [ops.E4M3, ops.E5M2, ops.E4M3, ops.E5M2, ops.E4M3]
+    sentinel = torch.full((4,), -7.0, device=gpu)
+    metas = [ops.new_meta(gpu) for _ in range(3)] + [ops.new_meta(gpu), sentinel.clone()]
+    xs = [t.to(gpu) for t in small] + [big, empty]
+    qs = ops.quantize_many(xs, fmts, metas=metas)
+    torch.cuda.synchronize()
+    for t, q, f in zip(small, qs[:3], fmts[:3]):
+        ref_q, ref_a, ref_s, ref_si = orc.quantize(t, f)
+        meta = q.meta.cpu()
+        assert meta[0].view(torch.int32) == ref_a.view(torch.int32)
+        assert meta[1].view(torch.int32) == ref_s.view(torch.int32)
+        assert meta[2].view(torch.int32) == ref_si.view(torch.int32)
+        assert torch.equal(_bytes(q.data), ref_q)
+    one = ops.quantize(big, ops.E5M2)
+    assert torch.equal(qs[3].data.view(torch.uint8), one.data.view(torch.uint8))
+    assert torch.equal(qs[3].meta, one.meta)
+    assert torch.equal(qs[4].meta, sentinel)
+    # power-of-two scales, one format for all
+    qp = ops.quantize_many(xs[:2], ops.E4M3, pow2=True)
+    for x, q in zip(xs[:2], qp):
+        r = ops.quantize(x, ops.E4M3, pow2=True)
+        assert torch.equal(q.data.view(torch.uint8), r.data.view(torch.uint8))
+        assert torch.equal(q.meta, r.meta)
+
+
+def test_quantize_many_rejects_bad_lists(gpu):
+    x = torch.randn(64, 64, device=gpu).to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        ops.quantize_many([])
+    with pytest.raises(ValueError):
+        ops.quantize_many([x] * 9)
+    with pytest.raises(ValueError):
+        ops.quantize_many([x, x], [ops.E4M3])

@@ -74,6 +74,28 @@ def test_plan_override_env(monkeypatch):
     assert L.bf8_geglu_partials(4096, 10240) >= 1
 
 
+def test_quantize_many_rejects_bad_arguments():
+    """The multi-tensor quantization checks its lists on the host (no launch)."""
+    L = _lib.lib()
+    null = ctypes.c_void_p(0)
+    n = (ctypes.c_int64 * 9)(*([64] * 9))
+    assert L.bf8_quantize_many_partials(2, n) == 2
+    assert L.bf8_quantize_many_partials(9, n) == 0
+    buf = ctypes.create_string_buffer(1 << 12)
+    ptr = ctypes.c_void_p((ctypes.addressof(buf) + 255) // 256 * 256)
+    ptrs = (ctypes.c_void_p * 2)(ptr, ptr)
+    rc = L.bf8_quantize_many_bf16(0, ptrs, n, (ctypes.c_int * 2)(0, 0), ptrs, ptrs, ptr, null)
+    assert rc == 1 and b"count 0" in L.bf8_last_error()
+    rc = L.bf8_quantize_many_bf16(2, ptrs, n, (ctypes.c_int * 2)(0, 7), ptrs, ptrs, ptr, null)
+    assert rc == 1 and b"bad fmt 7" in L.bf8_last_error()
+    odd = (ctypes.c_void_p * 2)(ptr, ctypes.c_void_p(ptr.value + 8))
+    rc = L.bf8_quantize_many_bf16(2, odd, n, (ctypes.c_int * 2)(0, 0), ptrs, ptrs, ptr, null)
+    assert rc == 1 and b"16-byte aligned" in L.bf8_last_error()
+    nometa = (ctypes.c_void_p * 2)(ptr, null)
+    rc = L.bf8_quantize_many_bf16(2, ptrs, n, (ctypes.c_int * 2)(0, 0), ptrs, nometa, ptr, null)
+    assert rc == 1 and b"meta is NULL" in L.bf8_last_error()
+
+
 def test_quantizing_geglu_and_scale_fold_reject_bad_arguments():
     """The epilogue-quantizing gate/up entries and the delayed scale fold check their
     arguments on the host (no launch): missing H8, a transposed copy with M % 32 != 0,
