@@ -63,9 +63,7 @@ def main():
     dst = torch.empty_like(src)
     for _ in range(args.iters):
         dst.copy_(src)
-        xq = ops.quantize(x, ops.E4M3)
-        gq = ops.quantize(w_gu, ops.E4M3)
-        dq = ops.quantize(w_d, ops.E4M3)
+        xq, gq, dq = ops.quantize_many([x, w_gu, w_d])
         H, _, hparts = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
         hq = ops.cast_partials(H, hparts, ops.E4M3)
         hm = hq.meta
