@@ -503,9 +503,7 @@ def _bench_c2_mx(torch, ops, workloads, dev, steps=30):
     I = c["w_gate"].shape[0]
 
     def step(fused=True):
-        xq = ops.quantize_mx(x)
-        gq = ops.quantize_mx(w_gu)
-        dq = ops.quantize_mx(w_d)
+        xq, gq, dq = ops.quantize_mx_many([x, w_gu, w_d])   # one launch, as the MX forward
         if fused:  # H quantized in the gate/up GEMM's epilogue (the product path)
             hq, _, _ = ops.gemm_geglu_mx_quant(xq.data, xq.scales, gq.data, gq.scales, I)
         else:
@@ -528,6 +526,8 @@ def _bench_c2_mx(torch, ops, workloads, dev, steps=30):
                                                            gq.scales, I), steps)
     d_s = _ev_time(torch, lambda: ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales), steps)
     h_s = _ev_time(torch, lambda: ops.quantize_mx(H), steps)
+    qm_s = _ev_time(torch, lambda: ops.quantize_mx_many([x, w_gu, w_d]), steps)
+    qs_s = _ev_time(torch, lambda: [ops.quantize_mx(t) for t in (x, w_gu, w_d)], steps)
     flop = 2.0 * M * (2 * I * K + K * I)
     return {"workload": f"c2 MLP forward [{M},{K}] x [2*{I},{K}] -> [{M},{I}] x [{K},{I}], MXFP8",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
@@ -539,7 +539,9 @@ def _bench_c2_mx(torch, ops, workloads, dev, steps=30):
             "gemm_down_us": round(d_s * 1e6, 2),
             "gemm_down_tflops": round(2.0 * M * K * I / d_s / 1e12, 1),
             "quantize_h_us": round(h_s * 1e6, 2),
-            "quantize_h_gbps": round((3.0 * M * I + M * I / 32) / h_s / 1e9, 1)}
+            "quantize_h_gbps": round((3.0 * M * I + M * I / 32) / h_s / 1e9, 1),
+            "quantize_x_wgu_wd_one_launch_us": round(qm_s * 1e6, 2),
+            "quantize_x_wgu_wd_separate_us": round(qs_s * 1e6, 2)}
 
 
 def _bench_c1_rowwise(torch, ops, workloads, dev, steps=50):

@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -28,6 +28,9 @@ SIGNATURES = {
     "bf8_quantize_many_bf16": (c_int, [c_int, POINTER(c_void_p), POINTER(c_int64),
                                        POINTER(c_int), POINTER(c_void_p), POINTER(c_void_p),
                                        c_void_p, c_void_p]),
+    "bf8_quantize_mx_many_bf16": (c_int, [c_int, POINTER(c_void_p), POINTER(c_int64),
+                                          POINTER(c_int64), POINTER(c_int), POINTER(c_void_p),
+                                          POINTER(c_void_p), c_void_p]),
     "bf8_gemm_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
     "bf8_gemm": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_int, c_int64, c_int64, c_int64,
                          c_int64, c_void_p, c_void_p, c_int, POINTER(c_int64), c_int, c_void_p,

@@ -29,18 +29,18 @@ constexpr int kMaxMxTileBlocks = 2048;
 // Rowwise: a 16-lane group handles 128 consecutive elements of a row (4 blocks, 4 lanes
 // each, 8 elements per lane) and writes the dword of their 4 scale bytes. Grid-stride over
 // (row, 128-element group) pairs; groups past the row's last block write padding scales.
+// (Block blk of the nblk blocks that quantize x.)
 template <int FMT>
-__global__ __launch_bounds__(kMxNT) void mx_row_kernel(const uint16_t* __restrict__ x,
-                                                       int64_t rows, int64_t cols,
-                                                       uint8_t* __restrict__ out,
-                                                       uint8_t* __restrict__ sc, int64_t ld_sc) {
+__device__ __forceinline__ void mx_row_body(const uint16_t* __restrict__ x, int64_t rows,
+                                            int64_t cols, uint8_t* __restrict__ out,
+                                            uint8_t* __restrict__ sc, int64_t ld_sc,
+                                            int64_t blk, int64_t nblk) {
   const int lane = threadIdx.x & 63;
   const int sub = lane & 15;                 // lane within the 16-lane group
   const int64_t groups_per_row = ld_sc / 4;  // dwords of scales per row
   const int64_t ngroups = rows * groups_per_row;
-  const int64_t gstride = (int64_t)gridDim.x * (kMxNT / 16);
-  for (int64_t g = (int64_t)blockIdx.x * (kMxNT / 16) + (threadIdx.x >> 4); g < ngroups;
-       g += gstride) {
+  const int64_t gstride = nblk * (kMxNT / 16);
+  for (int64_t g = blk * (kMxNT / 16) + (threadIdx.x >> 4); g < ngroups; g += gstride) {
     const int64_t r = g / groups_per_row, cg = g % groups_per_row;
     const int64_t c = cg * 128 + sub * 8;
     const bool valid = c < cols;
@@ -64,6 +64,53 @@ __global__ __launch_bounds__(kMxNT) void mx_row_kernel(const uint16_t* __restric
     if (sub == 0)
       *reinterpret_cast<uint32_t*>(sc + r * ld_sc + cg * 4) = e0 | (e1 << 8) | (e2 << 16) | (e3 << 24);
   }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kMxNT) void mx_row_kernel(const uint16_t* __restrict__ x,
+                                                       int64_t rows, int64_t cols,
+                                                       uint8_t* __restrict__ out,
+                                                       uint8_t* __restrict__ sc, int64_t ld_sc) {
+  mx_row_body<FMT>(x, rows, cols, out, sc, ld_sc, blockIdx.x, gridDim.x);
+}
+
+// Rowwise MX quantization of up to kMxMany tensors in one launch: tensor t owns blocks
+// [first, first + blocks) and runs exactly the grid-stride loop mx_row_kernel runs for it
+// alone, so its bytes and scales are unchanged; the shared launch fills the chip when one
+// tensor would not and saves a launch per extra tensor.
+constexpr int kMxMany = 8;
+
+struct MxManySeg {
+  const uint16_t* x;
+  int64_t rows, cols;
+  uint8_t* out;
+  uint8_t* sc;
+  int64_t ld_sc;
+  int64_t first, blocks;
+  int fmt;
+};
+
+struct MxManyArgs {
+  MxManySeg seg[kMxMany];
+  int count;
+};
+
+__global__ __launch_bounds__(kMxNT) void mx_row_many_kernel(MxManyArgs a) {
+  int t = 0;
+  for (int k = 1; k < a.count; ++k)
+    if ((int64_t)blockIdx.x >= a.seg[k].first) t = k;
+  const MxManySeg& g = a.seg[t];
+  const int64_t blk = (int64_t)blockIdx.x - g.first;
+  if (g.fmt == BF8_E4M3)
+    mx_row_body<BF8_E4M3>(g.x, g.rows, g.cols, g.out, g.sc, g.ld_sc, blk, g.blocks);
+  else
+    mx_row_body<BF8_E5M2>(g.x, g.rows, g.cols, g.out, g.sc, g.ld_sc, blk, g.blocks);
+}
+
+int64_t mx_row_blocks(int64_t rows, int64_t ld_sc) {
+  const int64_t groups = rows * (ld_sc / 4);
+  return std::max<int64_t>(1, std::min<int64_t>((groups + kMxNT / 16 - 1) / (kMxNT / 16),
+                                                kMxMaxRowBlocks));
 }
 
 // Columnwise, transposed: 64 x 64 tiles of x; each column's two 32-row blocks get their
@@ -199,9 +246,7 @@ int bf8_quantize_mx_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uin
   const uint16_t* xs = (const uint16_t*)x;
   if (out) {
     const int64_t ld = bf8_mx_scale_ld(cols);
-    const int64_t groups = rows * (ld / 4);
-    const unsigned grid = (unsigned)std::max<int64_t>(
-        1, std::min<int64_t>((groups + kMxNT / 16 - 1) / (kMxNT / 16), kMxMaxRowBlocks));
+    const unsigned grid = (unsigned)mx_row_blocks(rows, ld);
     if (fmt == BF8_E4M3)
       hipLaunchKernelGGL(mx_row_kernel<BF8_E4M3>, dim3(grid), dim3(kMxNT), 0, s, xs, rows, cols,
                          out, out_scales, ld);
@@ -224,6 +269,48 @@ int bf8_quantize_mx_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uin
     return launch_status("mx_col_kernel");
   }
   return BF8_OK;
+}
+
+int bf8_quantize_mx_many_bf16(int count, const void* const* x, const int64_t* rows,
+                              const int64_t* cols, const int* fmt, uint8_t* const* out,
+                              uint8_t* const* out_scales, void* stream) {
+  BF8_CHECK(count >= 1 && count <= kMxMany,
+            "bf8_quantize_mx_many_bf16: count %d outside [1, %d]", count, kMxMany);
+  BF8_CHECK(x && rows && cols && fmt && out && out_scales,
+            "bf8_quantize_mx_many_bf16: NULL array");
+  MxManyArgs a{};
+  int64_t total = 0;
+  for (int t = 0; t < count; ++t) {
+    BF8_CHECK(fmt[t] == BF8_E4M3 || fmt[t] == BF8_E5M2,
+              "bf8_quantize_mx_many_bf16: tensor %d: bad fmt %d", t, fmt[t]);
+    BF8_CHECK(rows[t] >= 0 && cols[t] >= 0, "bf8_quantize_mx_many_bf16: tensor %d: negative shape",
+              t);
+    BF8_CHECK(cols[t] % 32 == 0,
+              "bf8_quantize_mx_many_bf16: tensor %d: rowwise blocks need cols %% 32 == 0 (got %lld)",
+              t, (long long)cols[t]);
+    if (rows[t] == 0 || cols[t] == 0) continue;
+    BF8_CHECK(x[t] && out[t] && out_scales[t],
+              "bf8_quantize_mx_many_bf16: tensor %d: x, out or out_scales is NULL", t);
+    BF8_CHECK(((uintptr_t)x[t] & 15) == 0 && ((uintptr_t)out[t] & 7) == 0 &&
+                  ((uintptr_t)out_scales[t] & 3) == 0,
+              "bf8_quantize_mx_many_bf16: tensor %d: x 16-byte, out 8-byte, out_scales 4-byte "
+              "aligned", t);
+    MxManySeg& g = a.seg[a.count++];
+    g.x = (const uint16_t*)x[t];
+    g.rows = rows[t];
+    g.cols = cols[t];
+    g.out = out[t];
+    g.sc = out_scales[t];
+    g.ld_sc = bf8_mx_scale_ld(cols[t]);
+    g.first = total;
+    g.blocks = mx_row_blocks(rows[t], g.ld_sc);
+    g.fmt = fmt[t];
+    total += g.blocks;
+  }
+  if (a.count == 0) return BF8_OK;
+  hipLaunchKernelGGL(mx_row_many_kernel, dim3((unsigned)total), dim3(kMxNT), 0,
+                     as_stream(stream), a);
+  return launch_status("mx_row_many_kernel");
 }
 
 }  // extern "C"

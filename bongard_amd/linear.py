@@ -219,7 +219,17 @@ class Fp8GegluMlpMxFunction(torch.autograd.Function):
         I = int(intermediate)
         need_dx, need_dgu, need_dd = ctx.needs_input_grad[:3]
         train = need_dx or need_dgu or need_dd
-        xq = ops.quantize_mx(x, E4M3, rowwise=True, colwise=need_dgu)
+        if not train and (gu_q is None or down_q is None):
+            # inference: x and the uncached weights in one rowwise launch
+            ws = [w for w, q in ((w_gu, gu_q), (w_down, down_q)) if q is None]
+            qs = ops.quantize_mx_many([x] + [w.detach() for w in ws])
+            xq = qs[0]
+            if gu_q is None:
+                gu_q = qs[1]
+            if down_q is None:
+                down_q = qs[-1]
+        else:
+            xq = ops.quantize_mx(x, E4M3, rowwise=True, colwise=need_dgu)
         if gu_q is None:
             gu_q = quantize_weight_mx(w_gu, transpose=need_dx)
         # H is quantized (rowwise, plus the columnwise copy for the down wgrad) in the

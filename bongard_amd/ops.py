@@ -446,6 +446,36 @@ def quantize_mx(x, fmt=E4M3, *, rowwise=True, colwise=False):
     return MxFp8Tensor(out, sc, out_t, sc_t, fmt, rows, cols)
 
 
+def quantize_mx_many(xs, fmts=None):
+    """Rowwise :func:`quantize_mx` of up to 8 bf16 tensors in one launch; each result
+    equals that tensor's own ``quantize_mx(x, fmt)`` (bytes and scales). ``fmts``: one
+    format for all or one per tensor (default e4m3)."""
+    xs = [_bf16_2d(x) for x in xs]
+    count = len(xs)
+    if not 1 <= count <= 8:
+        raise ValueError(f"quantize_mx_many: {count} tensors (1 to 8 supported)")
+    _require_gpu(*xs)
+    dev = xs[0].device
+    if any(x.device != dev for x in xs):
+        raise ValueError("quantize_mx_many: tensors on different devices")
+    if fmts is None or isinstance(fmts, int):
+        fmts = [E4M3 if fmts is None else fmts] * count
+    if len(fmts) != count:
+        raise ValueError("quantize_mx_many: one format per tensor")
+    outs = [torch.empty(x.shape, dtype=TORCH_FP8[f], device=dev) for x, f in zip(xs, fmts)]
+    scs = [torch.empty((x.shape[0], mx_scale_ld(x.shape[1])), dtype=torch.uint8, device=dev)
+           for x in xs]
+    _lib.check(_lib.lib().bf8_quantize_mx_many_bf16(
+        count, (ctypes.c_void_p * count)(*[x.data_ptr() for x in xs]),
+        (ctypes.c_int64 * count)(*[x.shape[0] for x in xs]),
+        (ctypes.c_int64 * count)(*[x.shape[1] for x in xs]), (ctypes.c_int * count)(*fmts),
+        (ctypes.c_void_p * count)(*[o.data_ptr() for o in outs]),
+        (ctypes.c_void_p * count)(*[c.data_ptr() for c in scs]), _stream(dev)),
+        "bf8_quantize_mx_many_bf16")
+    return [MxFp8Tensor(o, c, None, None, f, x.shape[0], x.shape[1])
+            for x, o, c, f in zip(xs, outs, scs, fmts)]
+
+
 def gemm_mx(a, a_scales, b, b_scales, *, out_dtype=torch.bfloat16, bias=None, out=None):
     """``C = a @ b.T`` on MXFP8 (e4m3) operands a [M, K], b [N, K] with their E8M0 block
     scales [M, >= mx_scale_ld(K)], [N, ...]."""

@@ -284,6 +284,17 @@ int bf8_quantize_mx_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uin
                          uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
                          void* stream);
 
+/* bf8_quantize_mx_bf16's rowwise output for 1-8 tensors in one launch: tensor t (x[t]:
+ * bf16 [rows[t], cols[t]], cols[t] % 32 == 0) gets the bytes out[t] and scales
+ * out_scales[t] ([rows[t], bf8_mx_scale_ld(cols[t])]) of its own call; empty tensors are
+ * skipped. The arrays are host memory.
+ * Replaces the per-tensor MXFP8 quantizations of one TE forward under 'mxfp8' (input and
+ * weights of TELinear / TEMLP / FusedMLP: bongard/te_linear.py:98-103,
+ * bongard/fused_mlp.py:25-33) when no columnwise copies are needed. */
+int bf8_quantize_mx_many_bf16(int count, const void* const* x, const int64_t* rows,
+                              const int64_t* cols, const int* fmt, uint8_t* const* out,
+                              uint8_t* const* out_scales, void* stream);
+
 /* C[m, n] = sum_b 2^(ea[m,b] + eb[n,b] - 254) * sum_{k in block b} A[m, k] * B[n, k]
  * (+ bias[n]), e4m3 operands, fp32 accumulation; TN like bf8_gemm, K % 32 == 0. Scale
  * arrays 4-byte aligned with row strides >= bf8_mx_scale_ld(K), multiples of 4.

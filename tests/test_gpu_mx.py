@@ -312,3 +312,32 @@ def test_gemm_mx_every_tile(gpu, monkeypatch, tile):
     scale dwords run with one stage fewer), forced through the tuning override."""
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", tile)
     _mx_gemm_case(gpu, 300, 392, 544, seed=17)
+
+
+def test_quantize_mx_many_equals_quantize_mx(gpu):
+    """Rowwise MX quantization of several tensors in one launch gives each tensor's own
+    bytes and scales (formats mixed, a ragged row count, an empty tensor skipped); the MX
+    gated MLP's inference forward, which uses it, equals its training forward bit for bit."""
+    from bongard_amd import linear
+    g = torch.Generator().manual_seed(3)
+    xs = [torch.randn(300, 2560, generator=g).to(torch.bfloat16).to(gpu),
+          (torch.randn(8192, 4096, generator=g) * 40).to(torch.bfloat16).to(gpu),
+          torch.randn(64, 96, generator=g).to(torch.bfloat16).to(gpu),
+          torch.empty(0, 64, dtype=torch.bfloat16, device=gpu)]
+    xs[2][3, 5] = float("nan")
+    fmts = [ops.E4M3, ops.E5M2, ops.E4M3, ops.E4M3]
+    qs = ops.quantize_mx_many(xs, fmts)
+    for x, q, f in zip(xs[:3], qs, fmts):
+        r = ops.quantize_mx(x, f)
+        assert torch.equal(q.data.view(torch.uint8), r.data.view(torch.uint8))
+        assert torch.equal(q.scales, r.scales)
+    assert qs[3].data.numel() == 0
+    with pytest.raises(RuntimeError):
+        ops.quantize_mx_many([xs[0], torch.zeros(32, 48, dtype=torch.bfloat16, device=gpu)])
+    x = torch.randn(256, 256, generator=g).to(torch.bfloat16).to(gpu)
+    w_gu = (torch.randn(1024, 256, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    w_d = (torch.randn(256, 512, generator=g) * 0.014).to(torch.bfloat16).to(gpu)
+    y_train = linear.Fp8GegluMlpMxFunction.apply(x, w_gu.requires_grad_(), w_d, None, None, 512)
+    with torch.no_grad():
+        y_inf = linear.Fp8GegluMlpMxFunction.apply(x, w_gu, w_d, None, None, 512)
+    assert torch.equal(y_train.detach(), y_inf)

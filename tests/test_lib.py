@@ -96,6 +96,24 @@ def test_quantize_many_rejects_bad_arguments():
     assert rc == 1 and b"meta is NULL" in L.bf8_last_error()
 
 
+def test_quantize_mx_many_rejects_bad_arguments():
+    L = _lib.lib()
+    null = ctypes.c_void_p(0)
+    buf = ctypes.create_string_buffer(1 << 12)
+    ptr = ctypes.c_void_p((ctypes.addressof(buf) + 255) // 256 * 256)
+    ptrs = (ctypes.c_void_p * 2)(ptr, ptr)
+    rows = (ctypes.c_int64 * 2)(32, 32)
+    fm = (ctypes.c_int * 2)(0, 0)
+    rc = L.bf8_quantize_mx_many_bf16(9, ptrs, rows, rows, fm, ptrs, ptrs, null)
+    assert rc == 1 and b"count 9" in L.bf8_last_error()
+    rc = L.bf8_quantize_mx_many_bf16(2, ptrs, rows, (ctypes.c_int64 * 2)(32, 48), fm, ptrs,
+                                     ptrs, null)
+    assert rc == 1 and b"cols % 32" in L.bf8_last_error()
+    rc = L.bf8_quantize_mx_many_bf16(2, ptrs, rows, rows, fm, ptrs, (ctypes.c_void_p * 2)(ptr, null),
+                                     null)
+    assert rc == 1 and b"is NULL" in L.bf8_last_error()
+
+
 def test_quantizing_geglu_and_scale_fold_reject_bad_arguments():
     """The epilogue-quantizing gate/up entries and the delayed scale fold check their
     arguments on the host (no launch): missing H8, a transposed copy with M % 32 != 0,
