@@ -185,7 +185,10 @@ class Fp8LinearMxFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, wq):
         need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        xq = ops.quantize_mx(x, E4M3, rowwise=True, colwise=need_dw)
+        if wq is None and not (need_dx or need_dw):
+            xq, wq = ops.quantize_mx_many([x, weight.detach()])   # inference: one launch
+        else:
+            xq = ops.quantize_mx(x, E4M3, rowwise=True, colwise=need_dw)
         if wq is None:
             wq = quantize_weight_mx(weight, transpose=need_dx)
         y = ops.gemm_mx(xq.data, xq.scales, wq.data, wq.scales)

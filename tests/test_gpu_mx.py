@@ -341,3 +341,7 @@ def test_quantize_mx_many_equals_quantize_mx(gpu):
     with torch.no_grad():
         y_inf = linear.Fp8GegluMlpMxFunction.apply(x, w_gu, w_d, None, None, 512)
     assert torch.equal(y_train.detach(), y_inf)
+    y_train = linear.Fp8LinearMxFunction.apply(x, w_d.t().contiguous().requires_grad_(), None)
+    with torch.no_grad():
+        y_inf = linear.Fp8LinearMxFunction.apply(x, w_d.t().contiguous(), None)
+    assert torch.equal(y_train.detach(), y_inf)
