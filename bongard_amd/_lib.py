@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -39,6 +39,8 @@ SIGNATURES = {
     "bf8_gemm_geglu": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                c_void_p, c_void_p, c_int, c_void_p, c_int64, c_void_p, c_void_p,
                                c_void_p]),
+    "bf8_geglu_partials_elementwise": (c_int64, [c_int64, c_int64]),
+    "bf8_geglu_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "bf8_geglu_bwd_partials": (c_int64, [c_int64, c_int64]),
     "bf8_geglu_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
                               c_void_p]),

@@ -3,6 +3,8 @@
 Usage: ``python -m bongard_amd.build`` (also called by ``__graft_entry__.build()``).
 Every HIP source is compiled for gfx950 only, with packed-fp32 instruction selection
 disabled, into ``bongard_amd/_build/*.o`` and linked into ``bongard_amd/libbongard_fp8.so``.
+First ``csrc/gen_gelu_tables.py`` writes ``_build/gelu_tables.inc``, the gated-GELU tables
+taken from torch's CPU gelu kernels (the arithmetic the reference's bf16 chain runs).
 """
 
 import os
@@ -41,7 +43,7 @@ def hipcc():
 
 def _compile(src, extra):
     obj = OBJ / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{OBJ}", *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
@@ -51,6 +53,10 @@ def _compile(src, extra):
 def build(verbose=False, extra=()):
     """Compile every csrc/*.hip for gfx950 and link the shared library. Returns its path."""
     OBJ.mkdir(exist_ok=True)
+    res = subprocess.run([sys.executable, str(CSRC / "gen_gelu_tables.py"),
+                          str(OBJ / "gelu_tables.inc")], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"gelu table generation failed:\n{res.stdout}\n{res.stderr}")
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")

@@ -276,39 +276,6 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v) {
   return r;
 }
 
-// gelu_tanh(x) = 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
-// the identical x / (1 + exp(-2u)): no cancellation of 1 + tanh(u) for negative x, and
-// two transcendental instructions (v_exp_f32, v_rcp_f32) instead of a libm tanh.
-// gelu_tanh_exp: exp(-2u) = 2^(x (c1 + c2 x^2)) with the constants folded,
-// c1 = -2 sqrt(2/pi) / ln 2, c2 = 0.044715 c1 (x2 = x * x; one FMA and two multiplies).
-__device__ __forceinline__ float gelu_tanh_exp(float x, float x2) {
-  constexpr float kC1 = -2.3022082f;
-  constexpr float kC2 = -0.10294324f;
-  return __builtin_amdgcn_exp2f(x * __builtin_fmaf(x2, kC2, kC1));
-}
-
-__device__ __forceinline__ float gelu_tanh_f32(float x) {
-  return x * __builtin_amdgcn_rcpf(1.0f + gelu_tanh_exp(x, x * x));
-}
-
-// gelu_tanh and its derivative, both from s = 1 / (1 + exp(-2u)) = 0.5 (1 + tanh(u)):
-//   y = x s,   dy/dx = s + 2 x s (1 - s) u',  u' = sqrt(2/pi) (1 + 3 * 0.044715 x^2),
-// with 1 - s = e s (e = exp(-2u)) to avoid cancellation (and 1 - s = 1 where e
-// overflows, so the derivative stays finite for large negative x). y is bit-identical to
-// gelu_tanh_f32(x), so the backward sees the forward's activation.
-__device__ __forceinline__ void gelu_tanh_fwd_bwd(float x, float& y, float& dydx) {
-  const float kBeta = 0.7978845608028654f;
-  const float kKappa = 0.044715f;
-  const float x2 = x * x;
-  const float e = gelu_tanh_exp(x, x2);
-  const float s = __builtin_amdgcn_rcpf(1.0f + e);
-  y = x * s;
-  const float du = kBeta * (1.0f + 3.0f * kKappa * x2);
-  // 1 - s = e s; where exp(-2u) overflows (x below about -10) s is 0 and 1 - s is 1
-  const float oms = e > 1e30f ? 1.0f : s * e;
-  dydx = s + 2.0f * x * (s * oms) * du;
-}
-
 // ---- scale from an amax key --------------------------------------------------------
 // scale = fp32(fp8_max / max(f64(amax), 1e-12)) (f64 division, correctly rounded, then one
 // rounding to fp32: equal to the correctly rounded fp32 quotient since 53 >= 2 * 24 + 2);

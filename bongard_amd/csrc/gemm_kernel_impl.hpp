@@ -23,6 +23,7 @@
 
 #include <type_traits>
 
+#include "gelu.hpp"
 #include "gemm_kernel.hpp"
 
 namespace bf8 {
@@ -38,6 +39,11 @@ constexpr int kThreads = 256;  // four wave64
 constexpr int kGroupM = 8;
 constexpr int kNumXcd = 8;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset that always reads as zero
+
+// LDS bytes a variant needs besides its NS pipeline stages: the gated-GELU epilogue keeps
+// the gelu table (kGeluA) there.
+template <int EPI>
+constexpr int extra_lds() { return EPI == EPI_GEGLU ? kGeluABytes : 0; }
 
 // Buffer resource (4 SGPRs): base, stride 0, `bytes` valid bytes (offsets at or beyond
 // read as zero), raw-buffer flags of gfx9/gfx950.
@@ -347,8 +353,9 @@ gemm_kernel(GemmParams p) {
   constexpr int NH = 2 * (FM + FN);          // 16-byte fragment halves per sub-step
   static_assert(EPI != EPI_GEGLU || FN % 2 == 0, "GEGLU pairs gate and up sub-tiles");
   static_assert(!MX || (BM <= 256 && BN <= 256), "MX scale rows: one dword per lane");
-  static_assert(NS * kStage * T::OCC <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage];
+  constexpr int kTabOff = NS * kStage;       // GEGLU: the gelu table after the stages
+  static_assert((NS * kStage + extra_lds<EPI>()) * T::OCC <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage + extra_lds<EPI>()];
 
   // Dequant scales: read at the start, so their latency hides behind the first loads.
   const float sa = MX ? 1.0f : *p.a_sinv;
@@ -522,6 +529,16 @@ gemm_kernel(GemmParams p) {
   // mid-step wait drains every load instead (the next stage is then the last one issued,
   // or none: the trailing fragment reads of the final step go to a stale slot and are
   // never used). Prologue stages past the end are zero-filled.
+  if constexpr (EPI == EPI_GEGLU) {
+    // the gelu table (10 KB) into LDS ahead of the stage loads, so the prologue's wait for
+    // stage 0 also covers it; wave w copies KB w, w + 4 and, for w < 2, KB w + 8
+    static_assert(kGeluABytes == 10 * 1024, "gelu table copy assumes 10 KB");
+    const i32x4 rt = make_srd(kGeluA, (uint32_t)kGeluABytes);
+    const uint32_t tab = lds_addr(smem + kTabOff);
+    dma16(rt, tab + wid * 1024, lane * 16, wid * 1024);
+    dma16(rt, tab + (wid + 4) * 1024, lane * 16, (wid + 4) * 1024);
+    if (wid < 2) dma16(rt, tab + (wid + 8) * 1024, lane * 16, (wid + 8) * 1024);
+  }
 #pragma unroll
   for (int ls = 0; ls < NS; ++ls) {
 #pragma unroll
@@ -725,6 +742,7 @@ gemm_kernel(GemmParams p) {
     constexpr int CH = HF * 4;  // 16-byte chunks per staged H row
     uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
     const int wave_h0 = n0 + wn * HF * 32;
+    const uint16_t* tab_a = reinterpret_cast<const uint16_t*>(smem + kTabOff);
     uint32_t hkeys = 0;  // packed max of the |H| bf16 keys staged by this lane
     uint32_t hmax = 0;   // the same as one fp32-bit amax key
     auto run_pass = [&](auto pass_tag) {
@@ -734,6 +752,51 @@ gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int col = i * 32 + 8 * q + lcol;
+          if constexpr (pass == 0) {
+            // H of the run's FM rows: bf16 g, u pairs first, then all 4 FM gelu table reads
+            // (independent LDS reads in flight together), then the products. Gates outside
+            // the table (|g| < 2^-16 or >= 8, rare) and NaN products (from non-finite u)
+            // take a wave-uniform slow path.
+            uint32_t gw[2 * FM], uw[2 * FM], iw[2 * FM], tv[4 * FM], aw[2 * FM], w[2 * FM];
+            uint32_t outside = 0;
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+              gw[2 * j] = pack_bf16x2(acc[i][j][4 * q] * ag, acc[i][j][4 * q + 1] * ag);
+              gw[2 * j + 1] = pack_bf16x2(acc[i][j][4 * q + 2] * ag, acc[i][j][4 * q + 3] * ag);
+              uw[2 * j] = pack_bf16x2(acc[i + HF][j][4 * q] * au, acc[i + HF][j][4 * q + 1] * au);
+              uw[2 * j + 1] =
+                  pack_bf16x2(acc[i + HF][j][4 * q + 2] * au, acc[i + HF][j][4 * q + 3] * au);
+            }
+#pragma unroll
+            for (int k = 0; k < 2 * FM; ++k) iw[k] = gelu_index2(gw[k], outside);
+#pragma unroll
+            for (int k = 0; k < 2 * FM; ++k) {
+              tv[2 * k] = tab_a[iw[k] & 0xFFFFu];
+              tv[2 * k + 1] = tab_a[iw[k] >> 16];
+            }
+#pragma unroll
+            for (int k = 0; k < 2 * FM; ++k) aw[k] = tv[2 * k] | (tv[2 * k + 1] << 16);
+            if (__builtin_expect(__any(outside != 0), 0)) {
+#pragma unroll
+              for (int k = 0; k < 2 * FM; ++k)
+                aw[k] = gelu_finish(gw[k], tv[2 * k]) | (gelu_finish(gw[k] >> 16, tv[2 * k + 1]) << 16);
+            }
+            uint32_t bk = 0;  // packed max of the |h| keys of the run
+#pragma unroll
+            for (int k = 0; k < 2 * FM; ++k) {
+              w[k] = pack_bf16x2(bf16_lo(aw[k]) * bf16_lo(uw[k]), bf16_hi(aw[k]) * bf16_hi(uw[k]));
+              bk = pk_max_u16(bk, w[k] & 0x7FFF7FFFu);
+            }
+            if (__builtin_expect(__any(nan_key2(bk)), 0)) {
+#pragma unroll
+              for (int k = 0; k < 2 * FM; ++k) w[k] = nan_ffff_bf16x2(w[k]);
+            }
+            hkeys = pk_max_u16(hkeys, bk);
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+              stage_put<CH>(wbuf, j * 32 + lrow_m, col, make_uint2(w[2 * j], w[2 * j + 1]));
+            continue;
+          }
 #pragma unroll
           for (int j = 0; j < FM; ++j) {
             const float ga[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
@@ -741,18 +804,7 @@ gemm_kernel(GemmParams p) {
             const float ua[4] = {acc[i + HF][j][4 * q], acc[i + HF][j][4 * q + 1],
                                  acc[i + HF][j][4 * q + 2], acc[i + HF][j][4 * q + 3]};
             uint32_t w0, w1;  // packed bf16 pairs (columns 0-1, 2-3 of the run)
-            if constexpr (pass == 0) {
-              const uint32_t g01 = pack_bf16x2(ga[0] * ag, ga[1] * ag);
-              const uint32_t g23 = pack_bf16x2(ga[2] * ag, ga[3] * ag);
-              const uint32_t u01 = pack_bf16x2(ua[0] * au, ua[1] * au);
-              const uint32_t u23 = pack_bf16x2(ua[2] * au, ua[3] * au);
-              const uint32_t l01 = pack_bf16x2(gelu_tanh_f32(bf16_lo(g01)), gelu_tanh_f32(bf16_hi(g01)));
-              const uint32_t l23 = pack_bf16x2(gelu_tanh_f32(bf16_lo(g23)), gelu_tanh_f32(bf16_hi(g23)));
-              w0 = pack_bf16x2(bf16_lo(l01) * bf16_lo(u01), bf16_hi(l01) * bf16_hi(u01));
-              w1 = pack_bf16x2(bf16_lo(l23) * bf16_lo(u23), bf16_hi(l23) * bf16_hi(u23));
-              // |h| keys, both halves of a pair in one packed max
-              hkeys = pk_max_u16(hkeys, pk_max_u16(w0 & 0x7FFF7FFFu, w1 & 0x7FFF7FFFu));
-            } else if constexpr (pass == 1) {
+            if constexpr (pass == 1) {
               w0 = pack_bf16x2(ga[0] * ag, ga[1] * ag);
               w1 = pack_bf16x2(ga[2] * ag, ga[3] * ag);
             } else {
@@ -821,45 +873,48 @@ int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
 
 }  // namespace
 
+// The tile T with one stage fewer when the variant's stages (MX: + 2 KB of scale dwords
+// each) and its extra LDS (the gelu table of the GEGLU epilogue) would overflow the LDS.
+template <class T, int EPI, bool MX>
+struct FitTile {
+  static constexpr int bytes(int ns) {
+    return (ns * ((T::BM + T::BN) * kBK + (MX ? 2048 : 0)) + extra_lds<EPI>()) * T::OCC;
+  }
+  using type = std::conditional_t<bytes(T::NS) <= 160 * 1024, T,
+                                  GemmTile<T::WM, T::WN, T::FM, T::FN, T::NS - 1, T::OCC>>;
+  static_assert(bytes(type::NS) <= 160 * 1024, "stages do not fit the LDS");
+};
+
 template <class T>
 int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
                      hipStream_t stream, bool mx) {
-  if (mx) {
-    // MX block scales (e4m3 operands): each stage also holds 2 KB of scale dwords; a tile
-    // whose stages would then overflow the LDS runs with one stage fewer.
-    constexpr bool kFits = T::NS * ((T::BM + T::BN) * kBK + 2048) * T::OCC <= 160 * 1024;
-    using TM = std::conditional_t<kFits, T,
-                                  GemmTile<T::WM, T::WN, T::FM, T::FN, T::NS - 1, T::OCC>>;
-    static_assert(TM::NS * ((TM::BM + TM::BN) * kBK + 2048) * TM::OCC <= 160 * 1024,
-                  "MX stages do not fit the LDS");
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads);
-    if (epi == EPI_GEGLU) {
-      if constexpr (TM::FN % 2 == 0) {
-        hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_GEGLU, BF8_OUT_BF16, true>), grid, block, 0,
-                           stream, p);
-        return launch_status("gemm_kernel(geglu, mx)");
-      } else {
-        set_error("gemm: tile %dx%d has no gated-GELU variant", T::BM, T::BN);
-        return BF8_EINVAL;
-      }
-    } else if (out_dtype == BF8_OUT_BF16) {
-      hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_BF16, true>), grid, block, 0,
-                         stream, p);
-    } else {
-      hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_F32, true>), grid, block, 0,
-                         stream, p);
-    }
-    return launch_status("gemm_kernel(mx)");
-  }
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads);
   if (epi == EPI_GEGLU) {
     if constexpr (T::FN % 2 == 0) {
-      const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(kThreads);
-      hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI_GEGLU, BF8_OUT_BF16>), grid, block, 0, stream, p);
+      if (mx) {
+        using TG = typename FitTile<T, EPI_GEGLU, true>::type;
+        hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16, true>), grid, block, 0,
+                           stream, p);
+        return launch_status("gemm_kernel(geglu, mx)");
+      }
+      using TG = typename FitTile<T, EPI_GEGLU, false>::type;
+      hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16>), grid, block, 0, stream, p);
       return launch_status("gemm_kernel(geglu)");
     } else {
       set_error("gemm: tile %dx%d has no gated-GELU variant", T::BM, T::BN);
       return BF8_EINVAL;
     }
+  }
+  if (mx) {
+    // MX block scales (e4m3 operands): each stage also holds 2 KB of scale dwords
+    using TM = typename FitTile<T, EPI_LINEAR, true>::type;
+    if (out_dtype == BF8_OUT_BF16)
+      hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_BF16, true>), grid, block, 0,
+                         stream, p);
+    else
+      hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_F32, true>), grid, block, 0,
+                         stream, p);
+    return launch_status("gemm_kernel(mx)");
   }
   if (out_dtype == BF8_OUT_BF16) return launch_typed<T, EPI_LINEAR, BF8_OUT_BF16>(p, fmt_a, fmt_b, stream);
   return launch_typed<T, EPI_LINEAR, BF8_OUT_F32>(p, fmt_a, fmt_b, stream);

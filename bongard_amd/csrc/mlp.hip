@@ -1,25 +1,29 @@
-// Backward of the gated GELU(tanh) between the MLP's gate/up and down projections.
+// The gated GELU(tanh) between the MLP's gate/up and down projections as elementwise
+// kernels: its forward on given pre-activations, and its backward.
 //
 // Forward (bongard/te_linear.py:103): h = bf16(bf16(gelu_tanh(g)) * u) on bf16 g, u.
 // Autograd of that bf16 chain gives, per element:
-//   a   = bf16(gelu_tanh(g))                 (recomputed exactly as the forward kernel)
+//   a   = bf16(gelu_tanh(g))                 (the forward's activation)
 //   d_a = bf16(dh * u)                       (mul backward, grad wrt a)
 //   d_u = bf16(dh * a)                       (mul backward, grad wrt u)
-//   d_g = bf16(d_a * gelu_tanh'(g))          (gelu backward, fp32 inside)
-// (gelu_tanh_fwd_bwd in common.hpp). The kernel is one streaming pass (read dH, g, u;
-// write d_g, d_u) that also writes per-block amax partials of |dGU|, from which the
-// e5m2 cast of dGU derives its scale.
+//   d_g = bf16(d_a * F(g))                   (gelu backward, fp32 factor F of g)
+// a and F come from the tables of gelu.hpp, so every value is bit-identical to torch's CPU
+// chain. Each kernel is one streaming pass that also writes per-block amax partials of its
+// output (|H| or |dGU|), from which the following e4m3 / e5m2 cast derives its scale.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 
 #include "common.hpp"
+#include "gelu.hpp"
 
 namespace bf8 {
 namespace {
 
 constexpr int kNT = 256;
-constexpr int64_t kMaxBlocks = 2048;
+// Every block copies the gelu tables (34 KB) into LDS first, so the streaming grids stay
+// at a few blocks per CU.
+constexpr int64_t kMaxBlocks = 1024;
 
 int64_t bwd_blocks(int64_t M, int64_t I) {
   const int64_t vec = M * I / 8;
@@ -29,23 +33,97 @@ int64_t bwd_blocks(int64_t M, int64_t I) {
 }
 
 
-// The chain for the two elements of one packed bf16 pair (g, u, dh words): d_g, d_u as
-// packed bf16 pairs (NaNs canonical, as torch's bf16 rounding gives them), and the running
-// amax key of |d_g|, |d_u|. Intermediate roundings use the packed RNE conversion.
-__device__ __forceinline__ void geglu_bwd_pair(uint32_t dhw, uint32_t gw, uint32_t uw,
-                                               uint32_t& dg, uint32_t& du, uint32_t& m) {
-  const float x0 = bf16_lo(gw), x1 = bf16_hi(gw);
-  const float u0 = bf16_lo(uw), u1 = bf16_hi(uw);
-  const float d0 = bf16_lo(dhw), d1 = bf16_hi(dhw);
-  float y0, y1, s0, s1;
-  gelu_tanh_fwd_bwd(x0, y0, s0);
-  gelu_tanh_fwd_bwd(x1, y1, s1);
-  const uint32_t a = pack_bf16x2(y0, y1);             // bf16(gelu(g))
-  const uint32_t da = pack_bf16x2(d0 * u0, d1 * u1);   // bf16(dh * u)
-  du = canon_nan_bf16x2(pack_bf16x2(d0 * bf16_lo(a), d1 * bf16_hi(a)));
-  dg = canon_nan_bf16x2(pack_bf16x2(bf16_lo(da) * s0, bf16_hi(da) * s1));
-  const uint32_t kg = dg & 0x7FFF7FFFu, ku = du & 0x7FFF7FFFu;
-  m = max(m, max(max(kg << 16, kg & 0xFFFF0000u), max(ku << 16, ku & 0xFFFF0000u)));
+// The chain for 8 elements (4 packed bf16 pairs of dh, g, u): d_g, d_u as packed bf16
+// pairs (NaNs 0xFFFF) and the running amax key of |d_g|, |d_u|. ta / tf: the LDS copies
+// of the gelu tables; all 16 table reads are issued before any is used, gates outside the
+// tables take a wave-uniform slow path.
+__device__ __forceinline__ void geglu_bwd8(const uint32_t (&dhw)[4], const uint32_t (&gw)[4],
+                                           const uint32_t (&uw)[4], const uint16_t* ta,
+                                           const uint32_t* tf, uint32_t (&dg)[4],
+                                           uint32_t (&du)[4], uint32_t& m) {
+  uint32_t outside = 0, ia[4], jf[4], va[8], vf[8];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    ia[w] = gelu_index2(gw[w], outside);
+    jf[w] = gelu_factor_index2(gw[w], outside);
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    va[2 * w] = ta[ia[w] & 0xFFFFu];
+    va[2 * w + 1] = ta[ia[w] >> 16];
+    vf[2 * w] = tf[jf[w] & 0xFFFFu];
+    vf[2 * w + 1] = tf[jf[w] >> 16];
+  }
+  if (__builtin_expect(__any(outside != 0), 0)) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      va[2 * w] = gelu_finish(gw[w], va[2 * w]);
+      va[2 * w + 1] = gelu_finish(gw[w] >> 16, va[2 * w + 1]);
+      vf[2 * w] = gelu_factor_finish(gw[w], vf[2 * w]);
+      vf[2 * w + 1] = gelu_factor_finish(gw[w] >> 16, vf[2 * w + 1]);
+    }
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float d0 = bf16_lo(dhw[w]), d1 = bf16_hi(dhw[w]);
+    const uint32_t a = va[2 * w] | (va[2 * w + 1] << 16);                          // bf16(gelu(g))
+    const uint32_t da = pack_bf16x2(d0 * bf16_lo(uw[w]), d1 * bf16_hi(uw[w]));    // bf16(dh * u)
+    du[w] = nan_ffff_bf16x2(pack_bf16x2(d0 * bf16_lo(a), d1 * bf16_hi(a)));
+    dg[w] = nan_ffff_bf16x2(pack_bf16x2(bf16_lo(da) * __uint_as_float(vf[2 * w]),
+                                        bf16_hi(da) * __uint_as_float(vf[2 * w + 1])));
+    const uint32_t kg = dg[w] & 0x7FFF7FFFu, ku = du[w] & 0x7FFF7FFFu;
+    m = max(m, max(max(kg << 16, kg & 0xFFFF0000u), max(ku << 16, ku & 0xFFFF0000u)));
+  }
+}
+
+// H for 8 elements (4 packed pairs of g, u), with the table reads issued together.
+__device__ __forceinline__ uint4 geglu_fwd8(uint4 g, uint4 u, const uint16_t* ta) {
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+  uint32_t outside = 0, ia[4], va[8], h[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) ia[w] = gelu_index2(gw[w], outside);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    va[2 * w] = ta[ia[w] & 0xFFFFu];
+    va[2 * w + 1] = ta[ia[w] >> 16];
+  }
+  if (__builtin_expect(__any(outside != 0), 0)) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      va[2 * w] = gelu_finish(gw[w], va[2 * w]);
+      va[2 * w + 1] = gelu_finish(gw[w] >> 16, va[2 * w + 1]);
+    }
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) h[w] = geglu_mul_bf16x2(va[2 * w] | (va[2 * w + 1] << 16), uw[w]);
+  return make_uint4(h[0], h[1], h[2], h[3]);
+}
+
+// H [M, I] = gelu(g) * u from GU [M, 2I] (gate | up), and per-block amax keys of |H|.
+__global__ __launch_bounds__(kNT) void geglu_fwd_kernel(const uint16_t* __restrict__ GU,
+                                                        int64_t M, int64_t I,
+                                                        uint16_t* __restrict__ H,
+                                                        uint32_t* __restrict__ partials) {
+  __shared__ __attribute__((aligned(16))) uint16_t ta[kGeluABytes / 2];
+  load_gelu_tables<kNT>(ta, nullptr);
+  __syncthreads();
+  const int64_t per_row = I / 8;
+  const int64_t nvec = M * per_row;
+  const int64_t stride = (int64_t)gridDim.x * kNT;
+  uint32_t m = 0;
+  for (int64_t v = (int64_t)blockIdx.x * kNT + threadIdx.x; v < nvec; v += stride) {
+    const int64_t row = v / per_row;
+    const int64_t col = (v - row * per_row) * 8;
+    const uint4 g = *reinterpret_cast<const uint4*>(GU + row * 2 * I + col);
+    const uint4 u = *reinterpret_cast<const uint4*>(GU + row * 2 * I + I + col);
+    const uint4 h = geglu_fwd8(g, u, ta);
+    const uint32_t k = pk_max_u16(pk_max_u16(h.x & 0x7FFF7FFFu, h.y & 0x7FFF7FFFu),
+                                  pk_max_u16(h.z & 0x7FFF7FFFu, h.w & 0x7FFF7FFFu));
+    m = max(m, max(k << 16, k & 0xFFFF0000u));
+    *reinterpret_cast<uint4*>(H + row * I + col) = h;
+  }
+  m = block_max_u32<kNT>(m);
+  if (threadIdx.x == 0) partials[blockIdx.x] = m;
 }
 
 __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restrict__ dH,
@@ -53,6 +131,10 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restri
                                                         int64_t M, int64_t I,
                                                         uint16_t* __restrict__ dGU,
                                                         uint32_t* __restrict__ partials) {
+  __shared__ __attribute__((aligned(16))) uint16_t ta[kGeluABytes / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t tf[kGeluFBytes / 4];
+  load_gelu_tables<kNT>(ta, tf);
+  __syncthreads();
   const int64_t per_row = I / 8;
   const int64_t nvec = M * per_row;
   const int64_t stride = (int64_t)gridDim.x * kNT;
@@ -67,8 +149,7 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restri
     const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
     const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
     uint32_t dg[4], du[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) geglu_bwd_pair(dhw[w], gw[w], uw[w], dg[w], du[w], m);
+    geglu_bwd8(dhw, gw, uw, ta, tf, dg, du, m);
     *reinterpret_cast<uint4*>(dGU + row * 2 * I + col) = make_uint4(dg[0], dg[1], dg[2], dg[3]);
     *reinterpret_cast<uint4*>(dGU + row * 2 * I + I + col) = make_uint4(du[0], du[1], du[2], du[3]);
   }
@@ -101,6 +182,9 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_delayed_kernel(
     int64_t n_prev, float* __restrict__ meta_out, uint8_t* __restrict__ out,
     uint8_t* __restrict__ out_t, uint32_t* __restrict__ partials) {
   __shared__ uint32_t stage[kFusedWaves][2][kWaveTileDwords];
+  __shared__ __attribute__((aligned(16))) uint16_t ta[kGeluABytes / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t tf[kGeluFBytes / 4];
+  load_gelu_tables<kNT>(ta, tf);  // the scale step below synchronises the block
   const float scale =
       delayed_scale_block<kNT>(state, len, pos, prev, n_prev, Fp8Max<FMT>::value, meta_out);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -135,8 +219,7 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_delayed_kernel(
         const uint32_t gw[4] = {g[k].x, g[k].y, g[k].z, g[k].w};
         const uint32_t uw[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
         uint32_t dg[4], du[4];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) geglu_bwd_pair(dhw[w], gw[w], uw[w], dg[w], du[w], m);
+        geglu_bwd8(dhw, gw, uw, ta, tf, dg, du, m);
         const uint2 qg = quant8_bf16<FMT>(make_uint4(dg[0], dg[1], dg[2], dg[3]), scale);
         const uint2 qu = quant8_bf16<FMT>(make_uint4(du[0], du[1], du[2], du[3]), scale);
         if (out && r < M) {
@@ -175,6 +258,20 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_delayed_kernel(
 using namespace bf8;
 
 extern "C" {
+
+int64_t bf8_geglu_partials_elementwise(int64_t M, int64_t I) { return bwd_blocks(M, I); }
+
+int bf8_geglu_bf16(const void* GU, int64_t M, int64_t I, void* H, uint32_t* partials,
+                   void* stream) {
+  BF8_CHECK(M >= 0 && I >= 8 && I % 8 == 0, "bf8_geglu_bf16: need I %% 8 == 0 (I=%lld)", (long long)I);
+  BF8_CHECK(GU && H && partials, "bf8_geglu_bf16: NULL pointer");
+  BF8_CHECK((((uintptr_t)GU | (uintptr_t)H) & 15) == 0,
+            "bf8_geglu_bf16: pointers must be 16-byte aligned");
+  const int64_t nb = bwd_blocks(M, I);
+  hipLaunchKernelGGL(geglu_fwd_kernel, dim3((unsigned)nb), dim3(kNT), 0, as_stream(stream),
+                     (const uint16_t*)GU, M, I, (uint16_t*)H, partials);
+  return launch_status("geglu_fwd_kernel");
+}
 
 int64_t bf8_geglu_bwd_partials(int64_t M, int64_t I) { return bwd_blocks(M, I); }
 

@@ -638,6 +638,29 @@ def delayed_scale_fold(state, length, pos, prev_partials, fmt=E4M3, meta_out=Non
     return meta_out
 
 
+def geglu(GU, *, partials=None):
+    """H bf16 [M, I] = gelu_tanh(gate) * up from the bf16 pre-activations GU [M, 2I]
+    (gate | up), bit for bit the reference's bf16 chain, and the per-block amax partials
+    of |H| (for ``cast_partials``)."""
+    _require_gpu(GU)
+    if GU.dtype != torch.bfloat16 or GU.dim() != 2 or GU.shape[1] % 2:
+        raise ValueError(f"geglu: GU must be bf16 [M, 2I] (got {GU.dtype} {tuple(GU.shape)})")
+    GU = GU.contiguous()
+    M, I = GU.shape[0], GU.shape[1] // 2
+    L = _lib.lib()
+    H = torch.empty((M, I), dtype=torch.bfloat16, device=GU.device)
+    count = int(L.bf8_geglu_partials_elementwise(M, I))
+    if partials is None:
+        parts = torch.empty(count, dtype=torch.int32, device=GU.device)
+    else:
+        if partials.numel() < count or partials.dtype != torch.int32:
+            raise ValueError(f"geglu: partials must be int32 with >= {count} entries")
+        parts = partials[:count]
+    _lib.check(L.bf8_geglu_bf16(_ptr(GU), M, I, _ptr(H), _ptr(parts), _stream(GU.device)),
+               "bf8_geglu_bf16")
+    return H, parts
+
+
 def geglu_bwd_partials_count(M, intermediate):
     return int(_lib.lib().bf8_geglu_bwd_partials(int(M), int(intermediate)))
 

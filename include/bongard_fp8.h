@@ -146,8 +146,9 @@ int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt
  * pre-activations kept for the backward) or NULL. h_partials: uint32
  * [bf8_geglu_partials(M, I)] per-tile amax of |H| (fp32 bits), for
  * bf8_cast_partials_bf16. I % 128 == 0.
- * gelu_tanh is evaluated as x / (1 + exp(-2u)), the same function as
- * 0.5 x (1 + tanh(u)) without the cancellation of 1 + tanh(u) for negative x.
+ * bf16(gelu_tanh(g)) is torch's CPU gelu(approximate='tanh') on bf16 bit for bit (a
+ * table over 2^-16 <= |g| < 8 taken from it at build time, closed rules outside), so H
+ * equals the reference chain given g and u; a NaN H is 0xFFFF.
  * ------------------------------------------------------------------------------- */
 int64_t bf8_geglu_partials(int64_t M, int64_t I);
 int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw, int64_t M,
@@ -156,11 +157,25 @@ int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw,
                    uint32_t* h_partials, void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * The gated GELU on its own: H bf16 [M, I] = bf16(bf16(gelu_tanh(g)) * u) from GU bf16
+ * [M, 2I] (gate | up, the bf16 pre-activations), the step between the gate/up and down
+ * GEMMs of TEMLP.forward, F.gelu(gate, approximate='tanh') * up (bongard/te_linear.py:103),
+ * for pre-activations produced without the fused epilogue. Per-block amax partials of |H|
+ * go to partials [bf8_geglu_partials_elementwise(M, I)] (for bf8_cast_partials_bf16).
+ * gelu_tanh is torch's CPU function bit for bit (tables taken from it at build time), as
+ * in bf8_gemm_geglu's epilogue; NaN results are 0xFFFF. I % 8 == 0, 16-byte aligned.
+ * ------------------------------------------------------------------------------- */
+int64_t bf8_geglu_partials_elementwise(int64_t M, int64_t I);
+int bf8_geglu_bf16(const void* GU, int64_t M, int64_t I, void* H, uint32_t* partials,
+                   void* stream);
+
+/* ---------------------------------------------------------------------------------
  * Backward of the gated GELU: given dH bf16 [M, I] and GU bf16 [M, 2I] (from the
  * forward), write dGU bf16 [M, 2I] with
- *   d_gate = bf16(dH * u * gelu'(g)), d_up = bf16(dH * bf16(gelu(g)))
+ *   d_gate = bf16(bf16(dH * u) * gelu'(g)), d_up = bf16(dH * bf16(gelu(g)))
  * following autograd of F.gelu(g, approximate='tanh') * u in bf16
- * (bongard/te_linear.py:103), and per-block amax partials of |dGU| into partials
+ * (bongard/te_linear.py:103) bit for bit (gelu and its derivative factor are torch's CPU
+ * values), and per-block amax partials of |dGU| into partials
  * [bf8_geglu_bwd_partials(M, I)] for its e5m2 cast (bf8_cast_partials_bf16).
  * ------------------------------------------------------------------------------- */
 int64_t bf8_geglu_bwd_partials(int64_t M, int64_t I);

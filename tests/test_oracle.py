@@ -444,3 +444,176 @@ def test_mx_chains_track_the_bf16_products():
                      (out["dwgu"], torch.cat([gu[0].grad, gu[1].grad])), (out["dwd"], gu[2].grad)):
         assert got.shape == ref.shape
         assert (got.double() - ref).norm() / ref.norm() < 0.12
+
+
+# ---- tensorwise chains (torchao tensorwise / TE Float8CurrentScaling HYBRID) -------------
+# linear_fwd_bwd, mlp_forward and mlp_backward restate torchao's tensorwise forward and
+# backward (bongard/float8_training.py:16-22) and TEMLP.forward (bongard/te_linear.py:98-103).
+# Two kinds of check pin them: (1) every output within e4m3 / e5m2 error of fp64 autograd of
+# the unquantized bf16 linear / MLP, on non-square shapes whose tensor roles have scales
+# orders of magnitude apart (x ~ 1 with outliers, W ~ 0.02, dy ~ 1e-3), so a scale taken
+# from the wrong role, a transposed operand or a gate/up mix-up is far outside the bound;
+# (2) inputs whose quantization is exact (power-of-two scales, values on the fp8 grid), where
+# the chains must reproduce the exact products bit for bit and H must equal the Hugging Face
+# T5Gemma2MLP activation on them.
+def _rel(got, ref):
+    return ((got.double() - ref.double()).norm() / ref.double().norm()).item()
+
+
+def _tensorwise_inputs(seed, M=48, K=96, N=80):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[:3]] *= 20.0
+    w = torch.randn(N, K, generator=g) * 0.02
+    dy = torch.randn(M, N, generator=g) * 1e-3
+    return x.to(torch.bfloat16), w.to(torch.bfloat16), dy.to(torch.bfloat16)
+
+
+def test_linear_fwd_bwd_tracks_fp64_autograd():
+    x, w, dy = _tensorwise_inputs(41)
+    y, dx, dw = orc.linear_fwd_bwd(x, w, dy)
+    xr = x.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    yr = xr @ wr.t()
+    yr.backward(dy.double())
+    assert y.shape == yr.shape and dx.shape == xr.shape and dw.shape == wr.shape
+    assert _rel(y, yr.detach()) < 0.05         # e4m3 x e4m3
+    assert _rel(dx, xr.grad) < 0.08            # e5m2 x e4m3
+    assert _rel(dw, wr.grad) < 0.08
+    # the roles' scales differ by orders of magnitude: dividing by the wrong one is far off
+    _, _, xs, _ = orc.quantize(x, E4M3)
+    _, _, ws, _ = orc.quantize(w, E4M3)
+    _, _, ds, _ = orc.quantize(dy, E5M2)
+    logs = sorted(math.log10(float(s)) for s in (xs, ws, ds))
+    assert logs[1] - logs[0] > 1 and logs[2] - logs[1] > 1
+
+
+def _grid_tensor(gen, shape, top, unit):
+    """Integers in [-top, top] times ``unit`` with one element forced to +top * unit, so the
+    amax is top * unit; every value is exactly representable after scaling when top * unit
+    maps to fp8_max by a power of two."""
+    v = torch.randint(-top, top + 1, shape, generator=gen).double()
+    v.view(-1)[0] = top
+    return (v * unit).to(torch.bfloat16)
+
+
+def test_linear_fwd_bwd_exact_on_the_fp8_grid():
+    """amax_x = 7 * 2^-2 = 448 * 2^-8 (scale 2^8), amax_w = 7 * 2^-6 (scale 2^12), amax_dy
+    = 7 * 2^-12 = 57344 * 2^-25 (scale 2^25): every quantization is exact, so y, dx and dw
+    must equal the exact products (all partial sums are exact in fp32 and fp64)."""
+    g = torch.Generator().manual_seed(42)
+    M, K, N = 48, 96, 80
+    x = _grid_tensor(g, (M, K), 7, 2.0 ** -2)
+    w = _grid_tensor(g, (N, K), 7, 2.0 ** -6)
+    dy = _grid_tensor(g, (M, N), 7, 2.0 ** -12)
+    for t, fmt, want in ((x, E4M3, 2.0 ** 8), (w, E4M3, 2.0 ** 12), (dy, E5M2, 2.0 ** 25)):
+        _, _, s, _ = orc.quantize(t, fmt)
+        assert float(s) == want
+    y, dx, dw = orc.linear_fwd_bwd(x, w, dy)
+    assert torch.equal(y, (x.double() @ w.double().t()).float())
+    assert torch.equal(dx, (dy.double() @ w.double()).float())
+    assert torch.equal(dw, (dy.double().t() @ x.double()).float())
+
+
+def _hf_mlp(wg, wu, wd):
+    import types
+
+    from transformers.models.t5gemma2.modeling_t5gemma2 import T5Gemma2MLP
+    cfg = types.SimpleNamespace(hidden_size=wg.shape[1], intermediate_size=wg.shape[0],
+                                hidden_activation="gelu_pytorch_tanh", dropout_rate=0.0)
+    m = T5Gemma2MLP(cfg).to(torch.bfloat16)
+    with torch.no_grad():
+        m.gate_proj.weight.copy_(wg)
+        m.up_proj.weight.copy_(wu)
+        m.down_proj.weight.copy_(wd)
+    return m
+
+
+def test_mlp_forward_exact_on_the_fp8_grid_and_hf_activation():
+    """x, [W_gate; W_up] on the e4m3 grid with power-of-two scales: g and u equal the
+    bf16-rounded exact products of the right halves, and H equals the Hugging Face
+    T5Gemma2MLP activation act_fn(gate_proj(x)) * up_proj(x) bit for bit."""
+    gen = torch.Generator().manual_seed(43)
+    M, K, I = 32, 64, 48
+    x = _grid_tensor(gen, (M, K), 7, 2.0 ** -2)
+    wg = _grid_tensor(gen, (I, K), 7, 2.0 ** -6)
+    wu = _grid_tensor(gen, (I, K), 5, 2.0 ** -6)     # amax of [Wg; Wu] stays 7 * 2^-6
+    wd = (torch.randn(K, I, generator=gen) * 0.02).to(torch.bfloat16)
+    out = orc.mlp_forward(x, wg, wu, wd)
+    assert float(out["x_scale"]) == 2.0 ** 8 and float(out["w_scales"][0]) == 2.0 ** 12
+    assert torch.equal(out["g"], (x.double() @ wg.double().t()).to(torch.bfloat16))
+    assert torch.equal(out["u"], (x.double() @ wu.double().t()).to(torch.bfloat16))
+    m = _hf_mlp(wg, wu, wd)
+    with torch.no_grad():
+        hf_g, hf_u = m.gate_proj(x), m.up_proj(x)
+        hf_h = m.act_fn(hf_g) * hf_u
+    assert torch.equal(hf_g, out["g"]) and torch.equal(hf_u, out["u"])
+    assert torch.equal(out["h"], hf_h)
+    # H's own quantization and the down GEMM: within e4m3 error of the HF bf16 output
+    with torch.no_grad():
+        assert _rel(out["y"], m(x)) < 0.05
+
+
+def test_mlp_chains_track_fp64_autograd():
+    """mlp_forward + mlp_backward against fp64 autograd of the unquantized MLP with the
+    reference's rounding points (g, u, gelu(g), H rounded to bf16): shapes, and every output
+    within the compounded e4m3 / e5m2 error. A gate/up swap, a dgrad on W instead of W^T or
+    a dGU scale on the wrong tensor is far outside these bounds."""
+    gen = torch.Generator().manual_seed(44)
+    M, K, I = 64, 96, 80
+    x = torch.randn(M, K, generator=gen)
+    x[:, :2] *= 20.0
+    x = x.to(torch.bfloat16)
+    wg = (torch.randn(I, K, generator=gen) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(I, K, generator=gen) * 0.05).to(torch.bfloat16)
+    wd = (torch.randn(K, I, generator=gen) * 0.014).to(torch.bfloat16)
+    dy = (torch.randn(M, K, generator=gen) * 1e-3).to(torch.bfloat16)
+    fwd = orc.mlp_forward(x, wg, wu, wd)
+    dx, dwgu, dwd, dgu = orc.mlp_backward(fwd, x, wg, wu, wd, dy)
+    xr = x.double().requires_grad_(True)
+    ws = [t.double().requires_grad_(True) for t in (wg, wu, wd)]
+    gate, up = xr @ ws[0].t(), xr @ ws[1].t()
+    h = F.gelu(gate, approximate="tanh") * up
+    yr = h @ ws[2].t()
+    gate.retain_grad()
+    up.retain_grad()
+    yr.backward(dy.double())
+    assert fwd["y"].shape == yr.shape and dx.shape == xr.shape
+    assert dwgu.shape == (2 * I, K) and dwd.shape == wd.shape and dgu.shape == (M, 2 * I)
+    assert _rel(fwd["g"], gate.detach()) < 0.05 and _rel(fwd["u"], up.detach()) < 0.05
+    assert _rel(fwd["h"], h.detach()) < 0.08
+    assert _rel(fwd["y"], yr.detach()) < 0.10
+    assert _rel(dgu, torch.cat([gate.grad, up.grad], 1)) < 0.12
+    assert _rel(dx, xr.grad) < 0.15
+    assert _rel(dwgu, torch.cat([ws[0].grad, ws[1].grad])) < 0.15
+    assert _rel(dwd, ws[2].grad) < 0.12
+    # split gate/up scales (torchao, split TE): the same chain with one scale per half
+    fwd2 = orc.mlp_forward(x, wg, wu, wd, shared_gate_up_scale=False)
+    assert float(fwd2["w_scales"][0]) != float(fwd2["w_scales"][1])
+    assert _rel(fwd2["y"], yr.detach()) < 0.10
+
+
+def test_mlp_backward_exact_dh_on_the_fp8_grid():
+    """dy and W_down on their fp8 grids with power-of-two scales make dH = dY8 . Wd8 exact:
+    the chain's dGU must equal torch autograd of the HF activation at bf16(dy @ W_down),
+    and dW_down must equal dy^T . H8 / scale_H computed from H's own pinned quantization."""
+    gen = torch.Generator().manual_seed(45)
+    M, K, I = 32, 64, 48
+    x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+    wg = (torch.randn(I, K, generator=gen) * 0.05).to(torch.bfloat16)
+    wu = (torch.randn(I, K, generator=gen) * 0.05).to(torch.bfloat16)
+    wd = _grid_tensor(gen, (K, I), 7, 2.0 ** -6)
+    dy = _grid_tensor(gen, (M, K), 7, 2.0 ** -12)
+    fwd = orc.mlp_forward(x, wg, wu, wd)
+    assert float(fwd["wd_scale"]) == 2.0 ** 12
+    dx, dwgu, dwd, dgu = orc.mlp_backward(fwd, x, wg, wu, wd, dy)
+    dh = (dy.double() @ wd.double()).to(torch.bfloat16)
+    from transformers.activations import ACT2FN
+    gr = fwd["g"].clone().requires_grad_(True)
+    ur = fwd["u"].clone().requires_grad_(True)
+    (ACT2FN["gelu_pytorch_tanh"](gr) * ur).backward(dh)
+    assert torch.equal(dgu, torch.cat([gr.grad, ur.grad], 1))
+    hq, _, hs, _ = orc.quantize(fwd["h"], E4M3)
+    h_deq = hq.view(torch.float8_e4m3fn).double() / float(hs)
+    ref = dy.double().t() @ h_deq
+    assert (dwd.double() - ref).abs().max() <= 1e-6 * ref.abs().max()   # fp32 output rounding
