@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -24,6 +24,8 @@ SIGNATURES = {
                               c_void_p]),
     "bf8_quantize_bf16": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p]),
+    "bf8_quantize_bf16_noalloc": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
+                                          c_void_p, c_void_p]),
     "bf8_quantize_many_partials": (c_int64, [c_int, POINTER(c_int64)]),
     "bf8_quantize_many_bf16": (c_int, [c_int, POINTER(c_void_p), POINTER(c_int64),
                                        POINTER(c_int), POINTER(c_void_p), POINTER(c_void_p),

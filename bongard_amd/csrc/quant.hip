@@ -24,6 +24,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -56,6 +57,9 @@ constexpr int64_t kMaxCastBlocks = 4096;  // 16 blocks per CU (2048 when partial
 // Consumers reduce up to this many partials in every block; a longer list (the gated-GELU
 // GEMM writes one per tile: 5200 at M = 16.6k) is first reduced by a one-block kernel.
 constexpr int64_t kMaxInlinePartials = 2048;
+// Slots of the library-owned scratch of bf8_quantize_bf16_noalloc: the most amax partials
+// any tensor's quantization writes.
+constexpr int64_t kNoAllocSlots = kMaxAmaxBlocks;
 
 int64_t amax_blocks(int64_t n) {
   int64_t per_block = (int64_t)kNT * kVecPerThread * 8;  // bf16 elements per block pass
@@ -488,12 +492,61 @@ __global__ __launch_bounds__(kNT) void cast_many_kernel(ManyArgs a) {
 }  // namespace
 }  // namespace bf8
 
+// ---- library-owned scratch of bf8_quantize_bf16_noalloc ------------------------------
+// The amax partials of the allocation-free quantization live in a file-scope device array
+// (each GPU the library runs on holds its own copy, 8 KB, until the process ends). Host code
+// must not pass `scratch` itself to a kernel (in host code the name is a stand-in, not a
+// device address): the device address is looked up once per device with
+// hipGetSymbolAddress, with that device current, and kept in `g_scratch_ptr`.
+static __device__ __align__(256) uint32_t scratch[bf8::kNoAllocSlots];
+
+namespace bf8 {
+namespace {
+
+constexpr int kMaxDevices = 64;
+uint32_t* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The device address of this GPU's `scratch` (the GPU of `stream`; the current one for the
+// NULL stream), looked up on the first call for that GPU. No memory is allocated.
+int noalloc_scratch(hipStream_t stream, uint32_t** out) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("bf8_quantize_bf16_noalloc: no device for the stream (%s)", hipGetErrorString(e));
+    return BF8_EINVAL;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess || p == nullptr) {
+      set_error("bf8_quantize_bf16_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(e));
+      return BF8_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = static_cast<uint32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return BF8_OK;
+}
+
+}  // namespace
+}  // namespace bf8
+
 using namespace bf8;
 
 extern "C" {
 
 const char* bf8_last_error(void) { return bf8::g_err; }
-int bf8_abi_version(void) { return 11; }
+int bf8_abi_version(void) { return 12; }
 
 int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
 
@@ -577,6 +630,20 @@ int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_
   if (rc) return rc;
   return bf8_cast_partials_bf16(x, rows, cols, partials, amax_blocks(n), fmt, meta, out, out_t,
                                 stream);
+}
+
+int bf8_quantize_bf16_noalloc(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
+                              uint8_t* out_t, float* meta, void* stream) {
+  BF8_CHECK(rows >= 0 && cols >= 0, "bf8_quantize_bf16_noalloc: negative shape");
+  const int64_t need = amax_blocks(rows * cols);
+  BF8_CHECK(need <= kNoAllocSlots,
+            "bf8_quantize_bf16_noalloc: needs %lld amax slots, the library scratch holds %lld",
+            (long long)need, (long long)kNoAllocSlots);
+  uint32_t* partials = nullptr;
+  const int rc = noalloc_scratch(as_stream(stream), &partials);
+  if (rc != BF8_OK) return rc;
+  // the amax pass writes every slot [0, need) that the cast then reads: nothing to clear
+  return bf8_quantize_bf16(x, rows, cols, fmt, out, out_t, meta, partials, stream);
 }
 
 int64_t bf8_quantize_many_partials(int count, const int64_t* n) {

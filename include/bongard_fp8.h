@@ -8,7 +8,8 @@
  *     frees or synchronises, and enqueues its kernels on the given HIP stream
  *     (`stream` is a hipStream_t; NULL means the legacy default stream);
  *   - keeps no mutable global state besides the error message, so calls on different
- *     streams are independent.
+ *     streams are independent (except bf8_quantize_bf16_noalloc, which uses a
+ *     library-owned scratch array per GPU instead of a caller workspace).
  *
  * Formats are OCP FP8: BF8_E4M3 (max 448, no inf, NaN = 0x7F/0xFF) and BF8_E5M2
  * (max 57344, IEEE-like inf/NaN). Payloads are one byte per element.
@@ -93,6 +94,17 @@ int bf8_cast_partials_bf16(const void* x, int64_t rows, int64_t cols, const uint
  * {amax, scale, scale_inv, 0}. partials: uint32 [bf8_amax_partials(rows * cols)]. */
 int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
                       uint8_t* out_t, float* meta, uint32_t* partials, void* stream);
+
+/* bf8_quantize_bf16 without the partials argument: allocates nothing and takes no
+ * workspace. No counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The amax partials live in a library-owned device array of 2048 uint32 slots
+ * (8 KB per GPU, held until the process ends; any tensor needs at most 2048, larger needs
+ * are refused with BF8_EINVAL). The array is shared by every call on a GPU and keeps the
+ * last call's contents, so calls that overlap on one GPU (different streams, or host
+ * threads) race; serialize them. Results equal bf8_quantize_bf16's bit for bit. */
+int bf8_quantize_bf16_noalloc(const void* x, int64_t rows, int64_t cols, int fmt, uint8_t* out,
+                              uint8_t* out_t, float* meta, void* stream);
 
 /* bf8_quantize_bf16 (rowwise output only) of 1-8 tensors in two launches: one amax pass
  * over all of them, one cast pass. Tensor t (x[t]: bf16 [n[t]], out[t]: fp8 [n[t]], both
