@@ -19,6 +19,7 @@ bongard/float8_training.py:16-22, te.Linear under TELinear.forward
 bongard/fused_mlp.py:62-79).
 """
 
+import threading
 from dataclasses import dataclass
 from typing import Optional
 
@@ -34,6 +35,33 @@ class QuantizedWeight:
 
     q: ops.Fp8Tensor
     version: int
+
+
+class _Fp8Function(torch.autograd.Function):
+    """Base of the FP8 autograd functions: remembers whether grad mode was on when the
+    function was applied (torch runs ``forward`` itself with grad mode off)."""
+
+    _grad_at_apply = threading.local()
+
+    @classmethod
+    def apply(cls, *args, **kwargs):
+        tls = _Fp8Function._grad_at_apply
+        prev = getattr(tls, "on", None)
+        tls.on = torch.is_grad_enabled()
+        try:
+            return super().apply(*args, **kwargs)
+        finally:
+            tls.on = prev
+
+
+def _forward_needs(ctx, n):
+    """Which of the first n inputs a backward will need gradients for. Under no_grad /
+    inference_mode no backward runs, whatever the inputs' requires_grad says (autograd
+    still reports it in ``needs_input_grad``), so no transposed copies are made and the
+    inference forwards' shared quantize launches apply to trainable parameters too."""
+    on = getattr(_Fp8Function._grad_at_apply, "on", None)
+    grad = True if on is None else on
+    return tuple(bool(grad and b) for b in ctx.needs_input_grad[:n])
 
 
 def quantize_weight(weight, *, transpose=True, scaler=None):
@@ -59,15 +87,14 @@ def _quantize_input(x, scaler, x_amax, transpose):
     return scaler.quantize(x, rowwise=True, transpose=transpose, producer_count=int(x_amax))
 
 
-class Fp8LinearFunction(torch.autograd.Function):
+class Fp8LinearFunction(_Fp8Function):
     """y = x @ W^T (+ b) in FP8; x: bf16 [M, K] with M % 16 == 0 when grads are needed.
 
     ``scaling``: None (current scaling) or a LinearScaling (delayed scaling)."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, wq, scaling=None):
-        need_dx = ctx.needs_input_grad[0]
-        need_dw = ctx.needs_input_grad[1]
+        need_dx, need_dw = _forward_needs(ctx, 2)
         if scaling is None and wq is None and not (need_dx or need_dw):
             # current scaling, no transposed copies: x and W in one amax + one cast launch
             xq, wq = ops.quantize_many([x, weight.detach()])
@@ -104,7 +131,7 @@ class Fp8LinearFunction(torch.autograd.Function):
 AXISWISE_RECIPES = ("rowwise", "rowwise_with_gw_hp")
 
 
-class Fp8LinearAxiswiseFunction(torch.autograd.Function):
+class Fp8LinearAxiswiseFunction(_Fp8Function):
     """y = x @ W^T (+ b) under torchao's axiswise recipes; x: bf16 [M, K], M % 16 == 0 when
     grads are needed. Every cast is e4m3 with power-of-2 scales (torchao 0.17.0
     Float8LinearConfig.from_recipe_name, round_scales_to_power_of_2=True):
@@ -125,7 +152,7 @@ class Fp8LinearAxiswiseFunction(torch.autograd.Function):
     def forward(ctx, x, weight, bias, recipe):
         if recipe not in AXISWISE_RECIPES:
             raise ValueError(f"axiswise recipe must be one of {AXISWISE_RECIPES}")
-        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        need_dx, need_dw = _forward_needs(ctx, 2)
         hp_wgrad = recipe == "rowwise_with_gw_hp"
         xq = ops.quantize_axiswise(x, E4M3, rowwise=True, colwise=need_dw and not hp_wgrad)
         wq = ops.quantize_axiswise(weight.detach(), E4M3, rowwise=True,
@@ -171,7 +198,7 @@ def quantize_weight_mx(weight, *, transpose=True):
     return ops.quantize_mx(weight.detach(), E4M3, rowwise=True, colwise=transpose)
 
 
-class Fp8LinearMxFunction(torch.autograd.Function):
+class Fp8LinearMxFunction(_Fp8Function):
     """y = x @ W^T under TE's MXFP8BlockScaling (every tensor e4m3 in 32-element blocks
     with E8M0 scales); x: bf16 [M, K] with M % 32 == 0 when grads are needed.
 
@@ -184,7 +211,7 @@ class Fp8LinearMxFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, weight, wq):
-        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        need_dx, need_dw = _forward_needs(ctx, 2)
         if wq is None and not (need_dx or need_dw):
             xq, wq = ops.quantize_mx_many([x, weight.detach()])   # inference: one launch
         else:
@@ -209,7 +236,7 @@ class Fp8LinearMxFunction(torch.autograd.Function):
         return dx, dw, None
 
 
-class Fp8GegluMlpMxFunction(torch.autograd.Function):
+class Fp8GegluMlpMxFunction(_Fp8Function):
     """The gated MLP of :class:`Fp8GegluMlpFunction` under MXFP8 (e4m3 blocks of 32, E8M0
     scales, gradients e4m3 too): gate/up GEMM whose epilogue applies the gated GELU and
     quantizes H in blocks (no tensor-wide amax, no bf16 H in memory), down GEMM; backward through dH, the gelu chain's dGU and
@@ -220,7 +247,7 @@ class Fp8GegluMlpMxFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate):
         I = int(intermediate)
-        need_dx, need_dgu, need_dd = ctx.needs_input_grad[:3]
+        need_dx, need_dgu, need_dd = _forward_needs(ctx, 3)
         train = need_dx or need_dgu or need_dd
         if not train and (gu_q is None or down_q is None):
             # inference: x and the uncached weights in one rowwise launch
@@ -267,7 +294,7 @@ class Fp8GegluMlpMxFunction(torch.autograd.Function):
         return dx, dgu, dd, None, None, None
 
 
-class Fp8GegluMlpFunction(torch.autograd.Function):
+class Fp8GegluMlpFunction(_Fp8Function):
     """y = down(gelu_tanh(x Wg^T) * (x Wu^T)) with every GEMM in FP8.
 
     w_gu: bf16 [2I, K] (gate rows then up rows), w_down: bf16 [K_out, I]. ``gu_q`` and
@@ -283,7 +310,8 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
     def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scaling=None,
                 x_amax=None):
         I = int(intermediate)
-        train = any(ctx.needs_input_grad[:3])
+        need_dx, need_dgu, need_dd = _forward_needs(ctx, 3)
+        train = need_dx or need_dgu or need_dd
         if scaling is not None and split_scales:
             raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
         gs, ds = scaling if scaling is not None else (None, None)
@@ -299,31 +327,32 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
             if down_q is None:
                 down_q = qs[-1]
         else:
-            xq = _quantize_input(x, gs and gs.input, x_amax, ctx.needs_input_grad[1])
+            xq = _quantize_input(x, gs and gs.input, x_amax, need_dgu)
         if gu_q is None:
-            gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=ctx.needs_input_grad[0],
+            gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=need_dx,
                                     scaler=gs and gs.weight)
         stride = 4 if split_scales else 0
         M = xq.rows
         if ds is None:
             H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
                                            w_meta_stride=stride, keep_gu=train)
-            hq = ops.cast_partials(H, hparts, E4M3, rowwise=True,
-                                   transpose=ctx.needs_input_grad[2])
+            hq = ops.cast_partials(H, hparts, E4M3, rowwise=True, transpose=need_dd)
         else:
             count = ops.geglu_partials_count(M, I)
-            transpose = ctx.needs_input_grad[2]
+            transpose = need_dd
             if M % 32 == 0 or not transpose:
                 # H's scale is known before the GEMM: the epilogue casts H (and its
                 # transpose for the down wgrad) itself; no bf16 H round trip
-                def launch(st, length, pos, prev, parts):
-                    meta = ops.delayed_scale_fold(st, length, pos, prev, E4M3)
+                def replay(meta, parts):
                     q, gu, _, _ = ops.gemm_geglu_quant(xq.data, xq.meta, gu_q.data, gu_q.meta,
                                                        I, meta, transpose=transpose,
                                                        keep_gu=train, partials=parts)
                     return q, gu
 
-                hq, GU = ds.input.produce(count, x.device, launch)
+                def launch(st, length, pos, prev, parts):
+                    return replay(ops.delayed_scale_fold(st, length, pos, prev, E4M3), parts)
+
+                hq, GU = ds.input.produce(count, x.device, launch, replay)
             else:
                 H, GU, _ = ops.gemm_geglu(
                     xq.data, xq.meta, gu_q.data, gu_q.meta, I, keep_gu=train,
@@ -333,7 +362,7 @@ class Fp8GegluMlpFunction(torch.autograd.Function):
         h_meta = hq.meta
         if down_q is None:
             down_q = quantize_weight(
-                w_down, transpose=ctx.needs_input_grad[0] or ctx.needs_input_grad[1],
+                w_down, transpose=need_dx or need_dgu,
                 scaler=ds and ds.weight)
         y = ops.gemm(hq.data, E4M3, h_meta, down_q.data, E4M3, down_q.meta)
         ctx.intermediate = I

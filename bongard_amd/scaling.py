@@ -14,12 +14,43 @@ this step's amax partials, which the next quantization of the role folds in. No 
 pre-pass and no host synchronisation are needed.
 """
 
+import weakref
+from collections import deque
+
 import torch
 
 from . import ops
 from .ops import E4M3, E5M2
 
 DEFAULT_HISTORY = 16
+
+
+def checkpoint_region():
+    """``(frame, recomputing)`` of the non-reentrant ``torch.utils.checkpoint`` region the
+    current call runs in: ``frame`` identifies the region (None outside one) and
+    ``recomputing`` is True while backward replays the region's forward. The reference
+    trains with non-reentrant checkpointing of every text layer (bongard/model.py:124-132,
+    234-247), so a delayed-scaling forward runs twice per step: the replay must quantize
+    with the scales of the original call and leave the histories alone. The region is read
+    from the saved-tensor hooks torch.utils.checkpoint installs (its pack hook closes over
+    the region's frame), which must be the innermost such hooks around the FP8 module."""
+    try:
+        hooks = torch._C._autograd._top_saved_tensors_default_hooks(False)
+    except (AttributeError, RuntimeError, TypeError):
+        hooks = None
+    if hooks is not None:
+        pack = hooks[0]
+        name = getattr(pack, "__qualname__", "")
+        code = getattr(pack, "__code__", None)
+        cells = {}
+        if code is not None and pack.__closure__:
+            cells = dict(zip(code.co_freevars, (c.cell_contents for c in pack.__closure__)))
+        if name.startswith("_recomputation_hook"):
+            ref = cells.get("target_frame_ref")
+            return (ref() if ref is not None else None), True
+        if name.startswith("_checkpoint_hook"):
+            return cells.get("frame"), False
+    return None, False
 
 
 class DelayedScaler:
@@ -37,6 +68,9 @@ class DelayedScaler:
         self._bufs = [None, None]
         self._slot = 0        # buffer for this step's partials; the other one is pending
         self._pending = 0     # partial count of the previous step (0: none)
+        # checkpointed forwards: per region, the metas of its calls in call order, which the
+        # region's replay takes back in the same order (dropped with the region)
+        self._records = weakref.WeakKeyDictionary()
 
     def _ensure(self, device):
         if self.state is None:
@@ -59,9 +93,29 @@ class DelayedScaler:
         self._ensure(device)
         return self._buffer(self._slot, count, device)
 
+    def _remember(self, frame, meta):
+        if frame is not None:
+            self._records.setdefault(frame, deque()).append(meta)
+
+    def _recorded_meta(self, frame):
+        calls = self._records.get(frame) if frame is not None else None
+        if not calls:
+            raise RuntimeError(
+                "delayed scaling: a checkpointed forward is replayed but its original call "
+                "recorded no scale (the replayed region differs from the original one)")
+        return calls.popleft()
+
     def quantize(self, x, *, rowwise=True, transpose=False, producer_count=None):
-        """Quantize ``x`` (bf16, flattened to 2-D) with this role's delayed scale."""
+        """Quantize ``x`` (bf16, flattened to 2-D) with this role's delayed scale.
+
+        A replay of a checkpointed forward casts with the scale its original call used and
+        leaves the history, the pending amax partials and the step count unchanged, so the
+        backward sees the original bytes."""
         dev = x.device
+        frame, replay = checkpoint_region()
+        if replay:
+            meta = self._recorded_meta(frame)
+            return ops.cast(x, meta, self.fmt, rowwise=rowwise, transpose=transpose)
         self._ensure(dev)
         rows = x.numel() // x.shape[-1] if x.dim() else 1
         cols = x.shape[-1]
@@ -78,13 +132,23 @@ class DelayedScaler:
             self.recorded += 1
         self._pending = count
         self._slot ^= 1
+        self._remember(frame, q.meta)
         return q
 
-    def produce(self, count, device, launch):
+    def produce(self, count, device, launch, replay=None):
         """Runs a kernel that produces this role's tensor and casts it with the role's
         delayed scale in the same pass: ``launch(state, length, pos, prev_partials,
-        partials_out)`` (the arguments of ``cast_delayed``) returns the FP8 tensor and
-        writes ``count`` amax partials of the new tensor into ``partials_out``."""
+        partials_out)`` (the arguments of ``cast_delayed``) returns the FP8 tensor (or a
+        tuple whose first item is it) and writes ``count`` amax partials of the new tensor
+        into ``partials_out``. A replay of a checkpointed forward calls ``replay(meta,
+        partials_out)`` instead, with the meta of the original call and a throwaway partials
+        buffer, and leaves the role's state unchanged."""
+        frame, again = checkpoint_region()
+        if again:
+            if replay is None:
+                raise RuntimeError("delayed scaling: this producer cannot be replayed")
+            scratch = torch.empty(max(int(count), 1), dtype=torch.int32, device=device)
+            return replay(self._recorded_meta(frame), scratch)
         self._ensure(device)
         out_parts = self._buffer(self._slot, count, device)
         prev = self._bufs[self._slot ^ 1][:self._pending] if self._pending else None
@@ -93,11 +157,27 @@ class DelayedScaler:
             self.recorded += 1
         self._pending = int(count)
         self._slot ^= 1
+        self._remember(frame, (q[0] if isinstance(q, tuple) else q).meta)
         return q
+
+    def fold_pending(self):
+        """Pushes the amax of the last quantization into the history now instead of at the
+        next one (which then has nothing to fold): the scales that follow are the same
+        either way, and the state tensor alone then describes the role completely."""
+        if not self._pending or self.state is None:
+            return
+        prev = self._bufs[self._slot ^ 1][:self._pending]
+        ops.delayed_scale_fold(self.state, self.length, self.recorded % self.length, prev,
+                               self.fmt)
+        self.recorded += 1
+        self._pending = 0
 
     # -- persistence (``_extra_state``) -------------------------------------------------
     def to_tensor(self):
-        """float32 [3 + length + 4] on the CPU: length, amaxes recorded, format, state."""
+        """float32 [3 + length + 4] on the CPU: length, amaxes recorded, format, state (the
+        last quantization's amax folded into the history first, so that a run resumed from
+        this tensor continues with the scales of the uninterrupted one)."""
+        self.fold_pending()
         head = torch.tensor([self.length, self.recorded, self.fmt], dtype=torch.float32)
         if self.state is None:
             body = _fresh_state_cpu(self.length)

@@ -16,12 +16,13 @@ import torch
 
 from . import ops
 from .ops import E4M3, E5M2
+from .linear import _Fp8Function, _forward_needs
 from .te_linear import Float8CurrentScaling, TELinear, _pad_rows
 
 __all__ = ["project_state_kv"]
 
 
-class _SharedInputFp8Function(torch.autograd.Function):
+class _SharedInputFp8Function(_Fp8Function):
     """y_i = x @ W_i^T for several per-tensor-scaled FP8 projections of one input x
     [M, K] (M % 32 == 0): one e4m3 quantization of x (+ its transposed copy for the
     weight gradients), one GEMM per cached weight; backward per projection as
@@ -29,8 +30,9 @@ class _SharedInputFp8Function(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, wqs, *weights):
-        need_dx = ctx.needs_input_grad[0]
-        need_dw = any(ctx.needs_input_grad[2:])
+        needs = _forward_needs(ctx, len(ctx.needs_input_grad))
+        need_dx = needs[0]
+        need_dw = any(needs[2:])
         xq = ops.quantize(x, E4M3, transpose=need_dw)
         outs = [ops.gemm(xq.data, E4M3, xq.meta, wq.data, E4M3, wq.meta) for wq in wqs]
         ctx.n = len(wqs)

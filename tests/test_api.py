@@ -301,3 +301,31 @@ def test_pack_to_32_rows_need_no_pad_copy():
     flat, length, aligned = te_linear._pad_rows(y)
     assert (length, aligned) == (70, 96) and torch.equal(flat[:70], y)
     assert bool((flat[70:] == 0).all()) and flat.abs().max() == y.abs().max()
+
+
+def test_checkpoint_region_detection_on_cpu():
+    """The delayed scalers tell a checkpointed region's original forward from its replay in
+    backward (torch.utils.checkpoint, non-reentrant), and see neither outside a region."""
+    from torch.utils.checkpoint import checkpoint
+
+    from bongard_amd.scaling import checkpoint_region
+
+    seen = []
+
+    def region(t):
+        seen.append(checkpoint_region())
+        return (t * 2).sin()
+
+    assert checkpoint_region() == (None, False)
+    x = torch.randn(8, requires_grad=True)
+    y = checkpoint(region, x, use_reentrant=False)
+    y.sum().backward()
+    (f0, replay0), (f1, replay1) = seen
+    assert f0 is not None and replay0 is False      # the original forward names its region
+    assert f1 is f0 and replay1 is True             # the replay names the same region
+    seen.clear()
+    y2 = checkpoint(region, x, use_reentrant=False)
+    assert seen[0][0] is not f0                     # another region, another frame
+    y2.sum().backward()
+    region(x)                                       # a plain call: no region
+    assert seen[-1] == (None, False)

@@ -391,28 +391,45 @@ def test_fp8_linears_inside_a_compiled_region(gpu, kind):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-def test_inference_forward_shares_quantize_launches(gpu):
-    """Under no_grad the FP8 linear and gated MLP quantize x and their weights in shared
-    launches (ops.quantize_many); the output is bit-identical to the training forward's,
-    which quantizes each tensor on its own."""
+def _count_calls(monkeypatch, module, name):
+    calls = []
+    real = getattr(module, name)
+
+    def counted(*a, **k):
+        calls.append(name)
+        return real(*a, **k)
+
+    monkeypatch.setattr(module, name, counted)
+    return calls
+
+
+def test_inference_forward_shares_quantize_launches(gpu, monkeypatch):
+    """Under no_grad the FP8 linear and gated MLP quantize x and their (trainable) weights in
+    shared launches (ops.quantize_many); the output is bit-identical to the training
+    forward's, which quantizes each tensor on its own with transposed copies."""
     from bongard_amd import linear
+    calls = _count_calls(monkeypatch, ops, "quantize_many")
     g = torch.Generator().manual_seed(5)
     x = torch.randn(300, 256, generator=g).to(torch.bfloat16).to(gpu)
-    w = (torch.randn(384, 256, generator=g) * 0.05).to(torch.bfloat16).to(gpu)
-    w_gu = (torch.randn(2 * 512, 256, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
-    w_d = (torch.randn(256, 512, generator=g) * 0.014).to(torch.bfloat16).to(gpu)
+    w = torch.nn.Parameter((torch.randn(384, 256, generator=g) * 0.05).to(torch.bfloat16).to(gpu))
+    w_gu = torch.nn.Parameter((torch.randn(2 * 512, 256, generator=g) * 0.02).to(torch.bfloat16).to(gpu))
+    w_d = torch.nn.Parameter((torch.randn(256, 512, generator=g) * 0.014).to(torch.bfloat16).to(gpu))
     x16 = x[:288]
-    y_train = linear.Fp8LinearFunction.apply(x16, w.requires_grad_(), None, None)
+    y_train = linear.Fp8LinearFunction.apply(x16, w, None, None)
+    assert calls == []                   # training: per-tensor quantization with transposes
     with torch.no_grad():
         y_inf = linear.Fp8LinearFunction.apply(x16, w, None, None)
+    assert calls == ["quantize_many"]
     assert torch.equal(y_train.detach(), y_inf)
-    with torch.no_grad():   # a row count the training path would reject (M % 16 != 0)
+    with torch.inference_mode():         # any row count: no transposed copy is made
         y_odd = linear.Fp8LinearFunction.apply(x, w, None, None)
         xq, wq = ops.quantize(x), ops.quantize(w)
         y_sep = ops.gemm(xq.data, ops.E4M3, xq.meta, wq.data, ops.E4M3, wq.meta)
+    assert calls == ["quantize_many"] * 2
     assert torch.equal(y_odd, y_sep)
-    y_train = linear.Fp8GegluMlpFunction.apply(x16, w_gu.requires_grad_(), w_d, None, None,
-                                               512, False)
+    y_train = linear.Fp8GegluMlpFunction.apply(x16, w_gu, w_d, None, None, 512, False)
+    assert len(calls) == 2
     with torch.no_grad():
         y_inf = linear.Fp8GegluMlpFunction.apply(x16, w_gu, w_d, None, None, 512, False)
+    assert len(calls) == 3
     assert torch.equal(y_train.detach(), y_inf)

@@ -314,7 +314,7 @@ def test_gemm_mx_every_tile(gpu, monkeypatch, tile):
     _mx_gemm_case(gpu, 300, 392, 544, seed=17)
 
 
-def test_quantize_mx_many_equals_quantize_mx(gpu):
+def test_quantize_mx_many_equals_quantize_mx(gpu, monkeypatch):
     """Rowwise MX quantization of several tensors in one launch gives each tensor's own
     bytes and scales (formats mixed, a ragged row count, an empty tensor skipped); the MX
     gated MLP's inference forward, which uses it, equals its training forward bit for bit."""
@@ -334,14 +334,28 @@ def test_quantize_mx_many_equals_quantize_mx(gpu):
     assert qs[3].data.numel() == 0
     with pytest.raises(RuntimeError):
         ops.quantize_mx_many([xs[0], torch.zeros(32, 48, dtype=torch.bfloat16, device=gpu)])
+    # the inference forwards (no_grad) of the MX MLP and linear on trainable weights take
+    # the shared launch; their outputs equal the training forwards' bit for bit
+    calls = []
+    real = ops.quantize_mx_many
+
+    def counted(*a, **k):
+        calls.append(1)
+        return real(*a, **k)
+
+    monkeypatch.setattr(ops, "quantize_mx_many", counted)
     x = torch.randn(256, 256, generator=g).to(torch.bfloat16).to(gpu)
-    w_gu = (torch.randn(1024, 256, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
-    w_d = (torch.randn(256, 512, generator=g) * 0.014).to(torch.bfloat16).to(gpu)
-    y_train = linear.Fp8GegluMlpMxFunction.apply(x, w_gu.requires_grad_(), w_d, None, None, 512)
+    w_gu = torch.nn.Parameter((torch.randn(1024, 256, generator=g) * 0.02).to(torch.bfloat16).to(gpu))
+    w_d = torch.nn.Parameter((torch.randn(256, 512, generator=g) * 0.014).to(torch.bfloat16).to(gpu))
+    y_train = linear.Fp8GegluMlpMxFunction.apply(x, w_gu, w_d, None, None, 512)
+    assert len(calls) == 0
     with torch.no_grad():
         y_inf = linear.Fp8GegluMlpMxFunction.apply(x, w_gu, w_d, None, None, 512)
+    assert len(calls) == 1
     assert torch.equal(y_train.detach(), y_inf)
-    y_train = linear.Fp8LinearMxFunction.apply(x, w_d.t().contiguous().requires_grad_(), None)
+    w_o = torch.nn.Parameter(w_d.detach().t().contiguous())
+    y_train = linear.Fp8LinearMxFunction.apply(x, w_o, None)
     with torch.no_grad():
-        y_inf = linear.Fp8LinearMxFunction.apply(x, w_d.t().contiguous(), None)
+        y_inf = linear.Fp8LinearMxFunction.apply(x, w_o, None)
+    assert len(calls) == 2
     assert torch.equal(y_train.detach(), y_inf)
