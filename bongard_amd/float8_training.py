@@ -20,6 +20,7 @@ from dataclasses import dataclass, replace
 import torch
 from torch.nn import functional as F
 
+from . import custom_ops as _custom_ops
 from . import linear as _linear
 
 RECIPES = ("tensorwise", "rowwise", "rowwise_with_gw_hp")
@@ -66,10 +67,10 @@ class Float8Linear(torch.nn.Linear):
         new.config = config
         return new
 
-    # The FP8 kernels are opaque to torch.compile (ctypes calls into the HIP library):
-    # under the reference's regional compile (bongard/model.py:249-281) a compiled layer
-    # runs this forward eagerly, between its compiled pieces, as it does TE's modules.
-    @torch.compiler.disable
+    # Under the reference's regional compile (bongard/model.py:249-281) this forward is
+    # traced: the FP8 linear is then one custom op (bongard_amd.custom_ops) in the compiled
+    # graph; eager calls take the autograd function directly (less dispatch overhead).
+    # Both run the same kernels, so compiled and eager results are bit-identical.
     def forward(self, inputs):
         if inputs.device.type != "cuda":
             raise RuntimeError("FP8 training forward needs the MI355X device (no CPU emulation)")
@@ -84,7 +85,9 @@ class Float8Linear(torch.nn.Linear):
             flat = F.pad(flat, (0, 0, 0, aligned - length))
         weight = self.weight if self.weight.dtype == torch.bfloat16 else self.weight.to(torch.bfloat16)
         bias = None if self.bias is None else self.bias.to(torch.bfloat16)
-        if self.config.recipe == "tensorwise":
+        if torch.compiler.is_compiling():
+            out = _custom_ops.fp8_linear(flat, weight, bias, self.config.recipe)
+        elif self.config.recipe == "tensorwise":
             out = _linear.Fp8LinearFunction.apply(flat, weight, bias, None)
         else:
             out = _linear.Fp8LinearAxiswiseFunction.apply(flat, weight, bias, self.config.recipe)

@@ -87,6 +87,36 @@ def _quantize_input(x, scaler, x_amax, transpose):
     return scaler.quantize(x, rowwise=True, transpose=transpose, producer_count=int(x_amax))
 
 
+def linear_forward(x, weight, bias, wq, scaling, need_dx, need_dw):
+    """Tensorwise FP8 linear forward: ``(y, (x8t, x_meta, w8t, w_meta))``, the transposed
+    copies None where no gradient needs them. ``wq``: a cached quantized weight or None;
+    ``scaling``: None (current scaling) or a LinearScaling (delayed scaling)."""
+    if scaling is None and wq is None and not (need_dx or need_dw):
+        # current scaling, no transposed copies: x and W in one amax + one cast launch
+        xq, wq = ops.quantize_many([x, weight.detach()])
+    else:
+        xq = _quantize(x, E4M3, scaling and scaling.input, transpose=need_dw)
+    if wq is None:
+        wq = quantize_weight(weight, transpose=need_dx, scaler=scaling and scaling.weight)
+    y = ops.gemm(xq.data, E4M3, xq.meta, wq.data, E4M3, wq.meta, bias=bias)
+    return y, (xq.data_t if need_dw else None, xq.meta, wq.data_t if need_dx else None, wq.meta)
+
+
+def linear_backward(dy, saved, scaling, need_dx, need_dw):
+    """Tensorwise FP8 linear backward: dY in e5m2 (its own scale), dX = dY8 . W8 on W's
+    transposed copy, dW = dY8^T . X8 on the transposed copies of dY and X."""
+    x8t, x_meta, w8t, w_meta = saved
+    dy = dy.contiguous()
+    dyq = _quantize(dy, E5M2, scaling and scaling.grad_output, rowwise=need_dx,
+                    transpose=need_dw)
+    dx = dw = None
+    if need_dx:
+        dx = ops.gemm(dyq.data, E5M2, dyq.meta, w8t, E4M3, w_meta)
+    if need_dw:
+        dw = ops.gemm(dyq.data_t, E5M2, dyq.meta, x8t, E4M3, x_meta)
+    return dx, dw
+
+
 class Fp8LinearFunction(_Fp8Function):
     """y = x @ W^T (+ b) in FP8; x: bf16 [M, K] with M % 16 == 0 when grads are needed.
 
@@ -95,40 +125,59 @@ class Fp8LinearFunction(_Fp8Function):
     @staticmethod
     def forward(ctx, x, weight, bias, wq, scaling=None):
         need_dx, need_dw = _forward_needs(ctx, 2)
-        if scaling is None and wq is None and not (need_dx or need_dw):
-            # current scaling, no transposed copies: x and W in one amax + one cast launch
-            xq, wq = ops.quantize_many([x, weight.detach()])
-        else:
-            xq = _quantize(x, E4M3, scaling and scaling.input, transpose=need_dw)
-        if wq is None:
-            wq = quantize_weight(weight, transpose=need_dx,
-                                 scaler=scaling and scaling.weight)
-        y = ops.gemm(xq.data, E4M3, xq.meta, wq.data, E4M3, wq.meta, bias=bias)
+        y, saved = linear_forward(x, weight, bias, wq, scaling, need_dx, need_dw)
         ctx.scaling = scaling
         ctx.has_bias = bias is not None
-        ctx.save_for_backward(xq.data_t if need_dw else None, xq.meta,
-                              wq.data_t if need_dx else None, wq.meta)
+        ctx.save_for_backward(*saved)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x8t, x_meta, w8t, w_meta = ctx.saved_tensors
         need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        dy = dy.contiguous()
-        scaling = ctx.scaling
-        dyq = _quantize(dy, E5M2, scaling and scaling.grad_output, rowwise=need_dx,
-                        transpose=need_dw)
-        dx = dw = db = None
-        if need_dx:
-            dx = ops.gemm(dyq.data, E5M2, dyq.meta, w8t, E4M3, w_meta)
-        if need_dw:
-            dw = ops.gemm(dyq.data_t, E5M2, dyq.meta, x8t, E4M3, x_meta)
-        if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = dy.sum(0)
+        dx, dw = linear_backward(dy, ctx.saved_tensors, ctx.scaling, need_dx, need_dw)
+        db = dy.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
         return dx, dw, db, None, None
 
 
 AXISWISE_RECIPES = ("rowwise", "rowwise_with_gw_hp")
+
+
+def linear_axiswise_forward(x, weight, bias, recipe, need_dx, need_dw):
+    """Forward of torchao's axiswise recipes (see Fp8LinearAxiswiseFunction): ``(y, saved)``
+    with saved = (x8t, x_col_sinv, w8t, w_col_sinv) for 'rowwise' (None where unneeded)
+    and (x, weight) for 'rowwise_with_gw_hp' (its backward re-quantizes W and keeps dW in
+    high precision)."""
+    if recipe not in AXISWISE_RECIPES:
+        raise ValueError(f"axiswise recipe must be one of {AXISWISE_RECIPES}")
+    hp_wgrad = recipe == "rowwise_with_gw_hp"
+    xq = ops.quantize_axiswise(x, E4M3, rowwise=True, colwise=need_dw and not hp_wgrad)
+    wq = ops.quantize_axiswise(weight.detach(), E4M3, rowwise=True,
+                               colwise=need_dx and not hp_wgrad)
+    y = ops.gemm_axiswise(xq.data, E4M3, xq.row_sinv, wq.data, E4M3, wq.row_sinv, bias=bias)
+    if hp_wgrad:
+        return y, (x if need_dw else None, weight.detach() if need_dx else None)
+    return y, (xq.data_t, xq.col_sinv, wq.data_t, wq.col_sinv)
+
+
+def linear_axiswise_backward(dy, saved, recipe, need_dx, need_dw):
+    dy = dy.contiguous()
+    dx = dw = None
+    if recipe == "rowwise":
+        x8t, x_cs, w8t, w_cs = saved
+        dyq = ops.quantize_axiswise(dy, E4M3, rowwise=need_dx, colwise=need_dw)
+        if need_dx:
+            dx = ops.gemm_axiswise(dyq.data, E4M3, dyq.row_sinv, w8t, E4M3, w_cs)
+        if need_dw:
+            dw = ops.gemm_axiswise(dyq.data_t, E4M3, dyq.col_sinv, x8t, E4M3, x_cs)
+    else:
+        x, weight = saved
+        if need_dx:
+            dyq = ops.quantize_axiswise(dy, E4M3, rowwise=True)
+            wt = ops.quantize(weight, E4M3, rowwise=False, transpose=True, pow2=True)
+            dx = ops.gemm_axiswise(dyq.data, E4M3, dyq.row_sinv, wt.data_t, E4M3, wt.meta[2:3])
+        if need_dw:
+            dw = torch.mm(dy.t().contiguous(), x)
+    return dx, dw
 
 
 class Fp8LinearAxiswiseFunction(_Fp8Function):
@@ -150,45 +199,18 @@ class Fp8LinearAxiswiseFunction(_Fp8Function):
 
     @staticmethod
     def forward(ctx, x, weight, bias, recipe):
-        if recipe not in AXISWISE_RECIPES:
-            raise ValueError(f"axiswise recipe must be one of {AXISWISE_RECIPES}")
         need_dx, need_dw = _forward_needs(ctx, 2)
-        hp_wgrad = recipe == "rowwise_with_gw_hp"
-        xq = ops.quantize_axiswise(x, E4M3, rowwise=True, colwise=need_dw and not hp_wgrad)
-        wq = ops.quantize_axiswise(weight.detach(), E4M3, rowwise=True,
-                                   colwise=need_dx and not hp_wgrad)
-        y = ops.gemm_axiswise(xq.data, E4M3, xq.row_sinv, wq.data, E4M3, wq.row_sinv, bias=bias)
+        y, saved = linear_axiswise_forward(x, weight, bias, recipe, need_dx, need_dw)
         ctx.recipe = recipe
         ctx.has_bias = bias is not None
-        if hp_wgrad:
-            ctx.save_for_backward(x if need_dw else None, weight.detach() if need_dx else None)
-        else:
-            ctx.save_for_backward(xq.data_t, xq.col_sinv, wq.data_t, wq.col_sinv)
+        ctx.save_for_backward(*saved)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        dy = dy.contiguous()
-        dx = dw = db = None
-        if ctx.recipe == "rowwise":
-            x8t, x_cs, w8t, w_cs = ctx.saved_tensors
-            dyq = ops.quantize_axiswise(dy, E4M3, rowwise=need_dx, colwise=need_dw)
-            if need_dx:
-                dx = ops.gemm_axiswise(dyq.data, E4M3, dyq.row_sinv, w8t, E4M3, w_cs)
-            if need_dw:
-                dw = ops.gemm_axiswise(dyq.data_t, E4M3, dyq.col_sinv, x8t, E4M3, x_cs)
-        else:
-            x, weight = ctx.saved_tensors
-            if need_dx:
-                dyq = ops.quantize_axiswise(dy, E4M3, rowwise=True)
-                wt = ops.quantize(weight, E4M3, rowwise=False, transpose=True, pow2=True)
-                dx = ops.gemm_axiswise(dyq.data, E4M3, dyq.row_sinv, wt.data_t, E4M3,
-                                       wt.meta[2:3])
-            if need_dw:
-                dw = torch.mm(dy.t().contiguous(), x)
-        if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = dy.sum(0)
+        dx, dw = linear_axiswise_backward(dy, ctx.saved_tensors, ctx.recipe, need_dx, need_dw)
+        db = dy.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
         return dx, dw, db, None
 
 
@@ -294,6 +316,128 @@ class Fp8GegluMlpMxFunction(_Fp8Function):
         return dx, dgu, dd, None, None, None
 
 
+def mlp_forward(x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scaling, x_amax,
+                needs):
+    """Forward of the FP8 gated MLP (see Fp8GegluMlpFunction): ``(y, saved)`` with saved =
+    (GU, x8t, x_meta, h8t, h_meta, gu8t, gu_meta, d8t, d_meta), the tensors the backward
+    reads (None where no gradient needs them). ``needs``: (dx, dW_gu, dW_down) wanted."""
+    I = int(intermediate)
+    need_dx, need_dgu, need_dd = needs
+    train = need_dx or need_dgu or need_dd
+    if scaling is not None and split_scales:
+        raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
+    gs, ds = scaling if scaling is not None else (None, None)
+    if (scaling is None and x_amax is None and not train and not split_scales
+            and (gu_q is None or down_q is None)):
+        # current-scaling inference: x and the uncached weights in one amax + one cast
+        # launch (the rowwise copies are all the forward needs)
+        ws = [w for w, q in ((w_gu, gu_q), (w_down, down_q)) if q is None]
+        qs = ops.quantize_many([x] + [w.detach() for w in ws])
+        xq = qs[0]
+        if gu_q is None:
+            gu_q = _GateUp(qs[1].data, None, qs[1].meta.view(1, 4))
+        if down_q is None:
+            down_q = qs[-1]
+    else:
+        xq = _quantize_input(x, gs and gs.input, x_amax, need_dgu)
+    if gu_q is None:
+        gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=need_dx,
+                                scaler=gs and gs.weight)
+    stride = 4 if split_scales else 0
+    M = xq.rows
+    if ds is None:
+        H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
+                                       w_meta_stride=stride, keep_gu=train)
+        hq = ops.cast_partials(H, hparts, E4M3, rowwise=True, transpose=need_dd)
+    else:
+        count = ops.geglu_partials_count(M, I)
+        transpose = need_dd
+        if M % 32 == 0 or not transpose:
+            # H's scale is known before the GEMM: the epilogue casts H (and its
+            # transpose for the down wgrad) itself; no bf16 H round trip
+            def replay(meta, parts):
+                q, gu, _, _ = ops.gemm_geglu_quant(xq.data, xq.meta, gu_q.data, gu_q.meta,
+                                                   I, meta, transpose=transpose,
+                                                   keep_gu=train, partials=parts)
+                return q, gu
+
+            def launch(st, length, pos, prev, parts):
+                return replay(ops.delayed_scale_fold(st, length, pos, prev, E4M3), parts)
+
+            hq, GU = ds.input.produce(count, x.device, launch, replay)
+        else:
+            H, GU, _ = ops.gemm_geglu(
+                xq.data, xq.meta, gu_q.data, gu_q.meta, I, keep_gu=train,
+                partials=ds.input.partials_for_producer(count, x.device))
+            hq = ds.input.quantize(H, rowwise=True, transpose=transpose,
+                                   producer_count=count)
+    h_meta = hq.meta
+    if down_q is None:
+        down_q = quantize_weight(
+            w_down, transpose=need_dx or need_dgu,
+            scaler=ds and ds.weight)
+    y = ops.gemm(hq.data, E4M3, h_meta, down_q.data, E4M3, down_q.meta)
+    return y, (GU, xq.data_t, xq.meta, hq.data_t, h_meta, gu_q.data_t, gu_q.meta, down_q.data_t,
+               down_q.meta)
+
+
+def mlp_backward(dy, saved, intermediate, split_scales, scaling, needs):
+    """Backward of the FP8 gated MLP: ``(dx, dW_gu, dW_down)`` (None where not wanted)."""
+    (GU, x8t, x_meta, h8t, h_meta, gu8t, gu_meta, d8t, d_meta) = saved
+    I = int(intermediate)
+    need_dx, need_dgu, need_dd = needs
+    gs, ds = scaling if scaling is not None else (None, None)
+    dy = dy.contiguous()
+    dyq = _quantize(dy, E5M2, ds and ds.grad_output, rowwise=True, transpose=need_dd)
+    dx = dgu = dd = None
+    if need_dd:
+        dd = ops.gemm(dyq.data_t, E5M2, dyq.meta, h8t, E4M3, h_meta)
+    if not (need_dx or need_dgu):
+        return dx, dgu, dd
+    dH = ops.gemm(dyq.data, E5M2, dyq.meta, d8t, E4M3, d_meta)
+    if gs is not None:
+        # delayed scaling: dGU's scale is known already, so the gelu backward writes
+        # fp8 dGU (and its transpose) in the same pass
+        M = dH.shape[0]
+        count = ops.geglu_bwd_delayed_partials_count(M, I)
+        scaler = gs.grad_output
+        dq = scaler.produce(count, dH.device, lambda st, L, pos, prev, parts:
+                            ops.geglu_bwd_delayed(dH, GU, st, L, pos, prev, scaler.fmt,
+                                                  rowwise=need_dx, transpose=need_dgu,
+                                                  partials_out=parts))
+        if need_dx:
+            dx = ops.gemm(dq.data, E5M2, dq.meta, gu8t, E4M3, gu_meta[0])
+        if need_dgu:
+            dgu = ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta)
+        return dx, dgu, dd
+    dGU, gparts = ops.geglu_bwd(dH, GU)
+    if not split_scales:
+        dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=need_dx, transpose=need_dgu)
+        g_meta = dq.meta
+        if need_dx:
+            dx = ops.gemm(dq.data, E5M2, g_meta, gu8t, E4M3, gu_meta[0])
+        if need_dgu:
+            dgu = ops.gemm(dq.data_t, E5M2, g_meta, x8t, E4M3, x_meta)
+    else:
+        # Separate gate/up projections: each gradient has its own e5m2 scale and its
+        # own dgrad GEMM; the input gradient is their bf16 sum (autograd of x used twice).
+        dx_parts, dw_parts = [], []
+        for half in range(2):
+            d_half = dGU[:, half * I:(half + 1) * I].contiguous()
+            dq = ops.quantize(d_half, E5M2, rowwise=need_dx, transpose=need_dgu)
+            if need_dx:
+                dx_parts.append(ops.gemm(dq.data, E5M2, dq.meta,
+                                         gu8t[:, half * I:(half + 1) * I], E4M3,
+                                         gu_meta[half]))
+            if need_dgu:
+                dw_parts.append(ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta))
+        if need_dx:
+            dx = dx_parts[0] + dx_parts[1]
+        if need_dgu:
+            dgu = torch.cat(dw_parts, 0)
+    return dx, dgu, dd
+
+
 class Fp8GegluMlpFunction(_Fp8Function):
     """y = down(gelu_tanh(x Wg^T) * (x Wu^T)) with every GEMM in FP8.
 
@@ -309,123 +453,18 @@ class Fp8GegluMlpFunction(_Fp8Function):
     @staticmethod
     def forward(ctx, x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scaling=None,
                 x_amax=None):
-        I = int(intermediate)
-        need_dx, need_dgu, need_dd = _forward_needs(ctx, 3)
-        train = need_dx or need_dgu or need_dd
-        if scaling is not None and split_scales:
-            raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
-        gs, ds = scaling if scaling is not None else (None, None)
-        if (scaling is None and x_amax is None and not train and not split_scales
-                and (gu_q is None or down_q is None)):
-            # current-scaling inference: x and the uncached weights in one amax + one cast
-            # launch (the rowwise copies are all the forward needs)
-            ws = [w for w, q in ((w_gu, gu_q), (w_down, down_q)) if q is None]
-            qs = ops.quantize_many([x] + [w.detach() for w in ws])
-            xq = qs[0]
-            if gu_q is None:
-                gu_q = _GateUp(qs[1].data, None, qs[1].meta.view(1, 4))
-            if down_q is None:
-                down_q = qs[-1]
-        else:
-            xq = _quantize_input(x, gs and gs.input, x_amax, need_dgu)
-        if gu_q is None:
-            gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=need_dx,
-                                    scaler=gs and gs.weight)
-        stride = 4 if split_scales else 0
-        M = xq.rows
-        if ds is None:
-            H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
-                                           w_meta_stride=stride, keep_gu=train)
-            hq = ops.cast_partials(H, hparts, E4M3, rowwise=True, transpose=need_dd)
-        else:
-            count = ops.geglu_partials_count(M, I)
-            transpose = need_dd
-            if M % 32 == 0 or not transpose:
-                # H's scale is known before the GEMM: the epilogue casts H (and its
-                # transpose for the down wgrad) itself; no bf16 H round trip
-                def replay(meta, parts):
-                    q, gu, _, _ = ops.gemm_geglu_quant(xq.data, xq.meta, gu_q.data, gu_q.meta,
-                                                       I, meta, transpose=transpose,
-                                                       keep_gu=train, partials=parts)
-                    return q, gu
-
-                def launch(st, length, pos, prev, parts):
-                    return replay(ops.delayed_scale_fold(st, length, pos, prev, E4M3), parts)
-
-                hq, GU = ds.input.produce(count, x.device, launch, replay)
-            else:
-                H, GU, _ = ops.gemm_geglu(
-                    xq.data, xq.meta, gu_q.data, gu_q.meta, I, keep_gu=train,
-                    partials=ds.input.partials_for_producer(count, x.device))
-                hq = ds.input.quantize(H, rowwise=True, transpose=transpose,
-                                       producer_count=count)
-        h_meta = hq.meta
-        if down_q is None:
-            down_q = quantize_weight(
-                w_down, transpose=need_dx or need_dgu,
-                scaler=ds and ds.weight)
-        y = ops.gemm(hq.data, E4M3, h_meta, down_q.data, E4M3, down_q.meta)
-        ctx.intermediate = I
+        y, saved = mlp_forward(x, w_gu, w_down, gu_q, down_q, intermediate, split_scales,
+                               scaling, x_amax, _forward_needs(ctx, 3))
+        ctx.intermediate = int(intermediate)
         ctx.split_scales = split_scales
         ctx.scaling = scaling
-        ctx.save_for_backward(GU, xq.data_t, xq.meta, hq.data_t, h_meta, gu_q.data_t,
-                              gu_q.meta, down_q.data_t, down_q.meta)
+        ctx.save_for_backward(*saved)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        (GU, x8t, x_meta, h8t, h_meta, gu8t, gu_meta, d8t, d_meta) = ctx.saved_tensors
-        I = ctx.intermediate
-        need_dx, need_dgu, need_dd = ctx.needs_input_grad[:3]
-        gs, ds = ctx.scaling if ctx.scaling is not None else (None, None)
-        dy = dy.contiguous()
-        dyq = _quantize(dy, E5M2, ds and ds.grad_output, rowwise=True, transpose=need_dd)
-        dx = dgu = dd = None
-        if need_dd:
-            dd = ops.gemm(dyq.data_t, E5M2, dyq.meta, h8t, E4M3, h_meta)
-        if not (need_dx or need_dgu):
-            return dx, dgu, dd, None, None, None, None, None, None
-        dH = ops.gemm(dyq.data, E5M2, dyq.meta, d8t, E4M3, d_meta)
-        if gs is not None:
-            # delayed scaling: dGU's scale is known already, so the gelu backward writes
-            # fp8 dGU (and its transpose) in the same pass
-            M = dH.shape[0]
-            count = ops.geglu_bwd_delayed_partials_count(M, I)
-            scaler = gs.grad_output
-            dq = scaler.produce(count, dH.device, lambda st, L, pos, prev, parts:
-                                ops.geglu_bwd_delayed(dH, GU, st, L, pos, prev, scaler.fmt,
-                                                      rowwise=need_dx, transpose=need_dgu,
-                                                      partials_out=parts))
-            if need_dx:
-                dx = ops.gemm(dq.data, E5M2, dq.meta, gu8t, E4M3, gu_meta[0])
-            if need_dgu:
-                dgu = ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta)
-            return dx, dgu, dd, None, None, None, None, None, None
-        dGU, gparts = ops.geglu_bwd(dH, GU)
-        if not ctx.split_scales:
-            dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=need_dx, transpose=need_dgu)
-            g_meta = dq.meta
-            if need_dx:
-                dx = ops.gemm(dq.data, E5M2, g_meta, gu8t, E4M3, gu_meta[0])
-            if need_dgu:
-                dgu = ops.gemm(dq.data_t, E5M2, g_meta, x8t, E4M3, x_meta)
-        else:
-            # Separate gate/up projections: each gradient has its own e5m2 scale and its
-            # own dgrad GEMM; the input gradient is their bf16 sum (autograd of x used twice).
-            dx_parts, dw_parts = [], []
-            for half in range(2):
-                d_half = dGU[:, half * I:(half + 1) * I].contiguous()
-                dq = ops.quantize(d_half, E5M2, rowwise=need_dx, transpose=need_dgu)
-                if need_dx:
-                    dx_parts.append(ops.gemm(dq.data, E5M2, dq.meta,
-                                             gu8t[:, half * I:(half + 1) * I], E4M3,
-                                             gu_meta[half]))
-                if need_dgu:
-                    dw_parts.append(ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta))
-            if need_dx:
-                dx = dx_parts[0] + dx_parts[1]
-            if need_dgu:
-                dgu = torch.cat(dw_parts, 0)
+        dx, dgu, dd = mlp_backward(dy, ctx.saved_tensors, ctx.intermediate, ctx.split_scales,
+                                   ctx.scaling, tuple(ctx.needs_input_grad[:3]))
         return dx, dgu, dd, None, None, None, None, None, None
 
 
