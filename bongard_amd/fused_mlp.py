@@ -15,8 +15,9 @@ pass (TE LayerNormMLP fuses norm and cast the same way, bongard/fused_mlp.py:25-
 the FP8 gated MLP of bongard_amd.linear.Fp8GegluMlpFunction (fc1 + gated-GELU epilogue,
 H quantized, fc2). fc1 keeps one shared scale for [gate; up], as TE's stacked fc1 weight
 does. Whether TE rounds the norm output to bf16 before its cast is not pinned by anything
-available; this path rounds it (the te_linear chain). The norm's backward recomputes the
-HF formula under autograd (bf16 in, fp32 math).
+available; this path rounds it (the te_linear chain). The norm's backward (dx and the
+weight gradient of the HF formula's autograd, fp32 math) is a kernel as well
+(bf8_rmsnorm_bwd_bf16).
 """
 
 from collections import Counter
@@ -39,7 +40,8 @@ def _rms_norm(x, weight, eps):
 
 class _FusedRMSNorm(torch.autograd.Function):
     """bf16 RMSNorm (zero-centred gamma) whose kernel also writes the amax partials of its
-    output into ``partials``; the backward differentiates :func:`_rms_norm`."""
+    output into ``partials``; the backward is one kernel pass over x and dy for dx plus a
+    fixed-order reduction for the weight gradient (the autograd of :func:`_rms_norm`)."""
 
     @staticmethod
     def forward(ctx, x, weight, eps, partials):
@@ -51,14 +53,9 @@ class _FusedRMSNorm(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x, weight = ctx.saved_tensors
-        with torch.enable_grad():
-            xr = x.detach().requires_grad_(ctx.needs_input_grad[0])
-            wr = weight.detach().requires_grad_(ctx.needs_input_grad[1])
-            y = _rms_norm(xr, wr, ctx.eps)
-            inputs = [t for t in (xr, wr) if t.requires_grad]
-            grads = iter(torch.autograd.grad(y, inputs, dy))
-        dx = next(grads) if ctx.needs_input_grad[0] else None
-        dw = next(grads) if ctx.needs_input_grad[1] else None
+        dx, dw = _ops.rmsnorm_backward(x, dy.contiguous(), weight, ctx.eps, zero_centered=True,
+                                       need_dx=ctx.needs_input_grad[0],
+                                       need_dw=ctx.needs_input_grad[1])
         return dx, dw, None, None
 
 

@@ -729,6 +729,34 @@ def rmsnorm(x, weight, eps, *, zero_centered=True, want_rstd=False, partials=Non
     return y, rstd, parts
 
 
+def rmsnorm_backward(x, dy, weight, eps, *, zero_centered=True, need_dx=True, need_dw=True):
+    """Gradients (dx bf16 [rows, cols] or None, dweight bf16 [cols] or None) of
+    :func:`rmsnorm` for the bf16 gradient dy of its output."""
+    _require_gpu(x, dy, weight)
+    x = _bf16_2d(x)
+    dy = _bf16_2d(dy)
+    rows, cols = x.shape
+    if tuple(dy.shape) != (rows, cols):
+        raise ValueError(f"rmsnorm_backward: dy must be [{rows}, {cols}]")
+    if weight.dtype != torch.bfloat16 or weight.numel() != cols:
+        raise ValueError(f"rmsnorm_backward: weight must be bf16 [{cols}]")
+    if not (need_dx or need_dw):
+        return None, None
+    weight = weight.contiguous()
+    L = _lib.lib()
+    dx = torch.empty_like(x) if need_dx else None
+    dw = torch.empty(cols, dtype=torch.bfloat16, device=x.device) if need_dw else None
+    ws, nbytes = None, 0
+    if need_dw:
+        nbytes = int(L.bf8_rmsnorm_bwd_workspace(rows, cols))
+        ws = gemm_workspace(nbytes, x.device)
+        nbytes = ws.numel()
+    _lib.check(L.bf8_rmsnorm_bwd_bf16(_ptr(x), _ptr(dy), rows, cols, _ptr(weight), float(eps),
+                                      int(bool(zero_centered)), _ptr(dx), _ptr(dw), _ptr(ws),
+                                      nbytes, _stream(x.device)), "bf8_rmsnorm_bwd_bf16")
+    return dx, dw
+
+
 def geglu_bwd_delayed_partials_count(M, intermediate):
     return int(_lib.lib().bf8_geglu_bwd_delayed_partials(int(M), int(intermediate)))
 

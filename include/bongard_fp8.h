@@ -371,6 +371,21 @@ int bf8_rmsnorm_bf16(const void* x, int64_t rows, int64_t cols, const void* gamm
                      int zero_centered, void* y, float* rstd, uint32_t* partials,
                      void* stream);
 
+/* Backward of bf8_rmsnorm_bf16 for the bf16 gradient dy [rows, cols] of y, the autograd of
+ * the fp32 formula above (the backward of TE LayerNormMLP's norm, bongard/fused_mlp.py:25-30,
+ * as FusedMLP trains it): with n = x r, g = f32(dy), dn = g (z + gamma) (z = 1 when
+ * zero_centered, else 0):
+ *   dx = bf16(r (dn - n * sum_j(dn_j n_j) / cols))          per row
+ *   dgamma = bf16(sum over rows of g n)                      per column
+ * r is recomputed as the forward computes it. dx [rows, cols] and dgamma [cols] (bf16) are
+ * each optional (not both NULL); dgamma needs ws: bf8_rmsnorm_bwd_workspace(rows, cols)
+ * bytes of fp32 block partials, added in a fixed order (deterministic). Same shape limits
+ * as the forward. */
+size_t bf8_rmsnorm_bwd_workspace(int64_t rows, int64_t cols);
+int bf8_rmsnorm_bwd_bf16(const void* x, const void* dy, int64_t rows, int64_t cols,
+                         const void* gamma, float eps, int zero_centered, void* dx,
+                         void* dgamma, void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -164,18 +164,25 @@ def test_fused_mlp_train_forward(gpu):
     wg, wu, wd = (m.weight.detach().clone() for m in (mlp.gate_proj, mlp.up_proj, mlp.down_proj))
     nw = norm.weight.detach().clone()
     x = torch.randn(rows, hidden, generator=g).to(torch.bfloat16)
+    dy = (torch.randn(rows, hidden, generator=g) * 1e-3).to(torch.bfloat16)
     f = fused_mlp.FusedMLP(mlp, norm, "fp8").to(gpu).train()
     xg = x.to(gpu).requires_grad_(True)
     y = f(xg)
-    y.float().pow(2).mean().backward()
+    y.backward(dy.to(gpu))
     torch.cuda.synchronize()
-    normed = orc.rmsnorm(x, nw, 1e-6)
-    fwd = orc.mlp_forward(normed, wg, wu, wd)
+    xr = x.clone().requires_grad_(True)
+    nr = nw.clone().requires_grad_(True)
+    normed = orc.rmsnorm(xr, nr, 1e-6)
+    fwd = orc.mlp_forward(normed.detach(), wg, wu, wd)
+    rdn, rdwgu, rdwd, _ = orc.mlp_backward(fwd, normed.detach(), wg, wu, wd, dy)
+    normed.backward(rdn.to(torch.bfloat16))
     # the norm output (a GPU reduction) is itself requantized to e4m3: a second source of
     # legitimate byte flips, hence the backward-sized max bound
     _close_requant(y, fwd["y"], "fused y", max_tol=0.10)
-    assert xg.grad is not None and f.fc1_weight.grad is not None
-    assert f.layer_norm_weight.grad is not None
+    _close_requant(xg.grad, xr.grad, "fused dx", max_tol=0.2)
+    _close_requant(f.fc1_weight.grad, rdwgu, "fused dW_fc1", max_tol=0.2)
+    _close_requant(f.fc2_weight.grad, rdwd, "fused dW_fc2", max_tol=0.2)
+    _close_requant(f.layer_norm_weight.grad, nr.grad, "fused dW_norm", max_tol=0.2)
     assert f.counts["real_tokens"] == rows and f.counts["kernel_tokens"] == 160
     f.eval()
     ref_eval = f._hf_mlp(f._hf_norm(xg.detach()))

@@ -89,3 +89,36 @@ def test_rmsnorm_plain_gamma_and_errors(gpu):
     with pytest.raises(Exception, match="cols"):
         ops.rmsnorm(torch.zeros(4, 8192, dtype=torch.bfloat16, device=gpu),
                     torch.zeros(8192, dtype=torch.bfloat16, device=gpu), 1e-6)
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 520), (333, 2560), (4099, 2560), (64, 4096)])
+def test_rmsnorm_backward_matches_autograd(gpu, rows, cols):
+    """dx and the weight gradient of the fused norm against fp64 autograd of the HF formula
+    on the same bf16 inputs: each within one bf16 ulp (plus 1e-5 of the RMS for the fp32
+    arithmetic), and within the same bar of torch's fp32 CPU autograd (the oracle chain)."""
+    x, w = _inputs(rows, cols, rows + 7 * cols)
+    g = torch.Generator().manual_seed(rows)
+    dy = (torch.randn(rows, cols, generator=g) * 1e-2).to(torch.bfloat16)
+    dx, dw = ops.rmsnorm_backward(x.to(gpu), dy.to(gpu), w.to(gpu), 1e-6)
+    torch.cuda.synchronize()
+    xr = x.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    y = xr * torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + wr)
+    y.backward(dy.double())
+    xc = x.clone().requires_grad_(True)
+    wc = w.clone().requires_grad_(True)
+    orc.rmsnorm(xc, wc, 1e-6).backward(dy)
+    for name, got, ref64, ref32 in (("dx", dx, xr.grad, xc.grad), ("dw", dw, wr.grad, wc.grad)):
+        got = got.cpu().double()
+        rms = ref64.pow(2).mean().sqrt()
+        bound = orc.bf16_ulp(ref64.float()).double() + 1e-5 * rms
+        err64 = (got - ref64).abs()
+        err32 = (got - ref32.double()).abs()
+        print(f"[norm bwd {rows}x{cols} {name}] max err/bound vs fp64 "
+              f"{(err64 / bound).max().item():.2f}, vs torch fp32 "
+              f"{(err32 / (2 * bound)).max().item():.2f}", flush=True)
+        assert bool((err64 <= bound).all()), name
+        assert bool((err32 <= 2 * bound).all()), name
+    dx_only, none = ops.rmsnorm_backward(x.to(gpu), dy.to(gpu), w.to(gpu), 1e-6, need_dw=False)
+    torch.cuda.synchronize()
+    assert none is None and torch.equal(dx_only.cpu(), dx.cpu())
