@@ -32,6 +32,7 @@ enum TileId {
   TILE_192x256,
   TILE_128x64,
   TILE_64x128,
+  TILE_256x128,
   NUM_TILES
 };
 
@@ -55,6 +56,7 @@ constexpr TileInfo kTiles[NUM_TILES] = {
     {192, 256, 1, 9.0, 8.0, "192x256", true},
     {128, 64, 2, 6.5, 0.0, "128x64", true},
     {64, 128, 2, 6.5, 4.0, "64x128", true},
+    {256, 128, 1, 0.1, 0.1, "256x128", true},
 };
 // Gated-GELU plans may not depend on K (the amax partial count is sized from M and I
 // alone); they are costed at a typical 20 K steps (hidden size 2560).
@@ -170,6 +172,7 @@ int launch_tile(const Plan& pl, const GemmParams& p, int epi, int out_dtype, int
     case TILE_192x256: return launch_gemm_tile<Tile192x256>(p, epi, out_dtype, fa, fb, s, mx);
     case TILE_128x64: return launch_gemm_tile<Tile128x64>(p, epi, out_dtype, fa, fb, s, mx);
     case TILE_64x128: return launch_gemm_tile<Tile64x128>(p, epi, out_dtype, fa, fb, s, mx);
+    case TILE_256x128: return launch_gemm_tile<Tile256x128>(p, epi, out_dtype, fa, fb, s, mx);
     default: return launch_gemm_tile<Tile128x128>(p, epi, out_dtype, fa, fb, s, mx);
   }
 }

@@ -65,6 +65,7 @@ using Tile128x128 = GemmTile<2, 2, 2, 2, 4, 1>;
 using Tile192x256 = GemmTile<2, 2, 3, 4, 2, 1>;
 using Tile128x64 = GemmTile<2, 2, 2, 1, 3, 2>;
 using Tile64x128 = GemmTile<2, 2, 1, 2, 3, 2>;
+using Tile256x128 = GemmTile<2, 2, 4, 2, 3, 1>;
 
 // Enqueues the GEMM for tile shape T (EPI_GEGLU: e4m3 x e4m3, bf16 H). Returns a BF8_*
 // status; the host entry points have validated p.

@@ -562,11 +562,14 @@ gemm_kernel(GemmParams p) {
     uint8_t* cur = stage_ptr(ls);
     uint8_t* nxt = stage_ptr(ls + 1);
     __builtin_amdgcn_sched_barrier(0);
+    // the first half's reads sit between its first NR MFMAs, so that they have landed
+    // (their wait precedes the barrier) while the last MFMAs still run
+    constexpr int NR = NM >= 8 ? NM - NM / 4 : NM;
 #pragma unroll
     for (int x = 0; x < NM; ++x) {
       mma_one(f0, x, std::integral_constant<int, 0>{});
 #pragma unroll
-      for (int h = x * NH / NM; h < (x + 1) * NH / NM; ++h) read_one(f1, cur, 1, h);
+      for (int h = x * NH / NR; h < (x + 1) * NH / NR && h < NH; ++h) read_one(f1, cur, 1, h);
       __builtin_amdgcn_sched_barrier(0);
     }
     // stage ls+1 landed (stages ls+2 .. ls+NS-1 may still be in flight)
@@ -615,7 +618,9 @@ gemm_kernel(GemmParams p) {
   const int lrow_m = lane & 31;
   const int lcol = (lane >> 5) * 4;
   // Axiswise scales (a_vec / b_vec): the factor of element (m, n) is a_sinv[m] * b_sinv[n]
-  // (either side a single value when its flag is 0), read here from global memory.
+  // (either side a single value when its flag is 0), read here from global memory. Every
+  // output is fma(acc, factor, bias) with one rounding, written out explicitly so that the
+  // bf16 and fp32 outputs round alike (bf16 = RNE of the fp32 result).
   const bool vec = EPI == EPI_LINEAR && (p.a_vec | p.b_vec);
   float rsa[FM];
 #pragma unroll
@@ -658,10 +663,10 @@ gemm_kernel(GemmParams p) {
 #pragma unroll
           for (int j = 0; j < FM; ++j) {
             uint2 w;
-            w.x = pack_bf16x2(acc[i][j][4 * q + 0] * (rsa[j] * cf[0]) + bias[0],
-                              acc[i][j][4 * q + 1] * (rsa[j] * cf[1]) + bias[1]);
-            w.y = pack_bf16x2(acc[i][j][4 * q + 2] * (rsa[j] * cf[2]) + bias[2],
-                              acc[i][j][4 * q + 3] * (rsa[j] * cf[3]) + bias[3]);
+            w.x = pack_bf16x2(__builtin_fmaf(acc[i][j][4 * q + 0], rsa[j] * cf[0], bias[0]),
+                              __builtin_fmaf(acc[i][j][4 * q + 1], rsa[j] * cf[1], bias[1]));
+            w.y = pack_bf16x2(__builtin_fmaf(acc[i][j][4 * q + 2], rsa[j] * cf[2], bias[2]),
+                              __builtin_fmaf(acc[i][j][4 * q + 3], rsa[j] * cf[3], bias[3]));
             stage_put<CH>(wbuf, j * 32 + lrow_m, col, w);
           }
           continue;
@@ -669,8 +674,10 @@ gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
           uint2 w;
-          w.x = pack_bf16x2(acc[i][j][4 * q + 0] * alpha + bias[0], acc[i][j][4 * q + 1] * alpha + bias[1]);
-          w.y = pack_bf16x2(acc[i][j][4 * q + 2] * alpha + bias[2], acc[i][j][4 * q + 3] * alpha + bias[3]);
+          w.x = pack_bf16x2(__builtin_fmaf(acc[i][j][4 * q + 0], alpha, bias[0]),
+                            __builtin_fmaf(acc[i][j][4 * q + 1], alpha, bias[1]));
+          w.y = pack_bf16x2(__builtin_fmaf(acc[i][j][4 * q + 2], alpha, bias[2]),
+                            __builtin_fmaf(acc[i][j][4 * q + 3], alpha, bias[3]));
           stage_put<CH>(wbuf, j * 32 + lrow_m, col, w);
         }
       }
@@ -715,10 +722,10 @@ gemm_kernel(GemmParams p) {
             if (m >= p.M) continue;
             float* c = cbase + (int64_t)m * p.ldc + n;
             *reinterpret_cast<float4*>(c) = make_float4(
-                acc[i][j][4 * q + 0] * (rsa[j] * cf[0]) + bias[0],
-                acc[i][j][4 * q + 1] * (rsa[j] * cf[1]) + bias[1],
-                acc[i][j][4 * q + 2] * (rsa[j] * cf[2]) + bias[2],
-                acc[i][j][4 * q + 3] * (rsa[j] * cf[3]) + bias[3]);
+                __builtin_fmaf(acc[i][j][4 * q + 0], rsa[j] * cf[0], bias[0]),
+                __builtin_fmaf(acc[i][j][4 * q + 1], rsa[j] * cf[1], bias[1]),
+                __builtin_fmaf(acc[i][j][4 * q + 2], rsa[j] * cf[2], bias[2]),
+                __builtin_fmaf(acc[i][j][4 * q + 3], rsa[j] * cf[3], bias[3]));
           }
           continue;
         }
@@ -728,8 +735,10 @@ gemm_kernel(GemmParams p) {
           if (m >= p.M) continue;
           float* c = cbase + (int64_t)m * p.ldc + n;
           *reinterpret_cast<float4*>(c) =
-              make_float4(acc[i][j][4 * q + 0] * alpha + bias[0], acc[i][j][4 * q + 1] * alpha + bias[1],
-                          acc[i][j][4 * q + 2] * alpha + bias[2], acc[i][j][4 * q + 3] * alpha + bias[3]);
+              make_float4(__builtin_fmaf(acc[i][j][4 * q + 0], alpha, bias[0]),
+                          __builtin_fmaf(acc[i][j][4 * q + 1], alpha, bias[1]),
+                          __builtin_fmaf(acc[i][j][4 * q + 2], alpha, bias[2]),
+                          __builtin_fmaf(acc[i][j][4 * q + 3], alpha, bias[3]));
         }
       }
     }
@@ -880,9 +889,11 @@ struct FitTile {
   static constexpr int bytes(int ns) {
     return (ns * ((T::BM + T::BN) * kBK + (MX ? 2048 : 0)) + extra_lds<EPI>()) * T::OCC;
   }
-  using type = std::conditional_t<bytes(T::NS) <= 160 * 1024, T,
+  // 256 bytes stay free for the epilogue's block reductions
+  static constexpr int kLimit = 160 * 1024 - 256;
+  using type = std::conditional_t<bytes(T::NS) <= kLimit, T,
                                   GemmTile<T::WM, T::WN, T::FM, T::FN, T::NS - 1, T::OCC>>;
-  static_assert(bytes(type::NS) <= 160 * 1024, "stages do not fit the LDS");
+  static_assert(bytes(type::NS) <= kLimit, "stages do not fit the LDS");
 };
 
 template <class T>

@@ -267,7 +267,8 @@ def test_mlp_down_gemm_on_own_h8(gpu):
 # ---- block-tile shapes and split-K -------------------------------------------------------
 # BONGARD_FP8_GEMM_TILE forces the library's plan (read on every call), so each tile shape
 # and the split-K fix-up are checked on shapes with M, N and K tails.
-TILES = ["256x256", "256x160", "160x256", "128x128"]
+TILES = ["256x256", "256x160", "160x256", "128x128", "192x256", "256x128", "128x64",
+         "64x128"]
 
 
 @pytest.mark.parametrize("splits", [1, 3])
@@ -296,7 +297,8 @@ def test_split_k_deterministic(gpu, monkeypatch, tile):
     _assert_fp32_close(outs[0], orc.scaled_mm(ra, sa, 0, rb, sb, 0), what=f"split4 {tile}")
 
 
-@pytest.mark.parametrize("tile", ["256x256", "160x256", "128x128"])
+@pytest.mark.parametrize("tile", ["256x256", "160x256", "128x128", "192x256", "256x128",
+                                  "64x128"])
 def test_geglu_tiles(gpu, monkeypatch, tile):
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", tile)
     _geglu_case(gpu, 300, 384, 528, seed=11)

@@ -123,7 +123,7 @@ def test_gemm_geglu_mx(gpu, M, I, K):
     assert (diff > 0).float().mean().item() <= 0.05
 
 
-GEGLU_TILES = ["256x256", "160x256", "192x256", "128x128", "64x128"]
+GEGLU_TILES = ["256x256", "160x256", "192x256", "128x128", "64x128", "256x128"]
 
 
 @pytest.mark.parametrize("tile", ["auto"] + GEGLU_TILES)
@@ -306,7 +306,7 @@ def test_fused_mlp_mxfp8_fwd_bwd(gpu):
 
 
 @pytest.mark.parametrize("tile", ["256x256", "256x160", "160x256", "128x128", "192x256",
-                                  "128x64", "64x128"])
+                                  "128x64", "64x128", "256x128"])
 def test_gemm_mx_every_tile(gpu, monkeypatch, tile):
     """Every block tile's MX variant (those whose stages would overflow the LDS with the
     scale dwords run with one stage fewer), forced through the tuning override."""
