@@ -4,7 +4,11 @@
     python -m bongard_amd.profile_summary pmc <results.db>
 
 ``trace``: per-kernel call count and average / min / max duration (us) from the
-kernel-dispatch records. ``pmc``: per-kernel, per-counter average value per dispatch.
+kernel-dispatch records, and the average over the kernel's longest run of back-to-back
+dispatches (no other kernel between them): a benchmark that times N launches of one
+kernel between two events produces exactly such a run, so that figure is the one to set
+beside the benchmark's own per-launch average. ``pmc``: per-kernel, per-counter average
+value per dispatch.
 """
 import sqlite3, sys, re
 def short(n):
@@ -25,10 +29,24 @@ def kernel_stats(path):
         d = (e - s) / 1e3
         a = agg.setdefault(short(name), [0, 0.0, 1e18, 0])
         a[0] += 1; a[1] += d; a[2] = min(a[2], d); a[3] = max(a[3], d)
+    # longest run of consecutive dispatches of one kernel, in dispatch-start order
+    runs, prev, cur = {}, None, []
+    for name, s, e in sorted(rows, key=lambda r: r[1]) + [(None, 0, 0)]:
+        k = short(name) if name is not None else None
+        if k != prev and cur:
+            if len(cur) > len(runs.get(prev, [])):
+                runs[prev] = cur
+            cur = []
+        if k is not None:
+            cur.append((e - s) / 1e3)
+        prev = k
     tot = sum(v[1] for v in agg.values())
-    out = [f"{'kernel':70s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'time%':>7s}"]
+    out = [f"{'kernel':70s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'time%':>7s}"
+           f" {'run':>4s} {'run_avg_us':>10s}"]
     for k, v in sorted(agg.items(), key=lambda kv: -kv[1][1]):
-        out.append(f"{k:70s} {v[0]:6d} {v[1]/v[0]:9.2f} {v[2]:9.2f} {v[3]:9.2f} {100*v[1]/tot:7.2f}")
+        r = runs.get(k, [])
+        out.append(f"{k:70s} {v[0]:6d} {v[1]/v[0]:9.2f} {v[2]:9.2f} {v[3]:9.2f} {100*v[1]/tot:7.2f}"
+                   f" {len(r):4d} {sum(r) / max(len(r), 1):10.2f}")
     return "\n".join(out)
 def pmc(path):
     db = sqlite3.connect(path); cur = db.cursor()
