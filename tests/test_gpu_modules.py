@@ -4,13 +4,18 @@ Linear layers (one quantization per operand): forward and gradients within max |
 1% of RMS of the oracle's fp64 dequantized GEMMs (after half a bf16 ulp of output
 rounding).
 
-Gated MLP: H (and in the backward dGU) is re-quantized inside the chain. H agrees with
-the oracle's H to 1-2 bf16 ulps (tanh and accumulation order differ), and where such a
-difference straddles an e4m3 (e5m2) rounding boundary the requantized byte moves by a
-whole fp8 step (6-25% of that element). Those flips are legitimate and sparse, so the
-end-to-end MLP bar is statistical: RMS(err) <= 0.5% of RMS(ref), and max |err| <= 5% of
-RMS(ref) forward, 10% backward (dGU is requantized to e5m2, whose step is twice e4m3's). The strict 1% bar on the MLP's own GEMMs (given its H8 bytes) is checked in
-tests/test_gpu_gemm.py::test_mlp_down_gemm_on_own_h8.
+Gated MLP: H (and in the backward dGU) is re-quantized inside the chain. The gelu chain
+itself is bit-exact (given g and u, H and dGU equal torch's CPU chain bit for bit:
+tests/test_gpu_gemm.py), but the gate/up GEMM accumulates in another order than the
+oracle's CPU matmul, so g and u, and then H, can differ by one bf16 ulp; where that
+straddles an e4m3 (e5m2) rounding boundary the requantized byte moves by a whole fp8 step
+(6-25% of that element). Those flips are legitimate and sparse, so the end-to-end MLP bar
+is statistical: RMS(err) <= 0.5% of RMS(ref) (measured 0.17-0.28%), and max |err| <= 5%
+of RMS(ref) for the TEMLP forward (measured 1.4-3.3%), 10% for its backward and the fused
+forward, 20% for the fused and delayed backwards (dGU is requantized to e5m2, whose step
+is twice e4m3's; measured up to 15%). The strict 1% bar holds for every GEMM given its own
+FP8 inputs (tests/test_gpu_gemm.py::test_mlp_down_gemm_on_own_h8, tests/test_gpu_configs.py
+at the c2-c5 sizes: ~1e-4 of RMS).
 """
 
 import types
