@@ -46,16 +46,20 @@ struct GemmParams {
                           // elements apart (a reduce kernel applies scales and bias)
 };
 
-// A workgroup is four wave64s arranged WM x WN; each wave owns FM x FN MFMA tiles of
-// 32 x 32 outputs, so the block tile is (WM*FM*32) x (WN*FN*32). NS LDS stages of
-// (BM + BN) x 128 bytes are in flight; OCC workgroups share a CU (the register budget
-// per wave is 512 / OCC VGPRs, LDS 160 KB / OCC).
-template <int WM_, int WN_, int FM_, int FN_, int NS_, int OCC_>
+// A workgroup is KG groups of four wave64s; the four waves of a group are arranged
+// WM x WN and each owns FM x FN MFMA tiles of 32 x 32 outputs, so the block tile is
+// (WM*FM*32) x (WN*FN*32). Each group has its own NS LDS stages of (BM + BN) x 128 bytes
+// in flight; with KG = 2 the groups take alternate K steps and add their accumulators
+// before the epilogue (two pipelines per CU for the short K loops of skinny GEMMs). OCC
+// workgroups share a CU (the register budget per wave is 512 / (OCC * KG) VGPRs, LDS
+// 160 KB / OCC).
+template <int WM_, int WN_, int FM_, int FN_, int NS_, int OCC_, int KG_ = 1>
 struct GemmTile {
-  static constexpr int WM = WM_, WN = WN_, FM = FM_, FN = FN_, NS = NS_, OCC = OCC_;
+  static constexpr int WM = WM_, WN = WN_, FM = FM_, FN = FN_, NS = NS_, OCC = OCC_, KG = KG_;
   static constexpr int BM = WM * FM * 32, BN = WN * FN * 32;
-  static_assert(WM * WN == 4, "four waves per workgroup");
-  static_assert(NS >= 2 && NS * (BM + BN) * 128 * OCC <= 160 * 1024, "LDS budget");
+  static_assert(WM * WN == 4, "four waves per group");
+  static_assert(KG == 1 || KG == 2, "one or two K groups");
+  static_assert(NS >= 2 && KG * NS * (BM + BN) * 128 * OCC <= 160 * 1024, "LDS budget");
 };
 
 using Tile256x256 = GemmTile<2, 2, 4, 4, 2, 1>;
@@ -66,6 +70,10 @@ using Tile192x256 = GemmTile<2, 2, 3, 4, 2, 1>;
 using Tile128x64 = GemmTile<2, 2, 2, 1, 3, 2>;
 using Tile64x128 = GemmTile<2, 2, 1, 2, 3, 2>;
 using Tile256x128 = GemmTile<2, 2, 4, 2, 3, 1>;
+// two K groups (skinny GEMMs): 8 waves, alternate K steps
+using Tile128x64k2 = GemmTile<2, 2, 2, 1, 3, 1, 2>;
+using Tile64x128k2 = GemmTile<2, 2, 1, 2, 3, 1, 2>;
+using Tile128x128k2 = GemmTile<2, 2, 2, 2, 2, 1, 2>;
 
 // Enqueues the GEMM for tile shape T (EPI_GEGLU: e4m3 x e4m3, bf16 H). Returns a BF8_*
 // status; the host entry points have validated p.

@@ -338,10 +338,12 @@ struct Frags {
 };
 
 template <class T, int FA, int FB, int EPI, int OUT, bool MX = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(T::OCC, T::OCC))) void
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads * T::KG, kThreads * T::KG),
+                          amdgpu_waves_per_eu(T::OCC * T::KG, T::OCC * T::KG))) void
 gemm_kernel(GemmParams p) {
   constexpr int BM = T::BM, BN = T::BN, FM = T::FM, FN = T::FN, WM = T::WM, NS = T::NS;
+  constexpr int KG = T::KG;
+  static_assert(KG == 1 || (EPI == EPI_LINEAR && !MX), "K groups: linear epilogues only");
   constexpr int kA = BM * kBK;               // A tile bytes per stage
   // MX: each stage also holds the E8M0 block scales of its K step: one dword (4 blocks of
   // 32) per tile row, A rows at kData + 4 r, B rows at kData + 1024 + 4 r (r < 256).
@@ -353,9 +355,9 @@ gemm_kernel(GemmParams p) {
   constexpr int NH = 2 * (FM + FN);          // 16-byte fragment halves per sub-step
   static_assert(EPI != EPI_GEGLU || FN % 2 == 0, "GEGLU pairs gate and up sub-tiles");
   static_assert(!MX || (BM <= 256 && BN <= 256), "MX scale rows: one dword per lane");
-  constexpr int kTabOff = NS * kStage;       // GEGLU: the gelu table after the stages
-  static_assert((NS * kStage + extra_lds<EPI>()) * T::OCC <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage + extra_lds<EPI>()];
+  constexpr int kTabOff = KG * NS * kStage;  // GEGLU: the gelu table after the stages
+  static_assert((KG * NS * kStage + extra_lds<EPI>()) * T::OCC <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[KG * NS * kStage + extra_lds<EPI>()];
 
   // Dequant scales: read at the start, so their latency hides behind the first loads.
   const float sa = MX ? 1.0f : *p.a_sinv;
@@ -376,13 +378,18 @@ gemm_kernel(GemmParams p) {
 
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int wid = t >> 6;
+  const int kg = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane(t >> 8);  // K group (uniform)
+  const int wid = (t >> 6) & 3;           // wave within the group
   const int wm = wid % WM, wn = wid / WM;
   const int wave_m0 = wm * FM * 32;
 
   const int ksteps = (p.K + kBK - 1) / kBK;
   const int kbeg = split * p.ksteps_per_split;
   const int nsteps = min(p.ksteps_per_split, ksteps - kbeg);  // >= 1 by construction
+  // K group kg takes the split's steps kg, kg + KG, ...: its local step ls is global step
+  // kbeg + kg + KG * ls; both groups run niters local steps (the group with one step fewer
+  // runs a zero-filled last one), so their barriers pair up.
+  const int niters = (nsteps + KG - 1) / KG;
 
   const i32x4 ra = make_srd(p.A, (uint32_t)((int64_t)p.M * p.lda));
   const i32x4 rb = make_srd(p.B, (uint32_t)((int64_t)p.N * p.ldb));
@@ -455,11 +462,12 @@ gemm_kernel(GemmParams p) {
       dma4(srd_sb, base + kData + 1024 + wid * 256, kill_sc ? kOob : sb_off, k0 >> 5);
   };
   // Stages past this split's last step are filled with zeros (never read); the partial
-  // last K step of the tensor masks lanes beyond K.
+  // last K step of the tensor masks lanes beyond K. (ls: the group's local step.)
+  auto kstep = [&](int ls) { return kg + KG * ls; };  // the split's step of local step ls
   auto stage_kill = [&](int ls) {
-    return ls >= nsteps || (kbeg + ls == ksteps - 1 && lane_ktail_dead);
+    return kstep(ls) >= nsteps || (kbeg + kstep(ls) == ksteps - 1 && lane_ktail_dead);
   };
-  auto stage_ptr = [&](int ls) { return smem + (ls % NS) * kStage; };
+  auto stage_ptr = [&](int ls) { return smem + (kg * NS + ls % NS) * kStage; };
 
   // B-tile row of each of the wave's n-subtiles; GEGLU puts gate rows in the first half
   // of the B tile and the matching up rows in the second.
@@ -543,7 +551,8 @@ gemm_kernel(GemmParams p) {
   for (int ls = 0; ls < NS; ++ls) {
 #pragma unroll
     for (int x = 0; x < ND; ++x)
-      dma_load(x, smem + ls * kStage, (uint32_t)(kbeg + ls) * kBK, stage_kill(ls), ls >= nsteps);
+      dma_load(x, stage_ptr(ls), (uint32_t)(kbeg + kstep(ls)) * kBK, stage_kill(ls),
+               kstep(ls) >= nsteps);
   }
   // stage 0 landed: the NS-1 later stages (ND loads each) may still be in flight
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 1)) : "memory");
@@ -553,10 +562,10 @@ gemm_kernel(GemmParams p) {
   // agree on both incoming paths
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
-    read_one(f0, smem, 0, h);
+    read_one(f0, stage_ptr(0), 0, h);
     __builtin_amdgcn_sched_barrier(0);
   }
-  read_scales(smem, scA, scB);
+  read_scales(stage_ptr(0), scA, scB);
   auto step = [&](auto with_dma, int ls) __attribute__((always_inline)) {
     constexpr bool kDma = decltype(with_dma)::value;
     uint8_t* cur = stage_ptr(ls);
@@ -579,9 +588,9 @@ gemm_kernel(GemmParams p) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t kn = (uint32_t)(kbeg + ls + NS) * kBK;
+    const uint32_t kn = (uint32_t)(kbeg + kstep(ls + NS)) * kBK;
     const bool killn = stage_kill(ls + NS);
-    const bool killn_sc = ls + NS >= nsteps;
+    const bool killn_sc = kstep(ls + NS) >= nsteps;
     read_scales(nxt, scA_n, scB_n);
 #pragma unroll
     for (int x = 0; x < NM; ++x) {
@@ -603,11 +612,38 @@ gemm_kernel(GemmParams p) {
     }
   };
   int ls = 0;
-  for (; ls < nsteps - NS; ++ls) step(std::true_type{}, ls);
-  for (; ls < nsteps; ++ls) step(std::false_type{}, ls);
+  for (; ls < niters - NS; ++ls) step(std::true_type{}, ls);
+  for (; ls < niters; ++ls) step(std::false_type{}, ls);
   // Let every wave finish with the stages before the epilogue reuses the space.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  if constexpr (KG == 2) {
+    // group 1 hands its accumulators to group 0 through LDS (wave w of each group holds the
+    // same output sub-tile; lane-major dwords, so the 64 lanes of a store hit 64 banks),
+    // then leaves; group 0 adds them and runs the epilogue alone
+    constexpr int kAccBytes = FN * FM * 16 * 64 * 4;  // one wave's accumulators
+    static_assert(4 * kAccBytes <= KG * NS * kStage, "accumulator exchange fits the ring");
+    float* xbuf = reinterpret_cast<float*>(smem + wid * kAccBytes);
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) xbuf[((i * FM + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] += xbuf[((i * FM + j) * 16 + e) * 64 + lane];
+    // the epilogue's staging may overwrite other waves' exchange regions: wait for all of
+    // group 0 (a barrier among its four waves; group 1 has left)
+    __syncthreads();
+  }
 
   // ---- epilogue --------------------------------------------------------------------
   // acc[i][j][r]: n-subtile i, m-subtile j; row m = wave_m0 + j*32 + (lane & 31) of the
@@ -868,7 +904,7 @@ gemm_kernel(GemmParams p) {
 
 template <class T, int EPI, int OUT>
 int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
-  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads);
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads * T::KG);
   if (fa == BF8_E4M3 && fb == BF8_E4M3)
     hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI, OUT>), grid, block, 0, s, p);
   else if (fa == BF8_E5M2 && fb == BF8_E4M3)
@@ -892,14 +928,24 @@ struct FitTile {
   // 256 bytes stay free for the epilogue's block reductions
   static constexpr int kLimit = 160 * 1024 - 256;
   using type = std::conditional_t<bytes(T::NS) <= kLimit, T,
-                                  GemmTile<T::WM, T::WN, T::FM, T::FN, T::NS - 1, T::OCC>>;
+                                  GemmTile<T::WM, T::WN, T::FM, T::FN, T::NS - 1, T::OCC, T::KG>>;
   static_assert(bytes(type::NS) <= kLimit, "stages do not fit the LDS");
 };
 
 template <class T>
 int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
                      hipStream_t stream, bool mx) {
-  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads);
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads * T::KG);
+  if constexpr (T::KG != 1) {
+    if (epi == EPI_GEGLU || mx) {
+      set_error("gemm: tile %dx%d with two K groups has linear non-MX epilogues only", T::BM,
+                T::BN);
+      return BF8_EINVAL;
+    }
+    if (out_dtype == BF8_OUT_BF16)
+      return launch_typed<T, EPI_LINEAR, BF8_OUT_BF16>(p, fmt_a, fmt_b, stream);
+    return launch_typed<T, EPI_LINEAR, BF8_OUT_F32>(p, fmt_a, fmt_b, stream);
+  } else {
   if (epi == EPI_GEGLU) {
     if constexpr (T::FN % 2 == 0) {
       if (mx) {
@@ -929,6 +975,7 @@ int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int
   }
   if (out_dtype == BF8_OUT_BF16) return launch_typed<T, EPI_LINEAR, BF8_OUT_BF16>(p, fmt_a, fmt_b, stream);
   return launch_typed<T, EPI_LINEAR, BF8_OUT_F32>(p, fmt_a, fmt_b, stream);
+  }
 }
 
 }  // namespace bf8

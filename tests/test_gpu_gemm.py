@@ -268,7 +268,7 @@ def test_mlp_down_gemm_on_own_h8(gpu):
 # BONGARD_FP8_GEMM_TILE forces the library's plan (read on every call), so each tile shape
 # and the split-K fix-up are checked on shapes with M, N and K tails.
 TILES = ["256x256", "256x160", "160x256", "128x128", "192x256", "256x128", "128x64",
-         "64x128"]
+         "64x128", "128x64k2", "64x128k2", "128x128k2"]
 
 
 @pytest.mark.parametrize("splits", [1, 3])
