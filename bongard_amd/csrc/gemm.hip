@@ -53,7 +53,7 @@ struct TileInfo {
 // every CU busy, over the tile's FLOP per step).
 constexpr TileInfo kTiles[NUM_TILES] = {
     {256, 256, 1, 9.6, 8.8, "256x256", true},
-    {256, 160, 1, 9.2, 0.0, "256x160", true},
+    {256, 160, 1, 9.2, 8.0, "256x160", true},
     {160, 256, 1, 9.0, 7.6, "160x256", true},
     {128, 128, 1, 8.0, 6.2, "128x128", true},
     {192, 256, 1, 9.0, 8.0, "192x256", true},
@@ -64,6 +64,17 @@ constexpr TileInfo kTiles[NUM_TILES] = {
     {64, 128, 1, 0.1, 0.0, "64x128k2", false},
     {128, 128, 1, 0.1, 0.0, "128x128k2", false},
 };
+// Whether `tile` has a gated-GELU variant for I = N / 2: tiles of 128 or 64 H columns take
+// any I (a multiple of 128); the 256x160 tile (80 gate + 80 up columns, one wave column)
+// needs I % 80 == 0 (its H stores are not column-masked) and has no MX variant (its MX H
+// blocks of 32 columns would straddle tiles).
+bool geglu_tile_ok(int tile, int64_t N, bool mx) {
+  if (kTiles[tile].geglu_rate <= 0) return false;
+  const int hcols = kTiles[tile].bn / 2;
+  if (hcols % 64 == 0) return true;
+  return !mx && (N / 2) % hcols == 0;
+}
+
 // Gated-GELU plans may not depend on K (the amax partial count is sized from M and I
 // alone); they are costed at a typical 20 K steps (hidden size 2560).
 constexpr int kGegluNominalSteps = 20;
@@ -138,7 +149,7 @@ bool env_override(int& tile, int& splits) {
 Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, bool mx = false) {
   const int64_t ksteps = std::max<int64_t>(cdiv(K, kStepBytes), 1);
   int otile, osplits;
-  if (env_override(otile, osplits) && (!geglu || kTiles[otile].geglu_rate > 0) &&
+  if (env_override(otile, osplits) && (!geglu || geglu_tile_ok(otile, N, mx)) &&
       (!mx || kTiles[otile].mx)) {
     Plan p = make_plan(otile, M, N, ksteps, geglu ? 1 : osplits);
     if (p.ws_bytes > ws_avail) p = make_plan(otile, M, N, ksteps, 1);
@@ -148,7 +159,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
   double best_cost = 0;
   bool have = false;
   for (int tile = 0; tile < NUM_TILES; ++tile) {
-    if ((geglu && kTiles[tile].geglu_rate <= 0) || (mx && !kTiles[tile].mx)) continue;
+    if ((geglu && !geglu_tile_ok(tile, N, mx)) || (mx && !kTiles[tile].mx)) continue;
     for (int s = 1; s <= (geglu ? 1 : kMaxSplits); ++s) {
       const Plan p = make_plan(tile, M, N, geglu ? kGegluNominalSteps : ksteps, s);
       if (p.splits != s || (s > 1 && p.kps < kMinStepsPerSplit) || p.ws_bytes > ws_avail)

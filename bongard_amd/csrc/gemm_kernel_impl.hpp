@@ -22,6 +22,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "gelu.hpp"
 #include "gemm_kernel.hpp"
@@ -33,6 +34,17 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// f(std::integral_constant<int, 0>{}) .. f(...<N - 1>{}), unrolled at compile time (the
+// index selects accumulator registers, so it must be a constant).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 constexpr int kBK = 128;       // K bytes per LDS stage
 constexpr int kThreads = 256;  // four wave64
@@ -337,6 +349,25 @@ struct Frags {
   v4u h[NH];
 };
 
+// Where the gated-GELU epilogue finds a gate value and its up partner. A wave's H columns
+// come in runs of 8 (run k: H columns 8k .. 8k+7 of the wave, a lane holding 4 of them,
+// register quad q of an n-subtile). Even FN: the wave's B rows are FN/2 gate subtiles then
+// FN/2 up subtiles (two wave columns side by side), so run k = (subtile k/4, quad k%4)
+// pairs with subtile k/4 + FN/2, same quad. Odd FN (one wave column, WN = 1): the wave's
+// B rows are the tile's, gate rows [0, BN/2) then up rows [BN/2, BN), with BN/2 a multiple
+// of 8 but not of 32, so run k's up rows start at BN/2 + 8k, inside subtile (BN/2+8k)/32 at
+// quad ((BN/2+8k) % 32)/8; the lane half (columns 4h..4h+3 of a quad) is the same on both
+// sides because BN/2 + 8k and 8k differ by a multiple of 8.
+template <int FN, int BN>
+struct GegluRuns {
+  static constexpr bool kOdd = FN % 2 != 0;
+  static constexpr int kRuns = kOdd ? BN / 16 : FN * 2;  // runs of 8 H columns per wave
+  static constexpr int gate_s(int k) { return k / 4; }
+  static constexpr int gate_q(int k) { return k % 4; }
+  static constexpr int up_s(int k) { return kOdd ? (BN / 2 + 8 * k) / 32 : k / 4 + FN / 2; }
+  static constexpr int up_q(int k) { return kOdd ? ((BN / 2 + 8 * k) % 32) / 8 : k % 4; }
+};
+
 template <class T, int FA, int FB, int EPI, int OUT, bool MX = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads * T::KG, kThreads * T::KG),
                           amdgpu_waves_per_eu(T::OCC * T::KG, T::OCC * T::KG))) void
@@ -353,7 +384,10 @@ gemm_kernel(GemmParams p) {
   constexpr int ND = DA + DB + (MX ? 2 : 0);  // loads per wave per stage
   constexpr int NM = FM * FN;                // MFMAs per sub-step
   constexpr int NH = 2 * (FM + FN);          // 16-byte fragment halves per sub-step
-  static_assert(EPI != EPI_GEGLU || FN % 2 == 0, "GEGLU pairs gate and up sub-tiles");
+  static_assert(EPI != EPI_GEGLU || FN % 2 == 0 || (T::WN == 1 && BN % 16 == 0 && BN % 64 != 0),
+                "GEGLU pairs gate and up sub-tiles: even FN, or one wave column whose gate "
+                "and up halves are whole runs of 8 columns");
+  static_assert(!(EPI == EPI_GEGLU && MX && FN % 2 != 0), "MX GEGLU: 32-column H blocks per tile");
   static_assert(!MX || (BM <= 256 && BN <= 256), "MX scale rows: one dword per lane");
   constexpr int kTabOff = KG * NS * kStage;  // GEGLU: the gelu table after the stages
   static_assert((KG * NS * kStage + extra_lds<EPI>()) * T::OCC <= 160 * 1024, "LDS budget");
@@ -464,17 +498,19 @@ gemm_kernel(GemmParams p) {
   // Stages past this split's last step are filled with zeros (never read); the partial
   // last K step of the tensor masks lanes beyond K. (ls: the group's local step.)
   auto kstep = [&](int ls) { return kg + KG * ls; };  // the split's step of local step ls
+  auto gstep = [&](int ls) { return kbeg + kstep(ls); };  // the tensor's K step
   auto stage_kill = [&](int ls) {
-    return kstep(ls) >= nsteps || (kbeg + kstep(ls) == ksteps - 1 && lane_ktail_dead);
+    return kstep(ls) >= nsteps || (gstep(ls) == ksteps - 1 && lane_ktail_dead);
   };
   auto stage_ptr = [&](int ls) { return smem + (kg * NS + ls % NS) * kStage; };
 
   // B-tile row of each of the wave's n-subtiles; GEGLU puts gate rows in the first half
-  // of the B tile and the matching up rows in the second.
+  // of the B tile and the matching up rows in the second (even FN: each wave takes its
+  // share of both halves; odd FN: the one wave column takes every row in order).
   int brow[FN];
 #pragma unroll
   for (int s = 0; s < FN; ++s) {
-    if (EPI == EPI_GEGLU)
+    if (EPI == EPI_GEGLU && FN % 2 == 0)
       brow[s] = (s < FN / 2 ? 0 : BN / 2) + wn * (FN / 2) * 32 + (s % (FN / 2)) * 32;
     else
       brow[s] = wn * FN * 32 + s * 32;
@@ -551,7 +587,7 @@ gemm_kernel(GemmParams p) {
   for (int ls = 0; ls < NS; ++ls) {
 #pragma unroll
     for (int x = 0; x < ND; ++x)
-      dma_load(x, stage_ptr(ls), (uint32_t)(kbeg + kstep(ls)) * kBK, stage_kill(ls),
+      dma_load(x, stage_ptr(ls), (uint32_t)gstep(ls) * kBK, stage_kill(ls),
                kstep(ls) >= nsteps);
   }
   // stage 0 landed: the NS-1 later stages (ND loads each) may still be in flight
@@ -588,7 +624,7 @@ gemm_kernel(GemmParams p) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t kn = (uint32_t)(kbeg + kstep(ls + NS)) * kBK;
+    const uint32_t kn = (uint32_t)gstep(ls + NS) * kBK;
     const bool killn = stage_kill(ls + NS);
     const bool killn_sc = kstep(ls + NS) >= nsteps;
     read_scales(nxt, scA_n, scB_n);
@@ -779,87 +815,82 @@ gemm_kernel(GemmParams p) {
       }
     }
   } else {
-    // Gated GELU: acc[i] (gate) pairs with acc[i + FN/2] (up). The wave owns H rows
-    // wave_m0 .. +ROWS and HF*32 columns of this tile. Pass 0 stages H (and accumulates
-    // its amax); passes 1, 2 stage the bf16 gate / up pre-activations when the caller
-    // keeps them for the backward.
-    constexpr int HF = FN / 2;
-    constexpr int CH = HF * 4;  // 16-byte chunks per staged H row
+    // Gated GELU: each run of 8 H columns pairs a gate quad with its up quad in the same
+    // lane (GegluRuns). The wave owns H rows wave_m0 .. +ROWS and RUNS*8 columns of this
+    // tile. Pass 0 stages H (and accumulates its amax); passes 1, 2 stage the bf16 gate /
+    // up pre-activations when the caller keeps them for the backward.
+    using Runs = GegluRuns<FN, BN>;
+    constexpr int RUNS = Runs::kRuns;
+    constexpr int CH = RUNS;  // 16-byte chunks per staged H row (8 bf16 per run)
     uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
-    const int wave_h0 = n0 + wn * HF * 32;
+    const int wave_h0 = n0 + wn * RUNS * 8;
     const uint16_t* tab_a = reinterpret_cast<const uint16_t*>(smem + kTabOff);
     uint32_t hkeys = 0;  // packed max of the |H| bf16 keys staged by this lane
     uint32_t hmax = 0;   // the same as one fp32-bit amax key
     auto run_pass = [&](auto pass_tag) {
       constexpr int pass = decltype(pass_tag)::value;
-#pragma unroll
-      for (int i = 0; i < HF; ++i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int col = i * 32 + 8 * q + lcol;
-          if constexpr (pass == 0) {
-            // H of the run's FM rows: bf16 g, u pairs first, then all 4 FM gelu table reads
-            // (independent LDS reads in flight together), then the products. Gates outside
-            // the table (|g| < 2^-16 or >= 8, rare) and NaN products (from non-finite u)
-            // take a wave-uniform slow path.
-            uint32_t gw[2 * FM], uw[2 * FM], iw[2 * FM], tv[4 * FM], aw[2 * FM], w[2 * FM];
-            uint32_t outside = 0;
-#pragma unroll
-            for (int j = 0; j < FM; ++j) {
-              gw[2 * j] = pack_bf16x2(acc[i][j][4 * q] * ag, acc[i][j][4 * q + 1] * ag);
-              gw[2 * j + 1] = pack_bf16x2(acc[i][j][4 * q + 2] * ag, acc[i][j][4 * q + 3] * ag);
-              uw[2 * j] = pack_bf16x2(acc[i + HF][j][4 * q] * au, acc[i + HF][j][4 * q + 1] * au);
-              uw[2 * j + 1] =
-                  pack_bf16x2(acc[i + HF][j][4 * q + 2] * au, acc[i + HF][j][4 * q + 3] * au);
-            }
-#pragma unroll
-            for (int k = 0; k < 2 * FM; ++k) iw[k] = gelu_index2(gw[k], outside);
-#pragma unroll
-            for (int k = 0; k < 2 * FM; ++k) {
-              tv[2 * k] = tab_a[iw[k] & 0xFFFFu];
-              tv[2 * k + 1] = tab_a[iw[k] >> 16];
-            }
-#pragma unroll
-            for (int k = 0; k < 2 * FM; ++k) aw[k] = tv[2 * k] | (tv[2 * k + 1] << 16);
-            if (__builtin_expect(__any(outside != 0), 0)) {
-#pragma unroll
-              for (int k = 0; k < 2 * FM; ++k)
-                aw[k] = gelu_finish(gw[k], tv[2 * k]) | (gelu_finish(gw[k] >> 16, tv[2 * k + 1]) << 16);
-            }
-            uint32_t bk = 0;  // packed max of the |h| keys of the run
-#pragma unroll
-            for (int k = 0; k < 2 * FM; ++k) {
-              w[k] = pack_bf16x2(bf16_lo(aw[k]) * bf16_lo(uw[k]), bf16_hi(aw[k]) * bf16_hi(uw[k]));
-              bk = pk_max_u16(bk, w[k] & 0x7FFF7FFFu);
-            }
-            if (__builtin_expect(__any(nan_key2(bk)), 0)) {
-#pragma unroll
-              for (int k = 0; k < 2 * FM; ++k) w[k] = nan_ffff_bf16x2(w[k]);
-            }
-            hkeys = pk_max_u16(hkeys, bk);
-#pragma unroll
-            for (int j = 0; j < FM; ++j)
-              stage_put<CH>(wbuf, j * 32 + lrow_m, col, make_uint2(w[2 * j], w[2 * j + 1]));
-            continue;
-          }
+      static_for<RUNS>([&](auto k_tag) __attribute__((always_inline)) {
+        constexpr int k = decltype(k_tag)::value;
+        constexpr int gs = Runs::gate_s(k), gq = Runs::gate_q(k);
+        constexpr int us = Runs::up_s(k), uq = Runs::up_q(k);
+        const int col = 8 * k + lcol;
+        if constexpr (pass == 0) {
+          // H of the run's FM rows: bf16 g, u pairs first, then all 4 FM gelu table reads
+          // (independent LDS reads in flight together), then the products. Gates outside
+          // the table (|g| < 2^-16 or >= 8, rare) and NaN products (from non-finite u)
+          // take a wave-uniform slow path.
+          uint32_t gw[2 * FM], uw[2 * FM], iw[2 * FM], tv[4 * FM], aw[2 * FM], w[2 * FM];
+          uint32_t outside = 0;
 #pragma unroll
           for (int j = 0; j < FM; ++j) {
-            const float ga[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                                 acc[i][j][4 * q + 3]};
-            const float ua[4] = {acc[i + HF][j][4 * q], acc[i + HF][j][4 * q + 1],
-                                 acc[i + HF][j][4 * q + 2], acc[i + HF][j][4 * q + 3]};
+            gw[2 * j] = pack_bf16x2(acc[gs][j][4 * gq] * ag, acc[gs][j][4 * gq + 1] * ag);
+            gw[2 * j + 1] = pack_bf16x2(acc[gs][j][4 * gq + 2] * ag, acc[gs][j][4 * gq + 3] * ag);
+            uw[2 * j] = pack_bf16x2(acc[us][j][4 * uq] * au, acc[us][j][4 * uq + 1] * au);
+            uw[2 * j + 1] = pack_bf16x2(acc[us][j][4 * uq + 2] * au, acc[us][j][4 * uq + 3] * au);
+          }
+#pragma unroll
+          for (int x = 0; x < 2 * FM; ++x) iw[x] = gelu_index2(gw[x], outside);
+#pragma unroll
+          for (int x = 0; x < 2 * FM; ++x) {
+            tv[2 * x] = tab_a[iw[x] & 0xFFFFu];
+            tv[2 * x + 1] = tab_a[iw[x] >> 16];
+          }
+#pragma unroll
+          for (int x = 0; x < 2 * FM; ++x) aw[x] = tv[2 * x] | (tv[2 * x + 1] << 16);
+          if (__builtin_expect(__any(outside != 0), 0)) {
+#pragma unroll
+            for (int x = 0; x < 2 * FM; ++x)
+              aw[x] = gelu_finish(gw[x], tv[2 * x]) | (gelu_finish(gw[x] >> 16, tv[2 * x + 1]) << 16);
+          }
+          uint32_t bk = 0;  // packed max of the |h| keys of the run
+#pragma unroll
+          for (int x = 0; x < 2 * FM; ++x) {
+            w[x] = pack_bf16x2(bf16_lo(aw[x]) * bf16_lo(uw[x]), bf16_hi(aw[x]) * bf16_hi(uw[x]));
+            bk = pk_max_u16(bk, w[x] & 0x7FFF7FFFu);
+          }
+          if (__builtin_expect(__any(nan_key2(bk)), 0)) {
+#pragma unroll
+            for (int x = 0; x < 2 * FM; ++x) w[x] = nan_ffff_bf16x2(w[x]);
+          }
+          hkeys = pk_max_u16(hkeys, bk);
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
+            stage_put<CH>(wbuf, j * 32 + lrow_m, col, make_uint2(w[2 * j], w[2 * j + 1]));
+        } else {
+#pragma unroll
+          for (int j = 0; j < FM; ++j) {
             uint32_t w0, w1;  // packed bf16 pairs (columns 0-1, 2-3 of the run)
             if constexpr (pass == 1) {
-              w0 = pack_bf16x2(ga[0] * ag, ga[1] * ag);
-              w1 = pack_bf16x2(ga[2] * ag, ga[3] * ag);
+              w0 = pack_bf16x2(acc[gs][j][4 * gq] * ag, acc[gs][j][4 * gq + 1] * ag);
+              w1 = pack_bf16x2(acc[gs][j][4 * gq + 2] * ag, acc[gs][j][4 * gq + 3] * ag);
             } else {
-              w0 = pack_bf16x2(ua[0] * au, ua[1] * au);
-              w1 = pack_bf16x2(ua[2] * au, ua[3] * au);
+              w0 = pack_bf16x2(acc[us][j][4 * uq] * au, acc[us][j][4 * uq + 1] * au);
+              w1 = pack_bf16x2(acc[us][j][4 * uq + 2] * au, acc[us][j][4 * uq + 3] * au);
             }
             stage_put<CH>(wbuf, j * 32 + lrow_m, col, make_uint2(w0, w1));
           }
         }
-      }
+      });
       if constexpr (pass == 0) hmax = max(hkeys << 16, hkeys & 0xFFFF0000u);
       if constexpr (pass == 0) {
         if (p.h8) {
@@ -953,6 +984,16 @@ int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int
         hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16, true>), grid, block, 0,
                            stream, p);
         return launch_status("gemm_kernel(geglu, mx)");
+      }
+      using TG = typename FitTile<T, EPI_GEGLU, false>::type;
+      hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16>), grid, block, 0, stream, p);
+      return launch_status("gemm_kernel(geglu)");
+    } else if constexpr (T::WN == 1 && T::BN % 16 == 0 && T::BN % 64 != 0) {
+      // one wave column, gate and up halves of BN/2 columns: tensor-scaled only (the MX H
+      // blocks of 32 columns would straddle tiles)
+      if (mx) {
+        set_error("gemm: tile %dx%d has no MX gated-GELU variant", T::BM, T::BN);
+        return BF8_EINVAL;
       }
       using TG = typename FitTile<T, EPI_GEGLU, false>::type;
       hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16>), grid, block, 0, stream, p);

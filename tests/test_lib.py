@@ -70,8 +70,11 @@ def test_plan_override_env(monkeypatch):
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:4")
     assert L.bf8_geglu_partials(300, 384) == 2 * 3
     assert L.bf8_gemm_workspace(512, 2560, 10240) == 4 * 512 * 2560 * 4
-    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x160")  # no gated-GELU variant
-    assert L.bf8_geglu_partials(4096, 10240) >= 1
+    # 80 gate + 80 up columns per tile: a gated-GELU variant for I % 80 == 0 only
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x160")
+    assert L.bf8_geglu_partials(512, 10240) == 2 * 128
+    assert L.bf8_geglu_partials(300, 640) == 2 * 8
+    assert L.bf8_geglu_partials(300, 384) != 2 * 5  # 384 % 80 != 0: the automatic plan
 
 
 def test_quantize_many_rejects_bad_arguments():
