@@ -20,6 +20,7 @@
 namespace bf8 {
 
 constexpr int kGeluABytes = (int)sizeof(kGeluA);  // 10240 (9728 used)
+constexpr int kGeluA32Bytes = (int)sizeof(kGeluA32);  // 26624 (positive: 0 .., negative: 16384 ..)
 constexpr int kGeluFBytes = (int)sizeof(kGeluF);  // 28672
 
 // Index into kGeluA for the bf16 g in the low 16 bits (clamped into the table when g lies
@@ -60,6 +61,22 @@ __device__ __forceinline__ uint32_t gelu_index2(uint32_t g2, uint32_t& outside) 
 }
 __device__ __forceinline__ uint32_t gelu_factor_index2(uint32_t g2, uint32_t& outside) {
   return table_index2<kGeluFLo, kGeluFSpan>(g2, outside);
+}
+
+// Byte offsets (two u16 halves) into kGeluA32 of the two bf16 values of a packed pair,
+// clamped into the table; `outside` as for table_index2. Positive inputs sit at bytes
+// 4 * (m - LO), negative ones 16384 bytes further on, so the sign bit of each half, shifted
+// right by one, is its offset.
+__device__ __forceinline__ uint32_t gelu_addr32x2(uint32_t g2, uint32_t& outside) {
+  static_assert(4 * kGeluASpan <= 16384 && sizeof(kGeluA32) >= 16384 + 4 * kGeluASpan,
+                "kGeluA32 layout");
+  asm volatile("" : "+v"(g2));  // keep the packed form (not the halves' sources) in view
+  constexpr unsigned short lo = (unsigned short)kGeluALo, span = (unsigned short)kGeluASpan;
+  const u16x2 rel = __builtin_bit_cast(u16x2, g2 & 0x7FFF7FFFu) - u16x2{lo, lo};
+  const u16x2 cl = __builtin_elementwise_min(rel, u16x2{(unsigned short)(span - 1),
+                                                        (unsigned short)(span - 1)});
+  outside |= __builtin_bit_cast(uint32_t, cl) ^ __builtin_bit_cast(uint32_t, rel);
+  return __builtin_bit_cast(uint32_t, cl << (unsigned short)2) | ((g2 >> 1) & 0x40004000u);
 }
 
 // Whether a packed pair of |bf16| keys (sign bits clear) holds a NaN.

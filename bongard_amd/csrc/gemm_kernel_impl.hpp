@@ -53,9 +53,10 @@ constexpr int kNumXcd = 8;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset that always reads as zero
 
 // LDS bytes a variant needs besides its NS pipeline stages: the gated-GELU epilogue keeps
-// the gelu table (kGeluA) there.
+// the fp32 gelu table (kGeluA32) there, at LDS offset 0 ahead of the stages, so that its
+// byte offsets (below 64 KB) address it directly from packed 16-bit arithmetic.
 template <int EPI>
-constexpr int extra_lds() { return EPI == EPI_GEGLU ? kGeluABytes : 0; }
+constexpr int extra_lds() { return EPI == EPI_GEGLU ? kGeluA32Bytes : 0; }
 
 // Buffer resource (4 SGPRs): base, stride 0, `bytes` valid bytes (offsets at or beyond
 // read as zero), raw-buffer flags of gfx9/gfx950.
@@ -389,7 +390,7 @@ gemm_kernel(GemmParams p) {
                 "and up halves are whole runs of 8 columns");
   static_assert(!(EPI == EPI_GEGLU && MX && FN % 2 != 0), "MX GEGLU: 32-column H blocks per tile");
   static_assert(!MX || (BM <= 256 && BN <= 256), "MX scale rows: one dword per lane");
-  constexpr int kTabOff = KG * NS * kStage;  // GEGLU: the gelu table after the stages
+  constexpr int kStageOff = extra_lds<EPI>();  // GEGLU: the gelu table, then the stages
   static_assert((KG * NS * kStage + extra_lds<EPI>()) * T::OCC <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[KG * NS * kStage + extra_lds<EPI>()];
 
@@ -502,7 +503,7 @@ gemm_kernel(GemmParams p) {
   auto stage_kill = [&](int ls) {
     return kstep(ls) >= nsteps || (gstep(ls) == ksteps - 1 && lane_ktail_dead);
   };
-  auto stage_ptr = [&](int ls) { return smem + (kg * NS + ls % NS) * kStage; };
+  auto stage_ptr = [&](int ls) { return smem + kStageOff + (kg * NS + ls % NS) * kStage; };
 
   // B-tile row of each of the wave's n-subtiles; GEGLU puts gate rows in the first half
   // of the B tile and the matching up rows in the second (even FN: each wave takes its
@@ -574,14 +575,14 @@ gemm_kernel(GemmParams p) {
   // or none: the trailing fragment reads of the final step go to a stale slot and are
   // never used). Prologue stages past the end are zero-filled.
   if constexpr (EPI == EPI_GEGLU) {
-    // the gelu table (10 KB) into LDS ahead of the stage loads, so the prologue's wait for
-    // stage 0 also covers it; wave w copies KB w, w + 4 and, for w < 2, KB w + 8
-    static_assert(kGeluABytes == 10 * 1024, "gelu table copy assumes 10 KB");
-    const i32x4 rt = make_srd(kGeluA, (uint32_t)kGeluABytes);
-    const uint32_t tab = lds_addr(smem + kTabOff);
-    dma16(rt, tab + wid * 1024, lane * 16, wid * 1024);
-    dma16(rt, tab + (wid + 4) * 1024, lane * 16, (wid + 4) * 1024);
-    if (wid < 2) dma16(rt, tab + (wid + 8) * 1024, lane * 16, (wid + 8) * 1024);
+    // the fp32 gelu table (26 KB) into LDS ahead of the stage loads, so the prologue's wait
+    // for stage 0 also covers it; wave w copies KB w, w + 4, .., below 26
+    static_assert(kGeluA32Bytes == 26 * 1024, "gelu table copy assumes 26 KB");
+    const i32x4 rt = make_srd(kGeluA32, (uint32_t)kGeluA32Bytes);
+    const uint32_t tab = lds_addr(smem);
+#pragma unroll
+    for (int c = 0; c < 6; ++c) dma16(rt, tab + (wid + 4 * c) * 1024, lane * 16, (wid + 4 * c) * 1024);
+    if (wid < 2) dma16(rt, tab + (wid + 24) * 1024, lane * 16, (wid + 24) * 1024);
   }
 #pragma unroll
   for (int ls = 0; ls < NS; ++ls) {
@@ -822,9 +823,8 @@ gemm_kernel(GemmParams p) {
     using Runs = GegluRuns<FN, BN>;
     constexpr int RUNS = Runs::kRuns;
     constexpr int CH = RUNS;  // 16-byte chunks per staged H row (8 bf16 per run)
-    uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
+    uint8_t* wbuf = smem + kStageOff + wid * (ROWS * CH * 16);
     const int wave_h0 = n0 + wn * RUNS * 8;
-    const uint16_t* tab_a = reinterpret_cast<const uint16_t*>(smem + kTabOff);
     uint32_t hkeys = 0;  // packed max of the |H| bf16 keys staged by this lane
     uint32_t hmax = 0;   // the same as one fp32-bit amax key
     auto run_pass = [&](auto pass_tag) {
@@ -839,7 +839,7 @@ gemm_kernel(GemmParams p) {
           // (independent LDS reads in flight together), then the products. Gates outside
           // the table (|g| < 2^-16 or >= 8, rare) and NaN products (from non-finite u)
           // take a wave-uniform slow path.
-          uint32_t gw[2 * FM], uw[2 * FM], iw[2 * FM], tv[4 * FM], aw[2 * FM], w[2 * FM];
+          uint32_t gw[2 * FM], uw[2 * FM], ad[2 * FM], ta[4 * FM], w[2 * FM];
           uint32_t outside = 0;
 #pragma unroll
           for (int j = 0; j < FM; ++j) {
@@ -848,24 +848,26 @@ gemm_kernel(GemmParams p) {
             uw[2 * j] = pack_bf16x2(acc[us][j][4 * uq] * au, acc[us][j][4 * uq + 1] * au);
             uw[2 * j + 1] = pack_bf16x2(acc[us][j][4 * uq + 2] * au, acc[us][j][4 * uq + 3] * au);
           }
+          // gelu(g) as fp32 from the table at LDS offset 0 (byte offsets in packed halves)
 #pragma unroll
-          for (int x = 0; x < 2 * FM; ++x) iw[x] = gelu_index2(gw[x], outside);
+          for (int x = 0; x < 2 * FM; ++x) ad[x] = gelu_addr32x2(gw[x], outside);
 #pragma unroll
           for (int x = 0; x < 2 * FM; ++x) {
-            tv[2 * x] = tab_a[iw[x] & 0xFFFFu];
-            tv[2 * x + 1] = tab_a[iw[x] >> 16];
+            ta[2 * x] = *reinterpret_cast<const uint32_t*>(smem + (ad[x] & 0xFFFFu));
+            ta[2 * x + 1] = *reinterpret_cast<const uint32_t*>(smem + (ad[x] >> 16));
           }
-#pragma unroll
-          for (int x = 0; x < 2 * FM; ++x) aw[x] = tv[2 * x] | (tv[2 * x + 1] << 16);
           if (__builtin_expect(__any(outside != 0), 0)) {
 #pragma unroll
-            for (int x = 0; x < 2 * FM; ++x)
-              aw[x] = gelu_finish(gw[x], tv[2 * x]) | (gelu_finish(gw[x] >> 16, tv[2 * x + 1]) << 16);
+            for (int x = 0; x < 2 * FM; ++x) {
+              ta[2 * x] = gelu_finish(gw[x], ta[2 * x] >> 16) << 16;
+              ta[2 * x + 1] = gelu_finish(gw[x] >> 16, ta[2 * x + 1] >> 16) << 16;
+            }
           }
           uint32_t bk = 0;  // packed max of the |h| keys of the run
 #pragma unroll
           for (int x = 0; x < 2 * FM; ++x) {
-            w[x] = pack_bf16x2(bf16_lo(aw[x]) * bf16_lo(uw[x]), bf16_hi(aw[x]) * bf16_hi(uw[x]));
+            w[x] = pack_bf16x2(__uint_as_float(ta[2 * x]) * bf16_lo(uw[x]),
+                               __uint_as_float(ta[2 * x + 1]) * bf16_hi(uw[x]));
             bk = pk_max_u16(bk, w[x] & 0x7FFF7FFFu);
           }
           if (__builtin_expect(__any(nan_key2(bk)), 0)) {

@@ -23,6 +23,9 @@ rules, which this script verifies on all 65,536 bf16 inputs before writing anyth
 Tables (bf16 magnitude bits m = bits & 0x7FFF, sign s):
   kGeluA[s * 2432 + (m - 0x3780)]  bf16 bits of a(x), 0x3780 <= m < 0x4100  (2^-16 .. 8),
                                    zero-padded to 10 KB (whole 1 KB copies into LDS)
+  kGeluA32[s * 4096 + (m - 0x3780)]  the same values as fp32 bits (bf16 << 16), negative
+                                   inputs from entry 4096 (byte 16384) on, zero-padded to
+                                   26 KB, for kernels that multiply them as read
   kGeluF[s * 3584 + (m - 0x3300)]  fp32 bits of F(x), 0x3300 <= m < 0x4100  (2^-25 .. 8)
 
 Run by bongard_amd/build.py before compiling (``python gen_gelu_tables.py OUT``).
@@ -33,6 +36,8 @@ from pathlib import Path
 
 A_LO, A_HI = 0x3780, 0x4100
 A_PAD_BYTES = 10 * 1024
+A32_PAD_BYTES = 26 * 1024
+A32_NEG = 4096  # first entry of the negative inputs in kGeluA32
 F_LO, F_HI = 0x3300, 0x4100
 
 
@@ -115,6 +120,10 @@ def tables():
 
 
 def render(ga, gf):
+    span = A_HI - A_LO
+    ga32 = [v << 16 for v in ga[:span]] + [0] * (A32_NEG - span) + [v << 16 for v in ga[span:2 * span]]
+    ga32 += [0] * (A32_PAD_BYTES // 4 - len(ga32))
+
     def rows(vals, fmt, per):
         return "\n".join("    " + ", ".join(fmt.format(v) for v in vals[i:i + per]) + ","
                          for i in range(0, len(vals), per))
@@ -125,6 +134,8 @@ def render(ga, gf):
         f"constexpr uint32_t kGeluFLo = 0x{F_LO:04X}u, kGeluFSpan = 0x{F_HI - F_LO:X}u;\n"
         f"static __device__ const uint16_t kGeluA[{len(ga)}] __attribute__((aligned(16))) = {{\n"
         f"{rows(ga, '0x{:04X}', 12)}\n}};\n"
+        f"static __device__ const uint32_t kGeluA32[{len(ga32)}] __attribute__((aligned(16))) = {{\n"
+        f"{rows(ga32, '0x{:08X}u', 8)}\n}};\n"
         f"static __device__ const uint32_t kGeluF[{len(gf)}] __attribute__((aligned(16))) = {{\n"
         f"{rows(gf, '0x{:08X}u', 8)}\n}};\n")
 
