@@ -61,4 +61,4 @@ if __name__ == "__main__":
         print(kernel_stats(sys.argv[2]))
     else:
         for k, v in sorted(pmc(sys.argv[2]).items()):
-            print(f"{k[0]:70s} {k[1]:11s} grid={k[2]:<10d} {v:14.1f} KiB/dispatch")
+            print(f"{k[0]:70s} {k[1]:22s} grid={k[2]:<10d} {v:16.1f} per dispatch")

@@ -15,7 +15,10 @@ per row and per column, and the fused RMSNorm of the same activation. ``c5``: th
 config-5 training step (the c2 MLP at M = 8192, forward and backward, delayed scaling with
 an amax history of 16). ``vs_hipblaslt``: this library's FP8 GEMM and hipBLASLt's (through
 ``torch._scaled_mm``) on the c2 / c4 / square shapes, each captured as a HIP graph of 20
-calls and timed from HIP events around its replay; prints one line per shape.
+calls and timed from HIP events around its replay; prints one line per shape. ``c4``: the
+config-4 decoder-branch step at M = 512 on pre-quantized weights (current-scaling quantize
+of the branch input and the attention output, fused QKV with three segment scales, O,
+gate/up + gated GELU, H cast, down), captured as one HIP graph and replayed.
 """
 
 import argparse
@@ -31,7 +34,7 @@ def main():
     p = argparse.ArgumentParser()
     p.add_argument("--iters", type=int, default=5)
     p.add_argument("--rows", type=int, default=4096)
-    p.add_argument("--case", choices=("c2", "square", "recipes", "c5", "vs_hipblaslt"),
+    p.add_argument("--case", choices=("c2", "square", "recipes", "c5", "vs_hipblaslt", "c4"),
                    default="c2")
     args = p.parse_args()
     dev = torch.device("cuda:0")
@@ -53,6 +56,9 @@ def main():
         return
     if args.case == "vs_hipblaslt":
         _vs_hipblaslt(dev, args.iters)
+        return
+    if args.case == "c4":
+        _c4(dev, args.iters)
         return
     c = workloads.config2(rows=args.rows)
     I = workloads.INTERMEDIATE
@@ -96,6 +102,36 @@ def _graph_time(fn, n=20, reps=5):
         torch.cuda.synchronize()
         ts.append(a.elapsed_time(b) / 1e3 / n)
     return sorted(ts)[len(ts) // 2]
+
+
+def _c4(dev, iters):
+    c = workloads.config4()
+    x = c["x"].to(dev)
+    I = c["w_gate"].shape[0]
+    g = torch.Generator().manual_seed(44)
+    attn = torch.randn(x.shape[0], c["w_o"].shape[1], generator=g).to(torch.bfloat16).to(dev)
+    metas = ops.new_meta(dev, 3)
+    rows = [c["w_q"].shape[0], c["w_k"].shape[0], c["w_v"].shape[0]]
+    w8 = torch.empty(sum(rows), x.shape[1], dtype=torch.float8_e4m3fn, device=dev)
+    start = 0
+    for i, name in enumerate(("w_q", "w_k", "w_v")):
+        ops.quantize(c[name].to(dev), ops.E4M3, meta=metas[i], out=w8[start:start + rows[i]])
+        start += rows[i]
+    ends = [rows[0], rows[0] + rows[1], sum(rows)]
+    oq = ops.quantize(c["w_o"].to(dev), ops.E4M3)
+    gq = ops.quantize(torch.cat([c["w_gate"], c["w_up"]]).to(dev), ops.E4M3)
+    dq = ops.quantize(c["w_down"].to(dev), ops.E4M3)
+
+    def step():
+        xq, aq = ops.quantize_many([x, attn])
+        ops.gemm(xq.data, 0, xq.meta, w8, 0, metas[0], seg_ends=ends, b_meta_stride=4)
+        ops.gemm(aq.data, 0, aq.meta, oq.data, 0, oq.meta)
+        H, _, hp = ops.gemm_geglu(xq.data, xq.meta, gq.data, gq.meta, I)
+        hq = ops.cast_partials(H, hp, ops.E4M3)
+        return ops.gemm(hq.data, 0, hq.meta, dq.data, 0, dq.meta)
+
+    t = _graph_time(step, n=max(iters, 1))
+    print(f"profile_target done: c4 step {t * 1e6:.2f} us (graph-replayed)", flush=True)
 
 
 def _vs_hipblaslt(dev, iters):
