@@ -82,9 +82,11 @@ constexpr int kGegluNominalSteps = 20;
 struct Plan {
   int tile = TILE_256x256;
   int splits = 1;
-  int kps = 0;  // K steps per split
+  int kps = 0;  // K steps per split (tail split: per piece)
   int tiles_m = 0, tiles_n = 0;
-  size_t ws_bytes = 0;  // split-K workspace: fp32 partials [splits][M][N]
+  int full_tiles = 0, tail_pieces = 0;  // tail split: whole tiles, K pieces per tail tile
+  size_t ws_bytes = 0;  // split-K workspace: fp32 partials [splits][M][N], or the tail
+                        // tiles' pieces [tails * pieces][BM][BN]
 };
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -102,6 +104,38 @@ Plan make_plan(int tile, int64_t M, int64_t N, int64_t ksteps, int splits) {
   return p;
 }
 
+// Tail split: with T tiles filling R rounds and a partial last round of t = T mod 256
+// tiles (t <= 128), the whole rounds run whole tiles and each of the t tail tiles is split
+// into pieces = min(256 / t, 8) K ranges, one workgroup each, so the last round has every
+// CU busy for a fraction of a tile instead of t CUs for a whole one. Valid for tiles that
+// run one workgroup per CU with one K group. Returns false when it does not apply.
+// Per-CU FP8 rate of a long run of K steps (no epilogue) for the tiles that take tail
+// splits: the 256x256 tile, ~1.5 us per 128-byte step on MI355X with every CU busy (8192^3
+// and c5's dX shape). Measured gain at c5 (interleaved A/B): dX (M=8192, N=2560,
+// K=20480) 343.5 -> 341.0 us, dW_gu (M=20480, N=2560, K=8192) 338.8 -> 332.6 us against
+// two rounds of 256x160 tiles; a shape with a smaller tail gains more.
+constexpr double kTailStepRate256 = 11.2;
+
+bool make_tail_plan(int tile, int64_t M, int64_t N, int64_t ksteps, Plan& p) {
+  const TileInfo& ti = kTiles[tile];
+  if (tile != TILE_256x256) return false;
+  p = Plan{};
+  p.tile = tile;
+  p.tiles_m = (int)cdiv(M, ti.bm);
+  p.tiles_n = (int)cdiv(N, ti.bn);
+  const int64_t T = (int64_t)p.tiles_m * p.tiles_n;
+  const int64_t tails = T % kNumCus;
+  if (T <= kNumCus || tails == 0 || tails > kNumCus / 2) return false;
+  int pieces = (int)std::min<int64_t>(kNumCus / tails, kMaxSplits);
+  p.kps = (int)cdiv(ksteps, pieces);
+  pieces = (int)cdiv(ksteps, p.kps);  // no empty piece
+  if (pieces < 2 || p.kps < kMinStepsPerSplit) return false;
+  p.full_tiles = (int)(T - tails);
+  p.tail_pieces = pieces;
+  p.ws_bytes = (size_t)tails * pieces * ti.bm * ti.bn * 4;
+  return true;
+}
+
 // A K step never takes less than this, however little MFMA work it holds: with few
 // workgroups per CU the loads of the stages in flight no longer cover their latency
 // (measured at M = 512: ~520 ns per step for one workgroup per CU, ~450 ns when the tile
@@ -113,8 +147,15 @@ constexpr double kStepFloorNsOcc2 = 450.0;
 // about two steps of pipeline fill and epilogue, plus the split-K partials' HBM round
 // trip and the reduction's launch. A step costs the MFMA work of the workgroups sharing
 // a CU in the busiest round, or the latency floor.
-double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu) {
+double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu, int64_t ksteps = 0) {
   const TileInfo& ti = kTiles[p.tile];
+  if (p.tail_pieces > 0) {
+    // whole rounds of whole tiles, one round of pieces, the pieces' partials written and
+    // read back, the reduction's launch
+    const double step_ns = 2.0 * ti.bm * ti.bn * kStepBytes / (kTailStepRate256 * 1e3);
+    const double rounds = (double)p.full_tiles / kNumCus;
+    return rounds * (ksteps + 2) * step_ns + (p.kps + 2) * step_ns + 2.0 * p.ws_bytes / 5e3 + 5000.0;
+  }
   const int64_t ctas = (int64_t)p.tiles_m * p.tiles_n * p.splits;
   const int64_t rounds = cdiv(ctas, (int64_t)kNumCus * ti.occ);
   const int64_t per_cu = std::min<int64_t>(ti.occ, cdiv(ctas, (int64_t)kNumCus));
@@ -126,8 +167,10 @@ double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu) {
   return t;
 }
 
-// Tuning override, read on every call: BONGARD_FP8_GEMM_TILE=<bm>x<bn>[:<splits>]
-// (e.g. "256x160:4"). Unknown values are ignored.
+// Tuning override, read on every call: BONGARD_FP8_GEMM_TILE=<bm>x<bn>[:<splits>|:t]
+// (e.g. "256x160:4"; ":t" the tail split, when the shape has one). Unknown values are
+// ignored.
+constexpr int kTailSplitOverride = -1;
 bool env_override(int& tile, int& splits) {
   tile = -1;
   splits = 1;
@@ -137,10 +180,10 @@ bool env_override(int& tile, int& splits) {
     const size_t n = std::strlen(kTiles[i].name);
     if (std::strncmp(e, kTiles[i].name, n) == 0 && (e[n] == 0 || e[n] == ':')) {
       tile = i;
-      if (e[n] == ':') splits = std::atoi(e + n + 1);
+      if (e[n] == ':') splits = e[n + 1] == 't' ? kTailSplitOverride : std::atoi(e + n + 1);
     }
   }
-  splits = splits < 1 ? 1 : (splits > kMaxSplits ? kMaxSplits : splits);
+  if (splits != kTailSplitOverride) splits = splits < 1 ? 1 : (splits > kMaxSplits ? kMaxSplits : splits);
   return tile >= 0;
 }
 
@@ -151,7 +194,12 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
   int otile, osplits;
   if (env_override(otile, osplits) && (!geglu || geglu_tile_ok(otile, N, mx)) &&
       (!mx || kTiles[otile].mx)) {
-    Plan p = make_plan(otile, M, N, ksteps, geglu ? 1 : osplits);
+    Plan p;
+    if (!geglu && osplits == kTailSplitOverride) {
+      if (make_tail_plan(otile, M, N, ksteps, p) && p.ws_bytes <= ws_avail) return p;
+      osplits = 1;
+    }
+    p = make_plan(otile, M, N, ksteps, geglu ? 1 : osplits);
     if (p.ws_bytes > ws_avail) p = make_plan(otile, M, N, ksteps, 1);
     return p;
   }
@@ -171,6 +219,15 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
         have = true;
       }
     }
+    Plan tp;
+    if (!geglu && make_tail_plan(tile, M, N, ksteps, tp) && tp.ws_bytes <= ws_avail) {
+      const double c = plan_cost(tp, M, N, false, ksteps);
+      if (!have || c < best_cost * 0.97) {
+        best = tp;
+        best_cost = c;
+        have = true;
+      }
+    }
   }
   if (geglu) best.kps = (int)ksteps;
   // A small tile that leaves one workgroup per CU (no K split) runs as its two-K-group
@@ -183,9 +240,9 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
     best.tile = best.tile == TILE_128x64 ? TILE_128x64k2 : TILE_64x128k2;
   }
   if (const char* d = std::getenv("BONGARD_FP8_GEMM_DEBUG"); d && d[0] == '1')
-    std::fprintf(stderr, "bf8 plan %s%s M=%lld N=%lld K=%lld: tile %s splits %d (%d x %d tiles)\n",
+    std::fprintf(stderr, "bf8 plan %s%s M=%lld N=%lld K=%lld: tile %s splits %d (%d x %d tiles, tail pieces %d)\n",
                  geglu ? "geglu" : "gemm", mx ? " mx" : "", (long long)M, (long long)N, (long long)K,
-                 kTiles[best.tile].name, best.splits, best.tiles_m, best.tiles_n);
+                 kTiles[best.tile].name, best.splits, best.tiles_m, best.tiles_n, best.tail_pieces);
   return best;
 }
 
@@ -210,18 +267,86 @@ struct SegEnds {
   int e[4];
 };
 
-// C = alpha(n) * sum_s P[s] + bias(n) for the split-K partials P [splits][M][N] (fp32),
-// summed in split order, so the result does not depend on which split finished first;
-// alpha(n) = a_scale_inv * b_scale_inv[segment of n]. Each thread does 8 columns.
+// The epilogue of a reduced partial sum: v (8 fp32 sums for columns n .. n+7 of row m) times
+// alpha(n) = a_scale_inv * b_scale_inv[segment of n] (or the axiswise factors, or 1 for MX),
+// plus bias, written to C as bf16 (RNE) or fp32.
+struct ReduceOut {
+  const float* a_sinv;
+  const float* b_sinv;
+  int b_stride, n_seg;
+  SegEnds seg_end;
+  const uint16_t* bias;
+  void* C;
+  int64_t ldc;
+  int a_vec, b_vec, unit;
+};
+
 template <int OUT>
-__global__ __launch_bounds__(256) void split_reduce_kernel(
-    const float* __restrict__ P, int splits, int64_t stride, int M, int N,
-    const float* __restrict__ a_sinv, const float* __restrict__ b_sinv, int b_stride,
-    int n_seg, SegEnds seg_end, const uint16_t* __restrict__ bias, void* __restrict__ C,
-    int64_t ldc, int a_vec, int b_vec, int unit) {
+__device__ __forceinline__ void reduce_store(const ReduceOut& o, float (&v)[8], int m, int n) {
+  const float sa = (o.a_vec || o.unit) ? 0.0f : *o.a_sinv;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {  // segments change at multiples of 4 columns
+    const int nh = n + 4 * h;
+    int seg = 0;
+#pragma unroll
+    for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < o.n_seg && nh >= o.seg_end.e[s2]) ? 1 : 0;
+    float b4[4] = {0.f, 0.f, 0.f, 0.f};
+    if (o.bias) {
+      const uint2 bb = *reinterpret_cast<const uint2*>(o.bias + nh);
+      b4[0] = bf16_lo(bb.x); b4[1] = bf16_hi(bb.x); b4[2] = bf16_lo(bb.y); b4[3] = bf16_hi(bb.y);
+    }
+    if (o.unit) {  // MX: the block scales were applied inside the MFMA
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] + b4[e];
+      continue;
+    }
+    if (o.a_vec | o.b_vec) {  // axiswise: (a_sinv[m] or a_sinv[0]) * (b_sinv[n] or b_sinv[0])
+      const float ra = o.a_vec ? o.a_sinv[m] : *o.a_sinv;
+      float cf[4];
+      if (o.b_vec) {
+        const float4 f = *reinterpret_cast<const float4*>(o.b_sinv + nh);
+        cf[0] = f.x; cf[1] = f.y; cf[2] = f.z; cf[3] = f.w;
+      } else {
+        cf[0] = cf[1] = cf[2] = cf[3] = *o.b_sinv;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] * (ra * cf[e]) + b4[e];
+      continue;
+    }
+    const float alpha = sa * o.b_sinv[seg * o.b_stride];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] * alpha + b4[e];
+  }
+  if (OUT == BF8_OUT_BF16) {
+    uint16_t* dst = reinterpret_cast<uint16_t*>(o.C) + m * o.ldc + n;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                 (float __attribute__((ext_vector_type(2)))){v[2 * e], v[2 * e + 1]},
+                 __bf16 __attribute__((ext_vector_type(2)))));
+    if ((o.ldc & 7) == 0) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      reinterpret_cast<uint2*>(dst)[0] = make_uint2(w[0], w[1]);
+      reinterpret_cast<uint2*>(dst)[1] = make_uint2(w[2], w[3]);
+    }
+  } else {
+    float* dst = reinterpret_cast<float*>(o.C) + m * o.ldc + n;
+    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// C = alpha(n) * sum_s P[s] + bias(n) for the split-K partials P [splits][M][N] (fp32),
+// summed in split order, so the result does not depend on which split finished first.
+// Each thread does 8 columns.
+template <int OUT>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ P, int splits,
+                                                           int64_t stride, int M, int N,
+                                                           ReduceOut o) {
   const int n8 = N >> 3;
   const int64_t total = (int64_t)M * n8;
-  const float sa = (a_vec || unit) ? 0.0f : *a_sinv;
   for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < total;
        g += (int64_t)gridDim.x * 256) {
     const int m = (int)(g / n8), n = (int)(g % n8) * 8;
@@ -239,59 +364,40 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(
       v[0] += lo.x; v[1] += lo.y; v[2] += lo.z; v[3] += lo.w;
       v[4] += hi.x; v[5] += hi.y; v[6] += hi.z; v[7] += hi.w;
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {  // segments change at multiples of 4 columns
-      const int nh = n + 4 * h;
-      int seg = 0;
-#pragma unroll
-      for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < n_seg && nh >= seg_end.e[s2]) ? 1 : 0;
-      float b4[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bias) {
-        const uint2 bb = *reinterpret_cast<const uint2*>(bias + nh);
-        b4[0] = bf16_lo(bb.x); b4[1] = bf16_hi(bb.x); b4[2] = bf16_lo(bb.y); b4[3] = bf16_hi(bb.y);
-      }
-      if (unit) {  // MX: the block scales were applied inside the MFMA
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] + b4[e];
-        continue;
-      }
-      if (a_vec | b_vec) {  // axiswise: (a_sinv[m] or a_sinv[0]) * (b_sinv[n] or b_sinv[0])
-        const float ra = a_vec ? a_sinv[m] : *a_sinv;
-        float cf[4];
-        if (b_vec) {
-          const float4 f = *reinterpret_cast<const float4*>(b_sinv + nh);
-          cf[0] = f.x; cf[1] = f.y; cf[2] = f.z; cf[3] = f.w;
-        } else {
-          cf[0] = cf[1] = cf[2] = cf[3] = *b_sinv;
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] * (ra * cf[e]) + b4[e];
-        continue;
-      }
-      const float alpha = sa * b_sinv[seg * b_stride];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[4 * h + e] = v[4 * h + e] * alpha + b4[e];
-    }
-    if (OUT == BF8_OUT_BF16) {
-      uint16_t* dst = reinterpret_cast<uint16_t*>(C) + m * ldc + n;
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
-                   (float __attribute__((ext_vector_type(2)))){v[2 * e], v[2 * e + 1]},
-                   __bf16 __attribute__((ext_vector_type(2)))));
-      if ((ldc & 7) == 0) {
-        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-      } else {
-        reinterpret_cast<uint2*>(dst)[0] = make_uint2(w[0], w[1]);
-        reinterpret_cast<uint2*>(dst)[1] = make_uint2(w[2], w[3]);
-      }
+    reduce_store<OUT>(o, v, m, n);
+  }
+}
+
+// The tail tiles of a tail-split schedule: tile t (walk position full_tiles + t) is the sum
+// of its pieces P[t * pieces + s] ([BM][BN] fp32 each), taken in piece order. A block covers
+// 2048 outputs of one tile, 8 columns a thread.
+template <int OUT>
+__global__ __launch_bounds__(256) void tail_reduce_kernel(const float* __restrict__ P, int pieces,
+                                                          int bm, int bn, int full_tiles,
+                                                          int tiles_m, int tiles_n, int M, int N,
+                                                          ReduceOut o) {
+  const int per_tile = bm * bn / 2048;
+  const int t = blockIdx.x / per_tile;
+  const int e = (blockIdx.x % per_tile) * 256 + threadIdx.x;
+  const int row = e / (bn / 8), col = (e % (bn / 8)) * 8;
+  int tm, tn;
+  walk_tile(tiles_m, tiles_n, full_tiles + t, tm, tn);
+  const int m = tm * bm + row, n = tn * bn + col;
+  if (m >= M || n >= N) return;  // N % 8 == 0: eight columns are all in or all out
+  const float* src = P + (int64_t)t * pieces * bm * bn + row * bn + col;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < pieces; ++s) {
+    const float4 lo = *reinterpret_cast<const float4*>(src + (int64_t)s * bm * bn);
+    const float4 hi = *reinterpret_cast<const float4*>(src + (int64_t)s * bm * bn + 4);
+    if (s == 0) {
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
     } else {
-      float* dst = reinterpret_cast<float*>(C) + m * ldc + n;
-      *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-      *reinterpret_cast<float4*>(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+      v[0] += lo.x; v[1] += lo.y; v[2] += lo.z; v[3] += lo.w;
+      v[4] += hi.x; v[5] += hi.y; v[6] += hi.z; v[7] += hi.w;
     }
   }
+  reduce_store<OUT>(o, v, m, n);
 }
 
 int launch_plan(const Plan& pl, GemmParams p, int epi, int out_dtype, int fa, int fb, void* ws,
@@ -300,6 +406,31 @@ int launch_plan(const Plan& pl, GemmParams p, int epi, int out_dtype, int fa, in
   p.tiles_n = pl.tiles_n;
   p.splits = pl.splits;
   p.ksteps_per_split = pl.kps;
+  ReduceOut o;
+  o.a_sinv = p.a_sinv; o.b_sinv = p.b_sinv; o.b_stride = p.b_stride; o.n_seg = p.n_seg;
+  for (int i = 0; i < 4; ++i) o.seg_end.e[i] = p.seg_end[i];
+  o.bias = p.bias; o.C = p.C; o.ldc = p.ldc; o.a_vec = p.a_vec; o.b_vec = p.b_vec;
+  o.unit = mx ? 1 : 0;
+  if (pl.tail_pieces > 0) {
+    // whole tiles write C; the tail tiles' pieces write raw partials, reduced after
+    p.full_tiles = pl.full_tiles;
+    p.tail_pieces = pl.tail_pieces;
+    p.tail_ws = static_cast<float*>(ws);
+    const int rc = launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
+    if (rc != BF8_OK) return rc;
+    const TileInfo& ti = kTiles[pl.tile];
+    const int tails = pl.tiles_m * pl.tiles_n - pl.full_tiles;
+    const unsigned blocks = (unsigned)(tails * (ti.bm * ti.bn / 2048));
+    if (out_dtype == BF8_OUT_BF16)
+      hipLaunchKernelGGL(tail_reduce_kernel<BF8_OUT_BF16>, dim3(blocks), dim3(256), 0, s,
+                         (const float*)ws, pl.tail_pieces, ti.bm, ti.bn, pl.full_tiles,
+                         pl.tiles_m, pl.tiles_n, p.M, p.N, o);
+    else
+      hipLaunchKernelGGL(tail_reduce_kernel<BF8_OUT_F32>, dim3(blocks), dim3(256), 0, s,
+                         (const float*)ws, pl.tail_pieces, ti.bm, ti.bn, pl.full_tiles,
+                         pl.tiles_m, pl.tiles_n, p.M, p.N, o);
+    return launch_status("tail_reduce_kernel");
+  }
   if (pl.splits == 1) return launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
   // K split: raw fp32 partials into the workspace, then the ordered reduction
   GemmParams q = p;
@@ -311,18 +442,12 @@ int launch_plan(const Plan& pl, GemmParams p, int epi, int out_dtype, int fa, in
   if (rc != BF8_OK) return rc;
   const int64_t items = (int64_t)p.M * (p.N / 8);
   const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(items, 256), 4096);
-  SegEnds se;
-  for (int i = 0; i < 4; ++i) se.e[i] = p.seg_end[i];
   if (out_dtype == BF8_OUT_BF16)
     hipLaunchKernelGGL(split_reduce_kernel<BF8_OUT_BF16>, dim3(blocks), dim3(256), 0, s,
-                       (const float*)ws, pl.splits, q.split_stride, p.M, p.N, p.a_sinv, p.b_sinv,
-                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc, p.a_vec, p.b_vec,
-                       mx ? 1 : 0);
+                       (const float*)ws, pl.splits, q.split_stride, p.M, p.N, o);
   else
     hipLaunchKernelGGL(split_reduce_kernel<BF8_OUT_F32>, dim3(blocks), dim3(256), 0, s,
-                       (const float*)ws, pl.splits, q.split_stride, p.M, p.N, p.a_sinv, p.b_sinv,
-                       p.b_stride, p.n_seg, se, p.bias, p.C, p.ldc, p.a_vec, p.b_vec,
-                       mx ? 1 : 0);
+                       (const float*)ws, pl.splits, q.split_stride, p.M, p.N, o);
   return launch_status("split_reduce_kernel");
 }
 

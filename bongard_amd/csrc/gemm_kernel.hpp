@@ -44,7 +44,28 @@ struct GemmParams {
   int64_t h8_sc_ld, h8t_sc_ld;
   int64_t split_stride;   // splits > 1: C is fp32 [splits][M][ldc], raw sums, this many
                           // elements apart (a reduce kernel applies scales and bias)
+  // Tail-split schedule (tail_pieces > 0, linear epilogues, splits == 1): workgroups
+  // [0, full_tiles) take whole tiles, walk positions 0 .. full_tiles-1, and write C; the
+  // others take one of tail_pieces K pieces (ksteps_per_split steps each) of a tile at walk
+  // position full_tiles + t and write its raw fp32 sums to tail_ws[t * tail_pieces + piece]
+  // ([BM][BN] each), which tail_reduce_kernel adds in piece order.
+  int full_tiles, tail_pieces;
+  float* tail_ws;
 };
+
+constexpr int kGroupM = 8;  // tile rows walked together (the tile order of a launch)
+
+// Tile (tm, tn) at position id of the tile walk: groups of kGroupM tile rows, each group
+// walked with the tile row changing fastest.
+__host__ __device__ inline void walk_tile(int tiles_m, int tiles_n, int id, int& tm, int& tn) {
+  const int per_group = kGroupM * tiles_n;
+  const int g = id / per_group;
+  const int first_m = g * kGroupM;
+  const int gm = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+  const int in_g = id - g * per_group;
+  tm = first_m + in_g % gm;
+  tn = in_g / gm;
+}
 
 // A workgroup is KG groups of four wave64s; the four waves of a group are arranged
 // WM x WN and each owns FM x FN MFMA tiles of 32 x 32 outputs, so the block tile is

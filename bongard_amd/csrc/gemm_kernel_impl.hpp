@@ -48,7 +48,6 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 constexpr int kBK = 128;       // K bytes per LDS stage
 constexpr int kThreads = 256;  // four wave64
-constexpr int kGroupM = 8;
 constexpr int kNumXcd = 8;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset that always reads as zero
 
@@ -101,26 +100,42 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
       (__attribute__((address_space(3))) const uint8_t*)(p));
 }
 
-// (tile row, tile column, K split) of this workgroup.
-__device__ __forceinline__ void block_coords(const GemmParams& p, int& tm, int& tn,
-                                             int& split) {
-  const int ntiles = p.tiles_m * p.tiles_n;
-  const int nb = ntiles * p.splits;
-  const int b = blockIdx.x;
-  // XCD-contiguous renumbering: blocks dispatched to XCD x (b % 8 == x) get ids
-  // [x*q + min(x, r), ...) with q = nb / 8, r = nb % 8.
+// XCD-contiguous renumbering of blocks [0, nb) (block b is dispatched to XCD b % 8): the
+// blocks of XCD x get positions [x*q + min(x, r), ...) with q = nb / 8, r = nb % 8.
+__device__ __forceinline__ int xcd_position(int b, int nb) {
   const int x = b % kNumXcd, idx = b / kNumXcd;
   const int q = nb / kNumXcd, r = nb % kNumXcd;
-  int id = x * q + (x < r ? x : r) + idx;
+  return x * q + (x < r ? x : r) + idx;
+}
+
+// (tile row, tile column, K split) of this workgroup; `tail_slot` >= 0 for a K piece of a
+// tail-split schedule (its partials' slot in tail_ws).
+__device__ __forceinline__ void block_coords(const GemmParams& p, int& tm, int& tn, int& split,
+                                             int& tail_slot) {
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int b = blockIdx.x;
+  tail_slot = -1;
+  if (p.tail_pieces > 0) {
+    if (b < p.full_tiles) {  // whole tiles, one round per 256 workgroups
+      walk_tile(p.tiles_m, p.tiles_n, xcd_position(b, p.full_tiles), tm, tn);
+      split = 0;
+      return;
+    }
+    // pieces: position = piece * tails + t, so an XCD's pieces share their K range and
+    // neighbouring tail tiles share operand rows (full_tiles is a multiple of 8, so
+    // b - full_tiles is on the same XCD as b)
+    const int tails = ntiles - p.full_tiles;
+    const int pos = xcd_position(b - p.full_tiles, tails * p.tail_pieces);
+    const int t = pos % tails;
+    split = pos / tails;
+    walk_tile(p.tiles_m, p.tiles_n, p.full_tiles + t, tm, tn);
+    tail_slot = t * p.tail_pieces + split;
+    return;
+  }
+  int id = xcd_position(b, ntiles * p.splits);
   split = id / ntiles;
   id -= split * ntiles;
-  const int per_group = kGroupM * p.tiles_n;
-  const int g = id / per_group;
-  const int first_m = g * kGroupM;
-  const int gm = min(p.tiles_m - first_m, kGroupM);
-  const int in_g = id - g * per_group;
-  tm = first_m + in_g % gm;
-  tn = in_g / gm;
+  walk_tile(p.tiles_m, p.tiles_n, id, tm, tn);
 }
 
 template <int FA, int FB>
@@ -406,8 +421,8 @@ gemm_kernel(GemmParams p) {
     if (!MX && p.h8) hs = *p.h8_scale;  // the quantization scale of H
   }
 
-  int tm, tn, split;
-  block_coords(p, tm, tn, split);
+  int tm, tn, split, tail_slot;
+  block_coords(p, tm, tn, split, tail_slot);
   const int m0 = tm * BM;
   const int n0 = tn * (EPI == EPI_GEGLU ? BN / 2 : BN);  // GEGLU: n0 indexes I
 
@@ -419,8 +434,10 @@ gemm_kernel(GemmParams p) {
   const int wave_m0 = wm * FM * 32;
 
   const int ksteps = (p.K + kBK - 1) / kBK;
-  const int kbeg = split * p.ksteps_per_split;
-  const int nsteps = min(p.ksteps_per_split, ksteps - kbeg);  // >= 1 by construction
+  // whole tiles of a tail-split schedule run every K step
+  const int kps = (p.tail_pieces > 0 && tail_slot < 0) ? ksteps : p.ksteps_per_split;
+  const int kbeg = split * kps;
+  const int nsteps = min(kps, ksteps - kbeg);  // >= 1 by construction
   // K group kg takes the split's steps kg, kg + KG, ...: its local step ls is global step
   // kbeg + kg + KG * ls; both groups run niters local steps (the group with one step fewer
   // runs a zero-filled last one), so their barriers pair up.
@@ -683,6 +700,26 @@ gemm_kernel(GemmParams p) {
   }
 
   // ---- epilogue --------------------------------------------------------------------
+  if constexpr (EPI == EPI_LINEAR) {
+    if (tail_slot >= 0) {
+      // a K piece of a tail-split tile: raw fp32 sums of the whole BM x BN tile (rows and
+      // columns past the tensor hold zeros), reduced with the other pieces later
+      float* base = p.tail_ws + (int64_t)tail_slot * (BM * BN);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < FM; ++j) {
+            const int m = wave_m0 + j * 32 + (lane & 31);
+            const int n = wn * FN * 32 + i * 32 + 8 * q + (lane >> 5) * 4;
+            *reinterpret_cast<float4*>(base + m * BN + n) =
+                make_float4(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                            acc[i][j][4 * q + 3]);
+          }
+      return;
+    }
+  }
   // acc[i][j][r]: n-subtile i, m-subtile j; row m = wave_m0 + j*32 + (lane & 31) of the
   // tile, column (within the n-subtile) 8*(r/4) + (lane >> 5)*4 + (r & 3): each lane
   // holds runs of four consecutive columns. bf16 results are staged through this wave's
@@ -935,9 +972,17 @@ gemm_kernel(GemmParams p) {
   }
 }
 
+// Workgroups of a launch: one per tile and K split, or for a tail-split schedule the whole
+// tiles plus the tail tiles' pieces.
+inline unsigned grid_blocks(const GemmParams& p) {
+  const int ntiles = p.tiles_m * p.tiles_n;
+  if (p.tail_pieces > 0) return (unsigned)(p.full_tiles + (ntiles - p.full_tiles) * p.tail_pieces);
+  return (unsigned)(ntiles * p.splits);
+}
+
 template <class T, int EPI, int OUT>
 int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
-  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads * T::KG);
+  const dim3 grid(grid_blocks(p)), block(kThreads * T::KG);
   if (fa == BF8_E4M3 && fb == BF8_E4M3)
     hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI, OUT>), grid, block, 0, s, p);
   else if (fa == BF8_E5M2 && fb == BF8_E4M3)
@@ -968,7 +1013,7 @@ struct FitTile {
 template <class T>
 int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
                      hipStream_t stream, bool mx) {
-  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits)), block(kThreads * T::KG);
+  const dim3 grid(grid_blocks(p)), block(kThreads * T::KG);
   if constexpr (T::KG != 1) {
     if (epi == EPI_GEGLU || mx) {
       set_error("gemm: tile %dx%d with two K groups has linear non-MX epilogues only", T::BM,

@@ -130,6 +130,13 @@ def test_gemm_axiswise(gpu, M, N, K, a_vec, b_vec):
     _axis_gemm_case(gpu, M, N, K, a_vec, b_vec, seed=M + N + K)
 
 
+def test_gemm_axiswise_tail_split(gpu, monkeypatch):
+    """Per-row and per-column scale vectors reach the tail tiles' reduction (tail split
+    forced: 272 tiles of 256x256, 16 of them split along K)."""
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:t")
+    _axis_gemm_case(gpu, 4160, 3848, 4096, 1, 1, seed=64, bias=True)
+
+
 def test_gemm_axiswise_bias(gpu):
     _axis_gemm_case(gpu, 200, 256, 512, 1, 1, seed=9, bias=True)
 

@@ -423,3 +423,67 @@ def test_operand_layout_is_checked(gpu):
     y = ops.gemm(a.data, 0, a.meta, b.data, 0, b.meta)
     torch.cuda.synchronize()
     assert y.shape == (64, 96)
+
+
+# ---- tail split ------------------------------------------------------------------------------
+# 256x256 tiles whose count leaves a partial last round run whole rounds of whole tiles and
+# split each tail tile along K over the last round (raw fp32 partials, reduced in piece
+# order). BONGARD_FP8_GEMM_TILE=256x256:t forces it; M=4160, N=3848 gives 17 x 16 = 272 tiles,
+# 16 of them in the tail, and K=4112 gives 33 K steps (the last one partial) in 7 pieces.
+TAIL_M, TAIL_N, TAIL_K = 4160, 3848, 4112
+
+
+def _tail_pieces(M, N, K):
+    """Pieces per tail tile of the forced tail plan, read back from its workspace size."""
+    tiles = -(-M // 256) * -(-N // 256)
+    tails = tiles % 256
+    ws = ops._lib.lib().bf8_gemm_workspace(M, N, K)
+    assert ws % (tails * 256 * 256 * 4) == 0, "not a tail-split plan"
+    return ws // (tails * 256 * 256 * 4)
+
+
+@pytest.mark.parametrize("fa,bias", [(ops.E4M3, False), (ops.E4M3, True), (ops.E5M2, False)])
+def test_tail_split(gpu, monkeypatch, fa, bias):
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:t")
+    assert _tail_pieces(TAIL_M, TAIL_N, TAIL_K) == 7
+    _gemm_case(gpu, TAIL_M, TAIL_N, TAIL_K, fa=fa, seed=61, bias=bias,
+               a_std=1e-3 if fa == ops.E5M2 else 1.0)
+
+
+def test_tail_split_deterministic_and_segments(gpu, monkeypatch):
+    """Repeated calls agree bit for bit (pieces are summed in order), and per-segment weight
+    scales (fused QKV) reach the tail tiles' reduction."""
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:t")
+    M, K = TAIL_M, 4096  # 32 K steps: 8 pieces of 4
+    g = torch.Generator().manual_seed(62)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    ws = [(torch.randn(n, K, generator=g) * s).to(torch.bfloat16)
+          for n, s in ((2048, 0.02), (1024, 0.5), (776, 0.001))]
+    N = sum(w.shape[0] for w in ws)
+    assert _tail_pieces(M, N, K) == 8
+    xq = _quant(x, ops.E4M3, gpu)
+    metas = ops.new_meta(gpu, 3)
+    w8 = torch.empty(N, K, dtype=torch.float8_e4m3fn, device=gpu)
+    start, ends = 0, []
+    for i, w in enumerate(ws):
+        ops.quantize(w.to(gpu), ops.E4M3, meta=metas[i], out=w8[start:start + w.shape[0]])
+        start += w.shape[0]
+        ends.append(start)
+    outs = [ops.gemm(xq.data, 0, xq.meta, w8, 0, metas[0], out_dtype=torch.float32,
+                     seg_ends=ends, b_meta_stride=4) for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    rx, _, sx, _ = orc.quantize(x, ops.E4M3)
+    start = 0
+    for w in ws:
+        rw, _, sw, _ = orc.quantize(w, ops.E4M3)
+        _assert_fp32_close(outs[0][:, start:start + w.shape[0]], orc.scaled_mm(rx, sx, 0, rw, sw, 0),
+                           what=f"tail segment {start}")
+        start += w.shape[0]
+
+
+def test_tail_split_auto_plan_c5_dgrad(gpu):
+    """The automatic plan of c5's dX GEMM (M=8192, N=2560, K=20480, e5m2 x e4m3) is a tail
+    split: 256 whole 256x256 tiles and 64 tail tiles in 4 pieces."""
+    assert _tail_pieces(8192, 2560, 20480) == 4

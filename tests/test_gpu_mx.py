@@ -96,6 +96,15 @@ def test_gemm_mx_bias(gpu):
     _mx_gemm_case(gpu, 200, 256, 512, seed=5, bias=True)
 
 
+def test_gemm_mx_tail_split(gpu, monkeypatch):
+    """MX operands under the tail split (272 tiles of 256x256, 16 of them split along K):
+    the tail tiles' pieces are reduced with unit scales."""
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:t")
+    M, N, K = 4160, 3848, 4096
+    assert ops._lib.lib().bf8_gemm_mx_workspace(M, N, K) % (16 * 256 * 256 * 4) == 0
+    _mx_gemm_case(gpu, M, N, K, seed=63, bias=True)
+
+
 @pytest.mark.parametrize("M,I,K", [(300, 384, 512), (512, 1024, 2560), (64, 128, 96)])
 def test_gemm_geglu_mx(gpu, M, I, K):
     g = torch.Generator().manual_seed(M + I)

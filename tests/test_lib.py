@@ -77,6 +77,22 @@ def test_plan_override_env(monkeypatch):
     assert L.bf8_geglu_partials(300, 384) != 2 * 5  # 384 % 80 != 0: the automatic plan
 
 
+def test_tail_split_plans(monkeypatch):
+    """Tail-split plans (whole 256x256 tiles, the partial last round's tiles split along K)
+    size their workspace as [tail tiles x pieces][256][256] fp32: c5's dX and dW_gu GEMMs
+    take one automatically; c2's down projection (160 tiles, one round) does not;
+    BONGARD_FP8_GEMM_TILE=256x256:t forces one where the shape has a tail."""
+    L = _lib.lib()
+    tile = 256 * 256 * 4
+    monkeypatch.delenv("BONGARD_FP8_GEMM_TILE", raising=False)
+    assert L.bf8_gemm_workspace(8192, 2560, 20480) == 64 * 4 * tile   # 320 tiles: 256 + 64
+    assert L.bf8_gemm_workspace(20480, 2560, 8192) == 32 * 8 * tile   # 800 tiles: 768 + 32
+    assert L.bf8_gemm_workspace(4096, 2560, 10240) == 0
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:t")
+    assert L.bf8_gemm_workspace(4160, 3848, 4112) == 16 * 7 * tile   # 33 K steps in 7 pieces
+    assert L.bf8_gemm_workspace(4096, 4096, 4096) == 0                # 256 tiles: no tail
+
+
 def test_quantize_many_rejects_bad_arguments():
     """The multi-tensor quantization checks its lists on the host (no launch)."""
     L = _lib.lib()
