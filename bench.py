@@ -96,10 +96,13 @@ def _timed(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
-def _graph_timed(torch, fn, steps, warmup):
-    """(seconds per replay, verified) for ``fn`` captured once as a HIP graph.
+def _graph_timed(torch, fn, steps, warmup, per_graph=1):
+    """(seconds per call, verified) for ``fn`` captured as a HIP graph of ``per_graph``
+    back-to-back calls and replayed ``steps`` times.
 
-    The replay's output must equal an eager call's bit for bit, else the time is not used.
+    Several calls per graph keep the host's graph-launch cost out of the figure for steps
+    of a few microseconds (the device time is what is measured). The replay's (last) output
+    must equal an eager call's bit for bit, else the time is not used.
     """
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -110,7 +113,8 @@ def _graph_timed(torch, fn, steps, warmup):
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out = fn()
+        for _ in range(per_graph):
+            out = fn()
     eager = fn().clone()
     torch.cuda.synchronize()
     graph.replay()
@@ -123,7 +127,17 @@ def _graph_timed(torch, fn, steps, warmup):
     for _ in range(steps):
         graph.replay()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps, ok
+    return (time.perf_counter() - t0) / steps / per_graph, ok
+
+
+# Calls per captured graph for the few-microsecond steps (c1, c4): device time without the
+# host's per-replay launch cost.
+GRAPH_CALLS = 20
+
+
+def _first(out):
+    """The first tensor of an op's result (gemm_geglu returns a tuple)."""
+    return out[0] if isinstance(out, tuple) else out
 
 
 def _ev_time(torch, fn, n):
@@ -364,16 +378,24 @@ def _bench_c1(torch, ops, workloads, dev, steps=50):
         return ops.gemm(xq.data, 0, xq.meta, wq.data, 0, wq.meta)
 
     s = _timed(torch, step, steps, 5)
-    s_graph, graph_ok = _graph_timed(torch, step, steps, 5)
+    s_graph1, graph1_ok = _graph_timed(torch, step, steps, 5)
+    s_graph, graph_ok = _graph_timed(torch, step, steps, 5, per_graph=GRAPH_CALLS)
     xq, wq = ops.quantize(x, ops.E4M3), ops.quantize(w, ops.E4M3)
-    g = _ev_time(torch, lambda: ops.gemm(xq.data, 0, xq.meta, wq.data, 0, wq.meta), steps)
+    g, g_ok = _graph_timed(torch, lambda: ops.gemm(xq.data, 0, xq.meta, wq.data, 0, wq.meta),
+                           steps, 5, per_graph=GRAPH_CALLS)
     flop = 2.0 * M * N * K
     return {"workload": f"linear [{M},{K}] x [{N},{K}]^T, both quantized per call",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
             "us_per_step_graph": round(s_graph * 1e6, 2) if graph_ok else None,
-            "gemm_us": round(g * 1e6, 2), "gemm_tflops": round(flop / g / 1e12, 1),
-            "note": "eager launches are host-bound at this size (five small kernels from "
-                    "Python); the graph replay shows the device time of the same step"}
+            "tflops_graph": round(flop / s_graph / 1e12, 1) if graph_ok else None,
+            "us_per_step_graph_one_step_per_replay": (round(s_graph1 * 1e6, 2)
+                                                      if graph1_ok else None),
+            "gemm_us": round(g * 1e6, 2) if g_ok else None,
+            "gemm_tflops": round(flop / g / 1e12, 1) if g_ok else None,
+            "note": "eager launches are host-bound at this size (three small kernels from "
+                    f"Python); graph figures are device time: {GRAPH_CALLS} steps (or GEMMs) "
+                    "per captured graph, so the host's graph-launch cost stays out; one step "
+                    "per replay is host-bound on the graph launch"}
 
 
 def _qkv_weight(torch, ops, c, dev):
@@ -452,7 +474,7 @@ def _bench_c4(torch, ops, workloads, dev, steps=50):
     }
     out, tot_s, tot_b, tot_f = {}, 0.0, 0.0, 0.0
     for name, (fn, N, KK, full_out) in gemms.items():
-        t = _ev_time(torch, fn, steps)
+        t, _ok = _graph_timed(torch, lambda fn=fn: _first(fn()), steps, 5, per_graph=GRAPH_CALLS)
         out_cols = N if full_out else N // 2
         nbytes = N * KK + M * KK + 2 * M * out_cols  # fp8 W + fp8 X + bf16 out
         f = 2.0 * M * N * KK
@@ -469,7 +491,7 @@ def _bench_c4(torch, ops, workloads, dev, steps=50):
         outs = [fn() for fn, _, _, _ in gemms.values()]
         return outs[-1]
 
-    s_graph, graph_ok = _graph_timed(torch, all_four, steps, 5)
+    s_graph, graph_ok = _graph_timed(torch, all_four, steps, 5, per_graph=GRAPH_CALLS)
     g_gbps = tot_b / s_graph / 1e9 if graph_ok else None
 
     # the same step with the activations' current-scaling quantization inside it (X, the
@@ -482,7 +504,7 @@ def _bench_c4(torch, ops, workloads, dev, steps=50):
         hq2 = ops.cast_partials(H2, hp2, ops.E4M3)
         return ops.gemm(hq2.data, 0, hq2.meta, dq.data, 0, dq.meta)
 
-    s_q, q_ok = _graph_timed(torch, with_quant, steps, 5)
+    s_q, q_ok = _graph_timed(torch, with_quant, steps, 5, per_graph=GRAPH_CALLS)
     q_bytes = tot_b + 3.0 * M * (K + oq.cols + I)   # + X, attention output, H casts
     return {"workload": "decoder-branch GEMMs at M=512 (QKV, O, gate/up+GELU, down), "
                         "pre-quantized e4m3 weights",
@@ -496,7 +518,8 @@ def _bench_c4(torch, ops, workloads, dev, steps=50):
             "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "tflops": round(tot_f / tot_s / 1e12, 1),
             "mfma_frac": round(tot_f / tot_s / 1e12 / FP8_PEAK_TFLOPS, 4),
             "note": "arithmetic intensity 600-1000 FLOP/B is above the 625 FLOP/B ridge for "
-                    "most of these GEMMs, so the MFMA roof binds before HBM"}
+                    "most of these GEMMs, so the MFMA roof binds before HBM; every figure is "
+                    f"device time from graphs of {GRAPH_CALLS} calls (or steps) per replay"}
 
 
 def _bench_c5(torch, workloads, dev, steps=10):
@@ -636,10 +659,11 @@ def _bench_c1_rowwise(torch, ops, workloads, dev, steps=50):
         return ops.gemm_axiswise(xq.data, 0, xq.row_sinv, wq.data, 0, wq.row_sinv)
 
     s = _timed(torch, step, steps, 5)
-    s_graph, graph_ok = _graph_timed(torch, step, steps, 5)
+    s_graph, graph_ok = _graph_timed(torch, step, steps, 5, per_graph=GRAPH_CALLS)
     xq, wq = ops.quantize_axiswise(x, ops.E4M3), ops.quantize_axiswise(w, ops.E4M3)
-    gs = _ev_time(torch, lambda: ops.gemm_axiswise(xq.data, 0, xq.row_sinv, wq.data, 0,
-                                                   wq.row_sinv), steps)
+    gs, _ok = _graph_timed(torch, lambda: ops.gemm_axiswise(xq.data, 0, xq.row_sinv, wq.data, 0,
+                                                            wq.row_sinv), steps, 5,
+                           per_graph=GRAPH_CALLS)
     flop = 2.0 * M * N * K
     a = workloads.config5()["x"].to(dev)
     R, C = a.shape
