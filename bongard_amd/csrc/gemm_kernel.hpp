@@ -74,9 +74,12 @@ __host__ __device__ inline void walk_tile(int tiles_m, int tiles_n, int id, int&
 // before the epilogue (two pipelines per CU for the short K loops of skinny GEMMs). OCC
 // workgroups share a CU (the register budget per wave is 512 / (OCC * KG) VGPRs, LDS
 // 160 KB / OCC).
-template <int WM_, int WN_, int FM_, int FN_, int NS_, int OCC_, int KG_ = 1>
+template <int WM_, int WN_, int FM_, int FN_, int NS_, int OCC_, int KG_ = 1, int XB_ = 0>
 struct GemmTile {
   static constexpr int WM = WM_, WN = WN_, FM = FM_, FN = FN_, NS = NS_, OCC = OCC_, KG = KG_;
+  // XB extra LDS slots for B tiles only: B (the operand streamed from HBM in the skinny
+  // gated-GELU GEMM) then loads NS + XB - 1 steps ahead, A NS - 1
+  static constexpr int XB = XB_;
   static constexpr int BM = WM * FM * 32, BN = WN * FN * 32;
   static_assert(WM * WN == 4, "four waves per group");
   static_assert(KG == 1 || KG == 2, "one or two K groups");

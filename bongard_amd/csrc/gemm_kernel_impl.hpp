@@ -389,7 +389,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads * T::KG, kThreads
                           amdgpu_waves_per_eu(T::OCC * T::KG, T::OCC * T::KG))) void
 gemm_kernel(GemmParams p) {
   constexpr int BM = T::BM, BN = T::BN, FM = T::FM, FN = T::FN, WM = T::WM, NS = T::NS;
-  constexpr int KG = T::KG;
+  constexpr int KG = T::KG, XB = T::XB;
+  constexpr int NSB = NS + XB;  // B slots: the NS stages' B parts, then XB B-only slots
   static_assert(KG == 1 || (EPI == EPI_LINEAR && !MX), "K groups: linear epilogues only");
   constexpr int kA = BM * kBK;               // A tile bytes per stage
   // MX: each stage also holds the E8M0 block scales of its K step: one dword (4 blocks of
@@ -405,9 +406,13 @@ gemm_kernel(GemmParams p) {
                 "and up halves are whole runs of 8 columns");
   static_assert(!(EPI == EPI_GEGLU && MX && FN % 2 != 0), "MX GEGLU: 32-column H blocks per tile");
   static_assert(!MX || (BM <= 256 && BN <= 256), "MX scale rows: one dword per lane");
+  static_assert(XB == 0 || (NS == 2 && KG == 1 && !MX), "extra B slots: two stages, one K group");
   constexpr int kStageOff = extra_lds<EPI>();  // GEGLU: the gelu table, then the stages
-  static_assert((KG * NS * kStage + extra_lds<EPI>()) * T::OCC <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[KG * NS * kStage + extra_lds<EPI>()];
+  constexpr int kB = BN * kBK;  // B tile bytes per stage
+  static_assert((KG * NS * kStage + XB * kB + extra_lds<EPI>()) * T::OCC <= 160 * 1024,
+                "LDS budget");
+  __shared__ __attribute__((aligned(1024)))
+  uint8_t smem[KG * NS * kStage + XB * kB + extra_lds<EPI>()];
 
   // Dequant scales: read at the start, so their latency hides behind the first loads.
   const float sa = MX ? 1.0f : *p.a_sinv;
@@ -502,12 +507,13 @@ gemm_kernel(GemmParams p) {
   // Load x of a stage (x < DA: A block x, DA <= x < DA + DB: B block x - DA, then (MX)
   // the A and B scale dwords). `kill` zero-fills data, `kill_sc` the scales (a partial
   // last K step keeps the scales of its blocks within K).
-  auto dma_load = [&](int x, uint8_t* stage, uint32_t k0, bool kill, bool kill_sc) {
+  auto dma_load = [&](int x, uint8_t* stage, uint32_t k0, bool kill, bool kill_sc,
+                      uint8_t* bdst) {
     const uint32_t base = lds_addr(stage);
     if (x < DA)
       dma16(ra, base + (x * 4 + wid) * 1024, kill ? kOob : a_off[x], k0);
     else if (x < DA + DB)
-      dma16(rb, base + kA + ((x - DA) * 4 + wid) * 1024, kill ? kOob : b_off[x - DA], k0);
+      dma16(rb, lds_addr(bdst) + ((x - DA) * 4 + wid) * 1024, kill ? kOob : b_off[x - DA], k0);
     else if (x == DA + DB)
       dma4(srd_sa, base + kData + wid * 256, kill_sc ? kOob : sa_off, k0 >> 5);
     else
@@ -521,6 +527,16 @@ gemm_kernel(GemmParams p) {
     return kstep(ls) >= nsteps || (gstep(ls) == ksteps - 1 && lane_ktail_dead);
   };
   auto stage_ptr = [&](int ls) { return smem + kStageOff + (kg * NS + ls % NS) * kStage; };
+  // the B tile of local step ls: the B part of a stage slot, or (XB) a B-only slot
+  auto b_ptr = [&](int ls) {
+    if constexpr (XB == 0) {
+      return stage_ptr(ls) + kA;
+    } else {
+      const int slot = ls % NSB;
+      return slot < NS ? smem + kStageOff + slot * kStage + kA
+                       : smem + kStageOff + NS * kStage + (slot - NS) * kB;
+    }
+  };
 
   // B-tile row of each of the wave's n-subtiles; GEGLU puts gate rows in the first half
   // of the B tile and the matching up rows in the second (even FN: each wave takes its
@@ -533,14 +549,14 @@ gemm_kernel(GemmParams p) {
     else
       brow[s] = wn * FN * 32 + s * 32;
   }
-  auto read_one = [&](Frags<NH>& f, const uint8_t* stage, int kk, int h) {
+  auto read_one = [&](Frags<NH>& f, const uint8_t* stage, const uint8_t* btile, int kk, int h) {
     const int fr = h >> 1;  // 0: b0, 1..FM: a0.., FM+1..: b1..
     if (fr == 0)
-      f.h[h] = read_half(stage + kA, brow[0], kk, h & 1, lane, MX);
+      f.h[h] = read_half(btile, brow[0], kk, h & 1, lane, MX);
     else if (fr <= FM)
       f.h[h] = read_half(stage, wave_m0 + (fr - 1) * 32, kk, h & 1, lane, MX);
     else
-      f.h[h] = read_half(stage + kA, brow[fr - FM], kk, h & 1, lane, MX);
+      f.h[h] = read_half(btile, brow[fr - FM], kk, h & 1, lane, MX);
   };
 
   v16f acc[FN][FM];
@@ -606,17 +622,25 @@ gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int x = 0; x < ND; ++x)
       dma_load(x, stage_ptr(ls), (uint32_t)gstep(ls) * kBK, stage_kill(ls),
-               kstep(ls) >= nsteps);
+               kstep(ls) >= nsteps, b_ptr(ls));
   }
-  // stage 0 landed: the NS-1 later stages (ND loads each) may still be in flight
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 1)) : "memory");
+  // (XB) the B tiles of steps NS .. NSB-1
+#pragma unroll
+  for (int ls = NS; ls < NSB; ++ls) {
+#pragma unroll
+    for (int x = DA; x < DA + DB; ++x)
+      dma_load(x, nullptr, (uint32_t)gstep(ls) * kBK, stage_kill(ls), true, b_ptr(ls));
+  }
+  // stage 0 landed: the NS-1 later stages (ND loads each) and the XB B tiles may still be
+  // in flight
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 1) + DB * XB) : "memory");
   __syncthreads();
   Frags<NH> f0, f1;
   // same read order as the loop's second half, so that the wait counts at the loop header
   // agree on both incoming paths
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
-    read_one(f0, stage_ptr(0), 0, h);
+    read_one(f0, stage_ptr(0), b_ptr(0), 0, h);
     __builtin_amdgcn_sched_barrier(0);
   }
   read_scales(stage_ptr(0), scA, scB);
@@ -624,6 +648,8 @@ gemm_kernel(GemmParams p) {
     constexpr bool kDma = decltype(with_dma)::value;
     uint8_t* cur = stage_ptr(ls);
     uint8_t* nxt = stage_ptr(ls + 1);
+    uint8_t* curb = b_ptr(ls);
+    uint8_t* nxtb = b_ptr(ls + 1);
     __builtin_amdgcn_sched_barrier(0);
     // the first half's reads sit between its first NR MFMAs, so that they have landed
     // (their wait precedes the barrier) while the last MFMAs still run
@@ -632,12 +658,15 @@ gemm_kernel(GemmParams p) {
     for (int x = 0; x < NM; ++x) {
       mma_one(f0, x, std::integral_constant<int, 0>{});
 #pragma unroll
-      for (int h = x * NH / NR; h < (x + 1) * NH / NR && h < NH; ++h) read_one(f1, cur, 1, h);
+      for (int h = x * NH / NR; h < (x + 1) * NH / NR && h < NH; ++h)
+        read_one(f1, cur, curb, 1, h);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // stage ls+1 landed (stages ls+2 .. ls+NS-1 may still be in flight)
+    // stage ls+1 landed (stages ls+2 .. ls+NS-1 may still be in flight; with XB, each
+    // step's loads are A of step ls+NS then B of step ls+NSB, so the B tile of step ls+2
+    // issued after A of ls+1 may be too)
     if constexpr (kDma)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 2)) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ND * (NS - 2) + DB * XB) : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -645,16 +674,22 @@ gemm_kernel(GemmParams p) {
     const uint32_t kn = (uint32_t)gstep(ls + NS) * kBK;
     const bool killn = stage_kill(ls + NS);
     const bool killn_sc = kstep(ls + NS) >= nsteps;
+    const uint32_t knb = (uint32_t)gstep(ls + NSB) * kBK;  // = kn without XB
+    const bool killnb = stage_kill(ls + NSB);
     read_scales(nxt, scA_n, scB_n);
 #pragma unroll
     for (int x = 0; x < NM; ++x) {
       mma_one(f1, x, std::integral_constant<int, 1>{});
 #pragma unroll
-      for (int h = x * NH / NM; h < (x + 1) * NH / NM; ++h) read_one(f0, nxt, 0, h);
+      for (int h = x * NH / NM; h < (x + 1) * NH / NM; ++h) read_one(f0, nxt, nxtb, 0, h);
       if constexpr (kDma) {
 #pragma unroll
-        for (int d = x * ND / NM; d < (x + 1) * ND / NM; ++d)
-          dma_load(d, cur, kn, killn, killn_sc);
+        for (int d = x * ND / NM; d < (x + 1) * ND / NM; ++d) {
+          if (XB == 0 || d < DA)
+            dma_load(d, cur, kn, killn, killn_sc, curb);
+          else
+            dma_load(d, cur, knb, killnb, true, curb);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -998,16 +1033,24 @@ int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
 
 // The tile T with one stage fewer when the variant's stages (MX: + 2 KB of scale dwords
 // each) and its extra LDS (the gelu table of the GEGLU epilogue) would overflow the LDS.
+// A gated-GELU tile cut to two stages keeps a third slot for B tiles alone when it fits
+// (the 256x160 tile of skinny gate/up GEMMs, whose B rows stream from HBM: B then loads
+// two steps ahead).
 template <class T, int EPI, bool MX>
 struct FitTile {
-  static constexpr int bytes(int ns) {
-    return (ns * ((T::BM + T::BN) * kBK + (MX ? 2048 : 0)) + extra_lds<EPI>()) * T::OCC;
+  static constexpr int bytes(int ns, int xb = 0) {
+    return (ns * ((T::BM + T::BN) * kBK + (MX ? 2048 : 0)) + xb * T::BN * kBK +
+            extra_lds<EPI>()) * T::OCC;
   }
   // 256 bytes stay free for the epilogue's block reductions
   static constexpr int kLimit = 160 * 1024 - 256;
-  using type = std::conditional_t<bytes(T::NS) <= kLimit, T,
-                                  GemmTile<T::WM, T::WN, T::FM, T::FN, T::NS - 1, T::OCC, T::KG>>;
-  static_assert(bytes(type::NS) <= kLimit, "stages do not fit the LDS");
+  static constexpr bool kCut = bytes(T::NS) > kLimit;
+  static constexpr int kXB = (kCut && EPI == EPI_GEGLU && !MX && T::NS - 1 == 2 && T::KG == 1 &&
+                              bytes(T::NS - 1, 1) <= kLimit) ? 1 : 0;
+  using type = std::conditional_t<!kCut, T,
+                                  GemmTile<T::WM, T::WN, T::FM, T::FN, T::NS - 1, T::OCC, T::KG,
+                                           kXB>>;
+  static_assert(bytes(type::NS, type::XB) <= kLimit, "stages do not fit the LDS");
 };
 
 template <class T>
