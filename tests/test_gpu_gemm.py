@@ -310,6 +310,15 @@ def test_geglu_tiles(gpu, monkeypatch, tile):
     _geglu_case(gpu, 300, I, 528, seed=11)
 
 
+@pytest.mark.parametrize("K", [64, 128, 256, 384, 640])
+def test_geglu_b_ahead_short_k(gpu, monkeypatch, K):
+    """The 256x160 gated-GELU tile loads B two steps ahead (a third LDS slot for B alone):
+    K loops shorter than, equal to and just past its pipeline (1 to 5 steps, a partial last
+    step at K = 64) against the oracle."""
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x160")
+    _geglu_case(gpu, 300, 640, K, seed=K)
+
+
 def test_skinny_down_projection_auto_plan(gpu):
     """c4's down projection (M=512, K=10240): the automatic plan splits K."""
     assert ops._lib.lib().bf8_gemm_workspace(512, 2560, 10240) > 0
