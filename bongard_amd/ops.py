@@ -13,6 +13,8 @@ Float8CurrentScaling behind bongard/te_linear.py:38-39,73-74.
 """
 
 import ctypes
+import functools
+import os
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
@@ -53,12 +55,62 @@ class Fp8Tensor:
         return self.meta[0]
 
 
+# Host cost matters at small shapes (eager forwards of a few microseconds of GPU work):
+# pointers and streams go to the C ABI as plain integers (ctypes converts them for the
+# void* parameters), the current stream is read through torch's raw-handle accessor, and
+# the plan-dependent counts are cached per shape.
 def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    return t.data_ptr() if t is not None else None
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _dev_index(device=None):
+    if device is None:
+        return torch.cuda.current_device()
+    if not isinstance(device, torch.device):
+        device = torch.device(device)
+    return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def _stream(device=None):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The caller's current HIP stream on ``device`` as an integer handle."""
+    idx = _dev_index(device)
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(idx).cuda_stream
+
+
+def _stream_key(device):
+    idx = _dev_index(device)
+    return idx, _stream(idx)
+
+
+def _tile_override():
+    # the GEMM planner reads this variable on every call; cached counts follow it
+    return os.environ.get("BONGARD_FP8_GEMM_TILE", "")
+
+
+@functools.lru_cache(maxsize=4096)
+def _amax_partials_cached(n):
+    return int(_lib.lib().bf8_amax_partials(n))
+
+
+@functools.lru_cache(maxsize=4096)
+def _many_partials_cached(sizes):
+    return int(_lib.lib().bf8_quantize_many_partials(
+        len(sizes), (ctypes.c_int64 * len(sizes))(*sizes)))
+
+
+@functools.lru_cache(maxsize=4096)
+def _gemm_ws_cached(M, N, K, override):
+    return int(_lib.lib().bf8_gemm_workspace(M, N, K))
+
+
+@functools.lru_cache(maxsize=4096)
+def _geglu_partials_cached(M, I, override):
+    return int(_lib.lib().bf8_geglu_partials(M, I))
 
 
 def _require_gpu(*tensors):
@@ -111,7 +163,7 @@ def _bf16_2d(x):
 
 
 def amax_partials_count(n):
-    return int(_lib.lib().bf8_amax_partials(int(n)))
+    return _amax_partials_cached(int(n))
 
 
 def new_meta(device, count=1):
@@ -125,8 +177,7 @@ _PARTIALS = {}
 
 
 def partials_buffer(count, device):
-    device = torch.device(device)
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    key = _stream_key(device)
     buf = _PARTIALS.get(key)
     if buf is None or buf.numel() < count:
         buf = torch.empty(max(int(count), 4096), dtype=torch.int32, device=device)
@@ -140,8 +191,7 @@ _GEMM_WS = {}
 
 
 def gemm_workspace(nbytes, device):
-    device = torch.device(device)
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    key = _stream_key(device)
     buf = _GEMM_WS.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
@@ -170,7 +220,7 @@ def quantize(x, fmt=E4M3, *, rowwise=True, transpose=False, meta=None, out=None,
     _check_cast_outputs("quantize", out if rowwise else None, out_t if transpose else None,
                         rows, cols)
     L = _lib.lib()
-    parts = partials_buffer(L.bf8_amax_partials(rows * cols), dev)
+    parts = partials_buffer(_amax_partials_cached(rows * cols), dev)
     _lib.check(L.bf8_quantize_bf16(_ptr(x), rows, cols, fmt | (SCALE_POW2 if pow2 else 0),
                                    _ptr(out if rowwise else None),
                                    _ptr(out_t if transpose else None), _ptr(meta),
@@ -197,11 +247,12 @@ def quantize_many(xs, fmts=None, *, pow2=False, metas=None):
     if len(fmts) != count:
         raise ValueError("quantize_many: one format per tensor")
     if metas is None:
-        metas = [new_meta(dev) for _ in range(count)]
+        metas = new_meta(dev, count).unbind(0) if count > 1 else (new_meta(dev),)
     outs = [torch.empty(x.shape, dtype=TORCH_FP8[f], device=dev) for x, f in zip(xs, fmts)]
     L = _lib.lib()
-    n = (ctypes.c_int64 * count)(*[x.numel() for x in xs])
-    parts = partials_buffer(max(1, L.bf8_quantize_many_partials(count, n)), dev)
+    sizes = tuple(x.numel() for x in xs)
+    n = (ctypes.c_int64 * count)(*sizes)
+    parts = partials_buffer(max(1, _many_partials_cached(sizes)), dev)
     flag = SCALE_POW2 if pow2 else 0
     _lib.check(L.bf8_quantize_many_bf16(
         count, (ctypes.c_void_p * count)(*[x.data_ptr() for x in xs]), n,
@@ -268,7 +319,7 @@ def cast(x, meta, fmt=E4M3, *, rowwise=True, transpose=False, out=None, out_t=No
 
 
 def _sinv_ptr(meta):
-    return ctypes.c_void_p(meta.data_ptr() + 8)
+    return meta.data_ptr() + 8
 
 
 def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=None,
@@ -300,7 +351,7 @@ def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=N
             raise TypeError("gemm: bias must be bfloat16")
         bias = bias.contiguous()
     L = _lib.lib()
-    ws_bytes = int(L.bf8_gemm_workspace(M, N, K))
+    ws_bytes = _gemm_ws_cached(M, N, K, _tile_override())
     ws = gemm_workspace(ws_bytes, a.device) if ws_bytes else None
     ws_bytes = ws.numel() if ws is not None else 0
     _lib.check(L.bf8_gemm(_ptr(a), a_fmt, a.stride(0), _ptr(b), b_fmt, b.stride(0), M, N, K,
@@ -347,7 +398,7 @@ def quantize_axiswise(x, fmt=E4M3, *, rowwise=True, colwise=False, pow2=True):
     ws, nbytes = None, 0
     if colwise:
         nbytes = int(L.bf8_axiswise_workspace(rows, cols))
-        key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+        key = _stream_key(dev)
         ws = _AXIS_WS.get(key)
         if ws is None or ws.numel() < nbytes:
             ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
@@ -394,7 +445,7 @@ def gemm_axiswise(a, a_fmt, a_sinv, b, b_fmt, b_sinv, *, out_dtype=torch.bfloat1
             raise TypeError("gemm_axiswise: bias must be bfloat16")
         bias = bias.contiguous()
     L = _lib.lib()
-    ws_bytes = int(L.bf8_gemm_workspace(M, N, K))
+    ws_bytes = _gemm_ws_cached(M, N, K, _tile_override())
     ws = gemm_workspace(ws_bytes, a.device) if ws_bytes else None
     ws_bytes = ws.numel() if ws is not None else 0
     _lib.check(L.bf8_gemm_axiswise(_ptr(a), a_fmt, a.stride(0), _ptr(b), b_fmt, b.stride(0), M, N,
@@ -555,7 +606,7 @@ def gemm_geglu_mx_quant(x8, x_scales, w8, w_scales, intermediate, *, colwise=Fal
 
 
 def geglu_partials_count(M, intermediate):
-    return int(_lib.lib().bf8_geglu_partials(int(M), int(intermediate)))
+    return _geglu_partials_cached(int(M), int(intermediate), _tile_override())
 
 
 def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu=False,
@@ -576,7 +627,7 @@ def gemm_geglu(x8, x_meta, w8, w_meta, intermediate, *, w_meta_stride=0, keep_gu
     L = _lib.lib()
     H = torch.empty((M, I), dtype=torch.bfloat16, device=x8.device)
     GU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=x8.device) if keep_gu else None
-    count = int(L.bf8_geglu_partials(M, I))
+    count = _geglu_partials_cached(M, I, _tile_override())
     if partials is None:
         parts = torch.empty(count, dtype=torch.int32, device=x8.device)
     else:
@@ -609,7 +660,7 @@ def gemm_geglu_quant(x8, x_meta, w8, w_meta, intermediate, h_meta, *, w_meta_str
     h8t = torch.empty((I, M), dtype=TORCH_FP8[E4M3], device=dev) if transpose else None
     H = torch.empty((M, I), dtype=torch.bfloat16, device=dev) if keep_h else None
     GU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=dev) if keep_gu else None
-    count = int(L.bf8_geglu_partials(M, I))
+    count = _geglu_partials_cached(M, I, _tile_override())
     if partials is None:
         parts = torch.empty(count, dtype=torch.int32, device=dev)
     else:
