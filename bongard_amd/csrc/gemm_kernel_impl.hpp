@@ -629,7 +629,7 @@ gemm_kernel(GemmParams p) {
   for (int ls = NS; ls < NSB; ++ls) {
 #pragma unroll
     for (int x = DA; x < DA + DB; ++x)
-      dma_load(x, nullptr, (uint32_t)gstep(ls) * kBK, stage_kill(ls), true, b_ptr(ls));
+      dma_load(x, stage_ptr(ls), (uint32_t)gstep(ls) * kBK, stage_kill(ls), true, b_ptr(ls));
   }
   // stage 0 landed: the NS-1 later stages (ND loads each) and the XB B tiles may still be
   // in flight
