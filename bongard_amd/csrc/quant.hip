@@ -81,17 +81,19 @@ __device__ __forceinline__ void amax_partials_body(const uint16_t* __restrict__ 
                                                    int64_t blk, int64_t nblk) {
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   const int64_t nvec = n >> 3;
-  const int64_t stride = nblk * kNT;
+  constexpr int64_t kChunk = (int64_t)kNT * kVecPerThread;  // vectors per block pass
+  const int64_t stride = nblk * kChunk;
   uint32_t m = 0;
-  int64_t i = blk * kNT + threadIdx.x;
+  int64_t i = blk * kChunk + threadIdx.x;
   // kVecPerThread independent 16-byte loads per lane in flight (HBM latency x bandwidth
-  // needs ~32 MB in flight chip-wide), also in the last, partial round: its missing loads
-  // are zero vectors (key 0), so a tail never degrades to one load in flight at a time
-  for (; i < nvec; i += kVecPerThread * stride) {
+  // needs ~32 MB in flight chip-wide), each pass of a block one contiguous 32 KB chunk,
+  // also in the last, partial round: its missing loads are zero vectors (key 0), so a tail
+  // never degrades to one load in flight at a time
+  for (; i < nvec; i += stride) {
     uint4 v[kVecPerThread];
 #pragma unroll
     for (int j = 0; j < kVecPerThread; ++j)
-      v[j] = i + j * stride < nvec ? xv[i + j * stride] : make_uint4(0u, 0u, 0u, 0u);
+      v[j] = i + j * kNT < nvec ? xv[i + j * kNT] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int j = 0; j < kVecPerThread; ++j) m = max(m, absmax_key8(v[j]));
   }
@@ -168,28 +170,29 @@ __device__ __forceinline__ void cast_body(const uint16_t* __restrict__ x, int64_
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint4* ov = reinterpret_cast<uint4*>(out);
   const int64_t n16 = n >> 4;
-  const int64_t stride = nblk * kNT;
-  int64_t i = blk * kNT + threadIdx.x;
-  // Two 16-element groups (i, i + stride) per lane and iteration; the next iteration's
-  // four loads are issued before this one is converted, and the first iteration's before
-  // the scale is resolved (whose partial-amax reduction then overlaps them).
+  const int64_t step = 2 * nblk * kNT;  // groups per pass of the grid
+  int64_t i = blk * 2 * kNT + threadIdx.x;
+  // Two 16-element groups (i, i + kNT) per lane and iteration, so each pass of a block
+  // reads one contiguous 16 KB chunk; the next iteration's four loads are issued before
+  // this one is converted, and the first iteration's before the scale is resolved (whose
+  // partial-amax reduction then overlaps them).
   uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = a0, b0 = a0, b1 = a0;
   if (i < n16) { a0 = xv[2 * i]; a1 = xv[2 * i + 1]; }
-  if (i + stride < n16) { b0 = xv[2 * (i + stride)]; b1 = xv[2 * (i + stride) + 1]; }
+  if (i + kNT < n16) { b0 = xv[2 * (i + kNT)]; b1 = xv[2 * (i + kNT) + 1]; }
   const float scale = resolve_scale<FMT>(src, blk == 0);
   uint32_t m = 0;
-  for (; i < n16; i += 2 * stride) {
+  for (; i < n16; i += step) {
     const uint4 c0 = a0, c1 = a1, d0 = b0, d1 = b1;
-    const int64_t inext = i + 2 * stride;
+    const int64_t inext = i + step;
     if (inext < n16) { a0 = xv[2 * inext]; a1 = xv[2 * inext + 1]; }
-    if (inext + stride < n16) { b0 = xv[2 * (inext + stride)]; b1 = xv[2 * (inext + stride) + 1]; }
+    if (inext + kNT < n16) { b0 = xv[2 * (inext + kNT)]; b1 = xv[2 * (inext + kNT) + 1]; }
     if (amax_out) m = max(m, max(absmax_key8(c0), absmax_key8(c1)));
     const uint2 qc0 = quant8_bf16<FMT>(c0, scale), qc1 = quant8_bf16<FMT>(c1, scale);
     ov[i] = make_uint4(qc0.x, qc0.y, qc1.x, qc1.y);
-    if (i + stride < n16) {
+    if (i + kNT < n16) {
       if (amax_out) m = max(m, max(absmax_key8(d0), absmax_key8(d1)));
       const uint2 qd0 = quant8_bf16<FMT>(d0, scale), qd1 = quant8_bf16<FMT>(d1, scale);
-      ov[i + stride] = make_uint4(qd0.x, qd0.y, qd1.x, qd1.y);
+      ov[i + kNT] = make_uint4(qd0.x, qd0.y, qd1.x, qd1.y);
     }
   }
   if (blk == 0) {
