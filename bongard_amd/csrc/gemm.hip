@@ -338,6 +338,30 @@ __device__ __forceinline__ void reduce_store(const ReduceOut& o, float (&v)[8], 
   }
 }
 
+// v = P[0] + P[1] + ... + P[count-1] (8 fp32 at src + s * stride), summed in index order.
+// count <= kMaxSplits. Every load is issued before the first add, so the partials come in
+// one memory latency instead of one per piece.
+__device__ __forceinline__ void sum_pieces(const float* src, int64_t stride, int count,
+                                           float (&v)[8]) {
+  float4 lo[kMaxSplits], hi[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
+    if (s < count) {
+      lo[s] = *reinterpret_cast<const float4*>(src + s * stride);
+      hi[s] = *reinterpret_cast<const float4*>(src + s * stride + 4);
+    }
+  }
+  v[0] = lo[0].x; v[1] = lo[0].y; v[2] = lo[0].z; v[3] = lo[0].w;
+  v[4] = hi[0].x; v[5] = hi[0].y; v[6] = hi[0].z; v[7] = hi[0].w;
+#pragma unroll
+  for (int s = 1; s < kMaxSplits; ++s) {
+    if (s < count) {
+      v[0] += lo[s].x; v[1] += lo[s].y; v[2] += lo[s].z; v[3] += lo[s].w;
+      v[4] += hi[s].x; v[5] += hi[s].y; v[6] += hi[s].z; v[7] += hi[s].w;
+    }
+  }
+}
+
 // C = alpha(n) * sum_s P[s] + bias(n) for the split-K partials P [splits][M][N] (fp32),
 // summed in split order, so the result does not depend on which split finished first.
 // Each thread does 8 columns.
@@ -352,18 +376,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
     const int m = (int)(g / n8), n = (int)(g % n8) * 8;
     const float* src = P + (int64_t)m * N + n;
     float v[8];
-    {
-      const float4 lo = *reinterpret_cast<const float4*>(src);
-      const float4 hi = *reinterpret_cast<const float4*>(src + 4);
-      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-    }
-    for (int s = 1; s < splits; ++s) {
-      const float4 lo = *reinterpret_cast<const float4*>(src + s * stride);
-      const float4 hi = *reinterpret_cast<const float4*>(src + s * stride + 4);
-      v[0] += lo.x; v[1] += lo.y; v[2] += lo.z; v[3] += lo.w;
-      v[4] += hi.x; v[5] += hi.y; v[6] += hi.z; v[7] += hi.w;
-    }
+    sum_pieces(src, stride, splits, v);
     reduce_store<OUT>(o, v, m, n);
   }
 }
@@ -385,18 +398,8 @@ __global__ __launch_bounds__(256) void tail_reduce_kernel(const float* __restric
   const int m = tm * bm + row, n = tn * bn + col;
   if (m >= M || n >= N) return;  // N % 8 == 0: eight columns are all in or all out
   const float* src = P + (int64_t)t * pieces * bm * bn + row * bn + col;
-  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < pieces; ++s) {
-    const float4 lo = *reinterpret_cast<const float4*>(src + (int64_t)s * bm * bn);
-    const float4 hi = *reinterpret_cast<const float4*>(src + (int64_t)s * bm * bn + 4);
-    if (s == 0) {
-      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-    } else {
-      v[0] += lo.x; v[1] += lo.y; v[2] += lo.z; v[3] += lo.w;
-      v[4] += hi.x; v[5] += hi.y; v[6] += hi.z; v[7] += hi.w;
-    }
-  }
+  float v[8];
+  sum_pieces(src, (int64_t)bm * bn, pieces, v);
   reduce_store<OUT>(o, v, m, n);
 }
 
