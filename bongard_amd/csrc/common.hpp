@@ -254,6 +254,24 @@ __device__ __forceinline__ void wave_transpose64_staged(const uint32_t* lds, int
   for (int k = 0; k < 4; ++k) t[k] = make_uint4(c[k][0], c[k][1], c[k][2], c[k][3]);
 }
 
+// Tile t of a grid of tile rows x tiles_c tile columns, in tile-row-pair order: tiles 2j
+// and 2j + 1 are one tile column of the tile rows 2i and 2i + 1 (a last, odd tile row
+// alone), so the four waves of a block (four consecutive t, tiles_c even) cover a 2 x 2
+// square of 64 x 64 tiles. Each 128-byte line of a transposed output (128 rows of one
+// column) and of an fp8 row output (128 columns of one row) is then written by one block,
+// at one time, through one L2, instead of as halves from tiles far apart in the walk.
+__device__ __forceinline__ void pair_tile(int64_t t, int64_t tiles_c, int64_t tile_rows,
+                                          int64_t& tr, int64_t& tcol) {
+  const int64_t rp = t / (2 * tiles_c), rem = t - rp * 2 * tiles_c;
+  if (2 * rp + 1 < tile_rows) {
+    tr = 2 * rp + (rem & 1);
+    tcol = rem >> 1;
+  } else {
+    tr = 2 * rp;
+    tcol = rem;
+  }
+}
+
 // Wavefront (64-lane) max reduction.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll

@@ -214,7 +214,9 @@ __global__ __launch_bounds__(kNT) void cast_kernel(const uint16_t* __restrict__ 
 }
 
 // Cast with a transposed copy, over kTR x 64 tiles of x, one tile per wave (grid-stride,
-// so the grid and the number of amax partials stay bounded). Per tile:
+// so the grid and the number of amax partials stay bounded), walked in tile-row pairs
+// (pair_tile) so that a block's four waves fill whole 128-byte lines of both outputs.
+// Per tile:
 //  - the wave loads the tile as 8-row x 128-byte pieces (kTR / 8 16-byte loads in flight
 //    per lane), quantizes, stores `out` (if requested) and stages the bytes in its own LDS
 //    region;
@@ -235,12 +237,15 @@ __global__ __launch_bounds__(kNT) void cast_transpose_kernel(
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const float scale = resolve_scale<FMT>(src, blockIdx.x == 0);
   const int64_t tiles_c = (cols + kTT - 1) / kTT;
-  const int64_t ntiles = tiles_c * ((rows + kTR - 1) / kTR);
+  const int64_t tile_rows = (rows + kTR - 1) / kTR;
+  const int64_t ntiles = tiles_c * tile_rows;
   const bool t16 = (rows & 15) == 0;  // out_t rows 16-byte aligned
   uint32_t m = 0;
   for (int64_t tile_id = (int64_t)blockIdx.x * kWavesPerBlock + wid; tile_id < ntiles;
        tile_id += (int64_t)gridDim.x * kWavesPerBlock) {
-    const int64_t r0 = (tile_id / tiles_c) * kTR, c0 = (tile_id % tiles_c) * kTT;
+    int64_t ti, tj;
+    pair_tile(tile_id, tiles_c, tile_rows, ti, tj);
+    const int64_t r0 = ti * kTR, c0 = tj * kTT;
     // load k: rows 8k + (lane >> 3), 16-byte chunk lane & 7 (8 rows x 128 bytes each)
     const int ch = lane & 7;
     const int64_t c = c0 + 8 * ch;
