@@ -66,6 +66,17 @@ def test_ragged_shapes(gpu, shape):
     _check_quant(x, ops.E5M2, gpu)
 
 
+@pytest.mark.parametrize("shape", [(8256, 4160), (8261, 4160)])
+def test_transpose_grid_wraps_with_odd_tile_counts(gpu, shape):
+    # more 64 x 64 tiles than one pass of the transposing grid (8,192 waves), an odd number
+    # of tile columns, and an odd tile-row count (8256 rows: 129 tile rows; 8261: a ragged
+    # last tile row and out_t rows that are not 16-byte aligned): the tile-row-pair walk
+    # must still cover every tile once
+    g = torch.Generator().manual_seed(shape[0])
+    x = (torch.randn(*shape, generator=g) * 2).to(torch.bfloat16)
+    _check_quant(x, ops.E4M3, gpu)
+
+
 def test_odd_total_rowwise_only(gpu):
     # n % 16 != 0 exercises the scalar tail of the row-major cast (no transpose).
     g = torch.Generator().manual_seed(7)
