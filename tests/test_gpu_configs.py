@@ -84,7 +84,10 @@ def test_c2_full_step(gpu):
     full = orc.mlp_forward(x, wg, wu, wd, precise=False)
     err = y32.cpu() - full["y"]
     rel, mx = rms(err) / rms(full["y"]), err.abs().max().item() / rms(full["y"])
-    print(f"[c2 end-to-end] RMS(err)/RMS = {rel:.3e}, max|err|/RMS = {mx:.3e}", flush=True)
+    h_diff = (H.cpu().view(torch.int16) != full["h"].view(torch.int16)).float().mean().item()
+    h8_diff = (hq.data.view(torch.uint8).cpu() != full["hq"].view(torch.uint8)).float().mean().item()
+    print(f"[c2 end-to-end] RMS(err)/RMS = {rel:.3e}, max|err|/RMS = {mx:.3e}; H bf16 differing "
+          f"from the oracle chain's: {h_diff:.2e}, H8 bytes differing: {h8_diff:.2e}", flush=True)
     assert rel <= 0.005
 
 
