@@ -44,7 +44,10 @@ def _linear_op(x: Tensor, weight: Tensor, bias: Optional[Tensor], recipe: str, n
     if recipe == "tensorwise":
         y, (x8t, xs, w8t, ws) = _linear.linear_forward(x, weight, bias, None, None, need_dx,
                                                        need_dw)
-        return (y, _or_empty(x8t, x, _F8), xs, _or_empty(w8t, x, _F8), ws)
+        # without gradients x and W share one quantize launch, whose two metas are rows of
+        # one [2, 4] tensor; a custom op's outputs may not alias each other, so each meta
+        # leaves as its own 4-float copy
+        return (y, _or_empty(x8t, x, _F8), xs.clone(), _or_empty(w8t, x, _F8), ws.clone())
     y, saved = _linear.linear_axiswise_forward(x, weight, bias, recipe, need_dx, need_dw)
     if recipe == "rowwise_with_gw_hp":   # the backward reads the op's inputs themselves
         e8, e32 = x.new_empty(0, dtype=_F8), x.new_empty(0, dtype=torch.float32)

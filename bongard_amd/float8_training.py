@@ -108,10 +108,6 @@ class TrainingLinear(Float8Linear):
         return F.linear(inputs, self.weight, self.bias)
 
 
-def _training_linear_class():
-    return TrainingLinear
-
-
 def convert_to_float8_training(model, *, config, module_filter_fn):
     """Swap every selected nn.Linear for a Float8Linear sharing its parameters."""
     for parent_name, parent in list(model.named_modules()):
@@ -152,5 +148,5 @@ def enable_float8(model, recipe, *, emulate=False):
     if not converted:
         raise ValueError("FP8 found no eligible trainable text Linear modules")
     for module in converted:
-        module.__class__ = _training_linear_class()
+        module.__class__ = TrainingLinear
     return len(converted)

@@ -25,43 +25,81 @@ from .ops import E4M3, E5M2
 DEFAULT_HISTORY = 16
 
 
-def checkpoint_region():
+def _saved_tensor_hook_stack():
+    """The saved-tensor default hooks in effect, innermost first, as (pack, unpack) pairs.
+    torch exposes only the top of the stack, so the stack is popped and pushed back in
+    order (nothing runs in between). Raises if the stack cannot be read: delayed scaling
+    must not guess whether it runs in a checkpoint replay."""
+    ag = torch._C._autograd
+    try:
+        if not ag._saved_tensors_hooks_is_enabled():
+            return []       # disabled: no region can have pushed hooks either
+        popped = []
+        try:
+            while True:
+                top = ag._top_saved_tensors_default_hooks(False)
+                if top is None:
+                    break
+                ag._pop_saved_tensors_default_hooks()
+                popped.append(top)
+        finally:
+            for pack, unpack in reversed(popped):
+                ag._push_saved_tensors_default_hooks(pack, unpack)
+        return popped
+    except (AttributeError, TypeError) as e:
+        raise RuntimeError("delayed scaling: this torch build does not expose the "
+                           "saved-tensor hook stack, so a checkpoint replay cannot be "
+                           "recognised") from e
+
+
+def _closure(fn):
+    code = getattr(fn, "__code__", None)
+    if code is None or not fn.__closure__:
+        return {}
+    return dict(zip(code.co_freevars, (c.cell_contents for c in fn.__closure__)))
+
+
+def checkpoint_region(forward_role=True):
     """``(frame, recomputing)`` of the non-reentrant ``torch.utils.checkpoint`` region the
     current call runs in: ``frame`` identifies the region (None outside one) and
     ``recomputing`` is True while backward replays the region's forward. The reference
     trains with non-reentrant checkpointing of every text layer (bongard/model.py:124-132,
     234-247), so a delayed-scaling forward runs twice per step: the replay must quantize
-    with the scales of the original call and leave the histories alone. The region is read
-    from the saved-tensor hooks torch.utils.checkpoint installs (its pack hook closes over
-    the region's frame), which must be the innermost such hooks around the FP8 module."""
-    try:
-        hooks = torch._C._autograd._top_saved_tensors_default_hooks(False)
-    except (AttributeError, RuntimeError, TypeError):
-        hooks = None
-    if hooks is not None:
-        pack = hooks[0]
+    with the scales of the original call and leave the histories alone.
+
+    The region is read from the saved-tensor hooks torch.utils.checkpoint installs (its
+    pack hook closes over the region's frame): the innermost of them on the hook stack, so
+    other hooks pushed inside the region (CPU offload of activations, say) do not hide it.
+    A forward that runs inside a backward pass with no such hook around it is a replay this
+    cannot attribute (reentrant checkpointing re-runs forwards that way): for a forward
+    tensor role (``forward_role``; gradient roles are quantized inside backward by design)
+    that raises."""
+    for pack, _ in _saved_tensor_hook_stack():
         name = getattr(pack, "__qualname__", "")
-        code = getattr(pack, "__code__", None)
-        cells = {}
-        if code is not None and pack.__closure__:
-            cells = dict(zip(code.co_freevars, (c.cell_contents for c in pack.__closure__)))
         if name.startswith("_recomputation_hook"):
-            ref = cells.get("target_frame_ref")
+            ref = _closure(pack).get("target_frame_ref")
             return (ref() if ref is not None else None), True
         if name.startswith("_checkpoint_hook"):
-            return cells.get("frame"), False
+            return _closure(pack).get("frame"), False
+    if forward_role and torch._C._current_graph_task_id() != -1:
+        raise RuntimeError(
+            "delayed scaling: an FP8 forward runs inside a backward pass outside a "
+            "non-reentrant torch.utils.checkpoint region (a reentrant checkpoint replay?); "
+            "its scales would advance as for a new step. Use "
+            "torch.utils.checkpoint.checkpoint(..., use_reentrant=False).")
     return None, False
 
 
 class DelayedScaler:
     """Delayed scaling state of one tensor role (e.g. a linear's input)."""
 
-    def __init__(self, fmt, history=DEFAULT_HISTORY):
+    def __init__(self, fmt, history=DEFAULT_HISTORY, *, gradient=False):
         if fmt not in (E4M3, E5M2):
             raise ValueError(f"bad fp8 format {fmt}")
         if not 1 <= int(history) <= 1024:
             raise ValueError("amax history length must be in [1, 1024]")
         self.fmt = fmt
+        self.gradient = bool(gradient)   # quantized in backward (grad_output roles)
         self.length = int(history)
         self.state = None     # device float32 [length + 4]: history, meta
         self.recorded = 0     # amaxes pushed into the history so far
@@ -112,7 +150,7 @@ class DelayedScaler:
         leaves the history, the pending amax partials and the step count unchanged, so the
         backward sees the original bytes."""
         dev = x.device
-        frame, replay = checkpoint_region()
+        frame, replay = checkpoint_region(not self.gradient)
         if replay:
             meta = self._recorded_meta(frame)
             return ops.cast(x, meta, self.fmt, rowwise=rowwise, transpose=transpose)
@@ -143,7 +181,7 @@ class DelayedScaler:
         into ``partials_out``. A replay of a checkpointed forward calls ``replay(meta,
         partials_out)`` instead, with the meta of the original call and a throwaway partials
         buffer, and leaves the role's state unchanged."""
-        frame, again = checkpoint_region()
+        frame, again = checkpoint_region(not self.gradient)
         if again:
             if replay is None:
                 raise RuntimeError("delayed scaling: this producer cannot be replayed")
@@ -214,7 +252,7 @@ class LinearScaling:
         self.history = int(history)
         self.input = DelayedScaler(E4M3, history)
         self.weight = DelayedScaler(E4M3, history)
-        self.grad_output = DelayedScaler(E5M2, history)
+        self.grad_output = DelayedScaler(E5M2, history, gradient=True)
 
     def to_tensor(self):
         return torch.cat([getattr(self, r).to_tensor() for r in self.ROLES])

@@ -465,12 +465,20 @@ def linear_fwd_bwd(x, w, dy, *, precise=True):
     return y, dx, dw
 
 
-def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True, quant=None):
-    """Backward of ``mlp_forward`` (shared gate/up scale) through the FP8 GEMMs.
+def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True, quant=None,
+                 shared_gate_up_scale=True):
+    """Backward of ``mlp_forward`` through the FP8 GEMMs.
 
-    dH = dY8 Wd8 (bf16), dWd = dY8^T H8, (dG, dU) = autograd of the bf16 gelu chain,
-    dGU quantized to e5m2 with one scale, dX = dGU8 Wgu8, dWgu = dGU8^T X8. The weights'
-    FP8 copies are the forward's; ``quant`` quantizes the roles 'dy' and 'dgu'.
+    dH = dY8 Wd8 (bf16), dWd = dY8^T H8, (dG, dU) = autograd of the bf16 gelu chain.
+    Shared gate/up scale (TE's fused ``gate_up``, bongard/te_linear.py:90-92): dGU is
+    quantized to e5m2 with one scale, dX = dGU8 Wgu8, dWgu = dGU8^T X8.
+    Split (``shared_gate_up_scale=False``: ``BONGARD_TE_SPLIT_GATE_UP=1``, two TELinears,
+    bongard/te_linear.py:93-95,98-103; torchao's separate gate/up linears): each of dG and
+    dU is quantized to e5m2 with its own current scale, each dgrad uses its own W half and
+    that half's scale and is rounded to bf16 (a TE linear's output dtype), and dX is the
+    bf16 sum of the two (autograd adding the gradients of x's two uses); dW_gate =
+    dG8^T X8 and dW_up = dU8^T X8. The weights' FP8 copies are the forward's; ``quant``
+    quantizes the roles 'dy' and 'dgu' (split: 'dg', 'du').
     Returns fp32 (dx, dw_gate_up [2I, K], dw_down) and the bf16 dGU.
     """
     quant = quant or _current
@@ -481,12 +489,27 @@ def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True, qu
                     E4M3, precise=precise)
     dg, du = geglu_bwd(fwd["g"], fwd["u"], dh.to(torch.bfloat16))
     dgu = torch.cat([dg, du], 1)
-    gq, gs = quant("dgu", dgu, E5M2)
-    wq, wsc = fwd["wgu_q"], fwd["w_scales"][0]
-    dx = scaled_mm(gq, gs, E5M2, wq.t().contiguous(), wsc, E4M3, precise=precise)
-    dwgu = scaled_mm(gq.t().contiguous(), gs, E5M2, fwd["xq"].t().contiguous(), fwd["x_scale"],
-                     E4M3, precise=precise)
-    return dx, dwgu, dwd, dgu
+    wq = fwd["wgu_q"]
+    xqt = fwd["xq"].t().contiguous()
+    if shared_gate_up_scale:
+        gq, gs = quant("dgu", dgu, E5M2)
+        wsc = fwd["w_scales"][0]
+        dx = scaled_mm(gq, gs, E5M2, wq.t().contiguous(), wsc, E4M3, precise=precise)
+        dwgu = scaled_mm(gq.t().contiguous(), gs, E5M2, xqt, fwd["x_scale"], E4M3,
+                         precise=precise)
+        return dx, dwgu, dwd, dgu
+    I = w_gate.shape[0]
+    dx = None
+    dws = []
+    for half, (role, d) in enumerate((("dg", dg), ("du", du))):
+        q, s = quant(role, d, E5M2)
+        w_half = wq[half * I:(half + 1) * I].t().contiguous()
+        part = scaled_mm(q, s, E5M2, w_half, fwd["w_scales"][half], E4M3,
+                         precise=precise).to(torch.bfloat16)
+        dx = part if dx is None else dx + part      # bf16 + bf16: one rounding of the sum
+        dws.append(scaled_mm(q.t().contiguous(), s, E5M2, xqt, fwd["x_scale"], E4M3,
+                             precise=precise))
+    return dx.float(), torch.cat(dws, 0), dwd, dgu
 
 
 # ---------------------------------------------------------------------------------------

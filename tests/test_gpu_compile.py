@@ -25,21 +25,50 @@ def _bits(t):
     return t.view(torch.int16) if t.dtype == torch.bfloat16 else t
 
 
-def test_opcheck_linear_and_mlp(gpu):
+_OPCHECK = ("test_schema", "test_autograd_registration", "test_faketensor")
+
+
+@pytest.mark.parametrize("need_dx,need_dw", [(True, True), (False, False), (True, False),
+                                             (False, True)])
+def test_opcheck_linear_and_mlp(gpu, need_dx, need_dw):
+    """Every gradient combination: without gradients the tensorwise forward quantizes x and
+    W in one launch, and its outputs must still not alias one another (test_schema)."""
     g = torch.Generator(device=gpu).manual_seed(1)
-    x = torch.randn(64, 128, device=gpu, generator=g).to(torch.bfloat16).requires_grad_(True)
-    w = (torch.randn(96, 128, device=gpu, generator=g) * 0.05).to(torch.bfloat16).requires_grad_(True)
+    x0 = torch.randn(64, 128, device=gpu, generator=g).to(torch.bfloat16)
+    w0 = (torch.randn(96, 128, device=gpu, generator=g) * 0.05).to(torch.bfloat16)
+    x = x0.clone().requires_grad_(need_dx)
+    w = w0.clone().requires_grad_(need_dw)
     for recipe in ("tensorwise", "rowwise", "rowwise_with_gw_hp"):
         torch.library.opcheck(torch.ops.bongard_fp8.linear.default,
-                              (x, w, None, recipe, True, True),
-                              test_utils=("test_schema", "test_autograd_registration",
-                                          "test_faketensor"))
-    w_gu = (torch.randn(256, 128, device=gpu, generator=g) * 0.02).to(torch.bfloat16).requires_grad_(True)
-    w_d = (torch.randn(128, 128, device=gpu, generator=g) * 0.02).to(torch.bfloat16).requires_grad_(True)
-    torch.library.opcheck(torch.ops.bongard_fp8.geglu_mlp.default,
-                          (x, w_gu, w_d, 128, False, True, True, True),
-                          test_utils=("test_schema", "test_autograd_registration",
-                                      "test_faketensor"))
+                              (x, w, None, recipe, need_dx, need_dw), test_utils=_OPCHECK)
+    w_gu = (torch.randn(256, 128, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    w_d = (torch.randn(128, 128, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    for split in (False, True):
+        a = w_gu.clone().requires_grad_(need_dw)
+        b = w_d.clone().requires_grad_(need_dw)
+        torch.library.opcheck(torch.ops.bongard_fp8.geglu_mlp.default,
+                              (x, a, b, 128, split, need_dx, need_dw, need_dw),
+                              test_utils=_OPCHECK)
+
+
+@pytest.mark.parametrize("recipe", ["tensorwise", "rowwise", "rowwise_with_gw_hp"])
+def test_float8_linear_compiled_without_grad_matches_eager(gpu, recipe):
+    """An eval-style compiled region (no_grad, or frozen weight and input) runs the op's
+    no-gradient form: fullgraph, and bit-identical to the eager autograd function."""
+    torch._dynamo.reset()
+    block = _ExactBlock(256, 512, recipe).to(gpu).train()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(4, 64, 256, generator=g).to(torch.bfloat16).to(gpu)
+    with torch.no_grad():
+        ref = block(x)
+        got = torch.compile(block, fullgraph=True)(x)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(ref), _bits(got)), recipe
+    for p in block.parameters():          # frozen weights, input without grad
+        p.requires_grad_(False)
+    torch._dynamo.reset()
+    got = torch.compile(block, fullgraph=True)(x)
+    assert torch.equal(_bits(ref), _bits(got)), f"{recipe} (frozen)"
 
 
 def _fp8_linear(i, o, std, recipe):

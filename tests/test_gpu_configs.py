@@ -88,7 +88,12 @@ def test_c2_full_step(gpu):
     h8_diff = (hq.data.view(torch.uint8).cpu() != full["hq"].view(torch.uint8)).float().mean().item()
     print(f"[c2 end-to-end] RMS(err)/RMS = {rel:.3e}, max|err|/RMS = {mx:.3e}; H bf16 differing "
           f"from the oracle chain's: {h_diff:.2e}, H8 bytes differing: {h8_diff:.2e}", flush=True)
+    # measured: RMS 1.33e-3, max 3.48e-2, H 2.03%, H8 0.143%; the bars leave room for
+    # another accumulation order, not for a systematic error (which moves every value)
     assert rel <= 0.005
+    assert mx <= 0.05
+    assert h_diff <= 0.04
+    assert h8_diff <= 0.005
 
 
 def _qkv(gpu, c):

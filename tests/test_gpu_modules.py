@@ -155,8 +155,28 @@ def test_temlp_split_gate_up(gpu, monkeypatch):
     torch.cuda.synchronize()
     fwd = orc.mlp_forward(x, wg, wu, wd, shared_gate_up_scale=False)
     _close_requant(y, fwd["y"], "split y")
-    assert t.gate_proj.weight.grad is not None and t.up_proj.weight.grad is not None
-    assert t.gate_proj.weight.grad.shape == wg.shape
+    # backward: dG and dU each with its own e5m2 scale, per-half dgrads summed in bf16
+    rdx, rdwgu, rdwd, _ = orc.mlp_backward(fwd, x, wg, wu, wd, dy, shared_gate_up_scale=False)
+    _close_requant(xg.grad, rdx, "split dx", max_tol=0.10)
+    _close_requant(t.gate_proj.weight.grad, rdwgu[:512], "split dW_gate", max_tol=0.10)
+    _close_requant(t.up_proj.weight.grad, rdwgu[512:], "split dW_up", max_tol=0.10)
+    _close_requant(t.down.weight.grad, rdwd, "split dW_down", max_tol=0.10)
+    # the same arithmetic as one compile-visible op (split_scales=True), under Inductor
+    torch._dynamo.reset()
+    from bongard_amd import custom_ops
+    w_gu = torch.cat([wg, wu], 0).to(gpu).requires_grad_(True)
+    w_d = wd.to(gpu).requires_grad_(True)
+    xc = x.to(gpu).requires_grad_(True)
+    fn = torch.compile(lambda a, b, c: custom_ops.fp8_geglu_mlp(a, b, c, 512, True),
+                       fullgraph=True)
+    yc = fn(xc, w_gu, w_d)
+    yc.backward(dy.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(yc.view(torch.int16), y.view(torch.int16))
+    assert torch.equal(xc.grad.view(torch.int16), xg.grad.view(torch.int16))
+    dw_split = torch.cat([t.gate_proj.weight.grad, t.up_proj.weight.grad], 0)
+    assert torch.equal(w_gu.grad.view(torch.int16), dw_split.view(torch.int16))
+    assert torch.equal(w_d.grad.view(torch.int16), t.down.weight.grad.view(torch.int16))
 
 
 def test_fused_mlp_train_forward(gpu):

@@ -617,3 +617,82 @@ def test_mlp_backward_exact_dh_on_the_fp8_grid():
     h_deq = hq.view(torch.float8_e4m3fn).double() / float(hs)
     ref = dy.double().t() @ h_deq
     assert (dwd.double() - ref).abs().max() <= 1e-6 * ref.abs().max()   # fp32 output rounding
+
+
+def test_mlp_backward_split_scales_exact_on_the_fp8_grid():
+    """Split gate/up scales (BONGARD_TE_SPLIT_GATE_UP=1: two TELinears, bongard/te_linear.py
+    :93-95,98-103). x, W_gate, W_up, W_down and dy lie on their fp8 grids with power-of-two
+    scales, W_gate's (2^12) and W_up's (2^10) a factor 4 apart, so every forward GEMM and dH
+    are exact. Each of dG, dU then has its own e5m2 scale (not the one a shared dGU scale
+    would give), dW_gate / dW_up are exactly dĜ^T X / dÛ^T X with each half dequantized by
+    its own scale, and dX is the bf16 sum of the two bf16 dgrads dĜ Wg and dÛ Wu. A swapped
+    half, a W half dequantized with the other half's scale (off by exactly 4) or one shared
+    dGU scale fails the bit-for-bit checks."""
+    gen = torch.Generator().manual_seed(46)
+    M, K, I = 32, 64, 48
+    x = _grid_tensor(gen, (M, K), 7, 2.0 ** -2)
+    wg = _grid_tensor(gen, (I, K), 7, 2.0 ** -6)
+    wu = _grid_tensor(gen, (I, K), 7, 2.0 ** -4)
+    wd = _grid_tensor(gen, (K, I), 7, 2.0 ** -6)
+    dy = _grid_tensor(gen, (M, K), 7, 2.0 ** -12)
+    fwd = orc.mlp_forward(x, wg, wu, wd, shared_gate_up_scale=False)
+    assert [float(s) for s in fwd["w_scales"]] == [2.0 ** 12, 2.0 ** 10]
+    assert torch.equal(fwd["g"], (x.double() @ wg.double().t()).to(torch.bfloat16))
+    assert torch.equal(fwd["u"], (x.double() @ wu.double().t()).to(torch.bfloat16))
+    dx, dwgu, dwd, dgu = orc.mlp_backward(fwd, x, wg, wu, wd, dy, shared_gate_up_scale=False)
+    assert dx.shape == (M, K) and dwgu.shape == (2 * I, K) and dwd.shape == (K, I)
+    # dGU itself: the same exact-dH chain as the shared form
+    _, _, _, dgu_shared = orc.mlp_backward(fwd, x, wg, wu, wd, dy)
+    assert torch.equal(dgu, dgu_shared)
+    dg, du = dgu[:, :I], dgu[:, I:]
+    deq = []
+    for d in (dg, du):
+        q, _, s, _ = orc.quantize(d, E5M2)
+        deq.append(orc.dequant(q, s, E5M2).double())
+    # each half's own scale differs from the shared dGU scale, and changes the values
+    _, _, s_shared, _ = orc.quantize(dgu, E5M2)
+    q_sh = orc.cast(dg, s_shared, E5M2)
+    assert not torch.equal(orc.dequant(q_sh, s_shared, E5M2).double(), deq[0]) or \
+        not torch.equal(orc.dequant(orc.cast(du, s_shared, E5M2), s_shared, E5M2).double(),
+                        deq[1])
+    assert torch.equal(dwgu[:I], (deq[0].t() @ x.double()).float())
+    assert torch.equal(dwgu[I:], (deq[1].t() @ x.double()).float())
+    part_g = (deq[0] @ wg.double()).float().to(torch.bfloat16)
+    part_u = (deq[1] @ wu.double()).float().to(torch.bfloat16)
+    assert torch.equal(dx, (part_g + part_u).float())
+    # the shared-scale backward of the same forward would not give these bits
+    dx_sh, dwgu_sh, _, _ = orc.mlp_backward(fwd, x, wg, wu, wd, dy)
+    assert not torch.equal(dx_sh, dx) and not torch.equal(dwgu_sh, dwgu)
+
+
+def test_mlp_backward_split_scales_tracks_fp64_autograd():
+    """The split-scale chain against fp64 autograd of the unquantized MLP, with W_up's
+    scale ~25x W_gate's and dy ~1e-3: every gradient within the compounded e4m3 / e5m2
+    error; a half dequantized with the other half's scale is off by ~25x."""
+    gen = torch.Generator().manual_seed(47)
+    M, K, I = 64, 96, 80
+    x = torch.randn(M, K, generator=gen)
+    x[:, :2] *= 20.0
+    x = x.to(torch.bfloat16)
+    wg = (torch.randn(I, K, generator=gen) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(I, K, generator=gen) * 0.5).to(torch.bfloat16)
+    wd = (torch.randn(K, I, generator=gen) * 0.014).to(torch.bfloat16)
+    dy = (torch.randn(M, K, generator=gen) * 1e-3).to(torch.bfloat16)
+    fwd = orc.mlp_forward(x, wg, wu, wd, shared_gate_up_scale=False)
+    ws = [float(s) for s in fwd["w_scales"]]
+    assert ws[0] / ws[1] > 10
+    dx, dwgu, dwd, dgu = orc.mlp_backward(fwd, x, wg, wu, wd, dy, shared_gate_up_scale=False)
+    xr = x.double().requires_grad_(True)
+    wr = [t.double().requires_grad_(True) for t in (wg, wu, wd)]
+    gate, up = xr @ wr[0].t(), xr @ wr[1].t()
+    h = F.gelu(gate, approximate="tanh") * up
+    yr = h @ wr[2].t()
+    gate.retain_grad()
+    up.retain_grad()
+    yr.backward(dy.double())
+    assert _rel(fwd["y"], yr.detach()) < 0.10
+    assert _rel(dgu, torch.cat([gate.grad, up.grad], 1)) < 0.12
+    assert _rel(dx, xr.grad) < 0.15
+    assert _rel(dwgu[:I], wr[0].grad) < 0.15
+    assert _rel(dwgu[I:], wr[1].grad) < 0.15
+    assert _rel(dwd, wr[2].grad) < 0.12
