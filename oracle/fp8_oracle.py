@@ -466,7 +466,7 @@ def linear_fwd_bwd(x, w, dy, *, precise=True):
 
 
 def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True, quant=None,
-                 shared_gate_up_scale=True):
+                 shared_gate_up_scale=True, dgu=None):
     """Backward of ``mlp_forward`` through the FP8 GEMMs.
 
     dH = dY8 Wd8 (bf16), dWd = dY8^T H8, (dG, dU) = autograd of the bf16 gelu chain.
@@ -478,7 +478,8 @@ def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True, qu
     that half's scale and is rounded to bf16 (a TE linear's output dtype), and dX is the
     bf16 sum of the two (autograd adding the gradients of x's two uses); dW_gate =
     dG8^T X8 and dW_up = dU8^T X8. The weights' FP8 copies are the forward's; ``quant``
-    quantizes the roles 'dy' and 'dgu' (split: 'dg', 'du').
+    quantizes the roles 'dy' and 'dgu' (split: 'dg', 'du'). ``dgu``: a bf16 [M, 2I] to use
+    in place of the chain's own dGU (checks the GEMM stage given a kernel's dGU).
     Returns fp32 (dx, dw_gate_up [2I, K], dw_down) and the bf16 dGU.
     """
     quant = quant or _current
@@ -487,8 +488,12 @@ def mlp_backward(fwd, x_bf16, w_gate, w_up, w_down, dy_bf16, *, precise=True, qu
     dh = scaled_mm(dq, ds, E5M2, wdq.t().contiguous(), wds, E4M3, precise=precise)
     dwd = scaled_mm(dq.t().contiguous(), ds, E5M2, fwd["hq"].t().contiguous(), fwd["h_scale"],
                     E4M3, precise=precise)
-    dg, du = geglu_bwd(fwd["g"], fwd["u"], dh.to(torch.bfloat16))
-    dgu = torch.cat([dg, du], 1)
+    if dgu is None:
+        dg, du = geglu_bwd(fwd["g"], fwd["u"], dh.to(torch.bfloat16))
+        dgu = torch.cat([dg, du], 1)
+    else:
+        I = w_gate.shape[0]
+        dg, du = dgu[:, :I], dgu[:, I:]
     wq = fwd["wgu_q"]
     xqt = fwd["xq"].t().contiguous()
     if shared_gate_up_scale:
