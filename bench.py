@@ -230,7 +230,8 @@ def main():
 
     traffic = _load_traffic()
     roofline = {
-        "kernel": "gemm_kernel<256x256 tile, e4m3 x e4m3, gated-GELU epilogue> (gate/up GEMM)",
+        "kernel": "gemm_kernel<256x256 tile of eight waves, e4m3 x e4m3, gated-GELU epilogue> "
+                  "(gate/up GEMM)",
         "bound": "mfma",
         "achieved": round(achieved, 1),
         "peak": FP8_PEAK_TFLOPS,

@@ -36,6 +36,7 @@ enum TileId {
   TILE_128x64k2,
   TILE_64x128k2,
   TILE_128x128k2,
+  TILE_256x256w8,
   NUM_TILES
 };
 
@@ -63,6 +64,7 @@ constexpr TileInfo kTiles[NUM_TILES] = {
     {128, 64, 1, 0.1, 0.0, "128x64k2", false},
     {64, 128, 1, 0.1, 0.0, "64x128k2", false},
     {128, 128, 1, 0.1, 0.0, "128x128k2", false},
+    {256, 256, 1, 10.0, 9.2, "256x256w8", false},
 };
 // Whether `tile` has a gated-GELU variant for I = N / 2: tiles of 128 or 64 H columns take
 // any I (a multiple of 128); the 256x160 tile (80 gate + 80 up columns, one wave column)
@@ -115,10 +117,12 @@ Plan make_plan(int tile, int64_t M, int64_t N, int64_t ksteps, int splits) {
 // K=20480) 343.5 -> 341.0 us, dW_gu (M=20480, N=2560, K=8192) 338.8 -> 332.6 us against
 // two rounds of 256x160 tiles; a shape with a smaller tail gains more.
 constexpr double kTailStepRate256 = 11.2;
+// the eight-wave 256x256 tile on the same long-K shapes (8192^3: 394.8 -> 385.4 us)
+constexpr double kTailStepRate256w8 = 11.5;
 
 bool make_tail_plan(int tile, int64_t M, int64_t N, int64_t ksteps, Plan& p) {
   const TileInfo& ti = kTiles[tile];
-  if (tile != TILE_256x256) return false;
+  if (tile != TILE_256x256 && tile != TILE_256x256w8) return false;
   p = Plan{};
   p.tile = tile;
   p.tiles_m = (int)cdiv(M, ti.bm);
@@ -152,7 +156,8 @@ double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu, int64_t ksteps
   if (p.tail_pieces > 0) {
     // whole rounds of whole tiles, one round of pieces, the pieces' partials written and
     // read back, the reduction's launch
-    const double step_ns = 2.0 * ti.bm * ti.bn * kStepBytes / (kTailStepRate256 * 1e3);
+    const double rate = p.tile == TILE_256x256w8 ? kTailStepRate256w8 : kTailStepRate256;
+    const double step_ns = 2.0 * ti.bm * ti.bn * kStepBytes / (rate * 1e3);
     const double rounds = (double)p.full_tiles / kNumCus;
     return rounds * (ksteps + 2) * step_ns + (p.kps + 2) * step_ns + 2.0 * p.ws_bytes / 5e3 + 5000.0;
   }
@@ -208,6 +213,9 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
   bool have = false;
   for (int tile = 0; tile < NUM_TILES; ++tile) {
     if ((geglu && !geglu_tile_ok(tile, N, mx)) || (mx && !kTiles[tile].mx)) continue;
+    // the eight-wave 256x256 tile replaces the four-wave one wherever it has a variant
+    // (measured faster on every large shape, same bits); MX keeps the four-wave tile
+    if (!mx && tile == TILE_256x256) continue;
     for (int s = 1; s <= (geglu ? 1 : kMaxSplits); ++s) {
       const Plan p = make_plan(tile, M, N, geglu ? kGegluNominalSteps : ksteps, s);
       if (p.splits != s || (s > 1 && p.kps < kMinStepsPerSplit) || p.ws_bytes > ws_avail)
@@ -259,6 +267,7 @@ int launch_tile(const Plan& pl, const GemmParams& p, int epi, int out_dtype, int
     case TILE_128x64k2: return launch_gemm_tile<Tile128x64k2>(p, epi, out_dtype, fa, fb, s, mx);
     case TILE_64x128k2: return launch_gemm_tile<Tile64x128k2>(p, epi, out_dtype, fa, fb, s, mx);
     case TILE_128x128k2: return launch_gemm_tile<Tile128x128k2>(p, epi, out_dtype, fa, fb, s, mx);
+    case TILE_256x256w8: return launch_gemm_tile<Tile256x256w8>(p, epi, out_dtype, fa, fb, s, mx);
     default: return launch_gemm_tile<Tile128x128>(p, epi, out_dtype, fa, fb, s, mx);
   }
 }

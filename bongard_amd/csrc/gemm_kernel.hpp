@@ -67,13 +67,13 @@ __host__ __device__ inline void walk_tile(int tiles_m, int tiles_n, int id, int&
   tn = in_g / gm;
 }
 
-// A workgroup is KG groups of four wave64s; the four waves of a group are arranged
-// WM x WN and each owns FM x FN MFMA tiles of 32 x 32 outputs, so the block tile is
-// (WM*FM*32) x (WN*FN*32). Each group has its own NS LDS stages of (BM + BN) x 128 bytes
-// in flight; with KG = 2 the groups take alternate K steps and add their accumulators
-// before the epilogue (two pipelines per CU for the short K loops of skinny GEMMs). OCC
-// workgroups share a CU (the register budget per wave is 512 / (OCC * KG) VGPRs, LDS
-// 160 KB / OCC).
+// A workgroup is KG groups of NW = WM x WN wave64s (four, or eight: two per SIMD); the
+// waves of a group are arranged WM x WN and each owns FM x FN MFMA tiles of 32 x 32
+// outputs, so the block tile is (WM*FM*32) x (WN*FN*32). Each group has its own NS LDS
+// stages of (BM + BN) x 128 bytes in flight; with KG = 2 the groups take alternate K steps
+// and add their accumulators before the epilogue (two pipelines per CU for the short K
+// loops of skinny GEMMs). OCC workgroups share a CU (the register budget per wave is
+// 512 / (OCC * KG * NW / 4) VGPRs, LDS 160 KB / OCC).
 template <int WM_, int WN_, int FM_, int FN_, int NS_, int OCC_, int KG_ = 1, int XB_ = 0>
 struct GemmTile {
   static constexpr int WM = WM_, WN = WN_, FM = FM_, FN = FN_, NS = NS_, OCC = OCC_, KG = KG_;
@@ -81,7 +81,9 @@ struct GemmTile {
   // gated-GELU GEMM) then loads NS + XB - 1 steps ahead, A NS - 1
   static constexpr int XB = XB_;
   static constexpr int BM = WM * FM * 32, BN = WN * FN * 32;
-  static_assert(WM * WN == 4, "four waves per group");
+  static constexpr int NW = WM * WN;  // waves per K group
+  static_assert(NW == 4 || (NW == 8 && KG == 1 && OCC == 1),
+                "four waves per group, or eight (two per SIMD) in a lone one-group workgroup");
   static_assert(KG == 1 || KG == 2, "one or two K groups");
   static_assert(NS >= 2 && KG * NS * (BM + BN) * 128 * OCC <= 160 * 1024, "LDS budget");
 };
@@ -94,6 +96,9 @@ using Tile192x256 = GemmTile<2, 2, 3, 4, 2, 1>;
 using Tile128x64 = GemmTile<2, 2, 2, 1, 3, 2>;
 using Tile64x128 = GemmTile<2, 2, 1, 2, 3, 2>;
 using Tile256x128 = GemmTile<2, 2, 4, 2, 3, 1>;
+// eight waves, two per SIMD, each with 128 accumulators of the 256 x 256 tile: while one
+// wave of a SIMD waits (LDS reads, the epilogue's dependency chains) the other issues
+using Tile256x256w8 = GemmTile<2, 4, 4, 2, 2, 1>;
 // two K groups (skinny GEMMs): 8 waves, alternate K steps
 using Tile128x64k2 = GemmTile<2, 2, 2, 1, 3, 1, 2>;
 using Tile64x128k2 = GemmTile<2, 2, 1, 2, 3, 1, 2>;

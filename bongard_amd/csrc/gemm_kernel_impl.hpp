@@ -47,7 +47,6 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 constexpr int kBK = 128;       // K bytes per LDS stage
-constexpr int kThreads = 256;  // four wave64
 constexpr int kNumXcd = 8;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset that always reads as zero
 
@@ -384,12 +383,17 @@ struct GegluRuns {
   static constexpr int up_q(int k) { return kOdd ? ((BN / 2 + 8 * k) % 32) / 8 : k % 4; }
 };
 
+// Threads of a workgroup of tile T.
+template <class T>
+constexpr int tile_threads() { return T::NW * 64 * T::KG; }
+
 template <class T, int FA, int FB, int EPI, int OUT, bool MX = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads * T::KG, kThreads * T::KG),
-                          amdgpu_waves_per_eu(T::OCC * T::KG, T::OCC * T::KG))) void
+__global__ __attribute__((amdgpu_flat_work_group_size(tile_threads<T>(), tile_threads<T>()),
+                          amdgpu_waves_per_eu(T::OCC * T::KG * T::NW / 4,
+                                              T::OCC * T::KG * T::NW / 4))) void
 gemm_kernel(GemmParams p) {
   constexpr int BM = T::BM, BN = T::BN, FM = T::FM, FN = T::FN, WM = T::WM, NS = T::NS;
-  constexpr int KG = T::KG, XB = T::XB;
+  constexpr int KG = T::KG, XB = T::XB, NW = T::NW;
   constexpr int NSB = NS + XB;  // B slots: the NS stages' B parts, then XB B-only slots
   static_assert(KG == 1 || (EPI == EPI_LINEAR && !MX), "K groups: linear epilogues only");
   constexpr int kA = BM * kBK;               // A tile bytes per stage
@@ -397,7 +401,8 @@ gemm_kernel(GemmParams p) {
   // 32) per tile row, A rows at kData + 4 r, B rows at kData + 1024 + 4 r (r < 256).
   constexpr int kData = (BM + BN) * kBK;
   constexpr int kStage = kData + (MX ? 2048 : 0);  // [A tile | B tile | scales]
-  constexpr int DA = BM / 32, DB = BN / 32;  // 1 KB DMA blocks per wave per stage
+  constexpr int DA = BM / (8 * NW), DB = BN / (8 * NW);  // 1 KB DMA blocks per wave per stage
+  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "whole 1 KB blocks per wave");
   constexpr int ND = DA + DB + (MX ? 2 : 0);  // loads per wave per stage
   constexpr int NM = FM * FN;                // MFMAs per sub-step
   constexpr int NH = 2 * (FM + FN);          // 16-byte fragment halves per sub-step
@@ -406,6 +411,7 @@ gemm_kernel(GemmParams p) {
                 "and up halves are whole runs of 8 columns");
   static_assert(!(EPI == EPI_GEGLU && MX && FN % 2 != 0), "MX GEGLU: 32-column H blocks per tile");
   static_assert(!MX || (BM <= 256 && BN <= 256), "MX scale rows: one dword per lane");
+  static_assert(!MX || NW == 4, "MX scale dwords: four waves of 64 rows");
   static_assert(XB == 0 || (NS == 2 && KG == 1 && !MX), "extra B slots: two stages, one K group");
   constexpr int kStageOff = extra_lds<EPI>();  // GEGLU: the gelu table, then the stages
   constexpr int kB = BN * kBK;  // B tile bytes per stage
@@ -433,8 +439,8 @@ gemm_kernel(GemmParams p) {
 
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int kg = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane(t >> 8);  // K group (uniform)
-  const int wid = (t >> 6) & 3;           // wave within the group
+  const int kg = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane(t / (NW * 64));  // K group
+  const int wid = (t >> 6) & (NW - 1);    // wave within the group
   const int wm = wid % WM, wn = wid / WM;
   const int wave_m0 = wm * FM * 32;
 
@@ -452,20 +458,20 @@ gemm_kernel(GemmParams p) {
   const i32x4 rb = make_srd(p.B, (uint32_t)((int64_t)p.N * p.ldb));
 
   static_assert(ND * (NS - 1) < 64, "vmcnt holds at most 63 outstanding loads");
-  // DMA: lane l of the wave's j-th 1 KB block (block j*4 + wid of the tile) covers tile
+  // DMA: lane l of the wave's j-th 1 KB block (block j*NW + wid of the tile) covers tile
   // row blk*8 + l/8, physical chunk l%8. Its logical chunk swz(row, l%8) only depends on
-  // l and wid & 1 (= blk & 1), so one K mask serves every block of the lane.
+  // l and wid & 1 (= blk & 1, NW even), so one K mask serves every block of the lane.
   const int lrow = lane >> 3;
   const int lchunk = (lane & 7) ^ (((wid & 1) << 2) | (lrow >> 1));
   uint32_t a_off[DA], b_off[DB];
 #pragma unroll
   for (int j = 0; j < DA; ++j) {
-    const int am = m0 + (j * 4 + wid) * 8 + lrow;
+    const int am = m0 + (j * NW + wid) * 8 + lrow;
     a_off[j] = am < p.M ? (uint32_t)((int64_t)am * p.lda + lchunk * 16) : kOob;
   }
 #pragma unroll
   for (int j = 0; j < DB; ++j) {
-    const int r = (j * 4 + wid) * 8 + lrow;
+    const int r = (j * NW + wid) * 8 + lrow;
     int bn;
     bool bvalid;
     if (EPI == EPI_GEGLU) {
@@ -511,9 +517,9 @@ gemm_kernel(GemmParams p) {
                       uint8_t* bdst) {
     const uint32_t base = lds_addr(stage);
     if (x < DA)
-      dma16(ra, base + (x * 4 + wid) * 1024, kill ? kOob : a_off[x], k0);
+      dma16(ra, base + (x * NW + wid) * 1024, kill ? kOob : a_off[x], k0);
     else if (x < DA + DB)
-      dma16(rb, lds_addr(bdst) + ((x - DA) * 4 + wid) * 1024, kill ? kOob : b_off[x - DA], k0);
+      dma16(rb, lds_addr(bdst) + ((x - DA) * NW + wid) * 1024, kill ? kOob : b_off[x - DA], k0);
     else if (x == DA + DB)
       dma4(srd_sa, base + kData + wid * 256, kill_sc ? kOob : sa_off, k0 >> 5);
     else
@@ -609,13 +615,13 @@ gemm_kernel(GemmParams p) {
   // never used). Prologue stages past the end are zero-filled.
   if constexpr (EPI == EPI_GEGLU) {
     // the fp32 gelu table (26 KB) into LDS ahead of the stage loads, so the prologue's wait
-    // for stage 0 also covers it; wave w copies KB w, w + 4, .., below 26
+    // for stage 0 also covers it; wave w copies KB w, w + NW, .., below 26
     static_assert(kGeluA32Bytes == 26 * 1024, "gelu table copy assumes 26 KB");
     const i32x4 rt = make_srd(kGeluA32, (uint32_t)kGeluA32Bytes);
     const uint32_t tab = lds_addr(smem);
 #pragma unroll
-    for (int c = 0; c < 6; ++c) dma16(rt, tab + (wid + 4 * c) * 1024, lane * 16, (wid + 4 * c) * 1024);
-    if (wid < 2) dma16(rt, tab + (wid + 24) * 1024, lane * 16, (wid + 24) * 1024);
+    for (int c = 0; c < (26 + NW - 1) / NW; ++c)
+      if (wid + NW * c < 26) dma16(rt, tab + (wid + NW * c) * 1024, lane * 16, (wid + NW * c) * 1024);
   }
 #pragma unroll
   for (int ls = 0; ls < NS; ++ls) {
@@ -784,6 +790,7 @@ gemm_kernel(GemmParams p) {
   };
   if constexpr (EPI == EPI_LINEAR && OUT == BF8_OUT_BF16) {
     constexpr int CH = FN * 4;  // 16-byte chunks per staged row (FN*32 bf16)
+    static_assert(NW * ROWS * CH * 16 <= NS * kStage, "per-wave staging fits the ring");
     uint8_t* wbuf = smem + wid * (ROWS * CH * 16);
     const int wave_n0 = n0 + wn * FN * 32;
 #pragma unroll
@@ -895,6 +902,7 @@ gemm_kernel(GemmParams p) {
     using Runs = GegluRuns<FN, BN>;
     constexpr int RUNS = Runs::kRuns;
     constexpr int CH = RUNS;  // 16-byte chunks per staged H row (8 bf16 per run)
+    static_assert(NW * ROWS * CH * 16 <= NS * kStage, "per-wave staging fits the ring");
     uint8_t* wbuf = smem + kStageOff + wid * (ROWS * CH * 16);
     const int wave_h0 = n0 + wn * RUNS * 8;
     uint32_t hkeys = 0;  // packed max of the |H| bf16 keys staged by this lane
@@ -1002,7 +1010,7 @@ gemm_kernel(GemmParams p) {
       run_pass(std::integral_constant<int, 1>{});
       run_pass(std::integral_constant<int, 2>{});
     }
-    hmax = block_max_u32<kThreads>(hmax);
+    hmax = block_max_u32<tile_threads<T>()>(hmax);
     if (t == 0 && p.partials) p.partials[blockIdx.x] = hmax;
   }
 }
@@ -1017,7 +1025,7 @@ inline unsigned grid_blocks(const GemmParams& p) {
 
 template <class T, int EPI, int OUT>
 int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
-  const dim3 grid(grid_blocks(p)), block(kThreads * T::KG);
+  const dim3 grid(grid_blocks(p)), block(tile_threads<T>());
   if (fa == BF8_E4M3 && fb == BF8_E4M3)
     hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI, OUT>), grid, block, 0, s, p);
   else if (fa == BF8_E5M2 && fb == BF8_E4M3)
@@ -1056,7 +1064,7 @@ struct FitTile {
 template <class T>
 int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
                      hipStream_t stream, bool mx) {
-  const dim3 grid(grid_blocks(p)), block(kThreads * T::KG);
+  const dim3 grid(grid_blocks(p)), block(tile_threads<T>());
   if constexpr (T::KG != 1) {
     if (epi == EPI_GEGLU || mx) {
       set_error("gemm: tile %dx%d with two K groups has linear non-MX epilogues only", T::BM,
@@ -1070,10 +1078,15 @@ int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int
   if (epi == EPI_GEGLU) {
     if constexpr (T::FN % 2 == 0) {
       if (mx) {
-        using TG = typename FitTile<T, EPI_GEGLU, true>::type;
-        hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16, true>), grid, block, 0,
-                           stream, p);
-        return launch_status("gemm_kernel(geglu, mx)");
+        if constexpr (T::NW == 4) {
+          using TG = typename FitTile<T, EPI_GEGLU, true>::type;
+          hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16, true>), grid, block,
+                             0, stream, p);
+          return launch_status("gemm_kernel(geglu, mx)");
+        } else {
+          set_error("gemm: tile %dx%d with %d waves has no MX variant", T::BM, T::BN, T::NW);
+          return BF8_EINVAL;
+        }
       }
       using TG = typename FitTile<T, EPI_GEGLU, false>::type;
       hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16>), grid, block, 0, stream, p);
@@ -1094,15 +1107,20 @@ int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int
     }
   }
   if (mx) {
-    // MX block scales (e4m3 operands): each stage also holds 2 KB of scale dwords
-    using TM = typename FitTile<T, EPI_LINEAR, true>::type;
-    if (out_dtype == BF8_OUT_BF16)
-      hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_BF16, true>), grid, block, 0,
-                         stream, p);
-    else
-      hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_F32, true>), grid, block, 0,
-                         stream, p);
-    return launch_status("gemm_kernel(mx)");
+    if constexpr (T::NW == 4) {
+      // MX block scales (e4m3 operands): each stage also holds 2 KB of scale dwords
+      using TM = typename FitTile<T, EPI_LINEAR, true>::type;
+      if (out_dtype == BF8_OUT_BF16)
+        hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_BF16, true>), grid, block,
+                           0, stream, p);
+      else
+        hipLaunchKernelGGL((gemm_kernel<TM, 0, 0, EPI_LINEAR, BF8_OUT_F32, true>), grid, block,
+                           0, stream, p);
+      return launch_status("gemm_kernel(mx)");
+    } else {
+      set_error("gemm: tile %dx%d with %d waves has no MX variant", T::BM, T::BN, T::NW);
+      return BF8_EINVAL;
+    }
   }
   if (out_dtype == BF8_OUT_BF16) return launch_typed<T, EPI_LINEAR, BF8_OUT_BF16>(p, fmt_a, fmt_b, stream);
   return launch_typed<T, EPI_LINEAR, BF8_OUT_F32>(p, fmt_a, fmt_b, stream);

@@ -270,7 +270,7 @@ def test_mlp_down_gemm_on_own_h8(gpu):
 # BONGARD_FP8_GEMM_TILE forces the library's plan (read on every call), so each tile shape
 # and the split-K fix-up are checked on shapes with M, N and K tails.
 TILES = ["256x256", "256x160", "160x256", "128x128", "192x256", "256x128", "128x64",
-         "64x128", "128x64k2", "64x128k2", "128x128k2"]
+         "64x128", "128x64k2", "64x128k2", "128x128k2", "256x256w8"]
 
 
 @pytest.mark.parametrize("splits", [1, 3])
@@ -300,12 +300,12 @@ def test_split_k_deterministic(gpu, monkeypatch, tile):
 
 
 @pytest.mark.parametrize("tile", ["256x256", "160x256", "128x128", "192x256", "256x128",
-                                  "64x128", "256x160"])
+                                  "64x128", "256x160", "256x256w8"])
 def test_geglu_tiles(gpu, monkeypatch, tile):
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", tile)
     # 256x160 pairs 80 gate with 80 up columns (I % 80 == 0); I = 640 suits every tile
     I = 640 if tile == "256x160" else 384
-    bm, bn = (int(v) for v in tile.split("x"))
+    bm, bn = (int(v) for v in tile.split("w")[0].split("x"))
     assert ops._lib.lib().bf8_geglu_partials(300, I) == -(-300 // bm) * (I // (bn // 2))
     _geglu_case(gpu, 300, I, 528, seed=11)
 
@@ -451,9 +451,10 @@ def _tail_pieces(M, N, K):
     return ws // (tails * 256 * 256 * 4)
 
 
+@pytest.mark.parametrize("tile", ["256x256", "256x256w8"])
 @pytest.mark.parametrize("fa,bias", [(ops.E4M3, False), (ops.E4M3, True), (ops.E5M2, False)])
-def test_tail_split(gpu, monkeypatch, fa, bias):
-    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:t")
+def test_tail_split(gpu, monkeypatch, fa, bias, tile):
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", f"{tile}:t")
     assert _tail_pieces(TAIL_M, TAIL_N, TAIL_K) == 7
     _gemm_case(gpu, TAIL_M, TAIL_N, TAIL_K, fa=fa, seed=61, bias=bias,
                a_std=1e-3 if fa == ops.E5M2 else 1.0)
