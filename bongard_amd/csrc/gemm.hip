@@ -1,7 +1,7 @@
 // Host entry points of the FP8 GEMM (bf8_gemm, bf8_gemm_geglu): argument checks, the
-// choice of block tile and K split for a shape, and split-K workspace sizing. The GEMM
-// kernels (which also add up K-split partials, inside the kernel) live in
-// gemm_kernel_impl.hpp, instantiated per tile shape in gemm_tile_*.hip.
+// choice of block tile and K split for a shape, split-K workspace sizing and the split-K
+// reduction. The GEMM kernels live in gemm_kernel_impl.hpp, instantiated per tile shape
+// in gemm_tile_*.hip.
 //
 // Semantics replace torch._scaled_mm / cuBLASLt under torchao Float8Linear
 // (bongard/float8_training.py:22) and TE's FP8 GEMM under te.Linear
@@ -87,9 +87,8 @@ struct Plan {
   int kps = 0;  // K steps per split (tail split: per piece)
   int tiles_m = 0, tiles_n = 0;
   int full_tiles = 0, tail_pieces = 0;  // tail split: whole tiles, K pieces per tail tile
-  size_t ws_bytes = 0;  // split-K workspace: the arrival counters (kFoldCounterBytes),
-                        // then fp32 partials [splits][M][N] or the tail tiles' pieces
-                        // [tails * pieces][BM][BN]
+  size_t ws_bytes = 0;  // split-K workspace: fp32 partials [splits][M][N], or the tail
+                        // tiles' pieces [tails * pieces][BM][BN]
 };
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -103,7 +102,7 @@ Plan make_plan(int tile, int64_t M, int64_t N, int64_t ksteps, int splits) {
   p.tiles_n = (int)cdiv(N, ti.bn);
   p.kps = (int)cdiv(ksteps, splits);
   p.splits = (int)cdiv(ksteps, p.kps);  // no empty split
-  if (p.splits > 1) p.ws_bytes = kFoldCounterBytes + (size_t)p.splits * M * N * 4;
+  if (p.splits > 1) p.ws_bytes = (size_t)p.splits * M * N * 4;
   return p;
 }
 
@@ -137,7 +136,7 @@ bool make_tail_plan(int tile, int64_t M, int64_t N, int64_t ksteps, Plan& p) {
   if (pieces < 2 || p.kps < kMinStepsPerSplit) return false;
   p.full_tiles = (int)(T - tails);
   p.tail_pieces = pieces;
-  p.ws_bytes = kFoldCounterBytes + (size_t)tails * pieces * ti.bm * ti.bn * 4;
+  p.ws_bytes = (size_t)tails * pieces * ti.bm * ti.bn * 4;
   return true;
 }
 
@@ -160,7 +159,7 @@ double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu, int64_t ksteps
     const double rate = p.tile == TILE_256x256w8 ? kTailStepRate256w8 : kTailStepRate256;
     const double step_ns = 2.0 * ti.bm * ti.bn * kStepBytes / (rate * 1e3);
     const double rounds = (double)p.full_tiles / kNumCus;
-    return rounds * (ksteps + 2) * step_ns + (p.kps + 2) * step_ns + 2.0 * p.ws_bytes / 5e3 + 2000.0;
+    return rounds * (ksteps + 2) * step_ns + (p.kps + 2) * step_ns + 2.0 * p.ws_bytes / 5e3 + 5000.0;
   }
   const int64_t ctas = (int64_t)p.tiles_m * p.tiles_n * p.splits;
   const int64_t rounds = cdiv(ctas, (int64_t)kNumCus * ti.occ);
@@ -169,7 +168,7 @@ double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu, int64_t ksteps
   const double work_ns = per_cu * 2.0 * ti.bm * ti.bn * kStepBytes / (rate * 1e3);
   const double step_ns = std::max(work_ns, ti.occ > 1 ? kStepFloorNsOcc2 : kStepFloorNs);
   double t = (double)rounds * (p.kps + 2) * step_ns;
-  if (p.splits > 1) t += 2.0 * p.splits * M * N * 4 / 5e3 + 2000.0;
+  if (p.splits > 1) t += 2.0 * p.splits * M * N * 4 / 5e3 + 5000.0;
   return t;
 }
 
@@ -206,8 +205,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
       osplits = 1;
     }
     p = make_plan(otile, M, N, ksteps, geglu ? 1 : osplits);
-    if (p.ws_bytes > ws_avail || (int64_t)p.tiles_m * p.tiles_n > kMaxFoldTiles)
-      p = make_plan(otile, M, N, ksteps, 1);
+    if (p.ws_bytes > ws_avail) p = make_plan(otile, M, N, ksteps, 1);
     return p;
   }
   Plan best;
@@ -220,8 +218,7 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
     if (!mx && tile == TILE_256x256) continue;
     for (int s = 1; s <= (geglu ? 1 : kMaxSplits); ++s) {
       const Plan p = make_plan(tile, M, N, geglu ? kGegluNominalSteps : ksteps, s);
-      if (p.splits != s || (s > 1 && p.kps < kMinStepsPerSplit) || p.ws_bytes > ws_avail ||
-          (s > 1 && (int64_t)p.tiles_m * p.tiles_n > kMaxFoldTiles))
+      if (p.splits != s || (s > 1 && p.kps < kMinStepsPerSplit) || p.ws_bytes > ws_avail)
         continue;
       const double c = plan_cost(p, M, N, geglu);
       if (!have || c < best_cost * 0.97) {  // prefer earlier (larger, unsplit) plans on ties
@@ -255,20 +252,6 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
                  geglu ? "geglu" : "gemm", mx ? " mx" : "", (long long)M, (long long)N, (long long)K,
                  kTiles[best.tile].name, best.splits, best.tiles_m, best.tiles_n, best.tail_pieces);
   return best;
-}
-
-// Tiles whose K splits add themselves up inside the GEMM (fold_splits_in_kernel<T>): the
-// small ones of skinny GEMMs, whose registers have room for the partials' loads.
-bool tile_folds_splits(int tile) {
-  switch (tile) {
-    case TILE_128x128: return fold_splits_in_kernel<Tile128x128>();
-    case TILE_128x64: return fold_splits_in_kernel<Tile128x64>();
-    case TILE_64x128: return fold_splits_in_kernel<Tile64x128>();
-    case TILE_128x64k2: return fold_splits_in_kernel<Tile128x64k2>();
-    case TILE_64x128k2: return fold_splits_in_kernel<Tile64x128k2>();
-    case TILE_128x128k2: return fold_splits_in_kernel<Tile128x128k2>();
-    default: return false;
-  }
 }
 
 int launch_tile(const Plan& pl, const GemmParams& p, int epi, int out_dtype, int fa, int fb,
@@ -435,59 +418,48 @@ int launch_plan(const Plan& pl, GemmParams p, int epi, int out_dtype, int fa, in
   p.tiles_n = pl.tiles_n;
   p.splits = pl.splits;
   p.ksteps_per_split = pl.kps;
-  float* parts = ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kFoldCounterBytes)
-                    : nullptr;
-  if (pl.tail_pieces > 0) {
-    // whole tiles write C; the tail tiles' pieces write raw partials, which a second
-    // kernel spread over every CU adds up (one CU per tail tile would read them all alone)
-    p.full_tiles = pl.full_tiles;
-    p.tail_pieces = pl.tail_pieces;
-    p.tail_ws = parts;
-    const int rc = launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
-    if (rc != BF8_OK) return rc;
-    ReduceOut o;
-    o.a_sinv = p.a_sinv; o.b_sinv = p.b_sinv; o.b_stride = p.b_stride; o.n_seg = p.n_seg;
-    for (int i = 0; i < 4; ++i) o.seg_end.e[i] = p.seg_end[i];
-    o.bias = p.bias; o.C = p.C; o.ldc = p.ldc; o.a_vec = p.a_vec; o.b_vec = p.b_vec;
-    o.unit = mx ? 1 : 0;
-    const TileInfo& ti = kTiles[pl.tile];
-    const int tails = pl.tiles_m * pl.tiles_n - pl.full_tiles;
-    const unsigned blocks = (unsigned)(tails * (ti.bm * ti.bn / 2048));
-    if (out_dtype == BF8_OUT_BF16)
-      hipLaunchKernelGGL(tail_reduce_kernel<BF8_OUT_BF16>, dim3(blocks), dim3(256), 0, s,
-                         (const float*)parts, pl.tail_pieces, ti.bm, ti.bn, pl.full_tiles,
-                         pl.tiles_m, pl.tiles_n, p.M, p.N, o);
-    else
-      hipLaunchKernelGGL(tail_reduce_kernel<BF8_OUT_F32>, dim3(blocks), dim3(256), 0, s,
-                         (const float*)parts, pl.tail_pieces, ti.bm, ti.bn, pl.full_tiles,
-                         pl.tiles_m, pl.tiles_n, p.M, p.N, o);
-    return launch_status("tail_reduce_kernel");
-  }
-  if (pl.splits == 1) return launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
-  // K split: the partials after the counters at the workspace's start
-  p.part_ws = parts;
-  p.split_stride = (int64_t)p.M * p.N;
-  if (tile_folds_splits(pl.tile)) {
-    // the last split of each tile to finish adds them up and writes C
-    p.fold_cnt = static_cast<uint32_t*>(ws);
-    return launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
-  }
-  // large tiles: raw partials, then the ordered reduction over every CU
-  const int rc = launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
-  if (rc != BF8_OK) return rc;
   ReduceOut o;
   o.a_sinv = p.a_sinv; o.b_sinv = p.b_sinv; o.b_stride = p.b_stride; o.n_seg = p.n_seg;
   for (int i = 0; i < 4; ++i) o.seg_end.e[i] = p.seg_end[i];
   o.bias = p.bias; o.C = p.C; o.ldc = p.ldc; o.a_vec = p.a_vec; o.b_vec = p.b_vec;
   o.unit = mx ? 1 : 0;
+  if (pl.tail_pieces > 0) {
+    // whole tiles write C; the tail tiles' pieces write raw partials, reduced after
+    p.full_tiles = pl.full_tiles;
+    p.tail_pieces = pl.tail_pieces;
+    p.tail_ws = static_cast<float*>(ws);
+    const int rc = launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
+    if (rc != BF8_OK) return rc;
+    const TileInfo& ti = kTiles[pl.tile];
+    const int tails = pl.tiles_m * pl.tiles_n - pl.full_tiles;
+    const unsigned blocks = (unsigned)(tails * (ti.bm * ti.bn / 2048));
+    if (out_dtype == BF8_OUT_BF16)
+      hipLaunchKernelGGL(tail_reduce_kernel<BF8_OUT_BF16>, dim3(blocks), dim3(256), 0, s,
+                         (const float*)ws, pl.tail_pieces, ti.bm, ti.bn, pl.full_tiles,
+                         pl.tiles_m, pl.tiles_n, p.M, p.N, o);
+    else
+      hipLaunchKernelGGL(tail_reduce_kernel<BF8_OUT_F32>, dim3(blocks), dim3(256), 0, s,
+                         (const float*)ws, pl.tail_pieces, ti.bm, ti.bn, pl.full_tiles,
+                         pl.tiles_m, pl.tiles_n, p.M, p.N, o);
+    return launch_status("tail_reduce_kernel");
+  }
+  if (pl.splits == 1) return launch_tile(pl, p, epi, out_dtype, fa, fb, s, mx);
+  // K split: raw fp32 partials into the workspace, then the ordered reduction
+  GemmParams q = p;
+  q.C = ws;
+  q.ldc = p.N;
+  q.split_stride = (int64_t)p.M * p.N;
+  q.bias = nullptr;
+  const int rc = launch_tile(pl, q, EPI_LINEAR, BF8_OUT_F32, fa, fb, s, mx);
+  if (rc != BF8_OK) return rc;
   const int64_t items = (int64_t)p.M * (p.N / 8);
   const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(items, 256), 4096);
   if (out_dtype == BF8_OUT_BF16)
     hipLaunchKernelGGL(split_reduce_kernel<BF8_OUT_BF16>, dim3(blocks), dim3(256), 0, s,
-                       (const float*)parts, pl.splits, p.split_stride, p.M, p.N, o);
+                       (const float*)ws, pl.splits, q.split_stride, p.M, p.N, o);
   else
     hipLaunchKernelGGL(split_reduce_kernel<BF8_OUT_F32>, dim3(blocks), dim3(256), 0, s,
-                       (const float*)parts, pl.splits, p.split_stride, p.M, p.N, o);
+                       (const float*)ws, pl.splits, q.split_stride, p.M, p.N, o);
   return launch_status("split_reduce_kernel");
 }
 

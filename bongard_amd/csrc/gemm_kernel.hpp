@@ -42,28 +42,16 @@ struct GemmParams {
   uint8_t* h8t;
   uint8_t* h8t_sc;
   int64_t h8_sc_ld, h8t_sc_ld;
-  // K pieces of one output tile (linear epilogues). A K split (splits > 1) writes its raw
-  // fp32 sums to part_ws [splits][M][N] (split_stride = M * N elements apart); on tiles
-  // that fold splits in the kernel it then counts itself in fold_cnt[tm * tiles_n + tn],
-  // and the split that arrives last adds the tile's splits in split order, resets the
-  // counter to zero and writes C with the full epilogue (scales, bias), so the result
-  // does not depend on which split finished first (other tiles leave the sums to
-  // split_reduce_kernel, which adds them in the same order). A
-  // tail-split schedule (tail_pieces > 0, splits == 1) runs workgroups [0, full_tiles) as
-  // whole tiles at walk positions 0 .. full_tiles-1 and the others as one of tail_pieces K
-  // pieces (ksteps_per_split steps each) of the tile at walk position full_tiles + t, whose
-  // raw sums go to tail_ws[t * tail_pieces + piece] ([BM][BN] each) for tail_reduce_kernel.
-  int64_t split_stride;
-  float* part_ws;
+  int64_t split_stride;   // splits > 1: C is fp32 [splits][M][ldc], raw sums, this many
+                          // elements apart (a reduce kernel applies scales and bias)
+  // Tail-split schedule (tail_pieces > 0, linear epilogues, splits == 1): workgroups
+  // [0, full_tiles) take whole tiles, walk positions 0 .. full_tiles-1, and write C; the
+  // others take one of tail_pieces K pieces (ksteps_per_split steps each) of a tile at walk
+  // position full_tiles + t and write its raw fp32 sums to tail_ws[t * tail_pieces + piece]
+  // ([BM][BN] each), which tail_reduce_kernel adds in piece order.
   int full_tiles, tail_pieces;
   float* tail_ws;
-  uint32_t* fold_cnt;
 };
-
-// Bytes at the start of a GEMM workspace that hold the per-tile arrival counters of the
-// in-kernel K-piece fix-up (zero between calls); the partial sums follow.
-constexpr size_t kFoldCounterBytes = 64 * 1024;
-constexpr int kMaxFoldTiles = (int)(kFoldCounterBytes / 4);
 
 constexpr int kGroupM = 8;  // tile rows walked together (the tile order of a launch)
 
@@ -115,12 +103,6 @@ using Tile256x256w8 = GemmTile<2, 4, 4, 2, 2, 1>;
 using Tile128x64k2 = GemmTile<2, 2, 2, 1, 3, 1, 2>;
 using Tile64x128k2 = GemmTile<2, 2, 1, 2, 3, 1, 2>;
 using Tile128x128k2 = GemmTile<2, 2, 2, 2, 2, 1, 2>;
-
-// Whether tile T's K splits add themselves up inside the GEMM (the last split of a tile to
-// finish sums them): small tiles only, whose register budget holds the summed partials'
-// loads next to the accumulators; larger tiles write raw partials for split_reduce_kernel.
-template <class T>
-constexpr bool fold_splits_in_kernel() { return T::BM * T::BN <= 128 * 128; }
 
 // Enqueues the GEMM for tile shape T (EPI_GEGLU: e4m3 x e4m3, bf16 H). Returns a BF8_*
 // status; the host entry points have validated p.

@@ -1,8 +1,6 @@
 // FP8 GEMM kernel for gfx950 (MI355X) on the double-rate f8f6f4 MFMA, with a dequant/bias
-// epilogue (K-split tiles fixed up inside the kernel by the last of their splits to finish;
-// tail-split pieces as raw partials), and a gated-GELU(tanh) epilogue for the MLP gate/up
-// projection.
-// Included by the gemm_tile_*.hip files only.
+// epilogue (or raw fp32 split-K partials), and a gated-GELU(tanh) epilogue for the MLP
+// gate/up projection. Included by the gemm_tile_*.hip files only.
 //
 // Semantics replace torch._scaled_mm / cuBLASLt under torchao Float8Linear
 // (bongard/float8_training.py:22) and TE's FP8 GEMM under te.Linear
@@ -746,8 +744,7 @@ gemm_kernel(GemmParams p) {
   if constexpr (EPI == EPI_LINEAR) {
     if (tail_slot >= 0) {
       // a K piece of a tail-split tile: raw fp32 sums of the whole BM x BN tile (rows and
-      // columns past the tensor hold zeros), added up with the other pieces by a second
-      // kernel spread over every CU
+      // columns past the tensor hold zeros), reduced with the other pieces later
       float* base = p.tail_ws + (int64_t)tail_slot * (BM * BN);
 #pragma unroll
       for (int i = 0; i < FN; ++i)
@@ -762,90 +759,6 @@ gemm_kernel(GemmParams p) {
                             acc[i][j][4 * q + 3]);
           }
       return;
-    }
-    if (p.splits > 1) {
-      // A K split of the tile: its raw fp32 sums go to its slice of part_ws, then it counts
-      // itself in the tile's arrival counter; the last split to arrive adds all splits in
-      // split order (its own read back like the others: the same fp32 values) and goes on
-      // to the ordinary epilogue, the others are done.
-      float* base = p.part_ws + (int64_t)split * p.split_stride;
-      const int lr = lane & 31, lc = (lane >> 5) * 4;
-      auto in_tensor = [&](int m, int n) { return m0 + m < p.M && n0 + n < p.N; };
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int j = 0; j < FM; ++j) {
-            const int m = wave_m0 + j * 32 + lr, n = wn * FN * 32 + i * 32 + 8 * q + lc;
-            if (in_tensor(m, n))
-              *reinterpret_cast<float4*>(base + (int64_t)(m0 + m) * p.N + n0 + n) =
-                  make_float4(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                              acc[i][j][4 * q + 3]);
-          }
-      if constexpr (!fold_splits_in_kernel<T>()) return;  // split_reduce_kernel adds them
-      // Every wave's stores have reached its XCD's L2 (vmcnt), then one wave writes the L2
-      // back (agent-scope release) so the other XCDs can read them, and counts the split.
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      __shared__ uint32_t fold_last;
-      if (t == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        uint32_t* cnt = p.fold_cnt + tm * p.tiles_n + tn;
-        const uint32_t before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = before == (uint32_t)(p.splits - 1);
-        if (last) {
-          // every split has counted: reset for the next call, then drop stale cached lines
-          // (this CU's and XCD's caches) before the other splits' sums are read
-          __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        }
-        fold_last = last ? 1u : 0u;
-      }
-      __syncthreads();
-      if (!fold_last) return;
-      // acc = P[0] + P[1] + ... in split order, one n-subtile at a time with PB splits' loads
-      // in flight together: PB * FM * 16 registers beside the accumulators, within the
-      // wave's budget of 512 / (OCC * KG * NW / 4)
-      constexpr int kBudget = 512 / (T::OCC * KG * NW / 4);
-      constexpr int kFree = kBudget - FM * FN * 16 - 128;
-      constexpr int PB = kFree / (FM * 16) >= 4 ? 4 : (kFree / (FM * 16) >= 2 ? 2 : 1);
-#pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        for (int s0 = 0; s0 < p.splits; s0 += PB) {
-          float4 v[PB][4][FM];
-#pragma unroll
-          for (int b = 0; b < PB; ++b)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-              for (int j = 0; j < FM; ++j) {
-                const int m = wave_m0 + j * 32 + lr, n = wn * FN * 32 + i * 32 + 8 * q + lc;
-                v[b][q][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (s0 + b < p.splits && in_tensor(m, n))
-                  v[b][q][j] = *reinterpret_cast<const float4*>(
-                      p.part_ws + (int64_t)(s0 + b) * p.split_stride + (int64_t)(m0 + m) * p.N +
-                      n0 + n);
-              }
-#pragma unroll
-          for (int b = 0; b < PB; ++b) {
-            if (s0 + b >= p.splits) break;
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-              for (int j = 0; j < FM; ++j) {
-                if (s0 + b == 0) {
-                  acc[i][j][4 * q + 0] = v[b][q][j].x; acc[i][j][4 * q + 1] = v[b][q][j].y;
-                  acc[i][j][4 * q + 2] = v[b][q][j].z; acc[i][j][4 * q + 3] = v[b][q][j].w;
-                } else {
-                  acc[i][j][4 * q + 0] += v[b][q][j].x; acc[i][j][4 * q + 1] += v[b][q][j].y;
-                  acc[i][j][4 * q + 2] += v[b][q][j].z; acc[i][j][4 * q + 3] += v[b][q][j].w;
-                }
-              }
-          }
-        }
-      }
     }
   }
   // acc[i][j][r]: n-subtile i, m-subtile j; row m = wave_m0 + j*32 + (lane & 31) of the
@@ -932,8 +845,9 @@ gemm_kernel(GemmParams p) {
         store_bf16x8(reinterpret_cast<uint16_t*>(p.C) + (int64_t)gm * p.ldc + gn, d, p.ldc);
     }
   } else if constexpr (EPI == EPI_LINEAR) {
-    // fp32 out (a K-split tile's last piece has summed the pieces into acc above)
-    float* cbase = reinterpret_cast<float*>(p.C);
+    // fp32 out; with a K split, raw partial sums into this split's slice of C
+    const bool raw = p.splits > 1;
+    float* cbase = reinterpret_cast<float*>(p.C) + (raw ? split * p.split_stride : 0);
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
@@ -943,14 +857,15 @@ gemm_kernel(GemmParams p) {
         int seg = 0;
 #pragma unroll
         for (int s2 = 0; s2 < 3; ++s2) seg += (s2 + 1 < p.n_seg && n >= p.seg_end[s2]) ? 1 : 0;
-        const float alpha = sa * (seg == 0 ? sb[0] : seg == 1 ? sb[1] : seg == 2 ? sb[2] : sb[3]);
+        const float alpha =
+            raw ? 1.0f : sa * (seg == 0 ? sb[0] : seg == 1 ? sb[1] : seg == 2 ? sb[2] : sb[3]);
         float bias[4] = {0.f, 0.f, 0.f, 0.f};
-        if (p.bias) {
+        if (p.bias && !raw) {
           const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
           bias[0] = bf16_lo(bb.x); bias[1] = bf16_hi(bb.x);
           bias[2] = bf16_lo(bb.y); bias[3] = bf16_hi(bb.y);
         }
-        if (vec) {
+        if (vec && !raw) {
           float cf[4];
           col_factors(n, alpha, cf);
 #pragma unroll

@@ -185,9 +185,8 @@ def partials_buffer(count, device):
     return buf
 
 
-# Per-(device, stream) split-K workspace of bf8_gemm, reused in stream order: per-tile
-# arrival counters (its first 64 KB, which the kernels leave zero after every call) and
-# the fp32 partial sums. Zero-filled once when allocated.
+# Per-(device, stream) split-K workspace of bf8_gemm (fp32 partial sums), reused in
+# stream order.
 _GEMM_WS = {}
 
 
@@ -195,7 +194,7 @@ def gemm_workspace(nbytes, device):
     key = _stream_key(device)
     buf = _GEMM_WS.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
+        buf = torch.empty(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
         _GEMM_WS[key] = buf
     return buf
 
@@ -781,9 +780,6 @@ def rmsnorm(x, weight, eps, *, zero_centered=True, want_rstd=False, partials=Non
     return y, rstd, parts
 
 
-_NORM_WS = {}   # per-(device, stream) weight-gradient partials of rmsnorm_backward
-
-
 def rmsnorm_backward(x, dy, weight, eps, *, zero_centered=True, need_dx=True, need_dw=True):
     """Gradients (dx bf16 [rows, cols] or None, dweight bf16 [cols] or None) of
     :func:`rmsnorm` for the bf16 gradient dy of its output."""
@@ -803,13 +799,8 @@ def rmsnorm_backward(x, dy, weight, eps, *, zero_centered=True, need_dx=True, ne
     dw = torch.empty(cols, dtype=torch.bfloat16, device=x.device) if need_dw else None
     ws, nbytes = None, 0
     if need_dw:
-        # its own buffer: the GEMM workspace's first bytes are the GEMMs' arrival counters
         nbytes = int(L.bf8_rmsnorm_bwd_workspace(rows, cols))
-        key = _stream_key(x.device)
-        ws = _NORM_WS.get(key)
-        if ws is None or ws.numel() < nbytes:
-            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=x.device)
-            _NORM_WS[key] = ws
+        ws = gemm_workspace(nbytes, x.device)
         nbytes = ws.numel()
     _lib.check(L.bf8_rmsnorm_bwd_bf16(_ptr(x), _ptr(dy), rows, cols, _ptr(weight), float(eps),
                                       int(bool(zero_centered)), _ptr(dx), _ptr(dw), _ptr(ws),

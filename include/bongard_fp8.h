@@ -134,14 +134,11 @@ int bf8_quantize_many_bf16(int count, const void* const* x, const int64_t* n, co
  * n_seg <= 4, ascending, last == N) assigns column n to the first segment whose end
  * exceeds n (fused QKV keeps one weight scale per projection). seg_ends may be NULL when
  * n_seg == 1. bias: bf16 [N] or NULL. C: [M, N] with row stride ldc elements.
- * ws: workspace for split-K partial sums (or, for a shape whose tiles leave a short
+ * ws: fp32 workspace for split-K partial sums (or, for a shape whose tiles leave a short
  * last round, the partials of the tail tiles' K pieces), bf8_gemm_workspace(M, N, K)
- * bytes (0 when the shape runs without either; ws may then be NULL), 256-byte aligned.
- * Its first 64 KB hold per-tile arrival counters (the last K piece of a tile to finish
- * adds the pieces up inside the kernel): they must be zero before the first call that
- * uses the workspace (clear it once when allocating it) and every call leaves them zero.
- * Calls that share a workspace must be stream-ordered. A smaller ws makes the call choose
- * a plan that fits it; results do not depend on the plan beyond fp32 summation order.
+ * bytes (0 when the shape runs without either; ws may then be NULL). A smaller ws makes
+ * the call choose a plan that fits it; results do not depend on the plan beyond fp32
+ * summation order.
  * ------------------------------------------------------------------------------- */
 size_t bf8_gemm_workspace(int64_t M, int64_t N, int64_t K);
 int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt_b,

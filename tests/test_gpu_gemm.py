@@ -446,8 +446,8 @@ def _tail_pieces(M, N, K):
     """Pieces per tail tile of the forced tail plan, read back from its workspace size."""
     tiles = -(-M // 256) * -(-N // 256)
     tails = tiles % 256
-    ws = ops._lib.lib().bf8_gemm_workspace(M, N, K) - 64 * 1024   # minus the counters
-    assert ws > 0 and ws % (tails * 256 * 256 * 4) == 0, "not a tail-split plan"
+    ws = ops._lib.lib().bf8_gemm_workspace(M, N, K)
+    assert ws % (tails * 256 * 256 * 4) == 0, "not a tail-split plan"
     return ws // (tails * 256 * 256 * 4)
 
 

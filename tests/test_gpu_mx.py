@@ -101,8 +101,7 @@ def test_gemm_mx_tail_split(gpu, monkeypatch):
     the tail tiles' pieces are reduced with unit scales."""
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:t")
     M, N, K = 4160, 3848, 4096
-    ws = ops._lib.lib().bf8_gemm_mx_workspace(M, N, K) - 64 * 1024   # minus the counters
-    assert ws > 0 and ws % (16 * 256 * 256 * 4) == 0
+    assert ops._lib.lib().bf8_gemm_mx_workspace(M, N, K) % (16 * 256 * 256 * 4) == 0
     _mx_gemm_case(gpu, M, N, K, seed=63, bias=True)
 
 

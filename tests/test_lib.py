@@ -13,9 +13,6 @@ ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "bongard_fp8.h"
 
 
-# bytes of per-tile arrival counters at the start of a split GEMM's workspace
-COUNTERS = 64 * 1024
-
 def _declared_functions():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
@@ -72,8 +69,7 @@ def test_plan_override_env(monkeypatch):
     assert L.bf8_gemm_workspace(512, 2560, 10240) == 0
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:4")
     assert L.bf8_geglu_partials(300, 384) == 2 * 3
-    # the tiles' arrival counters, then the four splits' fp32 partials
-    assert L.bf8_gemm_workspace(512, 2560, 10240) == COUNTERS + 4 * 512 * 2560 * 4
+    assert L.bf8_gemm_workspace(512, 2560, 10240) == 4 * 512 * 2560 * 4
     # 80 gate + 80 up columns per tile: a gated-GELU variant for I % 80 == 0 only
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x160")
     assert L.bf8_geglu_partials(512, 10240) == 2 * 128
@@ -83,18 +79,17 @@ def test_plan_override_env(monkeypatch):
 
 def test_tail_split_plans(monkeypatch):
     """Tail-split plans (whole 256x256 tiles, the partial last round's tiles split along K)
-    size their workspace as the arrival counters plus [tail tiles x pieces][256][256] fp32:
-    c5's dX and dW_gu GEMMs
+    size their workspace as [tail tiles x pieces][256][256] fp32: c5's dX and dW_gu GEMMs
     take one automatically; c2's down projection (160 tiles, one round) does not;
     BONGARD_FP8_GEMM_TILE=256x256:t forces one where the shape has a tail."""
     L = _lib.lib()
     tile = 256 * 256 * 4
     monkeypatch.delenv("BONGARD_FP8_GEMM_TILE", raising=False)
-    assert L.bf8_gemm_workspace(8192, 2560, 20480) == COUNTERS + 64 * 4 * tile   # 256 + 64
-    assert L.bf8_gemm_workspace(20480, 2560, 8192) == COUNTERS + 32 * 8 * tile   # 768 + 32
+    assert L.bf8_gemm_workspace(8192, 2560, 20480) == 64 * 4 * tile   # 320 tiles: 256 + 64
+    assert L.bf8_gemm_workspace(20480, 2560, 8192) == 32 * 8 * tile   # 800 tiles: 768 + 32
     assert L.bf8_gemm_workspace(4096, 2560, 10240) == 0
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256:t")
-    assert L.bf8_gemm_workspace(4160, 3848, 4112) == COUNTERS + 16 * 7 * tile   # 7 pieces
+    assert L.bf8_gemm_workspace(4160, 3848, 4112) == 16 * 7 * tile   # 33 K steps in 7 pieces
     assert L.bf8_gemm_workspace(4096, 4096, 4096) == 0                # 256 tiles: no tail
 
 
