@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -52,6 +52,9 @@ SIGNATURES = {
     "bf8_cast_delayed_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int, c_int,
                                       c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p]),
+    "bf8_cast_delayed_many_bf16": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                           c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                           c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "bf8_geglu_bwd_delayed_partials": (c_int64, [c_int64, c_int64]),
     "bf8_geglu_bwd_delayed": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int,
                                       c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,

@@ -360,16 +360,17 @@ __device__ inline float scale_from_partials_block(const uint32_t* __restrict__ p
 // Every block reduces the previous step's amax partials (n_prev of them; none on the
 // first step) and forms w = max(history[i != pos], that amax), the window after the
 // amax is pushed into slot pos. scale = fp32(fp8_max / f64(w)) when the window is finite
-// and w > 0, else the stored scale is kept. Block (0,0) pushes the amax and publishes the
-// meta. All blocks compute the same values, so reading the words block 0 rewrites is
-// harmless: slot pos is excluded, and the stored scale is only used when it is written
-// back unchanged. Block (0,0) also writes {w, scale, scale_inv, 0} to meta_out (if any),
-// a copy of this step's scale that later steps do not overwrite. Result valid in all
-// threads.
+// and w > 0, else the stored scale is kept. The leader block (by default block (0,0))
+// pushes the amax and publishes the meta. All blocks compute the same values, so reading
+// the words the leader rewrites is harmless: slot pos is excluded, and the stored scale is
+// only used when it is written back unchanged. The leader also writes {w, scale,
+// scale_inv, 0} to meta_out (if any), a copy of this step's scale that later steps do not
+// overwrite. Result valid in all threads.
 template <int NT>
 __device__ inline float delayed_scale_block(float* __restrict__ state, int len, int pos,
                                             const uint32_t* __restrict__ prev, int64_t n_prev,
-                                            float fp8_max, float* __restrict__ meta_out) {
+                                            float fp8_max, float* __restrict__ meta_out,
+                                            bool leader) {
   __shared__ float s_scale;
   uint32_t m = 0;
   for (int64_t i = threadIdx.x; i < n_prev; i += NT) m = max(m, prev[i]);
@@ -389,7 +390,7 @@ __device__ inline float delayed_scale_block(float* __restrict__ state, int len, 
     float scale = meta[1];
     if (finite && w > 0.0f) scale = (float)((double)fp8_max / (double)w);
     s_scale = scale;
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
+    if (leader) {
       if (have_new) {
         state[pos] = amax_new;
         meta[0] = amax_new;

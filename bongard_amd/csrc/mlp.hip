@@ -186,7 +186,8 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_delayed_kernel(
   __shared__ __attribute__((aligned(16))) uint32_t tf[kGeluFBytes / 4];
   load_gelu_tables<kNT>(ta, tf);  // the scale step below synchronises the block
   const float scale =
-      delayed_scale_block<kNT>(state, len, pos, prev, n_prev, Fp8Max<FMT>::value, meta_out);
+      delayed_scale_block<kNT>(state, len, pos, prev, n_prev, Fp8Max<FMT>::value, meta_out,
+                               blockIdx.x == 0);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t tiles_c = I / kTT;
   const int64_t ntiles = tiles_c * ((M + kTT - 1) / kTT);

@@ -146,7 +146,7 @@ __device__ __forceinline__ float resolve_scale(const ScaleSrc& s, bool leader) {
   if (s.scale) return *s.scale;
   if (s.state)
     return delayed_scale_block<kNT>(s.state, s.len, s.pos, s.prev, s.n_prev, Fp8Max<FMT>::value,
-                                    s.meta_out);
+                                    s.meta_out, leader);
   return scale_from_partials_block<kNT>(s.partials, s.np, Fp8Max<FMT>::value, s.meta_out,
                                         s.pow2 != 0, leader);
 }
@@ -228,34 +228,48 @@ constexpr int kTT = 64;   // tile columns
 constexpr int kWavesPerBlock = kNT / 64;
 constexpr int kMaxTransposeBlocks = 2048;
 
+// Block blk of the nblk blocks that cast x with its transposed copy; blk == 0 leads
+// (publishes the meta record, pushes a delayed amax). The first tile's loads are issued
+// before the scale is resolved, so a delayed or current scale's partials reduction runs
+// while they are in flight.
 template <int FMT>
-__global__ __launch_bounds__(kNT) void cast_transpose_kernel(
-    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, ScaleSrc src,
-    uint8_t* __restrict__ out, uint8_t* __restrict__ out_t, uint32_t* __restrict__ amax_out) {
+__device__ __forceinline__ void cast_transpose_body(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, const ScaleSrc& src,
+    uint8_t* __restrict__ out, uint8_t* __restrict__ out_t, uint32_t* __restrict__ amax_out,
+    int64_t blk, int64_t nblk) {
   constexpr int NL = kTR / 8;  // 16-byte loads per lane
   __shared__ uint32_t stage[kWavesPerBlock][(kTR / 64) * kWaveTileDwords];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const float scale = resolve_scale<FMT>(src, blockIdx.x == 0);
   const int64_t tiles_c = (cols + kTT - 1) / kTT;
   const int64_t tile_rows = (rows + kTR - 1) / kTR;
   const int64_t ntiles = tiles_c * tile_rows;
   const bool t16 = (rows & 15) == 0;  // out_t rows 16-byte aligned
-  uint32_t m = 0;
-  for (int64_t tile_id = (int64_t)blockIdx.x * kWavesPerBlock + wid; tile_id < ntiles;
-       tile_id += (int64_t)gridDim.x * kWavesPerBlock) {
+  const int ch = lane & 7;
+  // load k of tile tile_id: rows 8k + (lane >> 3), 16-byte chunk lane & 7 (8 rows x 128
+  // bytes each)
+  auto load_tile = [&](int64_t tile_id, uint4 (&v)[NL], int64_t& r0, int64_t& c0) {
     int64_t ti, tj;
     pair_tile(tile_id, tiles_c, tile_rows, ti, tj);
-    const int64_t r0 = ti * kTR, c0 = tj * kTT;
-    // load k: rows 8k + (lane >> 3), 16-byte chunk lane & 7 (8 rows x 128 bytes each)
-    const int ch = lane & 7;
+    r0 = ti * kTR;
+    c0 = tj * kTT;
     const int64_t c = c0 + 8 * ch;
-    uint4 v[NL];
 #pragma unroll
     for (int k = 0; k < NL; ++k) {
       const int64_t r = r0 + 8 * k + (lane >> 3);
       v[k] = make_uint4(0u, 0u, 0u, 0u);
-      if (r < rows && c < cols) v[k] = *reinterpret_cast<const uint4*>(x + r * cols + c);
+      if (tile_id < ntiles && r < rows && c < cols)
+        v[k] = *reinterpret_cast<const uint4*>(x + r * cols + c);
     }
+  };
+  int64_t tile_id = blk * kWavesPerBlock + wid;
+  uint4 v[NL];
+  int64_t r0, c0;
+  load_tile(tile_id, v, r0, c0);
+  const float scale = resolve_scale<FMT>(src, blk == 0);
+  uint32_t m = 0;
+  for (; tile_id < ntiles; tile_id += nblk * kWavesPerBlock) {
+    if (tile_id != blk * kWavesPerBlock + wid) load_tile(tile_id, v, r0, c0);
+    const int64_t c = c0 + 8 * ch;
     uint32_t* lds = stage[wid];
 #pragma unroll
     for (int k = 0; k < NL; ++k) {
@@ -289,7 +303,14 @@ __global__ __launch_bounds__(kNT) void cast_transpose_kernel(
       }
     }
   }
-  store_block_amax(m, amax_out, blockIdx.x);
+  store_block_amax(m, amax_out, blk);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kNT) void cast_transpose_kernel(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, ScaleSrc src,
+    uint8_t* __restrict__ out, uint8_t* __restrict__ out_t, uint32_t* __restrict__ amax_out) {
+  cast_transpose_body<FMT>(x, rows, cols, src, out, out_t, amax_out, blockIdx.x, gridDim.x);
 }
 
 int64_t transpose_blocks(int64_t rows, int64_t cols) {
@@ -333,7 +354,7 @@ __global__ __launch_bounds__(kNT) void delayed_fold_kernel(float* state, int len
                                                            const uint32_t* __restrict__ prev,
                                                            int64_t n_prev, float fp8_max,
                                                            float* meta_out) {
-  delayed_scale_block<kNT>(state, len, pos, prev, n_prev, fp8_max, meta_out);
+  delayed_scale_block<kNT>(state, len, pos, prev, n_prev, fp8_max, meta_out, true);
 }
 
 __global__ __launch_bounds__(kNT) void delayed_end_kernel(float* state, int len,
@@ -497,6 +518,48 @@ __global__ __launch_bounds__(kNT) void cast_many_kernel(ManyArgs a) {
     cast_body<BF8_E5M2>(g.x, g.n, src, g.out, nullptr, blk, g.cast_blocks);
 }
 
+// ---- several delayed casts in one launch ----------------------------------------------
+// Up to kMaxMany delayed-scaling casts (each with its own history, formats, optional
+// transposed copy and amax partials) in one launch: tensor t runs on blocks [first,
+// first + blocks) with the grid, block order and partials its own bf8_cast_delayed_bf16
+// launch would have, so its bytes, meta, history and partials are those of that call.
+struct DelayedSeg {
+  const uint16_t* x;
+  int64_t rows, cols;
+  ScaleSrc src;
+  int fmt;
+  uint8_t* out;
+  uint8_t* out_t;
+  uint32_t* amax_out;
+  int64_t first, blocks;
+};
+
+struct DelayedManyArgs {
+  DelayedSeg seg[kMaxMany];
+  int count;
+};
+
+__global__ __launch_bounds__(kNT) void cast_delayed_many_kernel(DelayedManyArgs a) {
+  int t = 0;
+  for (int k = 1; k < a.count; ++k)
+    if ((int64_t)blockIdx.x >= a.seg[k].first) t = k;
+  const DelayedSeg& g = a.seg[t];
+  const int64_t blk = (int64_t)blockIdx.x - g.first;
+  if (g.out_t) {
+    if (g.fmt == BF8_E4M3)
+      cast_transpose_body<BF8_E4M3>(g.x, g.rows, g.cols, g.src, g.out, g.out_t, g.amax_out, blk,
+                                    g.blocks);
+    else
+      cast_transpose_body<BF8_E5M2>(g.x, g.rows, g.cols, g.src, g.out, g.out_t, g.amax_out, blk,
+                                    g.blocks);
+  } else {
+    if (g.fmt == BF8_E4M3)
+      cast_body<BF8_E4M3>(g.x, g.rows * g.cols, g.src, g.out, g.amax_out, blk, g.blocks);
+    else
+      cast_body<BF8_E5M2>(g.x, g.rows * g.cols, g.src, g.out, g.amax_out, blk, g.blocks);
+  }
+}
+
 }  // namespace
 }  // namespace bf8
 
@@ -554,7 +617,7 @@ using namespace bf8;
 extern "C" {
 
 const char* bf8_last_error(void) { return bf8::g_err; }
-int bf8_abi_version(void) { return 13; }
+int bf8_abi_version(void) { return 14; }
 
 int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
 
@@ -703,6 +766,68 @@ int bf8_quantize_many_bf16(int count, const void* const* x, const int64_t* n, co
   if (rc != BF8_OK) return rc;
   hipLaunchKernelGGL(cast_many_kernel, dim3((unsigned)cast_total), dim3(kNT), 0, s, a);
   return launch_status("cast_many_kernel");
+}
+
+int bf8_cast_delayed_many_bf16(int count, const void* const* x, const int64_t* rows,
+                               const int64_t* cols, float* const* state, const int* len,
+                               const int* pos, const uint32_t* const* prev_partials,
+                               const int64_t* n_prev, const int* fmt, float* const* meta_out,
+                               uint8_t* const* out, uint8_t* const* out_t,
+                               uint32_t* const* partials_out, void* stream) {
+  BF8_CHECK(count >= 1 && count <= kMaxMany,
+            "bf8_cast_delayed_many_bf16: count %d outside [1, %d]", count, kMaxMany);
+  BF8_CHECK(x && rows && cols && state && len && pos && prev_partials && n_prev && fmt &&
+                meta_out && out && out_t && partials_out,
+            "bf8_cast_delayed_many_bf16: NULL array");
+  DelayedManyArgs a{};
+  int64_t total = 0;
+  for (int t = 0; t < count; ++t) {
+    BF8_CHECK(fmt[t] == BF8_E4M3 || fmt[t] == BF8_E5M2,
+              "bf8_cast_delayed_many_bf16: tensor %d: bad fmt %d", t, fmt[t]);
+    BF8_CHECK(rows[t] >= 0 && cols[t] >= 0, "bf8_cast_delayed_many_bf16: tensor %d: negative shape",
+              t);
+    BF8_CHECK(state[t] && len[t] >= 1 && len[t] <= 1024,
+              "bf8_cast_delayed_many_bf16: tensor %d: bad state/len", t);
+    BF8_CHECK(pos[t] >= 0 && pos[t] < len[t],
+              "bf8_cast_delayed_many_bf16: tensor %d: pos %d outside [0, %d)", t, pos[t], len[t]);
+    BF8_CHECK(n_prev[t] >= 0 && n_prev[t] <= kMaxInlinePartials &&
+                  (n_prev[t] == 0 || prev_partials[t]),
+              "bf8_cast_delayed_many_bf16: tensor %d: bad previous partials (%lld, at most %lld)",
+              t, (long long)n_prev[t], (long long)kMaxInlinePartials);
+    BF8_CHECK(out[t] || out_t[t], "bf8_cast_delayed_many_bf16: tensor %d: out and out_t are NULL",
+              t);
+    BF8_CHECK(((uintptr_t)x[t] & 15) == 0 && ((uintptr_t)out[t] & 15) == 0 &&
+                  ((uintptr_t)out_t[t] & 15) == 0,
+              "bf8_cast_delayed_many_bf16: tensor %d: x, out and out_t must be 16-byte aligned", t);
+    BF8_CHECK(!out_t[t] || cols[t] % 16 == 0,
+              "bf8_cast_delayed_many_bf16: tensor %d: transposed cast needs cols %% 16 == 0", t);
+    const int64_t n = rows[t] * cols[t];
+    if (n == 0) continue;  // as bf8_cast_delayed_bf16: nothing cast, state untouched
+    BF8_CHECK(x[t] != nullptr, "bf8_cast_delayed_many_bf16: tensor %d: x is NULL", t);
+    DelayedSeg& g = a.seg[a.count++];
+    g.x = (const uint16_t*)x[t];
+    g.rows = rows[t];
+    g.cols = cols[t];
+    g.src = ScaleSrc{};
+    g.src.state = state[t];
+    g.src.len = len[t];
+    g.src.pos = pos[t];
+    g.src.prev = prev_partials[t];
+    g.src.n_prev = n_prev[t];
+    g.src.meta_out = meta_out[t];
+    g.fmt = fmt[t];
+    g.out = out[t];
+    g.out_t = out_t[t];
+    g.amax_out = partials_out[t];
+    g.first = total;
+    g.blocks = out_t[t] ? transpose_blocks(rows[t], cols[t])
+                        : row_cast_blocks(n, partials_out[t] != nullptr);
+    total += g.blocks;
+  }
+  if (a.count == 0) return BF8_OK;
+  hipLaunchKernelGGL(cast_delayed_many_kernel, dim3((unsigned)total), dim3(kNT), 0,
+                     as_stream(stream), a);
+  return launch_status("cast_delayed_many_kernel");
 }
 
 int bf8_delayed_scale_begin(float* state, int len, int fmt, void* stream) {

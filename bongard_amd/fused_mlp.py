@@ -26,6 +26,7 @@ import torch
 
 from . import linear as _linear
 from . import ops as _ops
+from . import scaling as _scaling
 from .te_linear import (RECIPES, _is_mx, _make_recipe, _new_scaling, _pad_rows, _ScalingExtraState,
                         present)
 
@@ -136,12 +137,18 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
             if mx:
                 self._fp8_weights = (_linear.quantize_weight_mx(self.fc1_weight),
                                      _linear.quantize_weight_mx(self.fc2_weight))
+            elif fc1 is not None:
+                # delayed scaling: both weights with their transposed copies in one launch
+                wq, dq = _scaling.quantize_many([
+                    (fc1.weight, self.fc1_weight.detach(), True, True),
+                    (fc2.weight, self.fc2_weight.detach(), True, True)])
+                self._fp8_weights = (_linear._GateUp(wq.data, wq.data_t, wq.meta.view(1, 4)),
+                                     dq)
             else:
                 self._fp8_weights = (
                     _linear.quantize_gate_up(self.fc1_weight, self.intermediate_size,
-                                             split_scales=False, scaler=fc1 and fc1.weight),
-                    _linear.quantize_weight(self.fc2_weight, transpose=True,
-                                            scaler=fc2 and fc2.weight))
+                                             split_scales=False),
+                    _linear.quantize_weight(self.fc2_weight, transpose=True))
         gu_q, down_q = self._fp8_weights
         flat = flat.to(torch.bfloat16).contiguous()
         if mx:

@@ -26,6 +26,7 @@ from typing import Optional
 import torch
 
 from . import ops
+from . import scaling as _scaling
 from .ops import E4M3, E5M2
 
 
@@ -338,6 +339,14 @@ def mlp_forward(x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scali
             gu_q = _GateUp(qs[1].data, None, qs[1].meta.view(1, 4))
         if down_q is None:
             down_q = qs[-1]
+    elif gs is not None and x_amax is None and gu_q is None and down_q is None:
+        # delayed scaling with every operand quantized here: x, [W_gate; W_up] and W_down
+        # with the transposed copies the backward reads, in one launch
+        xq, wq, down_q = _scaling.quantize_many([
+            (gs.input, x, True, need_dgu),
+            (gs.weight, w_gu.detach(), True, need_dx),
+            (ds.weight, w_down.detach(), True, need_dx or need_dgu)])
+        gu_q = _GateUp(wq.data, wq.data_t, wq.meta.view(1, 4))
     else:
         xq = _quantize_input(x, gs and gs.input, x_amax, need_dgu)
     if gu_q is None:

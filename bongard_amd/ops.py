@@ -884,3 +884,52 @@ def cast_delayed(x, state, length, pos, prev_partials, fmt=E4M3, *, rowwise=True
         fmt, _ptr(meta_out), _ptr(out), _ptr(out_t), _ptr(partials_out), _stream(dev)),
         "bf8_cast_delayed_bf16")
     return Fp8Tensor(out, out_t, meta_out, fmt, rows, cols)
+
+
+def cast_delayed_many(jobs):
+    """Several :func:`cast_delayed` calls in one launch (bf8_cast_delayed_many_bf16).
+
+    ``jobs``: up to 8 dicts with the keys x, state, length, pos, prev_partials, fmt,
+    rowwise, transpose, partials_out, meta_out (the arguments of :func:`cast_delayed`).
+    Returns one :class:`Fp8Tensor` per job; bytes, metas, histories and partials equal
+    those of the calls made one by one in order."""
+    count = len(jobs)
+    if not 1 <= count <= 8:
+        raise ValueError(f"cast_delayed_many: {count} tensors (1 to 8 supported)")
+    fields = {k: [] for k in ("x", "rows", "cols", "state", "len", "pos", "prev", "n_prev",
+                              "fmt", "meta", "out", "out_t", "parts")}
+    results = []
+    dev = None
+    for j in jobs:
+        x = _bf16_2d(j["x"])
+        _require_gpu(x, j["state"])
+        dev = x.device if dev is None else dev
+        if x.device != dev:
+            raise ValueError("cast_delayed_many: tensors on different devices")
+        rows, cols = x.shape
+        fmt = j.get("fmt", E4M3)
+        meta = j.get("meta_out")
+        if meta is None:
+            meta = new_meta(dev)
+        out = (torch.empty((rows, cols), dtype=TORCH_FP8[fmt], device=dev)
+               if j.get("rowwise", True) else None)
+        out_t = (torch.empty((cols, rows), dtype=TORCH_FP8[fmt], device=dev)
+                 if j.get("transpose", False) else None)
+        prev = j.get("prev_partials")
+        for key, val in (("x", _ptr(x)), ("rows", rows), ("cols", cols),
+                         ("state", _ptr(j["state"])), ("len", int(j["length"])),
+                         ("pos", int(j["pos"])), ("prev", _ptr(prev)),
+                         ("n_prev", 0 if prev is None else prev.numel()), ("fmt", fmt),
+                         ("meta", _ptr(meta)), ("out", _ptr(out)), ("out_t", _ptr(out_t)),
+                         ("parts", _ptr(j.get("partials_out")))):
+            fields[key].append(val)
+        results.append(Fp8Tensor(out, out_t, meta, fmt, rows, cols))
+    P = ctypes.c_void_p * count
+    I64 = ctypes.c_int64 * count
+    I32 = ctypes.c_int * count
+    _lib.check(_lib.lib().bf8_cast_delayed_many_bf16(
+        count, P(*fields["x"]), I64(*fields["rows"]), I64(*fields["cols"]), P(*fields["state"]),
+        I32(*fields["len"]), I32(*fields["pos"]), P(*fields["prev"]), I64(*fields["n_prev"]),
+        I32(*fields["fmt"]), P(*fields["meta"]), P(*fields["out"]), P(*fields["out_t"]),
+        P(*fields["parts"]), _stream(dev)), "bf8_cast_delayed_many_bf16")
+    return results

@@ -149,11 +149,21 @@ class DelayedScaler:
         A replay of a checkpointed forward casts with the scale its original call used and
         leaves the history, the pending amax partials and the step count unchanged, so the
         backward sees the original bytes."""
-        dev = x.device
         frame, replay = checkpoint_region(not self.gradient)
         if replay:
             meta = self._recorded_meta(frame)
             return ops.cast(x, meta, self.fmt, rowwise=rowwise, transpose=transpose)
+        job, count = self._job(x, rowwise, transpose, producer_count)
+        q = ops.cast_delayed(x, job["state"], job["length"], job["pos"], job["prev_partials"],
+                             self.fmt, rowwise=rowwise, transpose=transpose,
+                             partials_out=job["partials_out"])
+        self._commit(job, count, frame, q)
+        return q
+
+    def _job(self, x, rowwise, transpose, producer_count):
+        """The arguments of this role's next delayed cast of ``x`` (a dict for
+        ops.cast_delayed_many) and the number of amax partials it leaves pending."""
+        dev = x.device
         self._ensure(dev)
         rows = x.numel() // x.shape[-1] if x.dim() else 1
         cols = x.shape[-1]
@@ -163,15 +173,19 @@ class DelayedScaler:
         else:
             count, out_parts = int(producer_count), None
         prev = self._bufs[self._slot ^ 1][:self._pending] if self._pending else None
-        q = ops.cast_delayed(x, self.state, self.length, self.recorded % self.length, prev,
-                             self.fmt, rowwise=rowwise, transpose=transpose,
-                             partials_out=out_parts)
-        if prev is not None:
+        job = dict(x=x, state=self.state, length=self.length, pos=self.recorded % self.length,
+                   prev_partials=prev, fmt=self.fmt, rowwise=rowwise, transpose=transpose,
+                   partials_out=out_parts)
+        return job, count
+
+    def _commit(self, job, count, frame, q):
+        """The bookkeeping after the cast of ``job``: its previous amax entered the
+        history, this cast's partials are pending, the region records the meta."""
+        if job["prev_partials"] is not None:
             self.recorded += 1
         self._pending = count
         self._slot ^= 1
         self._remember(frame, q.meta)
-        return q
 
     def produce(self, count, device, launch, replay=None):
         """Runs a kernel that produces this role's tensor and casts it with the role's
@@ -240,6 +254,32 @@ def _fresh_state_cpu(length):
     st[length + 1] = 1.0
     st[length + 2] = 1.0
     return st
+
+
+# The most previous partials a shared launch folds inline (bf8_cast_delayed_many_bf16).
+_MANY_MAX_PREV = 2048
+
+
+def quantize_many(requests):
+    """Each ``(scaler, x, rowwise, transpose)`` of ``requests`` quantized with its role's
+    delayed scale, in one launch: equal to ``scaler.quantize(x, rowwise=..., transpose=...)``
+    for each request in order (bytes, metas, histories, partials), which is what a
+    checkpoint replay, or a role whose pending partials exceed what one launch folds, runs
+    instead. A forward quantizes its input and weights together this way, as TE casts one
+    forward's operands with their transposes (bongard/te_linear.py:73-74)."""
+    if not requests:
+        return []
+    regions = [checkpoint_region(not sc.gradient) for sc, _, _, _ in requests]
+    if any(replay for _, replay in regions) or any(
+            sc._pending > _MANY_MAX_PREV for sc, _, _, _ in requests) or len(requests) > 8:
+        return [sc.quantize(x, rowwise=rw, transpose=tr) for sc, x, rw, tr in requests]
+    jobs = []
+    for sc, x, rw, tr in requests:
+        jobs.append(sc._job(x, rw, tr, None))
+    qs = ops.cast_delayed_many([job for job, _ in jobs])
+    for (sc, _, _, _), (job, count), (frame, _), q in zip(requests, jobs, regions, qs):
+        sc._commit(job, count, frame, q)
+    return qs
 
 
 class LinearScaling:

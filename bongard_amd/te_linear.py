@@ -33,6 +33,7 @@ import torch
 from torch.nn import functional as F
 
 from . import linear as _linear
+from . import scaling as _scaling
 from .scaling import LinearScaling
 
 RECIPES = ('nvfp4', 'mxfp8', 'fp8', 'fp8_delayed')
@@ -253,6 +254,12 @@ class TEMLP(torch.nn.Module):
         if flat.dtype != torch.bfloat16:
             flat = flat.to(torch.bfloat16)
         down_first = self.down._note_microbatch()
+        if (self.fused_gate_up and self.down.scaling is not None
+                and self.gate_up.scaling is not None):
+            first = self.gate_up._note_microbatch()
+            return self._delayed_forward(x, flat, length, aligned,
+                                         first or self.gate_up._fp8_weight is None,
+                                         down_first or self.down._fp8_weight is None)
         down_q = self.down.fp8_weight(down_first)
         if _is_mx(self.down.recipe):
             return self._mx_forward(x, flat, length, aligned, down_q)
@@ -282,6 +289,31 @@ class TEMLP(torch.nn.Module):
             out = out[:length]
         return out.reshape(*x.shape[:-1], out.shape[-1])
 
+
+    def _delayed_forward(self, x, flat, length, aligned, new_gu, new_down):
+        """'fp8_delayed' with the fused gate_up: the weights' FP8 copies, re-quantized
+        where a weight changed (both in one launch when both did), cached for the next
+        microbatches, and the gated MLP on them."""
+        I = self.intermediate_size
+        gs, dsc = self.gate_up.scaling, self.down.scaling
+        if new_gu and new_down:
+            wq, dq = _scaling.quantize_many([
+                (gs.weight, self.gate_up.weight.detach(), True, True),
+                (dsc.weight, self.down.weight.detach(), True, True)])
+            self.gate_up._fp8_weight = _linear._GateUp(wq.data, wq.data_t, wq.meta.view(1, 4))
+            self.down._fp8_weight = dq
+        elif new_gu:
+            self.gate_up._fp8_weight = _linear.quantize_gate_up(
+                self.gate_up.weight, I, split_scales=False, scaler=gs.weight)
+        elif new_down:
+            self.down._fp8_weight = _linear.quantize_weight(self.down.weight, transpose=True,
+                                                            scaler=dsc.weight)
+        out = _linear.Fp8GegluMlpFunction.apply(flat, self.gate_up.weight, self.down.weight,
+                                                self.gate_up._fp8_weight,
+                                                self.down._fp8_weight, I, False, (gs, dsc))
+        if aligned != length:
+            out = out[:length]
+        return out.reshape(*x.shape[:-1], out.shape[-1])
 
     def _mx_forward(self, x, flat, length, aligned, down_q):
         """MXFP8: blocks along K never straddle gate and up rows, so the stacked weight's

@@ -237,6 +237,20 @@ int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* stat
                           float* meta_out, uint8_t* out, uint8_t* out_t, uint32_t* partials_out,
                           void* stream);
 
+/* Up to 8 bf8_cast_delayed_bf16 calls in one launch (one training step's forward
+ * quantizes x, [W_gate; W_up] and W_down with their transposed copies at once, as TE casts
+ * one forward's operands with their transposes: bongard/te_linear.py:73-74). Entry t takes
+ * the arguments of the single call as element t of each array (out[t] or out_t[t] may be
+ * NULL, partials_out[t] too); n_prev[t] <= 2048. Each tensor runs on the grid of its own
+ * call, so bytes, metas, histories and partials equal those of the calls made one by one
+ * in array order. Tensors with no elements are skipped (their state is left unchanged). */
+int bf8_cast_delayed_many_bf16(int count, const void* const* x, const int64_t* rows,
+                               const int64_t* cols, float* const* state, const int* len,
+                               const int* pos, const uint32_t* const* prev_partials,
+                               const int64_t* n_prev, const int* fmt, float* const* meta_out,
+                               uint8_t* const* out, uint8_t* const* out_t,
+                               uint32_t* const* partials_out, void* stream);
+
 /* bf8_geglu_bwd fused with the delayed-scaling cast of its output (bf8_cast_delayed_bf16
  * semantics for state / len / pos / prev_partials / meta_out): for the 'fp8_delayed'
  * recipe, whose dGU scale is known before dGU exists. Writes dGU in fp8 directly, as

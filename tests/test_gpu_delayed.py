@@ -259,3 +259,36 @@ def test_geglu_delayed_fused_h_equals_two_pass(gpu, M, transpose):
               flush=True)
         assert all(parts)
     assert a.recorded == b.recorded == 3
+
+
+def test_delayed_casts_in_one_launch_equal_separate_casts(gpu):
+    """scaling.quantize_many (bf8_cast_delayed_many_bf16: x, [W_gate; W_up] and W_down of a
+    training forward, with transposed copies, and an e5m2 row-only tensor) against each
+    role's own delayed cast, over five steps (the histories fill and the previous partials
+    fold in): bytes, transposed bytes, metas, histories and pending partials identical; a
+    ragged shape (rows and columns off the 64-element tiles) included."""
+    shapes = [((384, 256), ops.E4M3, True, True), ((704, 256), ops.E4M3, True, True),
+              ((256, 320), ops.E4M3, True, True), ((200, 96), ops.E5M2, True, False)]
+    a = [scaling.DelayedScaler(fmt, 16) for _, fmt, _, _ in shapes]
+    b = [scaling.DelayedScaler(fmt, 16) for _, fmt, _, _ in shapes]
+    g = torch.Generator(device=gpu).manual_seed(31)
+    for step in range(5):
+        xs = [(torch.randn(*shp, device=gpu, generator=g) * (0.5 + step)).to(torch.bfloat16)
+              for shp, _, _, _ in shapes]
+        xs[1][3, 7] = 300.0 * (step + 1)   # an outlier that moves the amax
+        qa = scaling.quantize_many([(sc, x, rw, tr) for sc, x, (_, _, rw, tr)
+                                    in zip(a, xs, shapes)])
+        qb = [sc.quantize(x, rowwise=rw, transpose=tr) for sc, x, (_, _, rw, tr)
+              in zip(b, xs, shapes)]
+        torch.cuda.synchronize()
+        for i, (p, q) in enumerate(zip(qa, qb)):
+            same = [torch.equal(p.data.view(torch.uint8), q.data.view(torch.uint8)),
+                    torch.equal(p.meta, q.meta), torch.equal(a[i].state, b[i].state),
+                    a[i].recorded == b[i].recorded, a[i]._pending == b[i]._pending]
+            if shapes[i][3]:
+                same.append(torch.equal(p.data_t.view(torch.uint8), q.data_t.view(torch.uint8)))
+            pend_a = a[i]._bufs[a[i]._slot ^ 1][:a[i]._pending]
+            pend_b = b[i]._bufs[b[i]._slot ^ 1][:b[i]._pending]
+            same.append(torch.equal(pend_a, pend_b))
+            assert all(same), f"step {step} tensor {i}: {same}"
+    assert all(sc.recorded == 4 for sc in a)
