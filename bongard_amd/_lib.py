@@ -69,6 +69,13 @@ SIGNATURES = {
     "bf8_quantize_mx_bf16": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
                                      c_void_p, c_void_p, c_void_p]),
     "bf8_gemm_mx_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
+    "bf8_quantize_nvfp4_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                                        c_void_p, c_void_p, c_void_p, c_void_p]),
+    "bf8_dequant_nvfp4": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "bf8_gemm_bf16_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
+    "bf8_gemm_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                              c_void_p, c_void_p, c_void_p, c_int, c_int64, c_void_p, c_size_t,
+                              c_void_p]),
     "bf8_gemm_mx": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                             c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int,
                             c_int64, c_void_p, c_size_t, c_void_p]),

@@ -468,7 +468,8 @@ int gemm_entry(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int f
                const float* b_scale_inv, int b_vec, int b_scale_stride, const int64_t* seg_ends,
                int n_seg, const void* bias, void* C, int out_dtype, int64_t ldc, void* ws,
                size_t ws_bytes, void* stream) {
-  BF8_CHECK((fmt_a == BF8_E4M3 || fmt_a == BF8_E5M2) && (fmt_b == BF8_E4M3 || fmt_b == BF8_E5M2),
+  BF8_CHECK(((fmt_a == BF8_E4M3 || fmt_a == BF8_E5M2) && (fmt_b == BF8_E4M3 || fmt_b == BF8_E5M2)) ||
+                (fmt_a == kFmtBf16 && fmt_b == kFmtBf16),
             "bf8_gemm: bad formats %d/%d", fmt_a, fmt_b);
   BF8_CHECK(out_dtype == BF8_OUT_BF16 || out_dtype == BF8_OUT_F32, "bf8_gemm: bad out_dtype");
   BF8_CHECK(M >= 0 && N >= 0 && K >= 0, "bf8_gemm: negative shape");
@@ -527,6 +528,22 @@ int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt
              void* stream) {
   return gemm_entry(A, fmt_a, lda, B, fmt_b, ldb, M, N, K, a_scale_inv, 0, b_scale_inv, 0,
                     b_scale_stride, seg_ends, n_seg, bias, C, out_dtype, ldc, ws, ws_bytes, stream);
+}
+
+size_t bf8_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K) {
+  return bf8_gemm_workspace(M, N, 2 * K);  // plans are made on K bytes
+}
+
+int bf8_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                  int64_t K, const float* a_scale_inv, const float* b_scale_inv, void* C,
+                  int out_dtype, int64_t ldc, void* ws, size_t ws_bytes, void* stream) {
+  BF8_CHECK(K >= 0 && lda >= 0 && ldb >= 0, "bf8_gemm_bf16: negative size");
+  BF8_CHECK(K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0,
+            "bf8_gemm_bf16: need K, lda, ldb multiples of 8 (K=%lld lda=%lld ldb=%lld)",
+            (long long)K, (long long)lda, (long long)ldb);
+  return gemm_entry((const uint8_t*)A, kFmtBf16, 2 * lda, (const uint8_t*)B, kFmtBf16, 2 * ldb,
+                    M, N, 2 * K, a_scale_inv, 0, b_scale_inv, 0, 0, nullptr, 1, nullptr, C,
+                    out_dtype, ldc, ws, ws_bytes, stream);
 }
 
 int bf8_gemm_axiswise(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt_b,

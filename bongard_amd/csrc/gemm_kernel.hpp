@@ -9,6 +9,10 @@ namespace bf8 {
 
 enum GemmEpi { EPI_LINEAR = 0, EPI_GEGLU = 1 };
 
+// Operand format of a bf16 GEMM (both operands bf16: 64 K-values per 128-byte step, so K,
+// lda and ldb are passed in bytes); the FP8 formats are BF8_E4M3 (0) and BF8_E5M2 (1).
+constexpr int kFmtBf16 = 2;
+
 struct GemmParams {
   const uint8_t* A;  // [M, K] row-major, row stride lda bytes
   const uint8_t* B;  // [N, K] row-major (nn.Linear weight layout), row stride ldb bytes

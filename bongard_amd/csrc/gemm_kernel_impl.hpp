@@ -137,10 +137,25 @@ __device__ __forceinline__ void block_coords(const GemmParams& p, int& tm, int& 
   walk_tile(p.tiles_m, p.tiles_n, id, tm, tn);
 }
 
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
 template <int FA, int FB>
 __device__ __forceinline__ v16f mfma(v8i a, v8i b, v16f c) {
-  // scale operands 0: plain (unscaled) f8f6f4 MFMA; FA/FB select e4m3 (0) / e5m2 (1).
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
+  if constexpr (FA == kFmtBf16) {
+    static_assert(FB == kFmtBf16, "bf16 GEMMs take two bf16 operands");
+    // the 64 bytes of a sub-step are 32 bf16 K-values: two 32x32x16 MFMAs, one per
+    // 16-byte half of each lane's fragment (A and B halves pair up, so every K-value
+    // of the row meets its partner)
+    const v8bf a0 = __builtin_bit_cast(v8bf, __builtin_shufflevector(a, a, 0, 1, 2, 3));
+    const v8bf a1 = __builtin_bit_cast(v8bf, __builtin_shufflevector(a, a, 4, 5, 6, 7));
+    const v8bf b0 = __builtin_bit_cast(v8bf, __builtin_shufflevector(b, b, 0, 1, 2, 3));
+    const v8bf b1 = __builtin_bit_cast(v8bf, __builtin_shufflevector(b, b, 4, 5, 6, 7));
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, c, 0, 0, 0);
+  } else {
+    // scale operands 0: plain (unscaled) f8f6f4 MFMA; FA/FB select e4m3 (0) / e5m2 (1).
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
+  }
 }
 
 // Block-scaled (MX) form: each lane supplies the E8M0 scale of the 32 K-values it holds
@@ -1026,6 +1041,16 @@ inline unsigned grid_blocks(const GemmParams& p) {
 template <class T, int EPI, int OUT>
 int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
   const dim3 grid(grid_blocks(p)), block(tile_threads<T>());
+  if (fa == kFmtBf16 || fb == kFmtBf16) {
+    if constexpr (EPI == EPI_LINEAR) {
+      if (fa == kFmtBf16 && fb == kFmtBf16) {
+        hipLaunchKernelGGL((gemm_kernel<T, kFmtBf16, kFmtBf16, EPI, OUT>), grid, block, 0, s, p);
+        return launch_status("gemm_kernel(bf16)");
+      }
+    }
+    set_error("gemm: bf16 operands need a bf16 partner and a linear epilogue");
+    return BF8_EINVAL;
+  }
   if (fa == BF8_E4M3 && fb == BF8_E4M3)
     hipLaunchKernelGGL((gemm_kernel<T, 0, 0, EPI, OUT>), grid, block, 0, s, p);
   else if (fa == BF8_E5M2 && fb == BF8_E4M3)

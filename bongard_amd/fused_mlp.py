@@ -27,7 +27,7 @@ import torch
 from . import linear as _linear
 from . import ops as _ops
 from . import scaling as _scaling
-from .te_linear import (RECIPES, _is_mx, _make_recipe, _new_scaling, _pad_rows, _ScalingExtraState,
+from .te_linear import (RECIPES, _is_mx, _is_nvfp4, _make_recipe, _new_scaling, _pad_rows, _ScalingExtraState,
                         present)
 
 __all__ = ["RECIPES", "FusedMLP", "enable_fused_mlp", "hf_state_dict"]
@@ -133,6 +133,8 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
         self.counts['kernel_tokens'] += aligned
         fc1, fc2 = self.scaling if self.scaling is not None else (None, None)
         mx = _is_mx(self.recipe)
+        if _is_nvfp4(self.recipe):
+            return self._nvfp4_forward(x, flat, length, first)
         if first:
             if mx:
                 self._fp8_weights = (_linear.quantize_weight_mx(self.fc1_weight),
@@ -179,6 +181,28 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
         out = _linear.Fp8GegluMlpFunction.apply(normed, self.fc1_weight, self.fc2_weight, gu_q,
                                                 down_q, self.intermediate_size, False,
                                                 self.scaling, x_amax)
+        return out[:length].reshape_as(x)
+
+
+    def _nvfp4_forward(self, x, flat, length, first):
+        """'nvfp4': the fused norm, fc1 as an NVFP4 GEMM, the bf16 gated GELU, fc2 as an
+        NVFP4 GEMM (no GEMM epilogue takes the activation: the operands are dequantized
+        to bf16 for the MFMA)."""
+        if first:
+            self._fp8_weights = (_linear.quantize_weight_nvfp4(self.fc1_weight),
+                                 _linear.quantize_weight_nvfp4(self.fc2_weight))
+        gu_q, down_q = self._fp8_weights
+        flat = flat.to(torch.bfloat16).contiguous()
+        if _ops.rmsnorm_supported(flat.shape[1]):
+            # the norm's amax partials go unused: the NVFP4 quantizer finds its own amax
+            parts = torch.empty(_ops.rmsnorm_partials_count(flat.shape[0]), dtype=torch.int32,
+                                device=flat.device)
+            normed = _FusedRMSNorm.apply(flat, self.layer_norm_weight, self.eps, parts)
+        else:
+            normed = _rms_norm(flat, self.layer_norm_weight, self.eps)
+        gu = _linear.Fp8LinearNvfp4Function.apply(normed, self.fc1_weight, gu_q)
+        h = _linear.GegluFunction.apply(gu)
+        out = _linear.Fp8LinearNvfp4Function.apply(h, self.fc2_weight, down_q)
         return out[:length].reshape_as(x)
 
 

@@ -215,6 +215,70 @@ class Fp8LinearAxiswiseFunction(_Fp8Function):
         return dx, dw, db, None
 
 
+def quantize_weight_nvfp4(weight, *, transpose=True):
+    """NVFP4 copy of a weight [N, K]: blocks along K (forward), and with ``transpose`` the
+    columnwise copy [K, N] with blocks along N (the input-gradient GEMM's operand)."""
+    return ops.quantize_nvfp4(weight.detach(), rowwise=True, colwise=transpose)
+
+
+class Fp8LinearNvfp4Function(_Fp8Function):
+    """y = x @ W^T under TE's NVFP4BlockScaling as built here (every tensor e2m1 in blocks
+    of 16 along the GEMM's reduction dimension, e4m3 block scales, a per-tensor fp32 scale;
+    round to nearest even, no Hadamard transform, no stochastic rounding); x: bf16 [M, K]
+    with M % 16 == 0 when the weight needs a gradient. Each GEMM dequantizes its NVFP4
+    operands exactly to bf16 and runs the bf16 MFMA, the two tensor scales in its epilogue.
+
+      forward  y  = X^ . W^T           blocks along K on both
+      dgrad    dX = dY^ . (W^T)^       dY blocks along N, W's columnwise copy
+      wgrad    dW = (dY^T)^ . (X^T)^   columnwise copies of dY and X (blocks along M)
+
+    Reference: te.Linear under the 'nvfp4' recipe (bongard/te_linear.py:17,38,73-74).
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, wq):
+        need_dx, need_dw = _forward_needs(ctx, 2)
+        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw)
+        if wq is None:
+            wq = quantize_weight_nvfp4(weight, transpose=need_dx)
+        y = ops.gemm_nvfp4(xq.data, xq.scales, xq.meta, wq.data, wq.scales, wq.meta)
+        ctx.save_for_backward(xq.data_t, xq.scales_t, xq.meta,
+                              wq.data_t if need_dx else None,
+                              wq.scales_t if need_dx else None, wq.meta)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x4t, xst, x_meta, w4t, wst, w_meta = ctx.saved_tensors
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dyq = ops.quantize_nvfp4(dy.contiguous(), rowwise=need_dx, colwise=need_dw)
+        dx = dw = None
+        if need_dx:
+            dx = ops.gemm_nvfp4(dyq.data, dyq.scales, dyq.meta, w4t, wst, w_meta)
+        if need_dw:
+            dw = ops.gemm_nvfp4(dyq.data_t, dyq.scales_t, dyq.meta, x4t, xst, x_meta)
+        return dx, dw, None
+
+
+class GegluFunction(torch.autograd.Function):
+    """H = bf16(bf16(gelu_tanh(gate)) * up) of the bf16 pre-activations GU [M, 2I] (gate |
+    up) and its backward, on the elementwise kernels (bit-identical to the bf16 chain
+    F.gelu(gate, approximate='tanh') * up, bongard/te_linear.py:103): the activation between
+    two projections whose GEMMs cannot take it into their epilogue (the NVFP4 recipe)."""
+
+    @staticmethod
+    def forward(ctx, GU):
+        H, _ = ops.geglu(GU)
+        ctx.save_for_backward(GU)
+        return H
+
+    @staticmethod
+    def backward(ctx, dH):
+        (GU,) = ctx.saved_tensors
+        dGU, _ = ops.geglu_bwd(dH.contiguous(), GU)
+        return dGU
+
+
 def quantize_weight_mx(weight, *, transpose=True):
     """MXFP8 copy of a weight [N, K]: blocks along K (forward), and with ``transpose`` the
     [K, N] copy with blocks along N (the input-gradient GEMM's operand)."""

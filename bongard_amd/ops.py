@@ -933,3 +933,84 @@ def cast_delayed_many(jobs):
         I32(*fields["fmt"]), P(*fields["meta"]), P(*fields["out"]), P(*fields["out_t"]),
         P(*fields["parts"]), _stream(dev)), "bf8_cast_delayed_many_bf16")
     return results
+
+
+# ---- NVFP4 (e2m1 in 16-blocks, e4m3 block scales, fp32 tensor scale) -------------------
+@dataclass
+class NvFp4Tensor:
+    """An NVFP4 tensor of x [rows, cols]: ``data`` uint8 [rows, cols / 2] (two e2m1 codes a
+    byte) with ``scales`` uint8 e4m3 [rows, cols / 16] (blocks along cols) and/or the
+    columnwise copy ``data_t`` [cols, rows / 2] with ``scales_t`` [cols, rows / 16] (blocks
+    along rows), and ``meta`` fp32 [4] = {amax, S_enc, S_dec, 0}."""
+
+    data: Optional[torch.Tensor]
+    scales: Optional[torch.Tensor]
+    data_t: Optional[torch.Tensor]
+    scales_t: Optional[torch.Tensor]
+    meta: torch.Tensor
+    rows: int
+    cols: int
+
+
+def quantize_nvfp4(x, *, rowwise=True, colwise=False):
+    """NVFP4 quantization of a bf16 tensor (flattened to 2-D): an amax pass and the block
+    quantization (rowwise needs cols % 16 == 0, columnwise rows % 16 == 0)."""
+    _require_gpu(x)
+    x = _bf16_2d(x)
+    rows, cols = x.shape
+    dev = x.device
+    meta = new_meta(dev)
+    u8 = torch.uint8
+    out = torch.empty((rows, cols // 2), dtype=u8, device=dev) if rowwise else None
+    sc = torch.empty((rows, cols // 16), dtype=u8, device=dev) if rowwise else None
+    out_t = torch.empty((cols, rows // 2), dtype=u8, device=dev) if colwise else None
+    sc_t = torch.empty((cols, rows // 16), dtype=u8, device=dev) if colwise else None
+    L = _lib.lib()
+    parts = partials_buffer(max(1, int(L.bf8_amax_partials(rows * cols))), dev)
+    _lib.check(L.bf8_quantize_nvfp4_bf16(_ptr(x), rows, cols, _ptr(out), _ptr(sc), _ptr(out_t),
+                                         _ptr(sc_t), _ptr(meta), _ptr(parts), _stream(dev)),
+               "bf8_quantize_nvfp4_bf16")
+    return NvFp4Tensor(out, sc, out_t, sc_t, meta, rows, cols)
+
+
+def dequant_nvfp4(data, scales):
+    """bf16 [rows, 2 * data cols] = e2m1(code) * s per element (exact, without S_dec)."""
+    _require_gpu(data, scales)
+    rows, half = data.shape
+    out = torch.empty((rows, 2 * half), dtype=torch.bfloat16, device=data.device)
+    _lib.check(_lib.lib().bf8_dequant_nvfp4(_ptr(data.contiguous()), _ptr(scales.contiguous()),
+                                            rows, 2 * half, _ptr(out), _stream(data.device)),
+               "bf8_dequant_nvfp4")
+    return out
+
+
+def gemm_bf16(a, b, a_sinv, b_sinv, *, out_dtype=torch.bfloat16):
+    """``C = (a @ b.T accumulated in fp32) * a_sinv * b_sinv`` on bf16 a [M, K], b [N, K]
+    (row-major) with the bf16 MFMA; a_sinv, b_sinv: device fp32 scalars."""
+    _require_gpu(a, b, a_sinv, b_sinv)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise TypeError("gemm_bf16: a and b must be bfloat16")
+    if a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("gemm_bf16: a and b must be row-major")
+    M, K = a.shape
+    N, Kb = b.shape
+    if K != Kb:
+        raise ValueError(f"gemm_bf16: inner dims differ ({K} vs {Kb})")
+    out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    L = _lib.lib()
+    ws_bytes = int(L.bf8_gemm_bf16_workspace(M, N, K))
+    ws = gemm_workspace(ws_bytes, a.device) if ws_bytes else None
+    ws_bytes = ws.numel() if ws is not None else 0
+    _lib.check(L.bf8_gemm_bf16(_ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K,
+                               _ptr(a_sinv), _ptr(b_sinv), _ptr(out),
+                               OUT_BF16 if out_dtype == torch.bfloat16 else OUT_F32,
+                               out.stride(0), _ptr(ws), ws_bytes, _stream(a.device)),
+               "bf8_gemm_bf16")
+    return out
+
+
+def gemm_nvfp4(a_data, a_scales, a_meta, b_data, b_scales, b_meta, *, out_dtype=torch.bfloat16):
+    """``C = (A^ @ B^.T) * S_dec(a) * S_dec(b)`` for NVFP4 operands A [M, K], B [N, K]
+    (blocks along K): both dequantized exactly to bf16, then the bf16 MFMA GEMM."""
+    return gemm_bf16(dequant_nvfp4(a_data, a_scales), dequant_nvfp4(b_data, b_scales),
+                     a_meta[2:3], b_meta[2:3], out_dtype=out_dtype)

@@ -21,8 +21,13 @@ as the reference does for stateful scaling.
 'mxfp8' is TE's MXFP8BlockScaling: every tensor (gradients included) in e4m3 blocks of 32
 values sharing an E8M0 scale, on the gfx950 block-scaled MFMA
 (bongard_amd.linear.Fp8LinearMxFunction / Fp8GegluMlpMxFunction); stateless, so export
-works as for 'fp8'. 'nvfp4' is accepted by name but raises NotImplementedError when a
-module is built: NVFP4 (e4m3 scales per 16 values) has no bit-compatible gfx950 format.
+works as for 'fp8'. 'nvfp4' is TE's NVFP4BlockScaling as far as its arithmetic is fixed
+without TE: every tensor in e2m1 blocks of 16 with e4m3 block scales under a per-tensor fp32
+scale, round to nearest even, 1-D blocks along each GEMM's reduction dimension (TE's random
+Hadamard transform, stochastic rounding and 2-D weight blocks are not built). gfx950 has no
+MFMA for e4m3-scaled FP4 blocks, so the blocks are dequantized exactly to bf16 and multiplied
+on the bf16 MFMA, with the gated GELU between the projections as its own kernels
+(bongard_amd.linear.Fp8LinearNvfp4Function, GegluFunction); stateless, like 'mxfp8'.
 """
 
 import os
@@ -64,6 +69,16 @@ class MXFP8BlockScaling:
     fp8_format: str = "E4M3"
 
 
+@dataclass(frozen=True)
+class NVFP4BlockScaling:
+    """NVFP4: e2m1 values in 16-element blocks with e4m3 block scales and a per-tensor fp32
+    scale, for every tensor (round to nearest even; no Hadamard transform, no stochastic
+    rounding, 1-D blocks)."""
+
+    fp4_format: str = "E2M1"
+    block_size: int = 16
+
+
 def _make_recipe(name):
     if name == 'fp8':
         return Float8CurrentScaling()
@@ -71,13 +86,17 @@ def _make_recipe(name):
         return DelayedScaling()
     if name == 'mxfp8':
         return MXFP8BlockScaling()
-    raise NotImplementedError(
-        f"TE recipe {name!r} has no gfx950 kernels (NVFP4's e4m3 block scales have no "
-        "gfx950 counterpart); use 'mxfp8' or 'fp8'")
+    if name == 'nvfp4':
+        return NVFP4BlockScaling()
+    raise ValueError(f'TE recipe must be one of {RECIPES}')
 
 
 def _is_mx(recipe):
     return isinstance(recipe, MXFP8BlockScaling)
+
+
+def _is_nvfp4(recipe):
+    return isinstance(recipe, NVFP4BlockScaling)
 
 
 def _new_scaling(recipe):
@@ -174,6 +193,8 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
         if is_first_microbatch or self._fp8_weight is None:
             if _is_mx(self.recipe):
                 q = _linear.quantize_weight_mx(self.weight, transpose=True)
+            elif _is_nvfp4(self.recipe):
+                q = _linear.quantize_weight_nvfp4(self.weight, transpose=True)
             else:
                 q = _linear.quantize_weight(self.weight, transpose=True,
                                             scaler=self.scaling and self.scaling.weight)
@@ -202,6 +223,9 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
         if _is_mx(self.recipe):
             out = _linear.Fp8LinearMxFunction.apply(flat, self.weight,
                                                     self.fp8_weight(first_microbatch))
+        elif _is_nvfp4(self.recipe):
+            out = _linear.Fp8LinearNvfp4Function.apply(flat, self.weight,
+                                                       self.fp8_weight(first_microbatch))
         else:
             out = _linear.Fp8LinearFunction.apply(flat, self.weight, None,
                                                   self.fp8_weight(first_microbatch), self.scaling)
@@ -248,6 +272,16 @@ class TEMLP(torch.nn.Module):
 
     @torch.compiler.disable
     def _fp8_forward(self, x):
+        if _is_nvfp4(self.down.recipe):
+            # NVFP4: the projections' own forwards (pad to 32, weight cache, NVFP4 GEMMs)
+            # around the bf16 gated GELU
+            if self.fused_gate_up:
+                gu = self.gate_up(x)
+            else:
+                gu = torch.cat([self.gate_proj(x), self.up_proj(x)], -1)
+            shape = gu.shape
+            h = _linear.GegluFunction.apply(gu.reshape(-1, shape[-1]).contiguous())
+            return self.down(h.reshape(*shape[:-1], shape[-1] // 2))
         I = self.intermediate_size
         flat = x.reshape(-1, x.shape[-1])
         flat, length, aligned = _pad_rows(flat)

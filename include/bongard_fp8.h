@@ -339,6 +339,35 @@ int bf8_quantize_mx_many_bf16(int count, const void* const* x, const int64_t* ro
                               const int64_t* cols, const int* fmt, uint8_t* const* out,
                               uint8_t* const* out_scales, void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * NVFP4 (TE NVFP4BlockScaling under the 'nvfp4' recipe: bongard/te_linear.py:17,38,
+ * bongard/fused_mlp.py:9,32). Round to nearest even everywhere, 1-D blocks of 16 along
+ * the GEMM's reduction dimension; TE's random Hadamard transform, stochastic rounding of
+ * gradients and 2-D weight blocks are not implemented.
+ *   meta = {amax, S_enc = fp32(2688 / max(amax, 1e-12)), S_dec = fp32(1 / S_enc), 0}
+ *   per block of 16 with b = max |x|: s = e4m3(fp32(fp32(b / 6) * S_enc)) (the scale
+ *   byte), mult = s ? fp32(S_enc / s) : 0, code = e2m1_rne(fp32(x * mult)) saturating at
+ *   6 (sign bit 3; two codes a byte, the even element in the low nibble)
+ * bf8_quantize_nvfp4_bf16: amax pass into partials [bf8_amax_partials(rows * cols)], then
+ * out [rows, cols / 2] + out_scales [rows, cols / 16] (rowwise, cols % 16 == 0) and/or
+ * out_t [cols, rows / 2] + out_t_scales [cols, rows / 16] (the rowwise quantization of x^T,
+ * rows % 16 == 0). bf8_dequant_nvfp4: bf16 [rows, cols] = e2m1(code) * s (exact; S_dec is
+ * left to the GEMM). bf8_gemm_bf16: C = (A . B^T accumulated in fp32) * a_scale_inv *
+ * b_scale_inv on bf16 A [M, K], B [N, K] (row strides lda, ldb elements, K % 8 == 0) on
+ * the bf16 MFMA (gfx950's block-scaled MFMA takes FP4 only with power-of-two scales per 32
+ * values, so NVFP4 runs as these exact bf16 operands with the two S_dec in the epilogue);
+ * ws: bf8_gemm_bf16_workspace(M, N, K) bytes or 0.
+ * ------------------------------------------------------------------------------- */
+int bf8_quantize_nvfp4_bf16(const void* x, int64_t rows, int64_t cols, uint8_t* out,
+                            uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
+                            float* meta, uint32_t* partials, void* stream);
+int bf8_dequant_nvfp4(const uint8_t* q, const uint8_t* scales, int64_t rows, int64_t cols,
+                      void* out, void* stream);
+size_t bf8_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K);
+int bf8_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                  int64_t K, const float* a_scale_inv, const float* b_scale_inv, void* C,
+                  int out_dtype, int64_t ldc, void* ws, size_t ws_bytes, void* stream);
+
 /* C[m, n] = sum_b 2^(ea[m,b] + eb[n,b] - 254) * sum_{k in block b} A[m, k] * B[n, k]
  * (+ bias[n]), e4m3 operands, fp32 accumulation; TN like bf8_gemm, K % 32 == 0. Scale
  * arrays 4-byte aligned with row strides >= bf8_mx_scale_ld(K), multiples of 4.

@@ -575,6 +575,114 @@ class DelayedQuantizer:
 
 
 # ---------------------------------------------------------------------------------------
+# NVFP4: e2m1 values in blocks of 16 with e4m3 block scales under a per-tensor fp32 scale
+# (TE NVFP4BlockScaling, bongard/te_linear.py:17,38; bongard/fused_mlp.py:9,32; TE 2.19.0 is
+# absent, so this restates NVIDIA's published NVFP4 quantization with round-to-nearest-even
+# everywhere and 1-D blocks along the reduction dimension; TE's random Hadamard transform,
+# stochastic rounding of gradients and 2-D weight blocks are not restated -- parity
+# unpinned for those)
+# ---------------------------------------------------------------------------------------
+NVFP4_GLOBAL = 448.0 * 6.0     # e4m3 max x e2m1 max
+E2M1_VALUES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+
+
+def e2m1_code(p: torch.Tensor) -> torch.Tensor:
+    """uint8 e2m1 codes of fp32 values: round to nearest even on {0, .5, 1, 1.5, 2, 3, 4, 6}
+    (ties to the even code), saturating at 6, sign bit 3 copied from p (-0 -> 0x8; NaN ->
+    code 0 with its sign)."""
+    a = p.abs()
+    m = ((a > 0.25).int() + (a >= 0.75).int() + (a > 1.25).int() + (a >= 1.75).int()
+         + (a > 2.5).int() + (a >= 3.5).int() + (a > 5.0).int())
+    return (m | (torch.signbit(p).int() << 3)).to(torch.uint8)
+
+
+def e2m1_decode(codes: torch.Tensor) -> torch.Tensor:
+    """fp32 value of e2m1 codes (low 4 bits)."""
+    table = torch.tensor(E2M1_VALUES + tuple(-v for v in E2M1_VALUES), dtype=torch.float32)
+    return table[(codes & 0xF).long()]
+
+
+def nvfp4_global_scale(amax_f32: torch.Tensor):
+    """(S_enc, S_dec) = (f32(2688 / max(f64(amax), 1e-12)), f32(1 / S_enc))."""
+    a = amax_f32.to(torch.float64)
+    s_enc = (NVFP4_GLOBAL / torch.clamp(a, min=EPS)).to(torch.float32)
+    return s_enc, s_enc.reciprocal()
+
+
+def nvfp4_block_multiplier(s_enc: torch.Tensor, sbytes: torch.Tensor) -> torch.Tensor:
+    """fp32 multiplier of each block: f32(S_enc / s) (correctly rounded), 0 where s == 0."""
+    s = sbytes.view(torch.float8_e4m3fn).float()
+    return torch.where(s == 0, torch.zeros_like(s), s_enc / s)
+
+
+def quantize_nvfp4(x: torch.Tensor, axis: int = -1):
+    """NVFP4 quantization of bf16 x [R, C] in blocks of 16 along ``axis`` (-1: rowwise,
+    blocks along C; 0: columnwise, the rowwise quantization of x^T). Returns (packed
+    uint8 [., ./2] with the even element in the low nibble, block scale bytes e4m3
+    [., ./16], S_enc, S_dec, amax). Per block with b = max |x|:
+    s = e4m3(f32(f32(b / 6) * S_enc)), mult = s == 0 ? 0 : f32(S_enc / s),
+    q = e2m1(f32(x * mult))."""
+    if axis == 0:
+        x = x.t().contiguous()
+    a = amax(x)
+    s_enc, s_dec = nvfp4_global_scale(a)
+    R, C = x.shape
+    blocks = x.float().reshape(R, C // 16, 16)
+    bmax = blocks.abs().amax(-1)
+    v = (bmax / torch.tensor(6.0)) * s_enc
+    sbytes = cast(v, torch.tensor(1.0), E4M3)
+    mult = nvfp4_block_multiplier(s_enc, sbytes)
+    codes = e2m1_code(blocks * mult[..., None]).reshape(R, C)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).to(torch.uint8)
+    return packed, sbytes, s_enc, s_dec, a
+
+
+def dequant_nvfp4(packed: torch.Tensor, sbytes: torch.Tensor) -> torch.Tensor:
+    """fp32 e2m1(q) * s per element ([R, 2 * packed cols]), without the global S_dec."""
+    R = packed.shape[0]
+    codes = torch.stack([packed & 0xF, packed >> 4], -1).reshape(R, -1)
+    s = sbytes.view(torch.float8_e4m3fn).float()
+    return e2m1_decode(codes) * s.repeat_interleave(16, dim=1)
+
+
+def scaled_mm_nvfp4(aq, a_sb, a_sdec, bq, b_sb, b_sdec):
+    """fp32 result of (A^ @ B^T) * a_sdec * b_sdec in fp64 (A^, B^ the block-dequantized
+    operands, exact)."""
+    a = dequant_nvfp4(aq, a_sb).double()
+    b = dequant_nvfp4(bq, b_sb).double()
+    return (a @ b.t() * float(a_sdec) * float(b_sdec)).to(torch.float32)
+
+
+def linear_fwd_bwd_nvfp4(x, w, dy):
+    """NVFP4 linear forward and backward, every tensor e2m1 in 16-blocks along the GEMM's
+    reduction dimension: y = X^ W^T; dX = dY^ (W^T)^; dW = (dY^T)^ (X^T)^. fp32 (y, dx, dw)."""
+    def q(t, axis):
+        p, sb, _, sdec, _ = quantize_nvfp4(t, axis)
+        return p, sb, sdec
+    y = scaled_mm_nvfp4(*q(x, -1), *q(w, -1))
+    dx = scaled_mm_nvfp4(*q(dy, -1), *q(w, 0))
+    dw = scaled_mm_nvfp4(*q(dy, 0), *q(x, 0))
+    return y, dx, dw
+
+
+def mlp_fwd_bwd_nvfp4(x, w_gate, w_up, w_down, dy):
+    """The gated MLP with its two projections in NVFP4 (gate/up stacked as one weight and
+    one global scale, as TE's fused gate_up; down on H) and the bf16 gelu chain between
+    them (g, u, H rounded to bf16). Returns fp32 (y, dx, dw_gate_up, dw_down)."""
+    I = w_gate.shape[0]
+    wgu = torch.cat([w_gate, w_up], 0)
+    gu = linear_fwd_bwd_nvfp4(x, wgu, torch.zeros(x.shape[0], 2 * I, dtype=torch.bfloat16))[0]
+    gu = gu.to(torch.bfloat16)
+    g, u = gu[:, :I], gu[:, I:]
+    h = geglu(g, u)
+    y, dh, dwd = linear_fwd_bwd_nvfp4(h, w_down, dy)
+    dg, du = geglu_bwd(g, u, dh.to(torch.bfloat16))
+    dgu = torch.cat([dg, du], 1)
+    _, dx, dwgu = linear_fwd_bwd_nvfp4(x, wgu, dgu)
+    return y, dx, dwgu, dwd
+
+
+# ---------------------------------------------------------------------------------------
 # helpers
 # ---------------------------------------------------------------------------------------
 def bf16_ulp(x: torch.Tensor) -> torch.Tensor:

@@ -84,13 +84,17 @@ def test_telinear_state_dict_and_eval():
     assert torch.equal(t2.weight, t.weight)
 
 
-def test_telinear_rejects_bias_and_block_recipes():
+def test_telinear_rejects_bias_and_builds_block_recipes():
     with pytest.raises(ValueError, match="bias-free"):
         te_linear.TELinear([nn.Linear(H, 16)], "fp8")
-    with pytest.raises(NotImplementedError, match="NVFP4"):
-        te_linear.TELinear([nn.Linear(H, 16, bias=False)], "nvfp4")
+    with pytest.raises(ValueError, match="TE recipe must be one of"):
+        te_linear.TELinear([nn.Linear(H, 16, bias=False)], "fp16")
     t = te_linear.TELinear([nn.Linear(H, 16, bias=False)], "mxfp8")
     assert t.recipe.fp8_format == "E4M3" and t.state_dict()["_extra_state"].numel() == 0
+    # NVFP4 is stateless too: an empty _extra_state, so export works as for 'fp8'
+    t = te_linear.TELinear([nn.Linear(H, 16, bias=False)], "nvfp4")
+    assert t.recipe.fp4_format == "E2M1" and t.recipe.block_size == 16
+    assert t.state_dict()["_extra_state"].numel() == 0
 
 
 def test_temlp_eval_matches_hf_mlp():

@@ -696,3 +696,188 @@ def test_mlp_backward_split_scales_tracks_fp64_autograd():
     assert _rel(dwgu[:I], wr[0].grad) < 0.15
     assert _rel(dwgu[I:], wr[1].grad) < 0.15
     assert _rel(dwd, wr[2].grad) < 0.12
+
+
+# ---- NVFP4 (TE 'nvfp4', bongard/te_linear.py:17,38) --------------------------------------
+# Pinned by: e2m1 known answers and an independent nearest-value search with exact
+# (fraction) comparisons over a dense sweep and every midpoint; a scalar restatement built
+# on the table-driven e4m3 encoder (encode_fp8_np) and that search, bit for bit on small
+# tensors; known answers of whole blocks; the reconstruction bound each block's rounding
+# implies; columnwise = rowwise of the transpose; a scalar brute-force GEMM.
+from fractions import Fraction  # noqa: E402
+
+
+def _e2m1_nearest(v: float) -> int:
+    """Independent e2m1 rounding: nearest grid value (exact comparisons), ties to the
+    even code, saturating at 6; the sign bit copied from v."""
+    a = Fraction(abs(v)) if math.isfinite(v) else Fraction(100)
+    best = None
+    for code, g in enumerate(orc.E2M1_VALUES):
+        d = abs(a - Fraction(g))
+        if best is None or d < best[0] or (d == best[0] and code % 2 == 0):
+            best = (d, code)
+    return best[1] | (8 if math.copysign(1.0, v) < 0 else 0)
+
+
+def test_e2m1_known_answers():
+    cases = [(0.0, 0), (0.25, 0), (0.2500001, 1), (0.5, 1), (0.75, 2), (1.0, 2), (1.25, 2),
+             (1.26, 3), (1.5, 3), (1.75, 4), (2.0, 4), (2.5, 4), (2.51, 5), (3.0, 5),
+             (3.5, 6), (4.0, 6), (5.0, 6), (5.01, 7), (6.0, 7), (7.5, 7), (1e30, 7),
+             (float("inf"), 7), (-0.0, 8), (-0.3, 9), (-6.0, 15)]
+    got = orc.e2m1_code(torch.tensor([v for v, _ in cases], dtype=torch.float32))
+    assert got.tolist() == [c for _, c in cases]
+    assert orc.e2m1_decode(torch.arange(16, dtype=torch.uint8)).tolist() == \
+        [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+
+
+def test_e2m1_rounding_equals_nearest_even_search():
+    grid = torch.linspace(-8.0, 8.0, 4097, dtype=torch.float32)
+    mids = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], dtype=torch.float32)
+    eps = torch.tensor([1.0 - 2 ** -23, 1.0, 1.0 + 2 ** -22], dtype=torch.float32)
+    near = (mids[:, None] * eps[None, :]).flatten()
+    vals = torch.cat([grid, near, -near])
+    got = orc.e2m1_code(vals)
+    want = [_e2m1_nearest(float(v)) for v in vals]
+    assert got.tolist() == want
+
+
+def _nvfp4_scalar(x_rows):
+    """Scalar restatement on numpy float32 with the table-driven e4m3 encoder and the
+    independent e2m1 search: (codes per element, scale byte per block, S_enc)."""
+    xf = np.asarray(x_rows, dtype=np.float32)
+    amax_v = float(np.max(np.abs(xf)))
+    s_enc = np.float32(orc.NVFP4_GLOBAL / max(amax_v, 1e-12))
+    table = orc.fp8_value_table(E4M3)
+    codes, sbytes = [], []
+    for row in xf:
+        rc, rs = [], []
+        for k in range(0, len(row), 16):
+            blk = row[k:k + 16]
+            v = np.float32(np.float32(np.max(np.abs(blk)) / np.float32(6.0)) * s_enc)
+            sb = int(orc.encode_fp8_np(np.clip(np.array([v]), -448, 448), E4M3)[0])
+            s = np.float32(table[sb])
+            mult = np.float32(0.0) if s == 0 else np.float32(s_enc / s)
+            rc += [_e2m1_nearest(float(np.float32(e * mult))) for e in blk]
+            rs.append(sb)
+        codes.append(rc)
+        sbytes.append(rs)
+    return codes, sbytes, s_enc
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_nvfp4_quantize_equals_scalar_restatement(seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(6, 64, generator=g) * torch.rand(6, 1, generator=g) * 10
+    x[0, :16] = 0.0                      # an all-zero block: scale 0, codes 0
+    x[1, 3] = 1e-6                       # tiny beside its block's values
+    x = x.to(torch.bfloat16)
+    packed, sb, s_enc, s_dec, _ = orc.quantize_nvfp4(x)
+    codes, sbytes, s_enc_ref = _nvfp4_scalar(x.float().numpy())
+    assert float(s_enc) == float(s_enc_ref)
+    assert float(s_dec) == float(np.float32(1.0 / float(s_enc)))
+    assert sb.tolist() == sbytes
+    unpacked = torch.stack([packed & 0xF, packed >> 4], -1).reshape(6, 64)
+    assert unpacked.tolist() == codes
+
+
+def test_nvfp4_known_answers():
+    x = torch.zeros(1, 32)
+    x[0, 0] = 6.0        # amax 6: S_enc = 448, block 0 scale 448 (0x7E), multiplier 1
+    x[0, 1] = -1.0
+    x[0, 16] = 0.75      # block 1: b / 6 * 448 = 56 = 1.75 * 2^5 (0x66), multiplier 8: -> 6
+    x[0, 17] = 0.0625    # 0.0625 * 8 = 0.5
+    x[0, 18] = 0.03125   # 0.25: the tie rounds to 0
+    packed, sb, s_enc, s_dec, _ = orc.quantize_nvfp4(x.to(torch.bfloat16))
+    assert float(s_enc) == 448.0 and sb.tolist() == [[0x7E, 0x66]]
+    codes = torch.stack([packed & 0xF, packed >> 4], -1).reshape(-1)
+    assert codes[:2].tolist() == [7, 10] and codes[16:19].tolist() == [7, 1, 0]
+    deq = orc.dequant_nvfp4(packed, sb)     # e2m1 * s, exact: 6 * 448, -1 * 448, 6 * 56, 0.5 * 56
+    assert deq[0, :2].tolist() == [2688.0, -448.0] and deq[0, 16:18].tolist() == [336.0, 28.0]
+    back = deq * s_dec                       # S_dec = f32(1 / 448) is not exact
+    assert torch.allclose(back[0, [0, 1, 16, 17]], torch.tensor([6.0, -1.0, 0.75, 0.0625]),
+                          rtol=2 ** -23, atol=0)
+
+
+def test_nvfp4_reconstruction_bound_and_columnwise():
+    """|x - x^| <= one unit of the block's e2m1 grid (s / S_enc; the largest half-step
+    is 1 and saturation costs less); the columnwise copy is the rowwise quantization of
+    the transpose."""
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(48, 80, generator=g) * torch.rand(48, 1, generator=g) * 3).to(torch.bfloat16)
+    packed, sb, s_enc, s_dec, _ = orc.quantize_nvfp4(x)
+    deq = orc.dequant_nvfp4(packed, sb) * s_dec
+    unit = (sb.view(torch.float8_e4m3fn).float() / s_enc).repeat_interleave(16, dim=1)
+    assert bool(((deq - x.float()).abs() <= unit * (1 + 1e-6)).all())
+    pc, sc, se2, _, _ = orc.quantize_nvfp4(x, axis=0)
+    pt, st, se3, _, _ = orc.quantize_nvfp4(x.t().contiguous())
+    assert torch.equal(pc, pt) and torch.equal(sc, st) and float(se2) == float(se3) == float(s_enc)
+
+
+def test_scaled_mm_nvfp4_brute_force():
+    g = torch.Generator().manual_seed(6)
+    a = torch.randn(3, 32, generator=g).to(torch.bfloat16)
+    b = torch.randn(4, 32, generator=g).to(torch.bfloat16)
+    pa, sa, _, da, _ = orc.quantize_nvfp4(a)
+    pb, sb, _, db, _ = orc.quantize_nvfp4(b)
+    got = orc.scaled_mm_nvfp4(pa, sa, da, pb, sb, db)
+    A = orc.dequant_nvfp4(pa, sa).tolist()
+    B = orc.dequant_nvfp4(pb, sb).tolist()
+    for i in range(3):
+        for j in range(4):
+            ref = sum(A[i][k] * B[j][k] for k in range(32)) * float(da) * float(db)
+            assert abs(float(got[i, j]) - ref) <= 1e-6 * max(1.0, abs(ref))
+
+
+def test_nvfp4_chains_track_fp64_autograd():
+    """Linear and gated-MLP NVFP4 chains against fp64 autograd of the unquantized layers:
+    within the e2m1 error (a transposed operand or a scale on the wrong tensor is far off)."""
+    g = torch.Generator().manual_seed(48)
+    M, K, N = 64, 96, 80
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
+    y, dx, dw = orc.linear_fwd_bwd_nvfp4(x, w, dy)
+    xr, wr = x.double().requires_grad_(True), w.double().requires_grad_(True)
+    (xr @ wr.t()).backward(dy.double())
+    assert _rel(y, x.double() @ w.double().t()) < 0.25
+    assert _rel(dx, xr.grad) < 0.3 and _rel(dw, wr.grad) < 0.3
+    I = 64
+    wg = (torch.randn(I, K, generator=g) * 0.05).to(torch.bfloat16)
+    wu = (torch.randn(I, K, generator=g) * 0.05).to(torch.bfloat16)
+    wd = (torch.randn(K, I, generator=g) * 0.05).to(torch.bfloat16)
+    dy2 = (torch.randn(M, K, generator=g) * 1e-3).to(torch.bfloat16)
+    y2, dx2, dwgu, dwd = orc.mlp_fwd_bwd_nvfp4(x, wg, wu, wd, dy2)
+    xr = x.double().requires_grad_(True)
+    ws = [t.double().requires_grad_(True) for t in (wg, wu, wd)]
+    yr = (F.gelu(xr @ ws[0].t(), approximate="tanh") * (xr @ ws[1].t())) @ ws[2].t()
+    yr.backward(dy2.double())
+    assert _rel(y2, yr.detach()) < 0.35
+    assert _rel(dx2, xr.grad) < 0.45
+    assert _rel(dwgu, torch.cat([ws[0].grad, ws[1].grad])) < 0.45
+    assert _rel(dwd, ws[2].grad) < 0.45
+
+
+def _round_f32(fr: Fraction) -> float:
+    """Correctly rounded (ties to even) fp32 of an exact rational."""
+    v = float(np.float32(float(fr)))             # within one ulp; settle by exact midpoints
+    lo, hi = np.nextafter(np.float32(v), np.float32(-np.inf)), np.nextafter(np.float32(v), np.float32(np.inf))
+    best = min((abs(Fraction(float(c)) - fr), 0 if (np.float32(c).view(np.uint32) & 1) == 0 else 1,
+                float(c)) for c in (lo, np.float32(v), hi))
+    return best[2]
+
+
+def test_nvfp4_multiplier_is_the_correctly_rounded_quotient():
+    """mult = f32(S_enc / s) rounded once: checked with exact rationals over every finite
+    positive e4m3 block scale and several global scales (a product with a rounded 1 / s
+    differs on some of these pairs)."""
+    s_bytes = torch.arange(1, 0x7F, dtype=torch.uint8)
+    differs = 0
+    for amax_v in (0.37, 1.0, 3.14159, 64.5, 1234.5):
+        s_enc, _ = orc.nvfp4_global_scale(torch.tensor(amax_v, dtype=torch.float32))
+        got = orc.nvfp4_block_multiplier(s_enc, s_bytes)
+        sv = s_bytes.view(torch.float8_e4m3fn).float()
+        for b in range(len(s_bytes)):
+            want = _round_f32(Fraction(float(s_enc)) / Fraction(float(sv[b])))
+            assert float(got[b]) == want
+            differs += float(np.float32(float(s_enc) * np.float32(1.0 / float(sv[b])))) != want
+    assert differs > 0
