@@ -36,15 +36,6 @@ def _close(got, ref, what, tol=0.01):
     assert rel <= tol, what
 
 
-def _close_stat(got, ref, what, max_tol, rms_tol):
-    got, ref = got.float().cpu(), ref.float().cpu()
-    rms = max(_rms(ref), 1e-30)
-    max_rel = (got - ref).abs().max().item() / rms
-    rms_rel = _rms(got - ref) / rms
-    print(f"[{what}] max|err|/RMS = {max_rel:.3e}, RMS(err)/RMS = {rms_rel:.3e}", flush=True)
-    assert max_rel <= max_tol and rms_rel <= rms_tol, what
-
-
 def _inputs(rows, cols, seed):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(rows, cols, generator=g) * torch.rand(rows, 1, generator=g) * 4
