@@ -39,6 +39,8 @@ and two entries beyond the BASELINE configurations:
   c1_rowwise  c1 under torchao's 'rowwise' recipe (per-row power-of-2 scales), and the
               per-row + per-column quantization of [8192, 2560]
   c2_mxfp8    the c2 MLP forward under TE's 'mxfp8' recipe (block-scaled MFMA)
+  c2_nvfp4    the c2 MLP forward under TE's 'nvfp4' recipe (bf16 MFMA on exactly
+              dequantized NVFP4 operands)
   state_kv    the decoder's state-bank K/V projection of the c3 packed state
 
 ``cpu_baseline`` times the CPU oracle (torch CPU: amax, clamp, .to(float8), fp32 matmul,
@@ -58,6 +60,7 @@ sys.path.insert(0, str(ROOT))
 
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA (AMD public spec), no sparsity
 HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (the NVFP4 recipe's GEMMs)
 METRIC = "FP8 linear TFLOP/s & % MFMA peak at 4B shapes; quantize cast GB/s"
 PREWARM_STEPS = 20
 
@@ -272,6 +275,7 @@ def main():
             "fused_norm": _bench_norm(torch, ops, workloads, dev),
             "c1_rowwise": _bench_c1_rowwise(torch, ops, workloads, dev),
             "c2_mxfp8": _bench_c2_mx(torch, ops, workloads, dev),
+            "c2_nvfp4": _bench_c2_nvfp4(torch, ops, workloads, dev),
             "state_kv": _bench_state_kv(torch, workloads, dev),
         }
 
@@ -652,6 +656,61 @@ def _bench_c2_mx(torch, ops, workloads, dev, steps=30):
             "quantize_h_gbps": round((3.0 * M * I + M * I / 32) / h_s / 1e9, 1),
             "quantize_x_wgu_wd_one_launch_us": round(qm_s * 1e6, 2),
             "quantize_x_wgu_wd_separate_us": round(qs_s * 1e6, 2)}
+
+
+def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
+    """The c2 MLP forward under TE's 'nvfp4' recipe as TEMLP runs it: X, [W_gate; W_up] and
+    W_down quantized to NVFP4 (e2m1, 16-blocks, e4m3 block scales, per-tensor scale), each
+    GEMM on the bf16 MFMA over the exactly dequantized operands, the gated GELU as an
+    elementwise kernel on the stored [gate | up], H quantized to NVFP4 for the down GEMM."""
+    c = workloads.config2()
+    x = c["x"].to(dev)
+    w_gu = torch.cat([c["w_gate"], c["w_up"]]).to(dev)
+    w_d = c["w_down"].to(dev)
+    M, K = x.shape
+    I = c["w_gate"].shape[0]
+
+    def q(t):
+        return ops.quantize_nvfp4(t, rowwise=True, colwise=False)
+
+    def step():
+        xq, gq, dq = q(x), q(w_gu), q(w_d)
+        GU = ops.gemm_nvfp4(xq.data, xq.scales, xq.meta, gq.data, gq.scales, gq.meta)
+        H, _ = ops.geglu(GU)
+        hq = q(H)
+        return ops.gemm_nvfp4(hq.data, hq.scales, hq.meta, dq.data, dq.scales, dq.meta)
+
+    for _ in range(5):
+        step()
+    s = _timed(torch, step, steps, 3)
+    xq, gq, dq = q(x), q(w_gu), q(w_d)
+    xb, gb = ops.dequant_nvfp4(xq.data, xq.scales), ops.dequant_nvfp4(gq.data, gq.scales)
+    GU = ops.gemm_bf16(xb, gb, xq.meta[2:3], gq.meta[2:3])
+    H, _ = ops.geglu(GU)
+    hq = q(H)
+    hb, db = ops.dequant_nvfp4(hq.data, hq.scales), ops.dequant_nvfp4(dq.data, dq.scales)
+    gu_s = _ev_time(torch, lambda: ops.gemm_bf16(xb, gb, xq.meta[2:3], gq.meta[2:3]), steps)
+    d_s = _ev_time(torch, lambda: ops.gemm_bf16(hb, db, hq.meta[2:3], dq.meta[2:3]), steps)
+    qh_s = _ev_time(torch, lambda: q(H), steps)
+    dqh_s = _ev_time(torch, lambda: ops.dequant_nvfp4(hq.data, hq.scales), steps)
+    gl_s = _ev_time(torch, lambda: ops.geglu(GU), steps)
+    flop = 2.0 * M * (2 * I * K + K * I)
+    nh = M * I
+    return {"workload": f"c2 MLP forward [{M},{K}] x [2*{I},{K}] -> [{M},{I}] x [{K},{I}], NVFP4 "
+                        "(bf16 MFMA on exactly dequantized operands)",
+            "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
+            "gemm_gate_up_bf16_us": round(gu_s * 1e6, 2),
+            "gemm_gate_up_bf16_tflops": round(2.0 * M * 2 * I * K / gu_s / 1e12, 1),
+            "gemm_gate_up_frac_of_bf16_peak": round(2.0 * M * 2 * I * K / gu_s / 1e12
+                                                    / BF16_PEAK_TFLOPS, 4),
+            "gemm_down_bf16_us": round(d_s * 1e6, 2),
+            "gemm_down_bf16_tflops": round(2.0 * M * K * I / d_s / 1e12, 1),
+            "geglu_elementwise_us": round(gl_s * 1e6, 2),
+            "geglu_elementwise_gbps": round(6.0 * nh / gl_s / 1e9, 1),
+            "quantize_h_us": round(qh_s * 1e6, 2),
+            "quantize_h_gbps": round((4.0 + 0.5 + 1 / 16) * nh / qh_s / 1e9, 1),
+            "dequant_h_us": round(dqh_s * 1e6, 2),
+            "dequant_h_gbps": round((2.0 + 0.5 + 1 / 16) * nh / dqh_s / 1e9, 1)}
 
 
 def _bench_c1_rowwise(torch, ops, workloads, dev, steps=50):

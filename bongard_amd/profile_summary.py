@@ -2,13 +2,17 @@
 
     python -m bongard_amd.profile_summary trace <results.db>
     python -m bongard_amd.profile_summary pmc <results.db>
+    python -m bongard_amd.profile_summary steps <results.db> <first kernel> [skip]
 
 ``trace``: per-kernel call count and average / min / max duration (us) from the
 kernel-dispatch records, and the average over the kernel's longest run of back-to-back
 dispatches (no other kernel between them): a benchmark that times N launches of one
 kernel between two events produces exactly such a run, so that figure is the one to set
 beside the benchmark's own per-launch average. ``pmc``: per-kernel, per-counter average
-value per dispatch.
+value per dispatch. ``steps``: the dispatches cut into steps, each starting at a dispatch
+whose name contains ``first kernel`` (the first ``skip`` steps dropped, default 2: clock
+ramp), and per position in the step the kernel, its median and minimum duration (us); the
+steps must all launch the same kernel sequence.
 """
 import sqlite3, sys, re
 def short(n):
@@ -56,9 +60,32 @@ def pmc(path):
         a = agg.setdefault((short(name), c, g), [0, 0.0])
         a[0] += 1; a[1] += v
     return {k: v[1] / v[0] for k, v in agg.items()}
+def step_table(path, first, skip=2):
+    db = sqlite3.connect(path); cur = db.cursor()
+    rows = sorted(cur.execute("select name, start, end from kernels").fetchall(), key=lambda r: r[1])
+    steps = []
+    for name, s, e in rows:
+        if first in name:
+            steps.append([])
+        if steps:
+            steps[-1].append((short(name), (e - s) / 1e3))
+    steps = steps[skip:]
+    if not steps or any([k for k, _ in st] != [k for k, _ in steps[0]] for st in steps):
+        raise SystemExit("steps: no steps found, or the steps launch different kernel sequences")
+    out = [f"{'kernel':70s} {'median_us':>10s} {'min_us':>9s}"]
+    med_sum = min_sum = 0.0
+    for i, (k, _) in enumerate(steps[0]):
+        d = sorted(st[i][1] for st in steps)
+        med = d[len(d) // 2] if len(d) % 2 else 0.5 * (d[len(d) // 2 - 1] + d[len(d) // 2])
+        med_sum += med; min_sum += d[0]
+        out.append(f"{k:70s} {med:10.2f} {d[0]:9.2f}")
+    out.append(f"{'sum (' + str(len(steps)) + ' steps)':70s} {med_sum:10.2f} {min_sum:9.2f}")
+    return "\n".join(out)
 if __name__ == "__main__":
     if sys.argv[1] == "trace":
         print(kernel_stats(sys.argv[2]))
+    elif sys.argv[1] == "steps":
+        print(step_table(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 2))
     else:
         for k, v in sorted(pmc(sys.argv[2]).items()):
             print(f"{k[0]:70s} {k[1]:22s} grid={k[2]:<10d} {v:16.1f} per dispatch")

@@ -11,7 +11,9 @@ epilogue, H scale + cast, down GEMM). ``square``: one 8192^3 e4m3 GEMM, the stea
 main loop with no epilogue-heavy work. ``recipes``: the kernels of the other recipes and
 the fused norm: the config-2 MLP forward under MXFP8 (block quantize, MX gated-GELU GEMM with H
 quantized in its epilogue, MX down GEMM), the axiswise (torchao rowwise) quantization of a [8192, 2560] activation
-per row and per column, and the fused RMSNorm of the same activation. ``c5``: the
+per row and per column, the fused RMSNorm of the same activation, and the config-2 MLP
+forward under NVFP4 (block quantize, exact dequantization, bf16 MFMA GEMMs, elementwise
+gated GELU). ``c5``: the
 config-5 training step (the c2 MLP at M = 8192, forward and backward, delayed scaling with
 an amax history of 16). ``vs_hipblaslt``: this library's FP8 GEMM and hipBLASLt's (through
 ``torch._scaled_mm``) on the c2 / c4 / square shapes, each captured as a HIP graph of 20
@@ -199,6 +201,10 @@ def _recipes(dev, iters):
         ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales)
         ops.quantize_axiswise(a, ops.E4M3, rowwise=True, colwise=True)
         ops.rmsnorm(a, gamma, 1e-6)
+        xn, gn, dn = (ops.quantize_nvfp4(t) for t in (x, w_gu, w_d))
+        H, _ = ops.geglu(ops.gemm_nvfp4(xn.data, xn.scales, xn.meta, gn.data, gn.scales, gn.meta))
+        hn = ops.quantize_nvfp4(H)
+        ops.gemm_nvfp4(hn.data, hn.scales, hn.meta, dn.data, dn.scales, dn.meta)
     torch.cuda.synchronize()
     print(f"profile_target done: {iters} iterations (recipes), copy {COPY_BYTES} bytes", flush=True)
 
