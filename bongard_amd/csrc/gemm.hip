@@ -167,7 +167,18 @@ double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu, int64_t ksteps
   const double rate = geglu ? ti.geglu_rate : ti.rate;
   const double work_ns = per_cu * 2.0 * ti.bm * ti.bn * kStepBytes / (rate * 1e3);
   const double step_ns = std::max(work_ns, ti.occ > 1 ? kStepFloorNsOcc2 : kStepFloorNs);
-  double t = (double)rounds * (p.kps + 2) * step_ns;
+  // A last round that only part of the CUs run, after whole rounds, steps faster than a
+  // whole one (the busy CUs share the memory system and the power budget with fewer
+  // others): costed as 0.35 + 0.65 f of a round for a fraction f of the workgroup slots.
+  // Measured on c5's dW_down (M = 2560, N = 10240, K = 8192): one round and 56% of a
+  // second of eight-wave 256x256 tiles 164 us, two rounds and 50% of a third of 256x160
+  // tiles 188 us. A lone partial round (small M) is latency-bound and keeps its full cost.
+  const int64_t slots = (int64_t)kNumCus * ti.occ;
+  const int64_t whole = ctas / slots;
+  const double frac = (double)(ctas - whole * slots) / slots;
+  const double eff_rounds =
+      whole >= 1 && frac > 0 ? whole + 0.35 + 0.65 * frac : (double)rounds;
+  double t = eff_rounds * (p.kps + 2) * step_ns;
   if (p.splits > 1) t += 2.0 * p.splits * M * N * 4 / 5e3 + 5000.0;
   return t;
 }
