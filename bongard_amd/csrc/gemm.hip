@@ -37,6 +37,7 @@ enum TileId {
   TILE_64x128k2,
   TILE_128x128k2,
   TILE_256x256w8,
+  TILE_256x256w8x,
   NUM_TILES
 };
 
@@ -65,6 +66,7 @@ constexpr TileInfo kTiles[NUM_TILES] = {
     {64, 128, 1, 0.1, 0.0, "64x128k2", false},
     {128, 128, 1, 0.1, 0.0, "128x128k2", false},
     {256, 256, 1, 10.0, 9.2, "256x256w8", false},
+    {256, 256, 1, 10.0, 0.0, "256x256w8x", false},
 };
 // Whether `tile` has a gated-GELU variant for I = N / 2: tiles of 128 or 64 H columns take
 // any I (a multiple of 128); the 256x160 tile (80 gate + 80 up columns, one wave column)
@@ -120,9 +122,17 @@ constexpr double kTailStepRate256 = 11.2;
 // the eight-wave 256x256 tile on the same long-K shapes (8192^3: 394.8 -> 385.4 us)
 constexpr double kTailStepRate256w8 = 11.5;
 
+// Linear GEMMs with at least this many K steps run the eight-wave tile with its third B
+// slot (Tile256x256w8x): in a training step their operands come from HBM, not the MALL,
+// and B loaded two steps ahead hides that (operands rotated through more than the MALL
+// holds, interleaved A/B, bit-identical: c5's dW_down 197.7 -> 179.5 us, dX (K = 20480)
+// 355.8 -> 337.5 us, 8192^3 423.1 -> 403.5 us); with K = 2560 (20 steps) the extra slot
+// costs 1.5-2%, warm or cold.
+constexpr int64_t kExtraBSlotMinSteps = 48;
+
 bool make_tail_plan(int tile, int64_t M, int64_t N, int64_t ksteps, Plan& p) {
   const TileInfo& ti = kTiles[tile];
-  if (tile != TILE_256x256 && tile != TILE_256x256w8) return false;
+  if (tile != TILE_256x256 && tile != TILE_256x256w8 && tile != TILE_256x256w8x) return false;
   p = Plan{};
   p.tile = tile;
   p.tiles_m = (int)cdiv(M, ti.bm);
@@ -156,7 +166,8 @@ double plan_cost(const Plan& p, int64_t M, int64_t N, bool geglu, int64_t ksteps
   if (p.tail_pieces > 0) {
     // whole rounds of whole tiles, one round of pieces, the pieces' partials written and
     // read back, the reduction's launch
-    const double rate = p.tile == TILE_256x256w8 ? kTailStepRate256w8 : kTailStepRate256;
+    const double rate =
+        p.tile == TILE_256x256 ? kTailStepRate256 : kTailStepRate256w8;  // w8 and w8x alike
     const double step_ns = 2.0 * ti.bm * ti.bn * kStepBytes / (rate * 1e3);
     const double rounds = (double)p.full_tiles / kNumCus;
     return rounds * (ksteps + 2) * step_ns + (p.kps + 2) * step_ns + 2.0 * p.ws_bytes / 5e3 + 5000.0;
@@ -227,6 +238,8 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
     // the eight-wave 256x256 tile replaces the four-wave one wherever it has a variant
     // (measured faster on every large shape, same bits); MX keeps the four-wave tile
     if (!mx && tile == TILE_256x256) continue;
+    // the extra-B-slot twin of the eight-wave tile is substituted below, by K
+    if (tile == TILE_256x256w8x) continue;
     for (int s = 1; s <= (geglu ? 1 : kMaxSplits); ++s) {
       const Plan p = make_plan(tile, M, N, geglu ? kGegluNominalSteps : ksteps, s);
       if (p.splits != s || (s > 1 && p.kps < kMinStepsPerSplit) || p.ws_bytes > ws_avail)
@@ -249,6 +262,8 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
     }
   }
   if (geglu) best.kps = (int)ksteps;
+  if (!geglu && !mx && best.tile == TILE_256x256w8 && ksteps >= kExtraBSlotMinSteps)
+    best.tile = TILE_256x256w8x;  // same geometry, so the plan (tiles, pieces) stands
   // A small tile that leaves one workgroup per CU (no K split) runs as its two-K-group
   // twin: two pipelines per CU take alternate K steps (measured ~10% faster at M = 512,
   // e.g. N = 4096, K = 2560: 10.5 vs 11.5 us; with more tiles than CUs the one-group tile
@@ -279,6 +294,7 @@ int launch_tile(const Plan& pl, const GemmParams& p, int epi, int out_dtype, int
     case TILE_64x128k2: return launch_gemm_tile<Tile64x128k2>(p, epi, out_dtype, fa, fb, s, mx);
     case TILE_128x128k2: return launch_gemm_tile<Tile128x128k2>(p, epi, out_dtype, fa, fb, s, mx);
     case TILE_256x256w8: return launch_gemm_tile<Tile256x256w8>(p, epi, out_dtype, fa, fb, s, mx);
+    case TILE_256x256w8x: return launch_gemm_tile<Tile256x256w8x>(p, epi, out_dtype, fa, fb, s, mx);
     default: return launch_gemm_tile<Tile128x128>(p, epi, out_dtype, fa, fb, s, mx);
   }
 }

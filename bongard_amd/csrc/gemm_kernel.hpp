@@ -103,6 +103,9 @@ using Tile256x128 = GemmTile<2, 2, 4, 2, 3, 1>;
 // eight waves, two per SIMD, each with 128 accumulators of the 256 x 256 tile: while one
 // wave of a SIMD waits (LDS reads, the epilogue's dependency chains) the other issues
 using Tile256x256w8 = GemmTile<2, 4, 4, 2, 2, 1>;
+// the same with a third B slot in the 32 KB its stages leave free (B loads two steps
+// ahead): for long-K linear GEMMs whose operands come from HBM rather than the MALL
+using Tile256x256w8x = GemmTile<2, 4, 4, 2, 2, 1, 1, 1>;
 // two K groups (skinny GEMMs): 8 waves, alternate K steps
 using Tile128x64k2 = GemmTile<2, 2, 2, 1, 3, 1, 2>;
 using Tile64x128k2 = GemmTile<2, 2, 1, 2, 3, 1, 2>;

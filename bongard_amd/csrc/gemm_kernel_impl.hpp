@@ -1102,7 +1102,17 @@ template <class T>
 int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int fmt_b,
                      hipStream_t stream, bool mx) {
   const dim3 grid(grid_blocks(p)), block(tile_threads<T>());
-  if constexpr (T::KG != 1) {
+  if constexpr (T::XB > 0) {
+    // a tile that already fills the LDS with its extra B slot: linear, non-MX only
+    if (epi == EPI_GEGLU || mx) {
+      set_error("gemm: tile %dx%d with an extra B slot has linear non-MX epilogues only",
+                T::BM, T::BN);
+      return BF8_EINVAL;
+    }
+    if (out_dtype == BF8_OUT_BF16)
+      return launch_typed<T, EPI_LINEAR, BF8_OUT_BF16>(p, fmt_a, fmt_b, stream);
+    return launch_typed<T, EPI_LINEAR, BF8_OUT_F32>(p, fmt_a, fmt_b, stream);
+  } else if constexpr (T::KG != 1) {
     if (epi == EPI_GEGLU || mx) {
       set_error("gemm: tile %dx%d with two K groups has linear non-MX epilogues only", T::BM,
                 T::BN);

@@ -270,7 +270,7 @@ def test_mlp_down_gemm_on_own_h8(gpu):
 # BONGARD_FP8_GEMM_TILE forces the library's plan (read on every call), so each tile shape
 # and the split-K fix-up are checked on shapes with M, N and K tails.
 TILES = ["256x256", "256x160", "160x256", "128x128", "192x256", "256x128", "128x64",
-         "64x128", "128x64k2", "64x128k2", "128x128k2", "256x256w8"]
+         "64x128", "128x64k2", "64x128k2", "128x128k2", "256x256w8", "256x256w8x"]
 
 
 @pytest.mark.parametrize("splits", [1, 3])
@@ -451,7 +451,7 @@ def _tail_pieces(M, N, K):
     return ws // (tails * 256 * 256 * 4)
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x256w8"])
+@pytest.mark.parametrize("tile", ["256x256", "256x256w8", "256x256w8x"])
 @pytest.mark.parametrize("fa,bias", [(ops.E4M3, False), (ops.E4M3, True), (ops.E5M2, False)])
 def test_tail_split(gpu, monkeypatch, fa, bias, tile):
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", f"{tile}:t")
@@ -491,6 +491,24 @@ def test_tail_split_deterministic_and_segments(gpu, monkeypatch):
         _assert_fp32_close(outs[0][:, start:start + w.shape[0]], orc.scaled_mm(rx, sx, 0, rw, sw, 0),
                            what=f"tail segment {start}")
         start += w.shape[0]
+
+
+def test_long_k_plans_take_the_extra_b_slot(gpu, monkeypatch, capfd):
+    """The planner runs the eight-wave 256x256 tile with its third B slot from 48 K steps on
+    (c5's dW_down, K = 8192) and without it below (c5's dH, K = 2560); the gated-GELU GEMM
+    has no such variant. The choice is printed by BONGARD_FP8_GEMM_DEBUG=1."""
+    monkeypatch.setenv("BONGARD_FP8_GEMM_DEBUG", "1")
+    monkeypatch.delenv("BONGARD_FP8_GEMM_TILE", raising=False)
+    g = torch.Generator().manual_seed(63)
+    plans = {}
+    for M, N, K in ((2560, 10240, 8192), (8192, 10240, 2560)):
+        a = _quant(torch.randn(M, K, generator=g).to(torch.bfloat16), ops.E4M3, gpu)
+        b = _quant((torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16), ops.E4M3, gpu)
+        ops.gemm(a.data, 0, a.meta, b.data, 0, b.meta)
+        torch.cuda.synchronize()
+        line = [l for l in capfd.readouterr().err.splitlines() if l.startswith("bf8 plan gemm")]
+        plans[K] = line[-1].split(" tile ")[1].split()[0]
+    assert plans == {8192: "256x256w8x", 2560: "256x256w8"}, plans
 
 
 def test_tail_split_auto_plan_c5_dgrad(gpu):
