@@ -90,6 +90,24 @@ def test_gemm_bf16(gpu, M, N, K):
     assert torch.equal(y16.cpu().view(torch.int16), y32.cpu().to(torch.bfloat16).view(torch.int16))
 
 
+@pytest.mark.parametrize("tile", ["256x256w8", "256x256w8x", "256x160", "128x64k2"])
+def test_gemm_bf16_tiles(gpu, monkeypatch, tile):
+    """The bf16 operand format on forced tiles (the eight-wave tile with and without its third
+    B slot among them), with M, N and K tails: the fp32 output against the fp64 product."""
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(71)
+    M, N, K = 300, 328, 1040  # 2080 bytes of K: 16 whole 128-byte steps and a partial one
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    one = torch.tensor([1.0], device=gpu)
+    y = ops.gemm_bf16(a.to(gpu), b.to(gpu), one, one, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = a.double() @ b.double().t()
+    err = (y.cpu().double() - ref).abs().max().item() / _rms(ref)
+    print(f"[gemm_bf16 {tile}] max|err|/RMS = {err:.3e}", flush=True)
+    assert err <= 0.01
+
+
 def test_gemm_nvfp4_on_own_operands(gpu):
     x = _inputs(256, 512, 3)
     w = (torch.randn(384, 512, generator=torch.Generator().manual_seed(4)) * 0.02).to(torch.bfloat16)
