@@ -68,7 +68,7 @@ def test_ragged_shapes(gpu, shape):
 
 @pytest.mark.parametrize("shape", [(8256, 4160), (8261, 4160)])
 def test_transpose_grid_wraps_with_odd_tile_counts(gpu, shape):
-    # more 64 x 64 tiles than one pass of the transposing grid (8,192 waves), an odd number
+    # more 64 x 64 tiles than one pass of the transposing grid (4,096 waves), an odd number
     # of tile columns, and an odd tile-row count (8256 rows: 129 tile rows; 8261: a ragged
     # last tile row and out_t rows that are not 16-byte aligned): the tile-row-pair walk
     # must still cover every tile once
