@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_kernel(const uint16_t* __restri
 // Identical bytes to geglu_bwd_kernel followed by the delayed cast of its output.
 constexpr int kTT = 64;
 constexpr int kFusedWaves = kNT / 64;
-constexpr int64_t kMaxFusedBlocks = 1024;
+constexpr int64_t kMaxFusedBlocks = 512;
 
 int64_t fused_blocks(int64_t M, int64_t I) {
   const int64_t tiles = ((M + kTT - 1) / kTT) * (I / kTT);

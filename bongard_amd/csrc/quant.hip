@@ -9,7 +9,7 @@
 // Current scaling needs the whole tensor's amax before the first byte is cast, so a
 // quantization is two streaming passes: amax_partials_kernel writes one max per block
 // (at most kMaxAmaxBlocks, plain stores, no atomics), and the cast kernel reduces those
-// partials in every block (a <= 8 KB read, overlapped with the block's first data
+// partials in every block (a <= 4 KB read, overlapped with the block's first data
 // loads) to the scale before it streams the data; its block 0 publishes the meta record.
 // The same cast kernel consumes the per-tile partials of H written by the gate/up GEMM
 // epilogue and those of dGU written by the gated-GELU backward. Streaming loads and
@@ -52,8 +52,8 @@ namespace {
 
 constexpr int kNT = 256;            // threads per block for streaming kernels
 constexpr int kVecPerThread = 8;    // 16-byte loads in flight per lane (amax)
-constexpr int64_t kMaxAmaxBlocks = 2048;  // 8 blocks per CU; consumers read <= 8 KB of partials
-constexpr int64_t kMaxCastBlocks = 4096;  // 16 blocks per CU (2048 when partials are written)
+constexpr int64_t kMaxAmaxBlocks = 1024;  // 4 blocks per CU; consumers read <= 4 KB of partials
+constexpr int64_t kMaxCastBlocks = 2048;  // 8 blocks per CU
 // Consumers reduce up to this many partials in every block; a longer list (the gated-GELU
 // GEMM writes one per tile: 5200 at M = 16.6k) is first reduced by a one-block kernel.
 constexpr int64_t kMaxInlinePartials = 2048;
@@ -569,7 +569,7 @@ __global__ __launch_bounds__(kNT) void cast_delayed_many_kernel(DelayedManyArgs 
 
 // ---- library-owned scratch of bf8_quantize_bf16_noalloc ------------------------------
 // The amax partials of the allocation-free quantization live in a file-scope device array
-// (each GPU the library runs on holds its own copy, 8 KB, until the process ends). Host code
+// (each GPU the library runs on holds its own copy, 4 KB, until the process ends). Host code
 // must not pass `scratch` itself to a kernel (in host code the name is a stand-in, not a
 // device address): the device address is looked up once per device with
 // hipGetSymbolAddress, with that device current, and kept in `g_scratch_ptr`.

@@ -98,8 +98,8 @@ int bf8_quantize_bf16(const void* x, int64_t rows, int64_t cols, int fmt, uint8_
 /* bf8_quantize_bf16 without the partials argument: allocates nothing and takes no
  * workspace. No counterpart in the reference; it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). The amax partials live in a library-owned device array of 2048 uint32 slots
- * (8 KB per GPU, held until the process ends; any tensor needs at most 2048, larger needs
+ * hipMalloc). The amax partials live in a library-owned device array of 1024 uint32 slots
+ * (4 KB per GPU, held until the process ends; any tensor needs at most 1024, larger needs
  * are refused with BF8_EINVAL). The array is shared by every call on a GPU and keeps the
  * last call's contents, so calls that overlap on one GPU (different streams, or host
  * threads) race; serialize them. Results equal bf8_quantize_bf16's bit for bit. */
