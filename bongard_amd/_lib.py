@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -37,6 +37,10 @@ SIGNATURES = {
     "bf8_gemm": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_int, c_int64, c_int64, c_int64,
                          c_int64, c_void_p, c_void_p, c_int, POINTER(c_int64), c_int, c_void_p,
                          c_void_p, c_int, c_int64, c_void_p, c_size_t, c_void_p]),
+    "bf8_gemm_kmajor_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
+    "bf8_gemm_kmajor": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_int, c_int64, c_int64,
+                                c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int, c_int64,
+                                c_void_p, c_size_t, c_void_p]),
     "bf8_geglu_partials": (c_int64, [c_int64, c_int64]),
     "bf8_gemm_geglu": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                c_void_p, c_void_p, c_int, c_void_p, c_int64, c_void_p, c_void_p,

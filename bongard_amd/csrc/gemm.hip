@@ -216,11 +216,13 @@ bool env_override(int& tile, int& splits) {
 
 // Chooses the tile and K split for C[M, N] = A[M, K] . B[N, K]^T. GEGLU plans never split
 // and depend on (M, N) only, so the per-tile amax partial count is known without K.
-Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, bool mx = false) {
+Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, bool mx = false,
+                 bool kmajor = false) {
   const int64_t ksteps = std::max<int64_t>(cdiv(K, kStepBytes), 1);
   int otile, osplits;
   if (env_override(otile, osplits) && (!geglu || geglu_tile_ok(otile, N, mx)) &&
-      (!mx || kTiles[otile].mx)) {
+      (!mx || kTiles[otile].mx) &&
+      (!kmajor || otile == TILE_256x256w8 || otile == TILE_256x256w8x)) {
     Plan p;
     if (!geglu && osplits == kTailSplitOverride) {
       if (make_tail_plan(otile, M, N, ksteps, p) && p.ws_bytes <= ws_avail) return p;
@@ -235,6 +237,8 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
   bool have = false;
   for (int tile = 0; tile < NUM_TILES; ++tile) {
     if ((geglu && !geglu_tile_ok(tile, N, mx)) || (mx && !kTiles[tile].mx)) continue;
+    // K-major operands: the eight-wave 256x256 tiles only
+    if (kmajor && tile != TILE_256x256w8) continue;
     // the eight-wave 256x256 tile replaces the four-wave one wherever it has a variant
     // (measured faster on every large shape, same bits); MX keeps the four-wave tile
     if (!mx && tile == TILE_256x256) continue;
@@ -559,6 +563,50 @@ int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt
 
 size_t bf8_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K) {
   return bf8_gemm_workspace(M, N, 2 * K);  // plans are made on K bytes
+}
+
+size_t bf8_gemm_kmajor_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return choose_plan(M, N, K, false, (size_t)-1, false, true).ws_bytes;
+}
+
+int bf8_gemm_kmajor(const uint8_t* A, int fmt_a, int64_t lda, int a_kmajor, const uint8_t* B,
+                    int fmt_b, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                    const float* a_scale_inv, const float* b_scale_inv, void* C, int out_dtype,
+                    int64_t ldc, void* ws, size_t ws_bytes, void* stream) {
+  const char* who = "bf8_gemm_kmajor";
+  BF8_CHECK(fmt_a == BF8_E5M2 && fmt_b == BF8_E4M3,
+            "%s: formats %d x %d (supported: e5m2 x e4m3)", who, fmt_a, fmt_b);
+  BF8_CHECK(a_kmajor == 0 || a_kmajor == 1, "%s: a_kmajor must be 0 or 1", who);
+  BF8_CHECK(out_dtype == BF8_OUT_BF16 || out_dtype == BF8_OUT_F32, "%s: bad out_dtype", who);
+  BF8_CHECK(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", who);
+  if (a_kmajor)
+    BF8_CHECK(M % 16 == 0 && lda % 16 == 0 && lda >= M && K * lda < (1LL << 31),
+              "%s: A^T [K, M] needs M and lda multiples of 16, lda >= M, < 2 GiB", who);
+  else
+    BF8_CHECK(K % 16 == 0 && lda % 16 == 0 && lda >= K && M * lda < (1LL << 31),
+              "%s: A [M, K] needs K and lda multiples of 16, lda >= K, < 2 GiB", who);
+  BF8_CHECK(N % 16 == 0 && ldb % 16 == 0 && ldb >= N && K * ldb < (1LL << 31),
+            "%s: B^T [K, N] needs N and ldb multiples of 16, ldb >= N, < 2 GiB", who);
+  BF8_CHECK(ldc >= N && ldc % 4 == 0, "%s: need ldc >= N, ldc %% 4 == 0", who);
+  BF8_CHECK(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && ((uintptr_t)C & 15) == 0,
+            "%s: A, B, C must be 16-byte aligned", who);
+  BF8_CHECK(a_scale_inv && b_scale_inv, "%s: scale pointers are NULL", who);
+  BF8_CHECK(ws_bytes == 0 || (ws && ((uintptr_t)ws & 255) == 0),
+            "%s: workspace must be 256-byte aligned", who);
+  if (M == 0 || N == 0) return BF8_OK;
+  BF8_CHECK(K > 0, "%s: K == 0 is not supported", who);
+  BF8_CHECK(A && B && C, "%s: A, B or C is NULL", who);
+  GemmParams p{};
+  p.A = A; p.B = B; p.lda = lda; p.ldb = ldb;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.I = 0;
+  p.a_sinv = a_scale_inv; p.b_sinv = b_scale_inv;
+  p.n_seg = 1;
+  for (int s = 0; s < 4; ++s) p.seg_end[s] = (int)N;
+  p.C = C; p.ldc = ldc;
+  p.kmajor = a_kmajor ? 3 : 2;
+  const Plan pl = choose_plan(M, N, K, false, ws ? ws_bytes : 0, false, true);
+  return launch_plan(pl, p, EPI_LINEAR, out_dtype, fmt_a, fmt_b, ws, as_stream(stream));
 }
 
 int bf8_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,

@@ -55,6 +55,9 @@ struct GemmParams {
   // ([BM][BN] each), which tail_reduce_kernel adds in piece order.
   int full_tiles, tail_pieces;
   float* tail_ws;
+  // Operand layout (linear epilogues of the eight-wave 256 x 256 tiles): 0 = A [M, K] and
+  // B [N, K]; 2 = B given as B^T [K, N] (row stride ldb >= N); 3 = A as A^T [K, M] as well.
+  int kmajor;
 };
 
 constexpr int kGroupM = 8;  // tile rows walked together (the tile order of a launch)

@@ -185,6 +185,37 @@ __device__ __forceinline__ v4u read_half(const uint8_t* tile, int row0, int kk, 
   return *reinterpret_cast<const v4u*>(tile + row * kBK + (swz(row, c) << 4));
 }
 
+// K-major operand tiles (the stored tensor is the operand's transpose, [K][rows]): a stage
+// holds 128 K rows of 256 row bytes, and the 16-byte chunk c of K row k sits at position
+// c ^ kmaj_swz(k). A lane's 16-byte DMA piece of K row k takes logical chunk
+// (its position) ^ kmaj_swz(k); the XOR keeps the transposing reads below on distinct banks
+// (each half-wave reads eight K rows of two adjacent chunks: even and odd positions).
+__device__ __forceinline__ int kmaj_swz(int k) { return 2 * (k & 7); }
+
+// The same 16 bytes as read_half (lane l: operand row row0 + (l & 31), K bytes kk*64 +
+// (l >> 5)*32 + 16*half .. +15) from a K-major tile, as two ds_read_b64_tr_b8: in each group
+// of 16 lanes, output lane j receives byte j mod 8 of the 8-byte pieces addressed by lanes
+// (j >> 3) + 2 i, i = 0..7, so lane p + 2 i of group g addresses K row k0 + i, row bytes
+// c0 + 8 p (c0 = row0 + 16 (g & 1)), and lane j gets K values k0 .. k0+7 of row c0 + j.
+__device__ __forceinline__ v4u read_half_kmajor(const uint8_t* tile, int row0, int kk, int half,
+                                                int lane) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  const int g = lane >> 4, a = lane & 15;
+  const int chunk = (row0 >> 4) + (g & 1);  // 16-byte chunk of the operand rows read
+  v4u r;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int k = kk * 64 + (g >> 1) * 32 + 16 * half + 8 * t + (a >> 1);
+    const uint8_t* src = tile + k * 256 + ((chunk ^ kmaj_swz(k)) << 4) + 8 * (a & 1);
+    const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (__attribute__((address_space(3))) v2i*)(
+            (__attribute__((address_space(3))) uint8_t*)(src)));
+    r[2 * t] = (uint32_t)v[0];
+    r[2 * t + 1] = (uint32_t)v[1];
+  }
+  return r;
+}
+
 __device__ __forceinline__ v8i join(v4u lo, v4u hi) {
   v8i r;
   r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
@@ -402,7 +433,9 @@ struct GegluRuns {
 template <class T>
 constexpr int tile_threads() { return T::NW * 64 * T::KG; }
 
-template <class T, int FA, int FB, int EPI, int OUT, bool MX = false>
+// KM: operands stored K-major (bit 0: A given as A^T [K, M], bit 1: B given as B^T [K, N]),
+// read through the transposing LDS loads; eight-wave 256 x 256 linear tiles only.
+template <class T, int FA, int FB, int EPI, int OUT, bool MX = false, int KM = 0>
 __global__ __attribute__((amdgpu_flat_work_group_size(tile_threads<T>(), tile_threads<T>()),
                           amdgpu_waves_per_eu(T::OCC * T::KG * T::NW / 4,
                                               T::OCC * T::KG * T::NW / 4))) void
@@ -427,6 +460,9 @@ gemm_kernel(GemmParams p) {
   static_assert(!(EPI == EPI_GEGLU && MX && FN % 2 != 0), "MX GEGLU: 32-column H blocks per tile");
   static_assert(!MX || (BM <= 256 && BN <= 256), "MX scale rows: one dword per lane");
   static_assert(!MX || NW == 4, "MX scale dwords: four waves of 64 rows");
+  static_assert(KM == 0 || (NW == 8 && BM == 256 && BN == 256 && EPI == EPI_LINEAR && !MX),
+                "K-major operands: eight-wave 256 x 256 linear tiles");
+  constexpr bool AKM = (KM & 1) != 0, BKM = (KM & 2) != 0;
   static_assert(XB == 0 || (NS == 2 && KG == 1 && !MX), "extra B slots: two stages, one K group");
   constexpr int kStageOff = extra_lds<EPI>();  // GEGLU: the gelu table, then the stages
   constexpr int kB = BN * kBK;  // B tile bytes per stage
@@ -469,8 +505,9 @@ gemm_kernel(GemmParams p) {
   // runs a zero-filled last one), so their barriers pair up.
   const int niters = (nsteps + KG - 1) / KG;
 
-  const i32x4 ra = make_srd(p.A, (uint32_t)((int64_t)p.M * p.lda));
-  const i32x4 rb = make_srd(p.B, (uint32_t)((int64_t)p.N * p.ldb));
+  // K-major operands span K rows: rows past K read as zero through the buffer's size
+  const i32x4 ra = make_srd(p.A, (uint32_t)((int64_t)(AKM ? p.K : p.M) * p.lda));
+  const i32x4 rb = make_srd(p.B, (uint32_t)((int64_t)(BKM ? p.K : p.N) * p.ldb));
 
   static_assert(ND * (NS - 1) < 64, "vmcnt holds at most 63 outstanding loads");
   // DMA: lane l of the wave's j-th 1 KB block (block j*NW + wid of the tile) covers tile
@@ -479,10 +516,20 @@ gemm_kernel(GemmParams p) {
   const int lrow = lane >> 3;
   const int lchunk = (lane & 7) ^ (((wid & 1) << 2) | (lrow >> 1));
   uint32_t a_off[DA], b_off[DB];
+  // K-major: lane l of 1 KB block blk covers K row blk*4 + l/16 (of the step) and 16-byte
+  // position l%16 of that row's 256 bytes, holding logical chunk (l%16) ^ kmaj_swz(row)
+  const int kmrow = lane >> 4;
+  auto kmaj_chunk = [&](int j) { return (lane & 15) ^ kmaj_swz((j * NW + wid) * 4 + kmrow); };
 #pragma unroll
   for (int j = 0; j < DA; ++j) {
-    const int am = m0 + (j * NW + wid) * 8 + lrow;
-    a_off[j] = am < p.M ? (uint32_t)((int64_t)am * p.lda + lchunk * 16) : kOob;
+    if constexpr (AKM) {
+      const int am = m0 + kmaj_chunk(j) * 16;  // M % 16 == 0: whole chunks in or out
+      a_off[j] = am < p.M ? (uint32_t)((int64_t)((j * NW + wid) * 4 + kmrow) * p.lda + am)
+                          : kOob;
+    } else {
+      const int am = m0 + (j * NW + wid) * 8 + lrow;
+      a_off[j] = am < p.M ? (uint32_t)((int64_t)am * p.lda + lchunk * 16) : kOob;
+    }
   }
 #pragma unroll
   for (int j = 0; j < DB; ++j) {
@@ -498,6 +545,11 @@ gemm_kernel(GemmParams p) {
       bvalid = bn < p.N;
     }
     b_off[j] = bvalid ? (uint32_t)((int64_t)bn * p.ldb + lchunk * 16) : kOob;
+    if constexpr (BKM) {
+      const int bc = n0 + kmaj_chunk(j) * 16;  // N % 16 == 0: whole chunks in or out
+      b_off[j] = bc < p.N ? (uint32_t)((int64_t)((j * NW + wid) * 4 + kmrow) * p.ldb + bc)
+                          : kOob;
+    }
   }
   // MX: lane l of wave w loads the scale dword of tile row w * 64 + l (A and B), from
   // the [rows, ld] E8M0 arrays; rows outside the tile or the tensor read as zero.
@@ -526,15 +578,25 @@ gemm_kernel(GemmParams p) {
   const bool lane_ktail_dead = (p.K % kBK) != 0 && (ksteps - 1) * kBK + lchunk * 16 >= p.K;
 
   // Load x of a stage (x < DA: A block x, DA <= x < DA + DB: B block x - DA, then (MX)
-  // the A and B scale dwords). `kill` zero-fills data, `kill_sc` the scales (a partial
-  // last K step keeps the scales of its blocks within K).
+  // the A and B scale dwords). `kill` zero-fills this lane's data (a stage past the split,
+  // or the lane's chunk beyond K in the tensor's partial last step), `kill_sc` a stage past
+  // the split (the scales, and K-major operands, whose rows past K read as zero anyway).
   auto dma_load = [&](int x, uint8_t* stage, uint32_t k0, bool kill, bool kill_sc,
                       uint8_t* bdst) {
     const uint32_t base = lds_addr(stage);
-    if (x < DA)
-      dma16(ra, base + (x * NW + wid) * 1024, kill ? kOob : a_off[x], k0);
-    else if (x < DA + DB)
-      dma16(rb, lds_addr(bdst) + ((x - DA) * NW + wid) * 1024, kill ? kOob : b_off[x - DA], k0);
+    if (x < DA) {
+      if constexpr (AKM)
+        dma16(ra, base + (x * NW + wid) * 1024, kill_sc ? kOob : a_off[x], k0 * (uint32_t)p.lda);
+      else
+        dma16(ra, base + (x * NW + wid) * 1024, kill ? kOob : a_off[x], k0);
+    } else if (x < DA + DB) {
+      if constexpr (BKM)
+        dma16(rb, lds_addr(bdst) + ((x - DA) * NW + wid) * 1024,
+              kill_sc ? kOob : b_off[x - DA], k0 * (uint32_t)p.ldb);
+      else
+        dma16(rb, lds_addr(bdst) + ((x - DA) * NW + wid) * 1024, kill ? kOob : b_off[x - DA],
+              k0);
+    }
     else if (x == DA + DB)
       dma4(srd_sa, base + kData + wid * 256, kill_sc ? kOob : sa_off, k0 >> 5);
     else
@@ -572,12 +634,15 @@ gemm_kernel(GemmParams p) {
   }
   auto read_one = [&](Frags<NH>& f, const uint8_t* stage, const uint8_t* btile, int kk, int h) {
     const int fr = h >> 1;  // 0: b0, 1..FM: a0.., FM+1..: b1..
-    if (fr == 0)
-      f.h[h] = read_half(btile, brow[0], kk, h & 1, lane, MX);
-    else if (fr <= FM)
-      f.h[h] = read_half(stage, wave_m0 + (fr - 1) * 32, kk, h & 1, lane, MX);
-    else
-      f.h[h] = read_half(btile, brow[fr - FM], kk, h & 1, lane, MX);
+    if (fr == 0 || fr > FM) {
+      const int r0 = brow[fr == 0 ? 0 : fr - FM];
+      f.h[h] = BKM ? read_half_kmajor(btile, r0, kk, h & 1, lane)
+                   : read_half(btile, r0, kk, h & 1, lane, MX);
+    } else {
+      const int r0 = wave_m0 + (fr - 1) * 32;
+      f.h[h] = AKM ? read_half_kmajor(stage, r0, kk, h & 1, lane)
+                   : read_half(stage, r0, kk, h & 1, lane, MX);
+    }
   };
 
   v16f acc[FN][FM];
@@ -650,7 +715,8 @@ gemm_kernel(GemmParams p) {
   for (int ls = NS; ls < NSB; ++ls) {
 #pragma unroll
     for (int x = DA; x < DA + DB; ++x)
-      dma_load(x, stage_ptr(ls), (uint32_t)gstep(ls) * kBK, stage_kill(ls), true, b_ptr(ls));
+      dma_load(x, stage_ptr(ls), (uint32_t)gstep(ls) * kBK, stage_kill(ls), kstep(ls) >= nsteps,
+               b_ptr(ls));
   }
   // stage 0 landed: the NS-1 later stages (ND loads each) and the XB B tiles may still be
   // in flight
@@ -697,6 +763,7 @@ gemm_kernel(GemmParams p) {
     const bool killn_sc = kstep(ls + NS) >= nsteps;
     const uint32_t knb = (uint32_t)gstep(ls + NSB) * kBK;  // = kn without XB
     const bool killnb = stage_kill(ls + NSB);
+    const bool killnb_end = kstep(ls + NSB) >= nsteps;
     read_scales(nxt, scA_n, scB_n);
 #pragma unroll
     for (int x = 0; x < NM; ++x) {
@@ -709,7 +776,7 @@ gemm_kernel(GemmParams p) {
           if (XB == 0 || d < DA)
             dma_load(d, cur, kn, killn, killn_sc, curb);
           else
-            dma_load(d, cur, knb, killnb, true, curb);
+            dma_load(d, cur, knb, killnb, killnb_end, curb);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1053,6 +1120,22 @@ inline unsigned grid_blocks(const GemmParams& p) {
 template <class T, int EPI, int OUT>
 int launch_typed(const GemmParams& p, int fa, int fb, hipStream_t s) {
   const dim3 grid(grid_blocks(p)), block(tile_threads<T>());
+  if (p.kmajor) {
+    // K-major operands (the training backward's dgrad and wgrad GEMMs: e5m2 gradients
+    // against e4m3 weights or activations) on the eight-wave 256 x 256 tiles
+    if constexpr (EPI == EPI_LINEAR && T::NW == 8 && T::BM == 256 && T::BN == 256) {
+      if (fa == BF8_E5M2 && fb == BF8_E4M3 && (p.kmajor == 2 || p.kmajor == 3)) {
+        if (p.kmajor == 2)
+          hipLaunchKernelGGL((gemm_kernel<T, 1, 0, EPI, OUT, false, 2>), grid, block, 0, s, p);
+        else
+          hipLaunchKernelGGL((gemm_kernel<T, 1, 0, EPI, OUT, false, 3>), grid, block, 0, s, p);
+        return launch_status("gemm_kernel(k-major)");
+      }
+    }
+    set_error("gemm: K-major operands (layout %d) need e5m2 x e4m3 on an eight-wave 256x256 "
+              "tile (got %d x %d, %dx%d)", p.kmajor, fa, fb, T::BM, T::BN);
+    return BF8_EINVAL;
+  }
   if (fa == kFmtBf16 || fb == kFmtBf16) {
     if constexpr (EPI == EPI_LINEAR) {
       if (fa == kFmtBf16 && fb == kFmtBf16) {

@@ -157,11 +157,14 @@ def _mlp_fake(x, w_gu, w_down, intermediate, split_scales, need_dx, need_dgu, ne
     def t(shape, dtype, keep=True):
         return x.new_empty(shape if keep else (0,), dtype=dtype)
 
+    # the saved fp8 tensors: the forward's own (K-major backward) or transposed copies
+    km = _linear.mlp_kmajor(K, I, N)
     return (t((M, N), torch.bfloat16), t((M, 2 * I), torch.bfloat16, train),
-            t((K, M), _F8, need_dgu), t((4,), torch.float32), t((I, M), _F8, need_dd),
-            t((4,), torch.float32), t((K, 2 * I), _F8, need_dx),
+            t((M, K) if km else (K, M), _F8, need_dgu), t((4,), torch.float32),
+            t((M, I) if km else (I, M), _F8, need_dd), t((4,), torch.float32),
+            t((2 * I, K) if km else (K, 2 * I), _F8, need_dx),
             t((2 if split_scales else 1, 4), torch.float32),
-            t((I, N), _F8, need_dx or need_dgu), t((4,), torch.float32))
+            t((N, I) if km else (I, N), _F8, need_dx or need_dgu), t((4,), torch.float32))
 
 
 @torch.library.custom_op("bongard_fp8::geglu_mlp_backward", mutates_args=())
@@ -172,7 +175,8 @@ def _mlp_bwd_op(dy: Tensor, GU: Tensor, x8t: Tensor, xm: Tensor, h8t: Tensor, hm
     saved = (GU, _none_if_empty(x8t), xm, _none_if_empty(h8t), hm, _none_if_empty(gu8t), gum,
              _none_if_empty(d8t), dm)
     dx, dgu, dd = _linear.mlp_backward(dy, saved, intermediate, split_scales, None,
-                                       (need_dx, need_dgu, need_dd))
+                                       (need_dx, need_dgu, need_dd),
+                                       _linear.mlp_kmajor(in_features, intermediate, dy.shape[1]))
     return (_or_empty(dx, dy, torch.bfloat16), _or_empty(dgu, dy, torch.bfloat16),
             _or_empty(dd, dy, torch.bfloat16))
 

@@ -381,21 +381,34 @@ class Fp8GegluMlpMxFunction(_Fp8Function):
         return dx, dgu, dd, None, None, None
 
 
+def mlp_kmajor(hidden, intermediate, out_features):
+    """Whether the MLP's backward reads the forward's fp8 tensors as they are (its dgrad and
+    wgrad GEMMs take K-major operands, bf8_gemm_kmajor), so no transposed fp8 copy is made
+    anywhere: every operand row a multiple of 16 bytes."""
+    return hidden % 16 == 0 and int(intermediate) % 16 == 0 and out_features % 16 == 0
+
+
 def mlp_forward(x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scaling, x_amax,
                 needs):
     """Forward of the FP8 gated MLP (see Fp8GegluMlpFunction): ``(y, saved)`` with saved =
-    (GU, x8t, x_meta, h8t, h_meta, gu8t, gu_meta, d8t, d_meta), the tensors the backward
-    reads (None where no gradient needs them). ``needs``: (dx, dW_gu, dW_down) wanted."""
+    (GU, x8, x_meta, h8, h_meta, gu8, gu_meta, d8, d_meta), the tensors the backward reads
+    (None where no gradient needs them): with :func:`mlp_kmajor` the fp8 tensors the forward
+    computed with (X8, H8, W_gu8, W_down8), otherwise their transposed copies.
+    ``needs``: (dx, dW_gu, dW_down) wanted."""
     I = int(intermediate)
     need_dx, need_dgu, need_dd = needs
     train = need_dx or need_dgu or need_dd
     if scaling is not None and split_scales:
         raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
     gs, ds = scaling if scaling is not None else (None, None)
-    if (scaling is None and x_amax is None and not train and not split_scales
+    km = mlp_kmajor(x.shape[-1], I, w_down.shape[0])
+    # transposed copies wanted (the backward's operands when it cannot read K-major ones)
+    t_dx, t_dgu, t_dd = ((False, False, False) if km else (need_dx, need_dgu, need_dd))
+    if (scaling is None and x_amax is None and not (t_dx or t_dgu or t_dd) and not split_scales
             and (gu_q is None or down_q is None)):
-        # current-scaling inference: x and the uncached weights in one amax + one cast
-        # launch (the rowwise copies are all the forward needs)
+        # current scaling without transposed copies: x and the uncached weights in one amax
+        # + one cast launch (the rowwise copies are all the forward and a K-major backward
+        # need)
         ws = [w for w, q in ((w_gu, gu_q), (w_down, down_q)) if q is None]
         qs = ops.quantize_many([x] + [w.detach() for w in ws])
         xq = qs[0]
@@ -407,24 +420,24 @@ def mlp_forward(x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scali
         # delayed scaling with every operand quantized here: x, [W_gate; W_up] and W_down
         # with the transposed copies the backward reads, in one launch
         xq, wq, down_q = _scaling.quantize_many([
-            (gs.input, x, True, need_dgu),
-            (gs.weight, w_gu.detach(), True, need_dx),
-            (ds.weight, w_down.detach(), True, need_dx or need_dgu)])
+            (gs.input, x, True, t_dgu),
+            (gs.weight, w_gu.detach(), True, t_dx),
+            (ds.weight, w_down.detach(), True, t_dx or t_dgu)])
         gu_q = _GateUp(wq.data, wq.data_t, wq.meta.view(1, 4))
     else:
-        xq = _quantize_input(x, gs and gs.input, x_amax, need_dgu)
+        xq = _quantize_input(x, gs and gs.input, x_amax, t_dgu)
     if gu_q is None:
-        gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=need_dx,
+        gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=t_dx,
                                 scaler=gs and gs.weight)
     stride = 4 if split_scales else 0
     M = xq.rows
     if ds is None:
         H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
                                        w_meta_stride=stride, keep_gu=train)
-        hq = ops.cast_partials(H, hparts, E4M3, rowwise=True, transpose=need_dd)
+        hq = ops.cast_partials(H, hparts, E4M3, rowwise=True, transpose=t_dd)
     else:
         count = ops.geglu_partials_count(M, I)
-        transpose = need_dd
+        transpose = t_dd
         if M % 32 == 0 or not transpose:
             # H's scale is known before the GEMM: the epilogue casts H (and its
             # transpose for the down wgrad) itself; no bf16 H round trip
@@ -447,27 +460,43 @@ def mlp_forward(x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scali
     h_meta = hq.meta
     if down_q is None:
         down_q = quantize_weight(
-            w_down, transpose=need_dx or need_dgu,
+            w_down, transpose=t_dx or t_dgu,
             scaler=ds and ds.weight)
     y = ops.gemm(hq.data, E4M3, h_meta, down_q.data, E4M3, down_q.meta)
+    if km:
+        return y, (GU, xq.data if need_dgu else None, xq.meta, hq.data if need_dd else None,
+                   h_meta, gu_q.data if need_dx else None, gu_q.meta,
+                   down_q.data if need_dx or need_dgu else None, down_q.meta)
     return y, (GU, xq.data_t, xq.meta, hq.data_t, h_meta, gu_q.data_t, gu_q.meta, down_q.data_t,
                down_q.meta)
 
 
-def mlp_backward(dy, saved, intermediate, split_scales, scaling, needs):
-    """Backward of the FP8 gated MLP: ``(dx, dW_gu, dW_down)`` (None where not wanted)."""
+def mlp_backward(dy, saved, intermediate, split_scales, scaling, needs, kmajor=False):
+    """Backward of the FP8 gated MLP: ``(dx, dW_gu, dW_down)`` (None where not wanted).
+    ``kmajor``: the saved fp8 tensors are the forward's own (X8, H8, W_gu8, W_down8; see
+    :func:`mlp_kmajor`), read as K-major GEMM operands, and no transposed copy of dY or
+    dGU is made; otherwise they are the transposed copies."""
     (GU, x8t, x_meta, h8t, h_meta, gu8t, gu_meta, d8t, d_meta) = saved
     I = int(intermediate)
     need_dx, need_dgu, need_dd = needs
     gs, ds = scaling if scaling is not None else (None, None)
     dy = dy.contiguous()
-    dyq = _quantize(dy, E5M2, ds and ds.grad_output, rowwise=True, transpose=need_dd)
+    km = bool(kmajor)
+
+    def gemm_b(a, a_meta, b, b_meta, *, a_kmajor=False):
+        # dgrad / wgrad: e5m2 gradient A against the saved e4m3 B (B^T [K, N] when K-major)
+        if km:
+            return ops.gemm_kmajor(a, E5M2, a_meta, b, E4M3, b_meta, a_kmajor=a_kmajor)
+        return ops.gemm(a, E5M2, a_meta, b, E4M3, b_meta)
+
+    dyq = _quantize(dy, E5M2, ds and ds.grad_output, rowwise=True, transpose=need_dd and not km)
     dx = dgu = dd = None
     if need_dd:
-        dd = ops.gemm(dyq.data_t, E5M2, dyq.meta, h8t, E4M3, h_meta)
+        # dW_down = dY^T . H
+        dd = gemm_b(dyq.data if km else dyq.data_t, dyq.meta, h8t, h_meta, a_kmajor=True)
     if not (need_dx or need_dgu):
         return dx, dgu, dd
-    dH = ops.gemm(dyq.data, E5M2, dyq.meta, d8t, E4M3, d_meta)
+    dH = gemm_b(dyq.data, dyq.meta, d8t, d_meta)
     if gs is not None:
         # delayed scaling: dGU's scale is known already, so the gelu backward writes
         # fp8 dGU (and its transpose) in the same pass
@@ -476,34 +505,38 @@ def mlp_backward(dy, saved, intermediate, split_scales, scaling, needs):
         scaler = gs.grad_output
         dq = scaler.produce(count, dH.device, lambda st, L, pos, prev, parts:
                             ops.geglu_bwd_delayed(dH, GU, st, L, pos, prev, scaler.fmt,
-                                                  rowwise=need_dx, transpose=need_dgu,
+                                                  rowwise=need_dx or km,
+                                                  transpose=need_dgu and not km,
                                                   partials_out=parts))
         if need_dx:
-            dx = ops.gemm(dq.data, E5M2, dq.meta, gu8t, E4M3, gu_meta[0])
+            dx = gemm_b(dq.data, dq.meta, gu8t, gu_meta[0])
         if need_dgu:
-            dgu = ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta)
+            # dW_gu = dGU^T . X
+            dgu = gemm_b(dq.data if km else dq.data_t, dq.meta, x8t, x_meta, a_kmajor=True)
         return dx, dgu, dd
     dGU, gparts = ops.geglu_bwd(dH, GU)
     if not split_scales:
-        dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=need_dx, transpose=need_dgu)
+        dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=need_dx or km,
+                               transpose=need_dgu and not km)
         g_meta = dq.meta
         if need_dx:
-            dx = ops.gemm(dq.data, E5M2, g_meta, gu8t, E4M3, gu_meta[0])
+            dx = gemm_b(dq.data, g_meta, gu8t, gu_meta[0])
         if need_dgu:
-            dgu = ops.gemm(dq.data_t, E5M2, g_meta, x8t, E4M3, x_meta)
+            dgu = gemm_b(dq.data if km else dq.data_t, g_meta, x8t, x_meta, a_kmajor=True)
     else:
         # Separate gate/up projections: each gradient has its own e5m2 scale and its
         # own dgrad GEMM; the input gradient is their bf16 sum (autograd of x used twice).
         dx_parts, dw_parts = [], []
         for half in range(2):
             d_half = dGU[:, half * I:(half + 1) * I].contiguous()
-            dq = ops.quantize(d_half, E5M2, rowwise=need_dx, transpose=need_dgu)
+            dq = ops.quantize(d_half, E5M2, rowwise=need_dx or km, transpose=need_dgu and not km)
             if need_dx:
-                dx_parts.append(ops.gemm(dq.data, E5M2, dq.meta,
-                                         gu8t[:, half * I:(half + 1) * I], E4M3,
-                                         gu_meta[half]))
+                # the half's rows of W_gu8 (K-major) or columns of its transposed copy
+                w_half = gu8t[half * I:(half + 1) * I] if km else gu8t[:, half * I:(half + 1) * I]
+                dx_parts.append(gemm_b(dq.data, dq.meta, w_half, gu_meta[half]))
             if need_dgu:
-                dw_parts.append(ops.gemm(dq.data_t, E5M2, dq.meta, x8t, E4M3, x_meta))
+                dw_parts.append(gemm_b(dq.data if km else dq.data_t, dq.meta, x8t, x_meta,
+                                       a_kmajor=True))
         if need_dx:
             dx = dx_parts[0] + dx_parts[1]
         if need_dgu:
@@ -531,13 +564,14 @@ class Fp8GegluMlpFunction(_Fp8Function):
         ctx.intermediate = int(intermediate)
         ctx.split_scales = split_scales
         ctx.scaling = scaling
+        ctx.kmajor = mlp_kmajor(x.shape[-1], intermediate, w_down.shape[0])
         ctx.save_for_backward(*saved)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         dx, dgu, dd = mlp_backward(dy, ctx.saved_tensors, ctx.intermediate, ctx.split_scales,
-                                   ctx.scaling, tuple(ctx.needs_input_grad[:3]))
+                                   ctx.scaling, tuple(ctx.needs_input_grad[:3]), ctx.kmajor)
         return dx, dgu, dd, None, None, None, None, None, None
 
 

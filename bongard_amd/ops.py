@@ -361,6 +361,42 @@ def gemm(a, a_fmt, a_meta, b, b_fmt, b_meta, *, out_dtype=torch.bfloat16, bias=N
     return out
 
 
+@functools.lru_cache(maxsize=256)
+def _gemm_kmajor_ws_cached(M, N, K, override):
+    return int(_lib.lib().bf8_gemm_kmajor_workspace(M, N, K))
+
+
+def gemm_kmajor(a, a_fmt, a_meta, b_t, b_fmt, b_meta, *, a_kmajor=False,
+                out_dtype=torch.bfloat16, out=None):
+    """:func:`gemm` with B given as ``b_t`` = B^T [K, N] (and, when ``a_kmajor``, A as ``a``
+    = A^T [K, M]): the backward's dgrad and wgrad GEMMs on the fp8 tensors as their
+    producers wrote them, no transposed copies (bf8_gemm_kmajor; e5m2 x e4m3). Same
+    products and fp32 sums as :func:`gemm` on the transposed operands."""
+    _require_gpu(a, b_t, a_meta, b_meta)
+    _byte_matrix("gemm_kmajor", a=a, b_t=b_t)
+    if a_kmajor:
+        K, M = a.shape
+    else:
+        M, K = a.shape
+    Kb, N = b_t.shape
+    if K != Kb:
+        raise ValueError(f"gemm_kmajor: inner dims differ ({K} vs {Kb})")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("gemm_kmajor: out_dtype must be bfloat16 or float32")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    _out_matrix("gemm_kmajor", out, (M, N), out_dtype)
+    ws_bytes = _gemm_kmajor_ws_cached(M, N, K, _tile_override())
+    ws = gemm_workspace(ws_bytes, a.device) if ws_bytes else None
+    ws_bytes = ws.numel() if ws is not None else 0
+    _lib.check(_lib.lib().bf8_gemm_kmajor(
+        _ptr(a), a_fmt, a.stride(0), int(bool(a_kmajor)), _ptr(b_t), b_fmt, b_t.stride(0), M, N,
+        K, _sinv_ptr(a_meta), _sinv_ptr(b_meta), _ptr(out),
+        OUT_BF16 if out_dtype == torch.bfloat16 else OUT_F32, out.stride(0), _ptr(ws), ws_bytes,
+        _stream(a.device)), "bf8_gemm_kmajor")
+    return out
+
+
 @dataclass
 class AxisFp8Tensor:
     """An axiswise-scaled FP8 tensor (torchao AXISWISE granularity) of x [rows, cols]:

@@ -147,6 +147,21 @@ int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt
              int n_seg, const void* bias, void* C, int out_dtype, int64_t ldc, void* ws,
              size_t ws_bytes, void* stream);
 
+/* bf8_gemm for the training backward's dgrad and wgrad GEMMs on operands kept in the
+ * layout that produced them, so no transposed fp8 copy is needed: B is given as
+ * B^T [K, N] (row stride ldb >= N bytes, N % 16 == 0) and, when a_kmajor is 1, A as
+ * A^T [K, M] (lda >= M, M % 16 == 0), else A [M, K] as in bf8_gemm. e5m2 A x e4m3 B,
+ * one scale each, no bias; ws: bf8_gemm_kmajor_workspace(M, N, K) bytes. The products
+ * and their fp32 sums are those of bf8_gemm on the transposed copies, bit for bit (same K
+ * order). Replaces the dgrad (dX = dY . W) and wgrad (dW = dY^T . X) GEMMs of torchao's
+ * Float8Linear and TE's Linear backward (bongard/float8_training.py:22;
+ * bongard/te_linear.py:73-74), which transposes their operands' fp8 copies instead. */
+size_t bf8_gemm_kmajor_workspace(int64_t M, int64_t N, int64_t K);
+int bf8_gemm_kmajor(const uint8_t* A, int fmt_a, int64_t lda, int a_kmajor, const uint8_t* B,
+                    int fmt_b, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                    const float* a_scale_inv, const float* b_scale_inv, void* C, int out_dtype,
+                    int64_t ldc, void* ws, size_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Gate/up GEMM with the gated-GELU(tanh) epilogue.
  * Replaces TEMLP.forward's gate_up GEMM + F.gelu(gate, approximate='tanh') * up

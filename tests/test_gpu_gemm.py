@@ -515,3 +515,49 @@ def test_tail_split_auto_plan_c5_dgrad(gpu):
     """The automatic plan of c5's dX GEMM (M=8192, N=2560, K=20480, e5m2 x e4m3) is a tail
     split: 256 whole 256x256 tiles and 64 tail tiles in 4 pieces."""
     assert _tail_pieces(8192, 2560, 20480) == 4
+
+
+# ---- K-major operands (the backward's GEMMs without transposed fp8 copies) -------------
+@pytest.mark.parametrize("plan", ["256x256w8", "256x256w8x", "256x256w8:t", "auto"])
+@pytest.mark.parametrize("a_kmajor", [False, True])
+@pytest.mark.parametrize("M,N,K", [(304, 320, 1040), (512, 1024, 4096), (4352, 4096, 2048)])
+def test_gemm_kmajor_equals_transposed_copies(gpu, monkeypatch, plan, a_kmajor, M, N, K):
+    """gemm_kmajor on B^T [K, N] (and A^T [K, M]) as the quantizer writes them, read through
+    the transposing LDS loads, against gemm on the transposed copies under the same plan
+    (forced tile, unsplit or tail split): bf16 and fp32 outputs bit for bit; against the
+    oracle's fp64 product on the auto plan. Ragged M, N and a partial last K step."""
+    if plan != "auto":
+        monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", plan)
+    elif M * N * K > 2 ** 32:
+        pytest.skip("the oracle check runs on the smaller shapes")
+    g = torch.Generator().manual_seed(M + N + K)
+    a = (torch.randn(M, K, generator=g) * 1e-3).to(torch.bfloat16)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    # A^T and B^T as the tensors a backward holds: the quantized [K, M] / [K, N] arrays
+    at = a.t().contiguous().to(gpu)
+    bt = b.t().contiguous().to(gpu)
+    aq = ops.quantize(at, ops.E5M2, rowwise=True, transpose=True)   # data [K, M], data_t [M, K]
+    bq = ops.quantize(bt, ops.E4M3, rowwise=True, transpose=True)   # data [K, N], data_t [N, K]
+    a_op = aq.data if a_kmajor else aq.data_t
+    if plan == "auto":
+        got32 = ops.gemm_kmajor(a_op, ops.E5M2, aq.meta, bq.data, ops.E4M3, bq.meta,
+                                a_kmajor=a_kmajor, out_dtype=torch.float32)
+        got16 = ops.gemm_kmajor(a_op, ops.E5M2, aq.meta, bq.data, ops.E4M3, bq.meta,
+                                a_kmajor=a_kmajor)
+        torch.cuda.synchronize()
+        ra, _, sa, _ = orc.quantize(at.cpu(), ops.E5M2)
+        rb, _, sb, _ = orc.quantize(bt.cpu(), ops.E4M3)
+        ref = orc.scaled_mm(ra.t().contiguous(), sa, ops.E5M2, rb.t().contiguous(), sb, ops.E4M3)
+        _assert_fp32_close(got32, ref, what=f"kmajor a={a_kmajor} {M}x{N}x{K}")
+        assert torch.equal(got16.view(torch.int16), got32.to(torch.bfloat16).view(torch.int16))
+        return
+    for dt in (torch.bfloat16, torch.float32):
+        got = ops.gemm_kmajor(a_op, ops.E5M2, aq.meta, bq.data, ops.E4M3, bq.meta,
+                              a_kmajor=a_kmajor, out_dtype=dt)
+        want = ops.gemm(aq.data_t, ops.E5M2, aq.meta, bq.data_t, ops.E4M3, bq.meta,
+                        out_dtype=dt)
+        torch.cuda.synchronize()
+        same = torch.equal(got.view(torch.int16 if dt == torch.bfloat16 else torch.int32),
+                           want.view(torch.int16 if dt == torch.bfloat16 else torch.int32))
+        print(f"[kmajor {plan} a={a_kmajor} {M}x{N}x{K} {dt}] identical: {same}", flush=True)
+        assert same
