@@ -42,12 +42,12 @@ def _none_if_empty(t):
 def _linear_op(x: Tensor, weight: Tensor, bias: Optional[Tensor], recipe: str, need_dx: bool,
                need_dw: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     if recipe == "tensorwise":
-        y, (x8t, xs, w8t, ws) = _linear.linear_forward(x, weight, bias, None, None, need_dx,
-                                                       need_dw)
-        # without gradients x and W share one quantize launch, whose two metas are rows of
-        # one [2, 4] tensor; a custom op's outputs may not alias each other, so each meta
-        # leaves as its own 4-float copy
-        return (y, _or_empty(x8t, x, _F8), xs.clone(), _or_empty(w8t, x, _F8), ws.clone())
+        y, (x8, xs, w8, ws) = _linear.linear_forward(x, weight, bias, None, None, need_dx,
+                                                     need_dw)
+        # x and W share one quantize launch, whose two metas are rows of one [2, 4] tensor;
+        # a custom op's outputs may not alias each other, so each meta leaves as its own
+        # 4-float copy
+        return (y, _or_empty(x8, x, _F8), xs.clone(), _or_empty(w8, x, _F8), ws.clone())
     y, saved = _linear.linear_axiswise_forward(x, weight, bias, recipe, need_dx, need_dw)
     if recipe == "rowwise_with_gw_hp":   # the backward reads the op's inputs themselves
         e8, e32 = x.new_empty(0, dtype=_F8), x.new_empty(0, dtype=torch.float32)
@@ -70,7 +70,8 @@ def _linear_fake(x, weight, bias, recipe, need_dx, need_dw):
         return x.new_empty(shape if keep else (0,), dtype=torch.float32)
 
     if recipe == "tensorwise":
-        return y, f8((K, M), need_dw), f32((4,), True), f8((K, N), need_dx), f32((4,), True)
+        # the saved fp8 X and W are the forward's own (K-major backward)
+        return y, f8((M, K), need_dw), f32((4,), True), f8((N, K), need_dx), f32((4,), True)
     if recipe == "rowwise":
         return (y, f8((K, M), need_dw), f32((K,), need_dw), f8((K, N), need_dx),
                 f32((K,), need_dx))
@@ -141,10 +142,10 @@ def _mlp_op(x: Tensor, w_gu: Tensor, w_down: Tensor, intermediate: int, split_sc
                                                                    Tensor]:
     y, saved = _linear.mlp_forward(x, w_gu, w_down, None, None, intermediate, split_scales,
                                    None, None, (need_dx, need_dgu, need_dd))
-    GU, x8t, xm, h8t, hm, gu8t, gum, d8t, dm = saved
-    return (y, _or_empty(GU, x, torch.bfloat16), _or_empty(x8t, x, _F8), xm.clone(),
-            _or_empty(h8t, x, _F8), hm.clone(), _or_empty(gu8t, x, _F8), gum.clone(),
-            _or_empty(d8t, x, _F8), dm.clone())
+    GU, x8, xm, h8, hm, gu8, gum, d8, dm = saved
+    return (y, _or_empty(GU, x, torch.bfloat16), _or_empty(x8, x, _F8), xm.clone(),
+            _or_empty(h8, x, _F8), hm.clone(), _or_empty(gu8, x, _F8), gum.clone(),
+            _or_empty(d8, x, _F8), dm.clone())
 
 
 @_mlp_op.register_fake
@@ -157,32 +158,29 @@ def _mlp_fake(x, w_gu, w_down, intermediate, split_scales, need_dx, need_dgu, ne
     def t(shape, dtype, keep=True):
         return x.new_empty(shape if keep else (0,), dtype=dtype)
 
-    # the saved fp8 tensors: the forward's own (K-major backward) or transposed copies
-    km = _linear.mlp_kmajor(K, I, N)
+    # the saved fp8 tensors are the forward's own X8, H8, W_gu8, W_down8 (K-major backward)
     return (t((M, N), torch.bfloat16), t((M, 2 * I), torch.bfloat16, train),
-            t((M, K) if km else (K, M), _F8, need_dgu), t((4,), torch.float32),
-            t((M, I) if km else (I, M), _F8, need_dd), t((4,), torch.float32),
-            t((2 * I, K) if km else (K, 2 * I), _F8, need_dx),
+            t((M, K), _F8, need_dgu), t((4,), torch.float32), t((M, I), _F8, need_dd),
+            t((4,), torch.float32), t((2 * I, K), _F8, need_dx),
             t((2 if split_scales else 1, 4), torch.float32),
-            t((N, I) if km else (I, N), _F8, need_dx or need_dgu), t((4,), torch.float32))
+            t((N, I), _F8, need_dx or need_dgu), t((4,), torch.float32))
 
 
 @torch.library.custom_op("bongard_fp8::geglu_mlp_backward", mutates_args=())
-def _mlp_bwd_op(dy: Tensor, GU: Tensor, x8t: Tensor, xm: Tensor, h8t: Tensor, hm: Tensor,
-                gu8t: Tensor, gum: Tensor, d8t: Tensor, dm: Tensor, intermediate: int,
+def _mlp_bwd_op(dy: Tensor, GU: Tensor, x8: Tensor, xm: Tensor, h8: Tensor, hm: Tensor,
+                gu8: Tensor, gum: Tensor, d8: Tensor, dm: Tensor, intermediate: int,
                 split_scales: bool, in_features: int, need_dx: bool, need_dgu: bool,
                 need_dd: bool) -> tuple[Tensor, Tensor, Tensor]:
-    saved = (GU, _none_if_empty(x8t), xm, _none_if_empty(h8t), hm, _none_if_empty(gu8t), gum,
-             _none_if_empty(d8t), dm)
+    saved = (GU, _none_if_empty(x8), xm, _none_if_empty(h8), hm, _none_if_empty(gu8), gum,
+             _none_if_empty(d8), dm)
     dx, dgu, dd = _linear.mlp_backward(dy, saved, intermediate, split_scales, None,
-                                       (need_dx, need_dgu, need_dd),
-                                       _linear.mlp_kmajor(in_features, intermediate, dy.shape[1]))
+                                       (need_dx, need_dgu, need_dd))
     return (_or_empty(dx, dy, torch.bfloat16), _or_empty(dgu, dy, torch.bfloat16),
             _or_empty(dd, dy, torch.bfloat16))
 
 
 @_mlp_bwd_op.register_fake
-def _mlp_bwd_fake(dy, GU, x8t, xm, h8t, hm, gu8t, gum, d8t, dm, intermediate, split_scales,
+def _mlp_bwd_fake(dy, GU, x8, xm, h8, hm, gu8, gum, d8, dm, intermediate, split_scales,
                   in_features, need_dx, need_dgu, need_dd):
     M, N = dy.shape
     I = int(intermediate)

@@ -140,17 +140,16 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
                 self._fp8_weights = (_linear.quantize_weight_mx(self.fc1_weight),
                                      _linear.quantize_weight_mx(self.fc2_weight))
             elif fc1 is not None:
-                # delayed scaling: both weights with their transposed copies in one launch
+                # delayed scaling: both weights in one launch
                 wq, dq = _scaling.quantize_many([
-                    (fc1.weight, self.fc1_weight.detach(), True, True),
-                    (fc2.weight, self.fc2_weight.detach(), True, True)])
-                self._fp8_weights = (_linear._GateUp(wq.data, wq.data_t, wq.meta.view(1, 4)),
-                                     dq)
+                    (fc1.weight, self.fc1_weight.detach(), True, False),
+                    (fc2.weight, self.fc2_weight.detach(), True, False)])
+                self._fp8_weights = (_linear._GateUp(wq.data, None, wq.meta.view(1, 4)), dq)
             else:
                 self._fp8_weights = (
                     _linear.quantize_gate_up(self.fc1_weight, self.intermediate_size,
                                              split_scales=False),
-                    _linear.quantize_weight(self.fc2_weight, transpose=True))
+                    _linear.quantize_weight(self.fc2_weight))
         gu_q, down_q = self._fp8_weights
         flat = flat.to(torch.bfloat16).contiguous()
         if mx:

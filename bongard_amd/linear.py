@@ -65,7 +65,9 @@ def _forward_needs(ctx, n):
     return tuple(bool(grad and b) for b in ctx.needs_input_grad[:n])
 
 
-def quantize_weight(weight, *, transpose=True, scaler=None):
+def quantize_weight(weight, *, transpose=False, scaler=None):
+    """e4m3 copy of a weight [N, K] (current or the scaler's delayed scale). The backward
+    reads it as is (a K-major operand), so no transposed copy is made unless asked for."""
     return _quantize(weight.detach(), E4M3, scaler, rowwise=True, transpose=transpose)
 
 
@@ -88,38 +90,52 @@ def _quantize_input(x, scaler, x_amax, transpose):
     return scaler.quantize(x, rowwise=True, transpose=transpose, producer_count=int(x_amax))
 
 
+def linear_kmajor(in_features, out_features):
+    """Whether a tensorwise FP8 linear can train: its backward reads the forward's fp8 X and
+    W as they are (K-major dgrad / wgrad operands, bf8_gemm_kmajor), which needs both row
+    lengths to be multiples of 16 bytes (as transposed fp8 copies would)."""
+    return in_features % 16 == 0 and out_features % 16 == 0
+
+
+def _check_trainable(who, *dims):
+    bad = [d for d in dims if d % 16]
+    if bad:
+        raise ValueError(f"{who}: FP8 training needs feature sizes that are multiples of 16 "
+                         f"(got {list(dims)})")
+
+
 def linear_forward(x, weight, bias, wq, scaling, need_dx, need_dw):
-    """Tensorwise FP8 linear forward: ``(y, (x8t, x_meta, w8t, w_meta))``, the transposed
-    copies None where no gradient needs them. ``wq``: a cached quantized weight or None;
-    ``scaling``: None (current scaling) or a LinearScaling (delayed scaling)."""
-    if scaling is None and wq is None and not (need_dx or need_dw):
-        # current scaling, no transposed copies: x and W in one amax + one cast launch
+    """Tensorwise FP8 linear forward: ``(y, (x8, x_meta, w8, w_meta))``, X8 and W8 as the
+    backward reads them (None where no gradient needs them). ``wq``: a cached quantized
+    weight or None; ``scaling``: None (current scaling) or a LinearScaling (delayed).
+    No transposed copy is made: under current scaling x and W share one amax and one cast
+    launch, in training as in inference."""
+    if need_dx or need_dw:
+        _check_trainable("fp8 linear", x.shape[-1], weight.shape[0])
+    if scaling is None and wq is None:
         xq, wq = ops.quantize_many([x, weight.detach()])
     else:
-        xq = _quantize(x, E4M3, scaling and scaling.input, transpose=need_dw)
+        xq = _quantize(x, E4M3, scaling and scaling.input)
     if wq is None:
-        wq = quantize_weight(weight, transpose=need_dx, scaler=scaling and scaling.weight)
+        wq = quantize_weight(weight, scaler=scaling and scaling.weight)
     y = ops.gemm(xq.data, E4M3, xq.meta, wq.data, E4M3, wq.meta, bias=bias)
-    return y, (xq.data_t if need_dw else None, xq.meta, wq.data_t if need_dx else None, wq.meta)
+    return y, (xq.data if need_dw else None, xq.meta, wq.data if need_dx else None, wq.meta)
 
 
 def linear_backward(dy, saved, scaling, need_dx, need_dw):
-    """Tensorwise FP8 linear backward: dY in e5m2 (its own scale), dX = dY8 . W8 on W's
-    transposed copy, dW = dY8^T . X8 on the transposed copies of dY and X."""
-    x8t, x_meta, w8t, w_meta = saved
-    dy = dy.contiguous()
-    dyq = _quantize(dy, E5M2, scaling and scaling.grad_output, rowwise=need_dx,
-                    transpose=need_dw)
-    dx = dw = None
-    if need_dx:
-        dx = ops.gemm(dyq.data, E5M2, dyq.meta, w8t, E4M3, w_meta)
-    if need_dw:
-        dw = ops.gemm(dyq.data_t, E5M2, dyq.meta, x8t, E4M3, x_meta)
+    """Tensorwise FP8 linear backward: dY in e5m2 (its own scale), dX = dY8 . W8 and
+    dW = dY8^T . X8 with W8 and X8 (and dY8 for dW) read as K-major operands."""
+    x8, x_meta, w8, w_meta = saved
+    dyq = _quantize(dy.contiguous(), E5M2, scaling and scaling.grad_output)
+    dx = ops.gemm_kmajor(dyq.data, E5M2, dyq.meta, w8, E4M3, w_meta) if need_dx else None
+    dw = (ops.gemm_kmajor(dyq.data, E5M2, dyq.meta, x8, E4M3, x_meta, a_kmajor=True)
+          if need_dw else None)
     return dx, dw
 
 
 class Fp8LinearFunction(_Fp8Function):
-    """y = x @ W^T (+ b) in FP8; x: bf16 [M, K] with M % 16 == 0 when grads are needed.
+    """y = x @ W^T (+ b) in FP8; x: bf16 [M, K], W [N, K] with K and N multiples of 16
+    when grads are needed.
 
     ``scaling``: None (current scaling) or a LinearScaling (delayed scaling)."""
 
@@ -381,34 +397,24 @@ class Fp8GegluMlpMxFunction(_Fp8Function):
         return dx, dgu, dd, None, None, None
 
 
-def mlp_kmajor(hidden, intermediate, out_features):
-    """Whether the MLP's backward reads the forward's fp8 tensors as they are (its dgrad and
-    wgrad GEMMs take K-major operands, bf8_gemm_kmajor), so no transposed fp8 copy is made
-    anywhere: every operand row a multiple of 16 bytes."""
-    return hidden % 16 == 0 and int(intermediate) % 16 == 0 and out_features % 16 == 0
-
-
 def mlp_forward(x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scaling, x_amax,
                 needs):
     """Forward of the FP8 gated MLP (see Fp8GegluMlpFunction): ``(y, saved)`` with saved =
-    (GU, x8, x_meta, h8, h_meta, gu8, gu_meta, d8, d_meta), the tensors the backward reads
-    (None where no gradient needs them): with :func:`mlp_kmajor` the fp8 tensors the forward
-    computed with (X8, H8, W_gu8, W_down8), otherwise their transposed copies.
-    ``needs``: (dx, dW_gu, dW_down) wanted."""
+    (GU, x8, x_meta, h8, h_meta, gu8, gu_meta, d8, d_meta): the bf16 pre-activations and the
+    fp8 tensors the forward computed with (X8, H8, W_gu8, W_down8), which the backward reads
+    as they are (K-major dgrad / wgrad operands), None where no gradient needs them; no
+    transposed fp8 copy is made. ``needs``: (dx, dW_gu, dW_down) wanted."""
     I = int(intermediate)
     need_dx, need_dgu, need_dd = needs
     train = need_dx or need_dgu or need_dd
+    if train:
+        _check_trainable("fp8 gated MLP", x.shape[-1], I, w_down.shape[0])
     if scaling is not None and split_scales:
         raise NotImplementedError("delayed scaling needs the fused [gate; up] weight")
     gs, ds = scaling if scaling is not None else (None, None)
-    km = mlp_kmajor(x.shape[-1], I, w_down.shape[0])
-    # transposed copies wanted (the backward's operands when it cannot read K-major ones)
-    t_dx, t_dgu, t_dd = ((False, False, False) if km else (need_dx, need_dgu, need_dd))
-    if (scaling is None and x_amax is None and not (t_dx or t_dgu or t_dd) and not split_scales
+    if (scaling is None and x_amax is None and not split_scales
             and (gu_q is None or down_q is None)):
-        # current scaling without transposed copies: x and the uncached weights in one amax
-        # + one cast launch (the rowwise copies are all the forward and a K-major backward
-        # need)
+        # current scaling: x and the uncached weights in one amax + one cast launch
         ws = [w for w, q in ((w_gu, gu_q), (w_down, down_q)) if q is None]
         qs = ops.quantize_many([x] + [w.detach() for w in ws])
         xq = qs[0]
@@ -418,125 +424,98 @@ def mlp_forward(x, w_gu, w_down, gu_q, down_q, intermediate, split_scales, scali
             down_q = qs[-1]
     elif gs is not None and x_amax is None and gu_q is None and down_q is None:
         # delayed scaling with every operand quantized here: x, [W_gate; W_up] and W_down
-        # with the transposed copies the backward reads, in one launch
+        # in one launch
         xq, wq, down_q = _scaling.quantize_many([
-            (gs.input, x, True, t_dgu),
-            (gs.weight, w_gu.detach(), True, t_dx),
-            (ds.weight, w_down.detach(), True, t_dx or t_dgu)])
-        gu_q = _GateUp(wq.data, wq.data_t, wq.meta.view(1, 4))
+            (gs.input, x, True, False),
+            (gs.weight, w_gu.detach(), True, False),
+            (ds.weight, w_down.detach(), True, False)])
+        gu_q = _GateUp(wq.data, None, wq.meta.view(1, 4))
     else:
-        xq = _quantize_input(x, gs and gs.input, x_amax, t_dgu)
+        xq = _quantize_input(x, gs and gs.input, x_amax, False)
     if gu_q is None:
-        gu_q = quantize_gate_up(w_gu, I, split_scales, transpose=t_dx,
-                                scaler=gs and gs.weight)
+        gu_q = quantize_gate_up(w_gu, I, split_scales, scaler=gs and gs.weight)
     stride = 4 if split_scales else 0
     M = xq.rows
     if ds is None:
         H, GU, hparts = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I,
                                        w_meta_stride=stride, keep_gu=train)
-        hq = ops.cast_partials(H, hparts, E4M3, rowwise=True, transpose=t_dd)
+        hq = ops.cast_partials(H, hparts, E4M3, rowwise=True)
     else:
+        # H's scale is known before the GEMM: the epilogue casts H itself; no bf16 H round
+        # trip
         count = ops.geglu_partials_count(M, I)
-        transpose = t_dd
-        if M % 32 == 0 or not transpose:
-            # H's scale is known before the GEMM: the epilogue casts H (and its
-            # transpose for the down wgrad) itself; no bf16 H round trip
-            def replay(meta, parts):
-                q, gu, _, _ = ops.gemm_geglu_quant(xq.data, xq.meta, gu_q.data, gu_q.meta,
-                                                   I, meta, transpose=transpose,
-                                                   keep_gu=train, partials=parts)
-                return q, gu
 
-            def launch(st, length, pos, prev, parts):
-                return replay(ops.delayed_scale_fold(st, length, pos, prev, E4M3), parts)
+        def replay(meta, parts):
+            q, gu, _, _ = ops.gemm_geglu_quant(xq.data, xq.meta, gu_q.data, gu_q.meta, I, meta,
+                                               keep_gu=train, partials=parts)
+            return q, gu
 
-            hq, GU = ds.input.produce(count, x.device, launch, replay)
-        else:
-            H, GU, _ = ops.gemm_geglu(
-                xq.data, xq.meta, gu_q.data, gu_q.meta, I, keep_gu=train,
-                partials=ds.input.partials_for_producer(count, x.device))
-            hq = ds.input.quantize(H, rowwise=True, transpose=transpose,
-                                   producer_count=count)
+        def launch(st, length, pos, prev, parts):
+            return replay(ops.delayed_scale_fold(st, length, pos, prev, E4M3), parts)
+
+        hq, GU = ds.input.produce(count, x.device, launch, replay)
     h_meta = hq.meta
     if down_q is None:
-        down_q = quantize_weight(
-            w_down, transpose=t_dx or t_dgu,
-            scaler=ds and ds.weight)
+        down_q = quantize_weight(w_down, scaler=ds and ds.weight)
     y = ops.gemm(hq.data, E4M3, h_meta, down_q.data, E4M3, down_q.meta)
-    if km:
-        return y, (GU, xq.data if need_dgu else None, xq.meta, hq.data if need_dd else None,
-                   h_meta, gu_q.data if need_dx else None, gu_q.meta,
-                   down_q.data if need_dx or need_dgu else None, down_q.meta)
-    return y, (GU, xq.data_t, xq.meta, hq.data_t, h_meta, gu_q.data_t, gu_q.meta, down_q.data_t,
-               down_q.meta)
+    return y, (GU, xq.data if need_dgu else None, xq.meta, hq.data if need_dd else None, h_meta,
+               gu_q.data if need_dx else None, gu_q.meta,
+               down_q.data if need_dx or need_dgu else None, down_q.meta)
 
 
-def mlp_backward(dy, saved, intermediate, split_scales, scaling, needs, kmajor=False):
-    """Backward of the FP8 gated MLP: ``(dx, dW_gu, dW_down)`` (None where not wanted).
-    ``kmajor``: the saved fp8 tensors are the forward's own (X8, H8, W_gu8, W_down8; see
-    :func:`mlp_kmajor`), read as K-major GEMM operands, and no transposed copy of dY or
-    dGU is made; otherwise they are the transposed copies."""
-    (GU, x8t, x_meta, h8t, h_meta, gu8t, gu_meta, d8t, d_meta) = saved
+def mlp_backward(dy, saved, intermediate, split_scales, scaling, needs):
+    """Backward of the FP8 gated MLP: ``(dx, dW_gu, dW_down)`` (None where not wanted). Every
+    GEMM reads its fp8 operands as their producers wrote them (bf8_gemm_kmajor): dY8, the
+    saved H8, W_down8, W_gu8, X8 and dGU8; no transposed copy is made."""
+    (GU, x8, x_meta, h8, h_meta, gu8, gu_meta, d8, d_meta) = saved
     I = int(intermediate)
     need_dx, need_dgu, need_dd = needs
     gs, ds = scaling if scaling is not None else (None, None)
-    dy = dy.contiguous()
-    km = bool(kmajor)
+    dyq = _quantize(dy.contiguous(), E5M2, ds and ds.grad_output)
 
     def gemm_b(a, a_meta, b, b_meta, *, a_kmajor=False):
-        # dgrad / wgrad: e5m2 gradient A against the saved e4m3 B (B^T [K, N] when K-major)
-        if km:
-            return ops.gemm_kmajor(a, E5M2, a_meta, b, E4M3, b_meta, a_kmajor=a_kmajor)
-        return ops.gemm(a, E5M2, a_meta, b, E4M3, b_meta)
+        # e5m2 gradient A (or A^T) against the saved e4m3 B, given as B^T [K, N]
+        return ops.gemm_kmajor(a, E5M2, a_meta, b, E4M3, b_meta, a_kmajor=a_kmajor)
 
-    dyq = _quantize(dy, E5M2, ds and ds.grad_output, rowwise=True, transpose=need_dd and not km)
     dx = dgu = dd = None
     if need_dd:
-        # dW_down = dY^T . H
-        dd = gemm_b(dyq.data if km else dyq.data_t, dyq.meta, h8t, h_meta, a_kmajor=True)
+        dd = gemm_b(dyq.data, dyq.meta, h8, h_meta, a_kmajor=True)   # dW_down = dY^T . H
     if not (need_dx or need_dgu):
         return dx, dgu, dd
-    dH = gemm_b(dyq.data, dyq.meta, d8t, d_meta)
+    dH = gemm_b(dyq.data, dyq.meta, d8, d_meta)                     # dH = dY . W_down
     if gs is not None:
         # delayed scaling: dGU's scale is known already, so the gelu backward writes
-        # fp8 dGU (and its transpose) in the same pass
+        # fp8 dGU in the same pass
         M = dH.shape[0]
         count = ops.geglu_bwd_delayed_partials_count(M, I)
         scaler = gs.grad_output
         dq = scaler.produce(count, dH.device, lambda st, L, pos, prev, parts:
                             ops.geglu_bwd_delayed(dH, GU, st, L, pos, prev, scaler.fmt,
-                                                  rowwise=need_dx or km,
-                                                  transpose=need_dgu and not km,
                                                   partials_out=parts))
         if need_dx:
-            dx = gemm_b(dq.data, dq.meta, gu8t, gu_meta[0])
+            dx = gemm_b(dq.data, dq.meta, gu8, gu_meta[0])            # dX = dGU . W_gu
         if need_dgu:
-            # dW_gu = dGU^T . X
-            dgu = gemm_b(dq.data if km else dq.data_t, dq.meta, x8t, x_meta, a_kmajor=True)
+            dgu = gemm_b(dq.data, dq.meta, x8, x_meta, a_kmajor=True)  # dW_gu = dGU^T . X
         return dx, dgu, dd
     dGU, gparts = ops.geglu_bwd(dH, GU)
     if not split_scales:
-        dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=need_dx or km,
-                               transpose=need_dgu and not km)
-        g_meta = dq.meta
+        dq = ops.cast_partials(dGU, gparts, E5M2, rowwise=True)
         if need_dx:
-            dx = gemm_b(dq.data, g_meta, gu8t, gu_meta[0])
+            dx = gemm_b(dq.data, dq.meta, gu8, gu_meta[0])
         if need_dgu:
-            dgu = gemm_b(dq.data if km else dq.data_t, g_meta, x8t, x_meta, a_kmajor=True)
+            dgu = gemm_b(dq.data, dq.meta, x8, x_meta, a_kmajor=True)
     else:
         # Separate gate/up projections: each gradient has its own e5m2 scale and its
         # own dgrad GEMM; the input gradient is their bf16 sum (autograd of x used twice).
         dx_parts, dw_parts = [], []
         for half in range(2):
             d_half = dGU[:, half * I:(half + 1) * I].contiguous()
-            dq = ops.quantize(d_half, E5M2, rowwise=need_dx or km, transpose=need_dgu and not km)
+            dq = ops.quantize(d_half, E5M2)
             if need_dx:
-                # the half's rows of W_gu8 (K-major) or columns of its transposed copy
-                w_half = gu8t[half * I:(half + 1) * I] if km else gu8t[:, half * I:(half + 1) * I]
-                dx_parts.append(gemm_b(dq.data, dq.meta, w_half, gu_meta[half]))
+                dx_parts.append(gemm_b(dq.data, dq.meta, gu8[half * I:(half + 1) * I],
+                                       gu_meta[half]))
             if need_dgu:
-                dw_parts.append(gemm_b(dq.data if km else dq.data_t, dq.meta, x8t, x_meta,
-                                       a_kmajor=True))
+                dw_parts.append(gemm_b(dq.data, dq.meta, x8, x_meta, a_kmajor=True))
         if need_dx:
             dx = dx_parts[0] + dx_parts[1]
         if need_dgu:
@@ -564,19 +543,19 @@ class Fp8GegluMlpFunction(_Fp8Function):
         ctx.intermediate = int(intermediate)
         ctx.split_scales = split_scales
         ctx.scaling = scaling
-        ctx.kmajor = mlp_kmajor(x.shape[-1], intermediate, w_down.shape[0])
         ctx.save_for_backward(*saved)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         dx, dgu, dd = mlp_backward(dy, ctx.saved_tensors, ctx.intermediate, ctx.split_scales,
-                                   ctx.scaling, tuple(ctx.needs_input_grad[:3]), ctx.kmajor)
+                                   ctx.scaling, tuple(ctx.needs_input_grad[:3]))
         return dx, dgu, dd, None, None, None, None, None, None
 
 
-def quantize_gate_up(w_gu, intermediate, split_scales, *, transpose=True, scaler=None):
-    """Quantize [W_gate; W_up] into one [2I, K] fp8 buffer (+ [K, 2I] transposed copy).
+def quantize_gate_up(w_gu, intermediate, split_scales, *, transpose=False, scaler=None):
+    """Quantize [W_gate; W_up] into one [2I, K] fp8 buffer (+ with ``transpose`` a [K, 2I]
+    transposed copy, which the K-major backward does not need).
 
     split_scales: gate and up halves get separate metas (meta is then [2, 4]).
     scaler: a DelayedScaler for the shared scale (delayed scaling), or None.

@@ -16,7 +16,7 @@ import torch
 
 from . import ops
 from .ops import E4M3, E5M2
-from .linear import _Fp8Function, _forward_needs
+from .linear import _Fp8Function, _check_trainable, _forward_needs
 from .te_linear import Float8CurrentScaling, TELinear, _pad_rows
 
 __all__ = ["project_state_kv"]
@@ -24,43 +24,46 @@ __all__ = ["project_state_kv"]
 
 class _SharedInputFp8Function(_Fp8Function):
     """y_i = x @ W_i^T for several per-tensor-scaled FP8 projections of one input x
-    [M, K] (M % 32 == 0): one e4m3 quantization of x (+ its transposed copy for the
-    weight gradients), one GEMM per cached weight; backward per projection as
-    Fp8LinearFunction, the input gradients summed in bf16 in projection order."""
+    [M, K] (M % 32 == 0): one e4m3 quantization of x, one GEMM per cached weight; backward
+    per projection as Fp8LinearFunction (X8, W8_i and dY8 read as K-major operands), the
+    input gradients summed in bf16 in projection order."""
 
     @staticmethod
     def forward(ctx, x, wqs, *weights):
         needs = _forward_needs(ctx, len(ctx.needs_input_grad))
         need_dx = needs[0]
         need_dw = any(needs[2:])
-        xq = ops.quantize(x, E4M3, transpose=need_dw)
+        if need_dx or need_dw:
+            _check_trainable("shared-input projections", x.shape[-1],
+                             *[wq.data.shape[0] for wq in wqs])
+        xq = ops.quantize(x, E4M3)
         outs = [ops.gemm(xq.data, E4M3, xq.meta, wq.data, E4M3, wq.meta) for wq in wqs]
         ctx.n = len(wqs)
         ctx.need_dx = need_dx
-        saved = [xq.data_t, xq.meta]
+        saved = [xq.data if need_dw else None, xq.meta]
         for wq in wqs:
-            saved += [wq.data_t if need_dx else None, wq.meta]
+            saved += [wq.data if need_dx else None, wq.meta]
         ctx.save_for_backward(*saved)
         return tuple(outs)
 
     @staticmethod
     def backward(ctx, *dys):
         saved = ctx.saved_tensors
-        x8t, x_meta = saved[0], saved[1]
+        x8, x_meta = saved[0], saved[1]
         dx = None
         dws = []
         for i, dy in enumerate(dys):
-            w8t, w_meta = saved[2 + 2 * i], saved[3 + 2 * i]
+            w8, w_meta = saved[2 + 2 * i], saved[3 + 2 * i]
             need_dw = ctx.needs_input_grad[2 + i]
             if dy is None:
                 dws.append(None)
                 continue
-            dyq = ops.quantize(dy.contiguous(), E5M2, rowwise=ctx.need_dx, transpose=need_dw)
+            dyq = ops.quantize(dy.contiguous(), E5M2)
             if ctx.need_dx:
-                part = ops.gemm(dyq.data, E5M2, dyq.meta, w8t, E4M3, w_meta)
+                part = ops.gemm_kmajor(dyq.data, E5M2, dyq.meta, w8, E4M3, w_meta)
                 dx = part if dx is None else dx + part
-            dws.append(ops.gemm(dyq.data_t, E5M2, dyq.meta, x8t, E4M3, x_meta) if need_dw
-                       else None)
+            dws.append(ops.gemm_kmajor(dyq.data, E5M2, dyq.meta, x8, E4M3, x_meta, a_kmajor=True)
+                       if need_dw else None)
         return (dx, None, *dws)
 
 

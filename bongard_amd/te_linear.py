@@ -189,14 +189,15 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
         return self
 
     def fp8_weight(self, is_first_microbatch):
-        """Quantized weight (+ transposed copy); cached across microbatches like TE."""
+        """Quantized weight (the block-scaled recipes with their column-wise copy, which their
+        backward reads); cached across microbatches like TE."""
         if is_first_microbatch or self._fp8_weight is None:
             if _is_mx(self.recipe):
                 q = _linear.quantize_weight_mx(self.weight, transpose=True)
             elif _is_nvfp4(self.recipe):
                 q = _linear.quantize_weight_nvfp4(self.weight, transpose=True)
             else:
-                q = _linear.quantize_weight(self.weight, transpose=True,
+                q = _linear.quantize_weight(self.weight,
                                             scaler=self.scaling and self.scaling.weight)
             if is_first_microbatch is not None:
                 self._fp8_weight = q
@@ -332,16 +333,15 @@ class TEMLP(torch.nn.Module):
         gs, dsc = self.gate_up.scaling, self.down.scaling
         if new_gu and new_down:
             wq, dq = _scaling.quantize_many([
-                (gs.weight, self.gate_up.weight.detach(), True, True),
-                (dsc.weight, self.down.weight.detach(), True, True)])
-            self.gate_up._fp8_weight = _linear._GateUp(wq.data, wq.data_t, wq.meta.view(1, 4))
+                (gs.weight, self.gate_up.weight.detach(), True, False),
+                (dsc.weight, self.down.weight.detach(), True, False)])
+            self.gate_up._fp8_weight = _linear._GateUp(wq.data, None, wq.meta.view(1, 4))
             self.down._fp8_weight = dq
         elif new_gu:
             self.gate_up._fp8_weight = _linear.quantize_gate_up(
                 self.gate_up.weight, I, split_scales=False, scaler=gs.weight)
         elif new_down:
-            self.down._fp8_weight = _linear.quantize_weight(self.down.weight, transpose=True,
-                                                            scaler=dsc.weight)
+            self.down._fp8_weight = _linear.quantize_weight(self.down.weight, scaler=dsc.weight)
         out = _linear.Fp8GegluMlpFunction.apply(flat, self.gate_up.weight, self.down.weight,
                                                 self.gate_up._fp8_weight,
                                                 self.down._fp8_weight, I, False, (gs, dsc))

@@ -333,3 +333,18 @@ def test_checkpoint_region_detection_on_cpu():
     y2.sum().backward()
     region(x)                                       # a plain call: no region
     assert seen[-1] == (None, False)
+
+
+def test_fp8_training_needs_feature_sizes_of_16():
+    """The FP8 backward reads the forward's fp8 tensors as K-major GEMM operands, whose rows
+    must be whole 16-byte multiples: training a linear or gated MLP whose feature sizes are
+    not raises before any kernel runs (inference has no such bound)."""
+    from bongard_amd import linear
+    x = torch.zeros(32, 256, dtype=torch.bfloat16, requires_grad=True)
+    w = torch.zeros(376, 256, dtype=torch.bfloat16, requires_grad=True)
+    with pytest.raises(ValueError, match="multiples of 16"):
+        linear.Fp8LinearFunction.apply(x, w, None, None)
+    w_gu = torch.zeros(2 * 512, 256, dtype=torch.bfloat16, requires_grad=True)
+    w_d = torch.zeros(264, 512, dtype=torch.bfloat16, requires_grad=True)
+    with pytest.raises(ValueError, match="multiples of 16"):
+        linear.Fp8GegluMlpFunction.apply(x, w_gu, w_d, None, None, 512, False)

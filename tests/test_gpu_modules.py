@@ -168,7 +168,7 @@ def test_temlp_split_gate_up(gpu, monkeypatch):
     # the kernels' own dGU: the module's forward and dH calls, repeated (deterministic)
     from bongard_amd import linear as lin
     xq = ops.quantize(x.to(gpu), ops.E4M3, rowwise=True, transpose=True)
-    gu_q = lin.quantize_gate_up(torch.cat([wg, wu]).to(gpu), I, True)
+    gu_q = lin.quantize_gate_up(torch.cat([wg, wu]).to(gpu), I, True, transpose=True)
     _, GU, _ = ops.gemm_geglu(xq.data, xq.meta, gu_q.data, gu_q.meta, I, w_meta_stride=4,
                               keep_gu=True)
     dq = ops.quantize(wd.to(gpu), ops.E4M3, rowwise=True, transpose=True)
@@ -485,10 +485,10 @@ def _count_calls(monkeypatch, module, name):
 
 
 def test_inference_forward_shares_quantize_launches(gpu, monkeypatch):
-    """Under no_grad the FP8 linear and gated MLP quantize x and their (trainable) weights in
-    shared launches (ops.quantize_many); the output is bit-identical to the training
-    forward's, which for the linear quantizes each tensor on its own with transposed copies
-    (the gated MLP's training forward shares the launches as well)."""
+    """The FP8 linear and gated MLP quantize x and their weights in shared launches
+    (ops.quantize_many) under no_grad, and in training too, where their backward reads the
+    forward's own fp8 tensors as K-major operands (no transposed copy to make); outputs are
+    bit-identical either way."""
     from bongard_amd import linear
     calls = _count_calls(monkeypatch, ops, "quantize_many")
     g = torch.Generator().manual_seed(5)
@@ -498,22 +498,23 @@ def test_inference_forward_shares_quantize_launches(gpu, monkeypatch):
     w_d = torch.nn.Parameter((torch.randn(256, 512, generator=g) * 0.014).to(torch.bfloat16).to(gpu))
     x16 = x[:288]
     y_train = linear.Fp8LinearFunction.apply(x16, w, None, None)
-    assert calls == []                   # training: per-tensor quantization with transposes
+    assert calls == ["quantize_many"]    # training, K-major backward: shared launches
     with torch.no_grad():
         y_inf = linear.Fp8LinearFunction.apply(x16, w, None, None)
-    assert calls == ["quantize_many"]
+    assert calls == ["quantize_many"] * 2
     assert torch.equal(y_train.detach(), y_inf)
     with torch.inference_mode():         # any row count: no transposed copy is made
         y_odd = linear.Fp8LinearFunction.apply(x, w, None, None)
         xq, wq = ops.quantize(x), ops.quantize(w)
         y_sep = ops.gemm(xq.data, ops.E4M3, xq.meta, wq.data, ops.E4M3, wq.meta)
-    assert calls == ["quantize_many"] * 2
+    assert calls == ["quantize_many"] * 3
     assert torch.equal(y_odd, y_sep)
     # the gated MLP's backward reads the forward's own fp8 tensors (K-major GEMM operands),
     # so its training forward makes no transposed copy and shares the launches too
     y_train = linear.Fp8GegluMlpFunction.apply(x16, w_gu, w_d, None, None, 512, False)
-    assert len(calls) == 3
+    assert len(calls) == 4
     with torch.no_grad():
         y_inf = linear.Fp8GegluMlpFunction.apply(x16, w_gu, w_d, None, None, 512, False)
-    assert len(calls) == 4
+    assert len(calls) == 5
     assert torch.equal(y_train.detach(), y_inf)
+
