@@ -4,10 +4,12 @@ Forward: X and W are quantized to e4m3 with per-tensor current scaling, the GEMM
 the FP8 MFMA with fp32 accumulation and a dequant epilogue, output bf16.
 Backward (torchao tensorwise / TE Float8CurrentScaling "HYBRID" formats): grad_out is
 quantized to e5m2 with its own per-tensor scale;
-  dgrad  dX = dY8 . W8          (TN GEMM against W8's transposed copy)
-  wgrad  dW = dY8^T . X8        (TN GEMM on the transposed copies of dY8 and X8)
-The transposed copies come from the same cast kernels (LDS-staged transpose), so each
-operand is read from HBM once per quantization.
+  dgrad  dX = dY8 . W8          (W8 [N, K] read as a K-major operand)
+  wgrad  dW = dY8^T . X8        (dY8 and X8 read as K-major operands)
+The backward GEMMs read the forward's fp8 tensors as they are and turn them around in LDS
+(the LDS transpose read), so no transposed fp8 copy is written. The axiswise, MXFP8 and
+NVFP4 recipes scale along the other axis for the backward and quantize separately
+transposed copies.
 
 Scaling is per-tensor current scaling by default; passing ``scaling``
 (:class:`bongard_amd.scaling.LinearScaling`) switches a linear to delayed scaling with an
@@ -32,7 +34,8 @@ from .ops import E4M3, E5M2
 
 @dataclass
 class QuantizedWeight:
-    """Cached FP8 copy of a weight: rowwise [N, K], transposed [K, N], meta."""
+    """Cached FP8 copy of a weight (``q``: rowwise [N, K], a transposed [K, N] only where a
+    recipe asks for one, and meta) and the weight version it was made from."""
 
     q: ops.Fp8Tensor
     version: int

@@ -15,6 +15,7 @@ ramp), and per position in the step the kernel, its median and minimum duration 
 steps must all launch the same kernel sequence.
 """
 import sqlite3, sys, re
+W = 76  # kernel-name column: wide enough for the GEMM template arguments
 def short(n):
     n = n.replace("(anonymous namespace)", "anon")
     depth = 0
@@ -24,7 +25,7 @@ def short(n):
         elif ch == '(' and depth == 0:
             n = n[:i]; break
     n = n.replace("void ", "").replace("bf8::anon::", "")
-    return n[:70]
+    return n[:W]
 def kernel_stats(path):
     db = sqlite3.connect(path); cur = db.cursor()
     rows = cur.execute("select name, start, end from kernels").fetchall()
@@ -45,11 +46,11 @@ def kernel_stats(path):
             cur.append((e - s) / 1e3)
         prev = k
     tot = sum(v[1] for v in agg.values())
-    out = [f"{'kernel':70s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'time%':>7s}"
+    out = [f"{'kernel':{W}s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'time%':>7s}"
            f" {'run':>4s} {'run_avg_us':>10s}"]
     for k, v in sorted(agg.items(), key=lambda kv: -kv[1][1]):
         r = runs.get(k, [])
-        out.append(f"{k:70s} {v[0]:6d} {v[1]/v[0]:9.2f} {v[2]:9.2f} {v[3]:9.2f} {100*v[1]/tot:7.2f}"
+        out.append(f"{k:{W}s} {v[0]:6d} {v[1]/v[0]:9.2f} {v[2]:9.2f} {v[3]:9.2f} {100*v[1]/tot:7.2f}"
                    f" {len(r):4d} {sum(r) / max(len(r), 1):10.2f}")
     return "\n".join(out)
 def pmc(path):
@@ -72,14 +73,14 @@ def step_table(path, first, skip=2):
     steps = steps[skip:]
     if not steps or any([k for k, _ in st] != [k for k, _ in steps[0]] for st in steps):
         raise SystemExit("steps: no steps found, or the steps launch different kernel sequences")
-    out = [f"{'kernel':70s} {'median_us':>10s} {'min_us':>9s}"]
+    out = [f"{'kernel':{W}s} {'median_us':>10s} {'min_us':>9s}"]
     med_sum = min_sum = 0.0
     for i, (k, _) in enumerate(steps[0]):
         d = sorted(st[i][1] for st in steps)
         med = d[len(d) // 2] if len(d) % 2 else 0.5 * (d[len(d) // 2 - 1] + d[len(d) // 2])
         med_sum += med; min_sum += d[0]
-        out.append(f"{k:70s} {med:10.2f} {d[0]:9.2f}")
-    out.append(f"{'sum (' + str(len(steps)) + ' steps)':70s} {med_sum:10.2f} {min_sum:9.2f}")
+        out.append(f"{k:{W}s} {med:10.2f} {d[0]:9.2f}")
+    out.append(f"{'sum (' + str(len(steps)) + ' steps)':{W}s} {med_sum:10.2f} {min_sum:9.2f}")
     return "\n".join(out)
 if __name__ == "__main__":
     if sys.argv[1] == "trace":
@@ -88,4 +89,4 @@ if __name__ == "__main__":
         print(step_table(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 2))
     else:
         for k, v in sorted(pmc(sys.argv[2]).items()):
-            print(f"{k[0]:70s} {k[1]:22s} grid={k[2]:<10d} {v:16.1f} per dispatch")
+            print(f"{k[0]:{W}s} {k[1]:22s} grid={k[2]:<10d} {v:16.1f} per dispatch")

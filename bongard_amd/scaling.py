@@ -266,7 +266,7 @@ def quantize_many(requests):
     for each request in order (bytes, metas, histories, partials), which is what a
     checkpoint replay, or a role whose pending partials exceed what one launch folds, runs
     instead. A forward quantizes its input and weights together this way, as TE casts one
-    forward's operands with their transposes (bongard/te_linear.py:73-74)."""
+    forward's operands together (bongard/te_linear.py:73-74)."""
     if not requests:
         return []
     regions = [checkpoint_region(not sc.gradient) for sc, _, _, _ in requests]

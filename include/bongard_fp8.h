@@ -253,8 +253,8 @@ int bf8_cast_delayed_bf16(const void* x, int64_t rows, int64_t cols, float* stat
                           void* stream);
 
 /* Up to 8 bf8_cast_delayed_bf16 calls in one launch (one training step's forward
- * quantizes x, [W_gate; W_up] and W_down with their transposed copies at once, as TE casts
- * one forward's operands with their transposes: bongard/te_linear.py:73-74). Entry t takes
+ * quantizes x, [W_gate; W_up] and W_down at once, as TE casts one forward's operands
+ * together: bongard/te_linear.py:73-74). Entry t takes
  * the arguments of the single call as element t of each array (out[t] or out_t[t] may be
  * NULL, partials_out[t] too); n_prev[t] <= 2048. Each tensor runs on the grid of its own
  * call, so bytes, metas, histories and partials equal those of the calls made one by one
