@@ -253,6 +253,63 @@ __global__ __launch_bounds__(kNT) void geglu_bwd_delayed_kernel(
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
 }
 
+// geglu_bwd_delayed_kernel without the transposed output (the K-major backward reads dGU
+// as it is): a grid-stride stream over 8-element vectors of [M, I], kRowVecs per thread
+// per pass with all their loads issued first, so a wave writes 512 contiguous fp8 bytes of
+// d_g and of d_u per vector slot. Same chain, scale, bytes and partials count.
+constexpr int kRowVecs = 4;
+
+template <int FMT>
+__global__ __launch_bounds__(kNT) void geglu_bwd_delayed_rows_kernel(
+    const uint16_t* __restrict__ dH, const uint16_t* __restrict__ GU, int64_t M, int64_t I,
+    float* __restrict__ state, int len, int pos, const uint32_t* __restrict__ prev,
+    int64_t n_prev, float* __restrict__ meta_out, uint8_t* __restrict__ out,
+    uint32_t* __restrict__ partials) {
+  __shared__ __attribute__((aligned(16))) uint16_t ta[kGeluABytes / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t tf[kGeluFBytes / 4];
+  load_gelu_tables<kNT>(ta, tf);  // the scale step below synchronises the block
+  const float scale =
+      delayed_scale_block<kNT>(state, len, pos, prev, n_prev, Fp8Max<FMT>::value, meta_out,
+                               blockIdx.x == 0);
+  const int64_t per_row = I / 8;
+  const int64_t nvec = M * per_row;
+  const int64_t pass = (int64_t)gridDim.x * kNT * kRowVecs;
+  uint32_t m = 0;
+  for (int64_t v0 = (int64_t)blockIdx.x * kNT * kRowVecs + threadIdx.x; v0 < nvec; v0 += pass) {
+    uint4 dh[kRowVecs], g[kRowVecs], u[kRowVecs];
+    int64_t eo[kRowVecs], go[kRowVecs];  // element offsets in dH / out and in GU
+#pragma unroll
+    for (int j = 0; j < kRowVecs; ++j) {
+      const int64_t v = v0 + (int64_t)j * kNT;
+      const int64_t vv = v < nvec ? v : nvec - 1;  // loads of a clamped vector, not stored
+      const int64_t row = vv / per_row;
+      const int64_t col = (vv - row * per_row) * 8;
+      eo[j] = row * I + col;
+      go[j] = row * 2 * I + col;
+      dh[j] = *reinterpret_cast<const uint4*>(dH + eo[j]);
+      g[j] = *reinterpret_cast<const uint4*>(GU + go[j]);
+      u[j] = *reinterpret_cast<const uint4*>(GU + go[j] + I);
+    }
+#pragma unroll
+    for (int j = 0; j < kRowVecs; ++j) {
+      const uint32_t dhw[4] = {dh[j].x, dh[j].y, dh[j].z, dh[j].w};
+      const uint32_t gw[4] = {g[j].x, g[j].y, g[j].z, g[j].w};
+      const uint32_t uw[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+      uint32_t dg[4], du[4], mj = 0;
+      geglu_bwd8(dhw, gw, uw, ta, tf, dg, du, mj);
+      if (v0 + (int64_t)j * kNT < nvec) {
+        m = max(m, mj);
+        *reinterpret_cast<uint2*>(out + go[j]) =
+            quant8_bf16<FMT>(make_uint4(dg[0], dg[1], dg[2], dg[3]), scale);
+        *reinterpret_cast<uint2*>(out + go[j] + I) =
+            quant8_bf16<FMT>(make_uint4(du[0], du[1], du[2], du[3]), scale);
+      }
+    }
+  }
+  m = block_max_u32<kNT>(m);
+  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
 }  // namespace
 }  // namespace bf8
 
@@ -311,6 +368,17 @@ int bf8_geglu_bwd_delayed(const void* dH, const void* GU, int64_t M, int64_t I, 
   hipStream_t s = as_stream(stream);
   const uint16_t* dh = (const uint16_t*)dH;
   const uint16_t* gu = (const uint16_t*)GU;
+  if (!out_t) {
+    if (fmt == BF8_E4M3)
+      hipLaunchKernelGGL(geglu_bwd_delayed_rows_kernel<BF8_E4M3>, dim3((unsigned)nb), dim3(kNT), 0,
+                         s, dh, gu, M, I, state, len, pos, prev_partials, n_prev, meta_out, out,
+                         partials_out);
+    else
+      hipLaunchKernelGGL(geglu_bwd_delayed_rows_kernel<BF8_E5M2>, dim3((unsigned)nb), dim3(kNT), 0,
+                         s, dh, gu, M, I, state, len, pos, prev_partials, n_prev, meta_out, out,
+                         partials_out);
+    return launch_status("geglu_bwd_delayed_rows_kernel");
+  }
   if (fmt == BF8_E4M3)
     hipLaunchKernelGGL(geglu_bwd_delayed_kernel<BF8_E4M3>, dim3((unsigned)nb), dim3(kNT), 0, s,
                        dh, gu, M, I, state, len, pos, prev_partials, n_prev, meta_out, out, out_t,

@@ -150,11 +150,14 @@ def test_long_partial_lists(gpu, count):
     assert sc.state.cpu()[0].item() == amax
 
 
-@pytest.mark.parametrize("M,I", [(208, 384), (4096, 1024)])
-def test_geglu_bwd_delayed_fused_equals_two_pass(gpu, M, I):
-    """The fused gelu backward + delayed cast (one pass, fp8 dGU and its transpose) against
-    the two-pass form (bf16 dGU with producer partials, then the delayed cast), over
-    four steps of one scaler each: bytes, per-step meta and the history state identical."""
+@pytest.mark.parametrize("transpose", [True, False])
+@pytest.mark.parametrize("M,I", [(208, 384), (4096, 1024), (48, 192)])
+def test_geglu_bwd_delayed_fused_equals_two_pass(gpu, M, I, transpose):
+    """The fused gelu backward + delayed cast (one pass, fp8 dGU and, with ``transpose``, its
+    transpose; without it the rowwise streaming kernel, whose last pass is partial at these
+    shapes) against the two-pass form (bf16 dGU with producer partials, then the delayed
+    cast), over four steps of one scaler each: bytes, per-step meta and the history state
+    identical."""
     a = scaling.DelayedScaler(ops.E5M2, 16)
     b = scaling.DelayedScaler(ops.E5M2, 16)
     g = torch.Generator(device=gpu).manual_seed(M + I)
@@ -163,17 +166,20 @@ def test_geglu_bwd_delayed_fused_equals_two_pass(gpu, M, I):
         dH = (torch.randn(M, I, device=gpu, generator=g) * 1e-3 * (3 - step)).to(torch.bfloat16)
         count = ops.geglu_bwd_partials_count(M, I)
         dGU, _ = ops.geglu_bwd(dH, GU, partials=a.partials_for_producer(count, gpu))
-        qa = a.quantize(dGU, rowwise=True, transpose=True, producer_count=count)
+        qa = a.quantize(dGU, rowwise=True, transpose=transpose, producer_count=count)
         fcount = ops.geglu_bwd_delayed_partials_count(M, I)
         qb = b.produce(fcount, gpu, lambda st, L, pos, prev, parts: ops.geglu_bwd_delayed(
-            dH, GU, st, L, pos, prev, ops.E5M2, rowwise=True, transpose=True,
+            dH, GU, st, L, pos, prev, ops.E5M2, rowwise=True, transpose=transpose,
             partials_out=parts))
         torch.cuda.synchronize()
+        assert (qb.data_t is None) == (not transpose)
         parts = (torch.equal(qa.data.view(torch.uint8), qb.data.view(torch.uint8)),
-                 torch.equal(qa.data_t.view(torch.uint8), qb.data_t.view(torch.uint8)),
+                 not transpose or torch.equal(qa.data_t.view(torch.uint8),
+                                              qb.data_t.view(torch.uint8)),
                  torch.equal(qa.meta, qb.meta), torch.equal(a.state, b.state))
         same = all(parts)
-        print(f"[fused geglu bwd M={M} I={I} step {step}] identical: {same} {parts} "
+        print(f"[fused geglu bwd M={M} I={I} transpose={transpose} step {step}] identical: "
+              f"{same} {parts} "
               f"meta {qa.meta.tolist()} {qb.meta.tolist()}", flush=True)
         if not parts[0]:
             d = (qa.data.view(torch.uint8) != qb.data.view(torch.uint8)).nonzero()[:4].tolist()
