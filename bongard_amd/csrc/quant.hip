@@ -323,10 +323,11 @@ int64_t transpose_blocks(int64_t rows, int64_t cols) {
   return blocks < kMaxTransposeBlocks ? (blocks > 0 ? blocks : 1) : kMaxTransposeBlocks;
 }
 
-// Blocks of the row-major cast: up to kMaxCastBlocks; 1024 when it writes amax partials
+// Blocks of the row-major cast: up to kMaxCastBlocks; 512 when it writes amax partials
 // (a delayed-scaling cast, whose next step's blocks each fold them into the history, so
-// fewer partials and fewer folding blocks: c5 step 1915 -> 1877 us against 2048).
-constexpr int64_t kMaxPartialCastBlocks = 1024;
+// fewer partials and fewer folding blocks: c5 step 1915 -> 1877 us for 1024 against 2048,
+// and for 512 dY's e5m2 cast [8192, 2560] 15.6 -> 14.6 us, the step 1852 -> 1849 us).
+constexpr int64_t kMaxPartialCastBlocks = 512;
 static_assert(kMaxPartialCastBlocks <= kMaxInlinePartials, "consumers reduce them inline");
 int64_t row_cast_blocks(int64_t n, bool with_amax) {
   return grid_for_stream((n + 15) / 16, 2 * kNT, with_amax ? kMaxPartialCastBlocks : kMaxCastBlocks);

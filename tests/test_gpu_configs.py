@@ -234,7 +234,9 @@ def test_c5_delayed_training_steps_full_size(gpu):
 def test_c5_dgrad_wgrad_gemms_on_own_operands(gpu):
     """The backward GEMMs at c5 shapes (M=8192, K=2560, 2I=20480) with e5m2 gradients:
     dX = dGU8 . W8 (reduction over 2I) and dW = dGU8^T . X8 (reduction over the tokens),
-    on transposed copies written by the cast kernels; 1% of RMS on their own operands."""
+    on transposed copies written by the cast kernels; 1% of RMS on their own operands. The
+    training path's K-major GEMMs on the row copies (W8 and X8 as [K, rows], dGU8 as A^T
+    for dW) give the same fp32 sums bit for bit."""
     c = workloads.config5()
     x, wg, wu = c["x"], c["w_gate"], c["w_up"]
     M, K = x.shape
@@ -242,12 +244,19 @@ def test_c5_dgrad_wgrad_gemms_on_own_operands(gpu):
     g = torch.Generator().manual_seed(77)
     dgu = (torch.randn(M, 2 * I, generator=g) * 1e-4).to(torch.bfloat16)
     w_gu = torch.cat([wg, wu])
-    xq = ops.quantize(x.to(gpu), E4M3, rowwise=False, transpose=True)
-    wq = ops.quantize(w_gu.to(gpu), E4M3, rowwise=False, transpose=True)
+    xq = ops.quantize(x.to(gpu), E4M3, rowwise=True, transpose=True)
+    wq = ops.quantize(w_gu.to(gpu), E4M3, rowwise=True, transpose=True)
     gq = ops.quantize(dgu.to(gpu), E5M2, rowwise=True, transpose=True)
     dx = ops.gemm(gq.data, E5M2, gq.meta, wq.data_t, E4M3, wq.meta, out_dtype=torch.float32)
     dw = ops.gemm(gq.data_t, E5M2, gq.meta, xq.data_t, E4M3, xq.meta, out_dtype=torch.float32)
+    dx_k = ops.gemm_kmajor(gq.data, E5M2, gq.meta, wq.data, E4M3, wq.meta,
+                           out_dtype=torch.float32)
+    dw_k = ops.gemm_kmajor(gq.data, E5M2, gq.meta, xq.data, E4M3, xq.meta, a_kmajor=True,
+                           out_dtype=torch.float32)
     torch.cuda.synchronize()
+    assert torch.equal(dx_k, dx), "c5 dgrad: K-major GEMM differs from the transposed-copy GEMM"
+    assert torch.equal(dw_k, dw), "c5 wgrad: K-major GEMM differs from the transposed-copy GEMM"
+    del dx_k, dw_k
     assert_quantized_like_oracle(None, xq.meta, x, E4M3, "c5 X", data_t=xq.data_t)
     assert_quantized_like_oracle(None, wq.meta, w_gu, E4M3, "c5 W_gu", data_t=wq.data_t)
     assert_quantized_like_oracle(gq.data, gq.meta, dgu, E5M2, "c5 dGU", data_t=gq.data_t)

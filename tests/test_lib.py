@@ -55,7 +55,7 @@ def test_partials_counts():
     assert L.bf8_amax_partials(512 * 2560) >= 1
     # capped at the number of partials a consumer block reduces inline (8 per CU)
     assert L.bf8_amax_partials(1 << 30) == 1024
-    assert L.bf8_cast_amax_partials(1 << 15, 1 << 15, 0) == 1024
+    assert L.bf8_cast_amax_partials(1 << 15, 1 << 15, 0) == 512
     assert L.bf8_geglu_partials(4096, 10240) == 16 * 80
     assert L.bf8_gemm_workspace(4096, 2560, 10240) >= 0
 
