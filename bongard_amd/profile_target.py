@@ -17,7 +17,9 @@ gated GELU). ``c5``: the
 config-5 training step (the c2 MLP at M = 8192, forward and backward, delayed scaling with
 an amax history of 16). ``vs_hipblaslt``: this library's FP8 GEMM and hipBLASLt's (through
 ``torch._scaled_mm``) on the c2 / c4 / square shapes, each captured as a HIP graph of 20
-calls and timed from HIP events around its replay; prints one line per shape. ``c4``: the
+calls and timed from HIP events around its replay; prints one line per shape.
+``vs_hipblaslt_eager``: the same two libraries on 8192^3 and the c2 down shape, a few eager
+calls each (for per-dispatch PMC counters). ``c4``: the
 config-4 decoder-branch step at M = 512 on pre-quantized weights (current-scaling quantize
 of the branch input and the attention output, fused QKV with three segment scales, O,
 gate/up + gated GELU, H cast, down), captured as one HIP graph and replayed.
@@ -36,7 +38,8 @@ def main():
     p = argparse.ArgumentParser()
     p.add_argument("--iters", type=int, default=5)
     p.add_argument("--rows", type=int, default=4096)
-    p.add_argument("--case", choices=("c2", "square", "recipes", "c5", "vs_hipblaslt", "c4"),
+    p.add_argument("--case", choices=("c2", "square", "recipes", "c5", "vs_hipblaslt", "c4",
+                                      "vs_hipblaslt_eager"),
                    default="c2")
     args = p.parse_args()
     dev = torch.device("cuda:0")
@@ -55,6 +58,9 @@ def main():
         return
     if args.case == "c5":
         _c5(dev, args.iters)
+        return
+    if args.case == "vs_hipblaslt_eager":
+        _vs_hipblaslt_eager(dev, args.iters)
         return
     if args.case == "vs_hipblaslt":
         _vs_hipblaslt(dev, args.iters)
@@ -164,6 +170,24 @@ def _vs_hipblaslt(dev, iters):
         f = 2.0 * M * N * K
         print(f"{M}x{N}x{K}: hipBLASLt {t_lt * 1e6:8.2f} us {f / t_lt / 1e12:6.0f} TFLOP/s   "
               f"bf8_gemm {t_ours * 1e6:8.2f} us {f / t_ours / 1e12:6.0f} TFLOP/s", flush=True)
+
+
+def _vs_hipblaslt_eager(dev, iters):
+    """hipBLASLt (torch._scaled_mm) and bf8_gemm on 8192^3 and the c2 down shape, ``iters``
+    eager calls each (no graphs): a target for PMC counters per dispatch."""
+    meta = torch.tensor([1.0, 1.0, 1.0, 0.0], device=dev)
+    one = torch.tensor(1.0, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    for M, N, K in [(8192, 8192, 8192), (4096, 2560, 10240)]:
+        v = torch.randint(0, 0x70, (M, K), dtype=torch.int16, device=dev, generator=gen)
+        a = v.to(torch.uint8).view(torch.float8_e4m3fn)
+        v = torch.randint(0, 0x70, (N, K), dtype=torch.int16, device=dev, generator=gen)
+        b = v.to(torch.uint8).view(torch.float8_e4m3fn)
+        for _ in range(iters):
+            torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+            ops.gemm(a, ops.E4M3, meta, b, ops.E4M3, meta)
+    torch.cuda.synchronize()
+    print(f"profile_target done: {iters} x hipBLASLt and bf8_gemm on two shapes", flush=True)
 
 
 def _c5(dev, iters):

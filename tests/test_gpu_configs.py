@@ -11,8 +11,9 @@ inputs (bongard_amd.workloads) at the shapes bench.py times:
   c4  the decoder-branch GEMMs at M=512 on pre-quantized weights: QKV, O, gate/up + GEGLU,
       down.
   c5  three delayed-scaling training steps of the MLP at M=8192 (the bench step) against the
-      oracle chain driven by a DelayedQuantizer, and the dgrad / wgrad GEMMs at c5 shapes on
-      their own operands.
+      oracle chain driven by a DelayedQuantizer; twenty steps with rescaled inputs, so the
+      amax histories wrap, checked on the input roles' scales; and the dgrad / wgrad GEMMs at
+      c5 shapes on their own operands.
 
 Bars: see tests/parity_util.py. Large GEMM outputs are compared on a sample of rows.
 """
@@ -229,6 +230,52 @@ def test_c5_delayed_training_steps_full_size(gpu):
             mx = err.abs().max().item() / rms(want)
             print(f"[c5 step {step}] {name}: RMS(err)/RMS={rel:.2e} max/RMS={mx:.2e}", flush=True)
             assert rel <= 0.005, name
+
+
+def test_c5_delayed_history_wraps_full_size(gpu):
+    """Twenty c5 training steps (the 16-slot amax histories wrap) at full size, the inputs
+    rescaled every step: x with a spike at step 1 that leaves the window at step 18 and a
+    rising trend after it, W_gate||W_up shrinking (the window's maximum is its oldest
+    entry), dY cycling over five magnitudes, W_down fixed. Each step's delayed scale of the
+    four input roles is bit-exact against the oracle's closed-form DelayedScaling fed with
+    the same bf16 tensors' amaxes (the roles' scales need no GEMM of the oracle)."""
+    c = workloads.config5()
+    x, dy, wg, wu, wd = c["x"], c["dy"], c["w_gate"], c["w_up"], c["w_down"]
+    I = wg.shape[0]
+    L = c["history"]
+    steps = L + 4
+    sc = (scaling.LinearScaling(L), scaling.LinearScaling(L))
+    refs = {r: orc.DelayedScaling(L, f) for r, f in
+            (("x", orc.E4M3), ("w_gu", orc.E4M3), ("w_down", orc.E4M3), ("dy", orc.E5M2))}
+    w_gu0 = torch.cat([wg, wu])
+    w_d = wd.to(gpu).requires_grad_(True)
+
+    def scaled(t, f):
+        return (t.float() * f).to(torch.bfloat16)
+
+    for step in range(steps):
+        fx = 16.0 if step == 1 else 1.0 + step / 32
+        xs = scaled(x, fx)
+        ws = scaled(w_gu0, 1.0 - step / 64)
+        dys = scaled(dy, 2.0 ** -(step % 5))
+        want = {}
+        for role, t in (("x", xs), ("w_gu", ws), ("w_down", wd), ("dy", dys)):
+            want[role] = float(refs[role].begin()[0])
+            refs[role].end(float(orc.amax(t)))
+        xg = xs.to(gpu).requires_grad_(True)
+        w_gu = ws.to(gpu).requires_grad_(True)
+        w_d.grad = None
+        y = linear.Fp8GegluMlpFunction.apply(xg, w_gu, w_d, None, None, I, False, sc)
+        y.backward(dys.to(gpu))
+        torch.cuda.synchronize()
+        gs, dsc = sc
+        got = {"x": gs.input, "w_gu": gs.weight, "w_down": dsc.weight, "dy": dsc.grad_output}
+        for role, st in got.items():
+            g = st.state.cpu()[L + 1].item()
+            assert g == want[role], f"step {step} {role}: scale {g} != {want[role]}"
+        assert torch.isfinite(xg.grad).all() and torch.isfinite(w_gu.grad).all()
+    print(f"[c5 history wrap] {steps} steps, scales x {want['x']}, W_gu {want['w_gu']}, "
+          f"dY {want['dy']}", flush=True)
 
 
 def test_c5_dgrad_wgrad_gemms_on_own_operands(gpu):
