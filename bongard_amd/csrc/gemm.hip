@@ -284,6 +284,93 @@ Plan choose_plan(int64_t M, int64_t N, int64_t K, bool geglu, size_t ws_avail, b
   return best;
 }
 
+// ---- K-major operands on small shapes ------------------------------------------------
+// The K-major GEMM runs on the eight-wave 256x256 tiles only, which leave most CUs idle when
+// the output is small (M = 512, N = 2560, K = 2048: 20 tiles; measured 30 us against 12 us
+// for the row-major plan on a transposed copy of B). For a call with only B K-major whose
+// plan the cost model prices well above the row-major plan plus a byte transpose of B, the
+// entry point transposes B^T [K, N] into its workspace and runs the row-major plan. (The
+// wgrad form, A and B K-major, measured level or faster on the same shapes, so it always
+// runs K-major.)
+constexpr double kTransposeBytesPerNs = 2.5e3;  // a small transpose: ~2.5 TB/s read + write
+constexpr double kTransposeLaunchNs = 4000.0;
+constexpr double kKmajorFallbackGain = 0.8;  // transpose only when that is 20% cheaper
+
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct KmajorChoice {
+  Plan plan;
+  bool transpose_b = false;
+  size_t b_bytes = 0;  // the transposed B's share of the workspace (the plan's own follows)
+};
+
+KmajorChoice choose_kmajor(int64_t M, int64_t N, int64_t K, bool a_kmajor, size_t ws_avail) {
+  KmajorChoice c;
+  c.plan = choose_plan(M, N, K, false, ws_avail, false, true);
+  int otile, osplits;
+  if (a_kmajor || env_override(otile, osplits)) return c;  // a forced plan stays as asked
+  const size_t bb = align256((size_t)N * K);
+  if (ws_avail < bb) return c;
+  const int64_t ksteps = std::max<int64_t>(cdiv(K, kStepBytes), 1);
+  const Plan pr = choose_plan(M, N, K, false, ws_avail - bb);
+  // costed as the planner costed them: the two-K-group and extra-B-slot tiles replace
+  // their plain twins after the choice, on the twins' costs
+  auto costed = [&](Plan q) {
+    if (q.tile == TILE_128x64k2) q.tile = TILE_128x64;
+    if (q.tile == TILE_64x128k2) q.tile = TILE_64x128;
+    if (q.tile == TILE_256x256w8x) q.tile = TILE_256x256w8;
+    return plan_cost(q, M, N, false, ksteps);
+  };
+  const double ck = costed(c.plan);
+  const double cr = costed(pr) + 2.0 * (double)N * K / kTransposeBytesPerNs + kTransposeLaunchNs;
+  if (const char* d = std::getenv("BONGARD_FP8_GEMM_DEBUG"); d && d[0] == '1')
+    std::fprintf(stderr, "bf8 kmajor M=%lld N=%lld K=%lld: K-major %.0f ns, transposed B %.0f ns\n",
+                 (long long)M, (long long)N, (long long)K, ck, cr);
+  if (cr < kKmajorFallbackGain * ck) {
+    c.plan = pr;
+    c.transpose_b = true;
+    c.b_bytes = bb;
+  }
+  return c;
+}
+
+// B^T [rows = K, cols = N] (row stride ld) -> B [N, K] (row stride K): one 64 x 64 byte tile
+// per wave, staged in the wave's own LDS region and read back transposed; rows and cols are
+// multiples of 16 (whole 16-byte segments). No block barrier, so a wave past the last tile
+// may leave at once.
+constexpr int kTransposeWaves = 4;
+__global__ __launch_bounds__(kTransposeWaves * 64) void transpose_u8_kernel(
+    const uint8_t* __restrict__ src, int64_t rows, int64_t cols, int64_t ld,
+    uint8_t* __restrict__ dst) {
+  __shared__ uint32_t stage[kTransposeWaves][kWaveTileDwords];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t tiles_c = (cols + 63) / 64;
+  const int64_t t = (int64_t)blockIdx.x * kTransposeWaves + wid;
+  if (t >= tiles_c * ((rows + 63) / 64)) return;
+  const int64_t r0 = (t / tiles_c) * 64, c0 = (t % tiles_c) * 64;
+  uint32_t* lds = stage[wid];
+  const int ch = lane & 3;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int row = 16 * k + (lane >> 2);
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (r0 + row < rows && c0 + 16 * ch < cols)
+      v = *reinterpret_cast<const uint4*>(src + (r0 + row) * ld + c0 + 16 * ch);
+    lds[row * kWaveTilePitch + 4 * ch] = v.x;
+    lds[row * kWaveTilePitch + 4 * ch + 1] = v.y;
+    lds[row * kWaveTilePitch + 4 * ch + 2] = v.z;
+    lds[row * kWaveTilePitch + 4 * ch + 3] = v.w;
+  }
+  uint4 tq[4];
+  wave_transpose64_staged(lds, lane, tq);
+  const int64_t orow = c0 + 4 * (lane & 15), ocol = r0 + 16 * (lane >> 4);
+  if (ocol < rows) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (orow + c < cols) *reinterpret_cast<uint4*>(dst + (orow + c) * rows + ocol) = tq[c];
+  }
+}
+
 int launch_tile(const Plan& pl, const GemmParams& p, int epi, int out_dtype, int fa, int fb,
                 hipStream_t s, bool mx) {
   switch (pl.tile) {
@@ -567,7 +654,10 @@ size_t bf8_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K) {
 
 size_t bf8_gemm_kmajor_workspace(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return choose_plan(M, N, K, false, (size_t)-1, false, true).ws_bytes;
+  // the larger of the two layouts' needs (the B-only call may run on a transposed B)
+  const KmajorChoice b_only = choose_kmajor(M, N, K, false, (size_t)-1);
+  const size_t both = choose_kmajor(M, N, K, true, (size_t)-1).plan.ws_bytes;
+  return std::max(both, b_only.b_bytes + b_only.plan.ws_bytes);
 }
 
 int bf8_gemm_kmajor(const uint8_t* A, int fmt_a, int64_t lda, int a_kmajor, const uint8_t* B,
@@ -605,8 +695,21 @@ int bf8_gemm_kmajor(const uint8_t* A, int fmt_a, int64_t lda, int a_kmajor, cons
   for (int s = 0; s < 4; ++s) p.seg_end[s] = (int)N;
   p.C = C; p.ldc = ldc;
   p.kmajor = a_kmajor ? 3 : 2;
-  const Plan pl = choose_plan(M, N, K, false, ws ? ws_bytes : 0, false, true);
-  return launch_plan(pl, p, EPI_LINEAR, out_dtype, fmt_a, fmt_b, ws, as_stream(stream));
+  hipStream_t s = as_stream(stream);
+  const KmajorChoice ch = choose_kmajor(M, N, K, a_kmajor != 0, ws ? ws_bytes : 0);
+  if (!ch.transpose_b) return launch_plan(ch.plan, p, EPI_LINEAR, out_dtype, fmt_a, fmt_b, ws, s);
+  // B^T [K, N] -> B [N, K] in the workspace, then the row-major plan on it
+  uint8_t* bt = static_cast<uint8_t*>(ws);
+  const int64_t tiles = ((K + 63) / 64) * ((N + 63) / 64);
+  hipLaunchKernelGGL(transpose_u8_kernel, dim3((unsigned)((tiles + kTransposeWaves - 1) / kTransposeWaves)),
+                     dim3(kTransposeWaves * 64), 0, s, B, K, N, ldb, bt);
+  const int rc = launch_status("transpose_u8_kernel");
+  if (rc != BF8_OK) return rc;
+  p.B = bt;
+  p.ldb = K;
+  p.kmajor = 0;
+  return launch_plan(ch.plan, p, EPI_LINEAR, out_dtype, fmt_a, fmt_b,
+                     ch.plan.ws_bytes ? bt + ch.b_bytes : nullptr, s);
 }
 
 int bf8_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,

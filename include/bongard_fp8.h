@@ -153,7 +153,9 @@ int bf8_gemm(const uint8_t* A, int fmt_a, int64_t lda, const uint8_t* B, int fmt
  * A^T [K, M] (lda >= M, M % 16 == 0), else A [M, K] as in bf8_gemm. e5m2 A x e4m3 B,
  * one scale each, no bias; ws: bf8_gemm_kmajor_workspace(M, N, K) bytes. The products
  * and their fp32 sums are those of bf8_gemm on the transposed copies, bit for bit (same K
- * order). Replaces the dgrad (dX = dY . W) and wgrad (dW = dY^T . X) GEMMs of torchao's
+ * order). On small outputs, where the K-major tiles would leave most CUs idle, a call with
+ * a_kmajor == 0 may transpose B into ws and run bf8_gemm's plan on it (the workspace size
+ * covers that; with a smaller ws the call stays K-major). Replaces the dgrad (dX = dY . W) and wgrad (dW = dY^T . X) GEMMs of torchao's
  * Float8Linear and TE's Linear backward (bongard/float8_training.py:22;
  * bongard/te_linear.py:73-74), which transposes their operands' fp8 copies instead. */
 size_t bf8_gemm_kmajor_workspace(int64_t M, int64_t N, int64_t K);

@@ -15,7 +15,7 @@ by the quantize tests.
 import pytest
 import torch
 
-from bongard_amd import ops, workloads
+from bongard_amd import _lib, ops, workloads
 from oracle import fp8_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -561,3 +561,24 @@ def test_gemm_kmajor_equals_transposed_copies(gpu, monkeypatch, plan, a_kmajor, 
                            want.view(torch.int16 if dt == torch.bfloat16 else torch.int32))
         print(f"[kmajor {plan} a={a_kmajor} {M}x{N}x{K} {dt}] identical: {same}", flush=True)
         assert same
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 2560, 2048), (1024, 2560, 2560), (304, 320, 1040),
+                                   (512, 4096, 2560)])
+def test_gemm_kmajor_small_output_runs_on_transposed_b(gpu, M, N, K):
+    """Shapes whose K-major 256x256 plan would leave most CUs idle: gemm_kmajor (B given as
+    B^T [K, N]) transposes B into its workspace and runs the row-major plan, so its bf16 and
+    fp32 outputs equal gemm on the quantizer's transposed copy of B bit for bit."""
+    assert _lib.lib().bf8_gemm_kmajor_workspace(M, N, K) >= N * K
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    a = (torch.randn(M, K, generator=g) * 1e-3).to(torch.bfloat16).to(gpu)
+    bt = (torch.randn(K, N, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    aq = ops.quantize(a, ops.E5M2)
+    bq = ops.quantize(bt, ops.E4M3, rowwise=True, transpose=True)   # data [K, N], data_t [N, K]
+    for dt in (torch.bfloat16, torch.float32):
+        got = ops.gemm_kmajor(aq.data, ops.E5M2, aq.meta, bq.data, ops.E4M3, bq.meta,
+                              out_dtype=dt)
+        want = ops.gemm(aq.data, ops.E5M2, aq.meta, bq.data_t, ops.E4M3, bq.meta, out_dtype=dt)
+        torch.cuda.synchronize()
+        iv = torch.int16 if dt == torch.bfloat16 else torch.int32
+        assert torch.equal(got.view(iv), want.view(iv)), f"{M}x{N}x{K} {dt}"

@@ -161,3 +161,19 @@ def test_quantizing_geglu_and_scale_fold_reject_bad_arguments():
     assert rc == 1 and b"outside" in L.bf8_last_error()
     rc = L.bf8_delayed_scale_fold(ptr, 16, 0, null, 5, 0, null, null)
     assert rc == 1 and b"previous partials" in L.bf8_last_error()
+
+
+def test_kmajor_workspace_covers_transposed_b(monkeypatch):
+    """A K-major GEMM whose 256x256 plan would leave most CUs idle (a small output) may run
+    on B transposed into its workspace: the workspace query then covers N x K bytes plus
+    the row-major plan's own; large shapes keep the K-major plan (c5's GEMMs: same
+    workspace as bf8_gemm, which plans them alike), and a forced tile keeps it too."""
+    L = _lib.lib()
+    monkeypatch.delenv("BONGARD_FP8_GEMM_TILE", raising=False)
+    for M, N, K in [(512, 2560, 2048), (1024, 2560, 2560), (304, 320, 1040)]:
+        assert L.bf8_gemm_kmajor_workspace(M, N, K) >= N * K
+    for M, N, K in [(8192, 2560, 20480), (20480, 2560, 8192), (8192, 10240, 2560),
+                    (2560, 10240, 8192)]:
+        assert L.bf8_gemm_kmajor_workspace(M, N, K) == L.bf8_gemm_workspace(M, N, K)
+    monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256w8")
+    assert L.bf8_gemm_kmajor_workspace(512, 2560, 2048) == 0
