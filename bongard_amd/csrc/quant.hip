@@ -112,12 +112,23 @@ __global__ __launch_bounds__(kNT) void amax_partials_kernel(const uint16_t* __re
   amax_partials_body(x, n, partials, blockIdx.x, gridDim.x);
 }
 
-__global__ __launch_bounds__(kNT) void scale_from_partials_kernel(
+// One block of 1024 threads, four independent loads per thread and pass: a producer with
+// thousands of partials (the gated-GELU GEMM's one per tile: 5,840 at M = 18494) is
+// reduced in a few memory round trips (c3: 8.3 -> 5.0 us per call, against one block of
+// 256 threads with one load each per pass).
+constexpr int kScaleNT = 1024;
+__global__ __launch_bounds__(kScaleNT) void scale_from_partials_kernel(
     const uint32_t* __restrict__ partials, int64_t np, float fp8_max, int pow2,
     float* __restrict__ meta) {
   uint32_t m = 0;
-  for (int64_t i = threadIdx.x; i < np; i += kNT) m = max(m, partials[i]);
-  m = block_max_u32<kNT>(m);
+  for (int64_t i = threadIdx.x; i < np; i += 4 * kScaleNT) {
+    uint32_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = i + j * kScaleNT < np ? partials[i + j * kScaleNT] : 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = max(m, v[j]);
+  }
+  m = block_max_u32<kScaleNT>(m);
   if (threadIdx.x == 0) write_meta_from_amax(m, fp8_max, meta, pow2 != 0);
 }
 
@@ -415,7 +426,7 @@ int launch_cast(const void* x, int64_t rows, int64_t cols, ScaleSrc src, int fmt
   if (!src.scale && !src.state && src.np > kMaxInlinePartials) {
     // current scaling from many partials: meta first, then a cast with its scale
     float* meta = src.meta_out;
-    hipLaunchKernelGGL(scale_from_partials_kernel, dim3(1), dim3(kNT), 0, s, src.partials,
+    hipLaunchKernelGGL(scale_from_partials_kernel, dim3(1), dim3(kScaleNT), 0, s, src.partials,
                        src.np, fp8_max_host(fmt), src.pow2, meta);
     const int rc = launch_status("scale_from_partials_kernel");
     if (rc != BF8_OK) return rc;
@@ -647,7 +658,7 @@ int bf8_scale_from_partials(const uint32_t* partials, int64_t n_partials, int fm
   BF8_CHECK(fmt == BF8_E4M3 || fmt == BF8_E5M2, "bf8_scale_from_partials: bad fmt %d", fmt);
   BF8_CHECK(partials && meta, "bf8_scale_from_partials: NULL pointer");
   BF8_CHECK(n_partials >= 1, "bf8_scale_from_partials: n_partials < 1");
-  hipLaunchKernelGGL(scale_from_partials_kernel, dim3(1), dim3(kNT), 0, as_stream(stream),
+  hipLaunchKernelGGL(scale_from_partials_kernel, dim3(1), dim3(kScaleNT), 0, as_stream(stream),
                      partials, n_partials, fp8_max_host(fmt), pow2, meta);
   return launch_status("scale_from_partials_kernel");
 }
