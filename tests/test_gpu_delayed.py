@@ -27,6 +27,8 @@ def _inputs(seed, steps, shape):
             x[3, 5] = float("inf")      # a non-finite amax: scales hold for `length` steps
         if t == 9:
             x[0, 0] = 3000.0            # an outlier that saturates the next cast
+        if t == 11:
+            x[1, 1] = float("nan")      # a NaN amax: the window is not finite, scales hold
         out.append(x.to(torch.bfloat16))
     return out
 
@@ -51,7 +53,8 @@ def test_delayed_cast_sequence(gpu, transpose, fmt):
             assert torch.equal(q.data_t.view(torch.uint8).cpu(), want.t().contiguous())
         # the device history holds the amaxes of steps < t (the oracle's before end())
         hist = sc.state[:length].cpu().numpy()
-        assert np.array_equal(hist, ref.history), f"step {t}: history {hist} != {ref.history}"
+        assert np.array_equal(hist, ref.history, equal_nan=True), \
+            f"step {t}: history {hist} != {ref.history}"
         ref.end(float(orc.amax(x)))
 
 
