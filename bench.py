@@ -40,7 +40,7 @@ and two entries beyond the BASELINE configurations:
               per-row + per-column quantization of [8192, 2560]
   c2_mxfp8    the c2 MLP forward under TE's 'mxfp8' recipe (block-scaled MFMA)
   c2_nvfp4    the c2 MLP forward under TE's 'nvfp4' recipe (bf16 MFMA on exactly
-              dequantized NVFP4 operands)
+              dequantized NVFP4 operands, the gated GELU in the gate/up epilogue)
   state_kv    the decoder's state-bank K/V projection of the c3 packed state
 
 ``cpu_baseline`` times the CPU oracle (torch CPU: amax, clamp, .to(float8), fp32 matmul,
@@ -661,8 +661,10 @@ def _bench_c2_mx(torch, ops, workloads, dev, steps=30):
 def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
     """The c2 MLP forward under TE's 'nvfp4' recipe as TEMLP runs it: X, [W_gate; W_up] and
     W_down quantized to NVFP4 (e2m1, 16-blocks, e4m3 block scales, per-tensor scale), each
-    GEMM on the bf16 MFMA over the exactly dequantized operands, the gated GELU as an
-    elementwise kernel on the stored [gate | up], H quantized to NVFP4 for the down GEMM."""
+    GEMM on the bf16 MFMA over the exactly dequantized operands, the gated GELU in the
+    gate/up GEMM's epilogue (no [gate | up] stored without grad), H quantized to NVFP4 for
+    the down GEMM. The unfused step (the linear GEMM, then the elementwise gated GELU over
+    the stored [gate | up], bit-identical H) is timed beside it."""
     c = workloads.config2()
     x = c["x"].to(dev)
     w_gu = torch.cat([c["w_gate"], c["w_up"]]).to(dev)
@@ -675,6 +677,13 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
 
     def step():
         xq, gq, dq = q(x), q(w_gu), q(w_d)
+        H, _, _ = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, gq.data, gq.scales,
+                                       gq.meta, I)
+        hq = q(H)
+        return ops.gemm_nvfp4(hq.data, hq.scales, hq.meta, dq.data, dq.scales, dq.meta)
+
+    def step_unfused():
+        xq, gq, dq = q(x), q(w_gu), q(w_d)
         GU = ops.gemm_nvfp4(xq.data, xq.scales, xq.meta, gq.data, gq.scales, gq.meta)
         H, _ = ops.geglu(GU)
         hq = q(H)
@@ -682,7 +691,9 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
 
     for _ in range(5):
         step()
+        step_unfused()
     s = _timed(torch, step, steps, 3)
+    su = _timed(torch, step_unfused, steps, 3)
     xq, gq, dq = q(x), q(w_gu), q(w_d)
     xb, gb = ops.dequant_nvfp4(xq.data, xq.scales), ops.dequant_nvfp4(gq.data, gq.scales)
     GU = ops.gemm_bf16(xb, gb, xq.meta[2:3], gq.meta[2:3])
@@ -690,6 +701,8 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
     hq = q(H)
     hb, db = ops.dequant_nvfp4(hq.data, hq.scales), ops.dequant_nvfp4(dq.data, dq.scales)
     gu_s = _ev_time(torch, lambda: ops.gemm_bf16(xb, gb, xq.meta[2:3], gq.meta[2:3]), steps)
+    gg_s = _ev_time(torch, lambda: ops.gemm_geglu_bf16(xb, gb, xq.meta[2:3], gq.meta[2:3], I),
+                    steps)
     d_s = _ev_time(torch, lambda: ops.gemm_bf16(hb, db, hq.meta[2:3], dq.meta[2:3]), steps)
     qh_s = _ev_time(torch, lambda: q(H), steps)
     dqh_s = _ev_time(torch, lambda: ops.dequant_nvfp4(hq.data, hq.scales), steps)
@@ -697,8 +710,13 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
     flop = 2.0 * M * (2 * I * K + K * I)
     nh = M * I
     return {"workload": f"c2 MLP forward [{M},{K}] x [2*{I},{K}] -> [{M},{I}] x [{K},{I}], NVFP4 "
-                        "(bf16 MFMA on exactly dequantized operands)",
+                        "(bf16 MFMA on exactly dequantized operands, gated GELU in the gate/up "
+                        "epilogue)",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
+            "us_per_step_unfused_geglu": round(su * 1e6, 2),
+            "gemm_gate_up_geglu_bf16_us": round(gg_s * 1e6, 2),
+            "gemm_gate_up_geglu_frac_of_bf16_peak": round(2.0 * M * 2 * I * K / gg_s / 1e12
+                                                          / BF16_PEAK_TFLOPS, 4),
             "gemm_gate_up_bf16_us": round(gu_s * 1e6, 2),
             "gemm_gate_up_bf16_tflops": round(2.0 * M * 2 * I * K / gu_s / 1e12, 1),
             "gemm_gate_up_frac_of_bf16_peak": round(2.0 * M * 2 * I * K / gu_s / 1e12

@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -80,6 +80,9 @@ SIGNATURES = {
     "bf8_gemm_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
                               c_void_p, c_void_p, c_void_p, c_int, c_int64, c_void_p, c_size_t,
                               c_void_p]),
+    "bf8_gemm_geglu_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64,
+                                    c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+                                    c_void_p, c_void_p]),
     "bf8_gemm_mx": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                             c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int,
                             c_int64, c_void_p, c_size_t, c_void_p]),

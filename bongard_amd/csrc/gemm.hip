@@ -744,11 +744,12 @@ int64_t bf8_geglu_partials(int64_t M, int64_t I) {
 }
 
 // The gate/up GEMM + gated GELU; h_scale set: H quantized in the epilogue (H8, H8t).
+// K, ldx and ldw in bytes; fmt: BF8_E4M3 operands, or kFmtBf16 (two bytes per element)
 static int geglu_entry(const char* who, const uint8_t* X, int64_t ldx, const uint8_t* W,
                        int64_t ldw, int64_t M, int64_t I, int64_t K, const float* x_scale_inv,
                        const float* w_scale_inv, int w_scale_stride, void* H, int64_t ldh,
                        const float* h_scale, uint8_t* H8, uint8_t* H8t, void* GU,
-                       uint32_t* h_partials, void* stream) {
+                       uint32_t* h_partials, void* stream, int fmt = BF8_E4M3) {
   BF8_CHECK(M >= 1 && I >= 1 && K >= 16, "%s: bad shape", who);
   BF8_CHECK(I % 128 == 0, "%s: I must be a multiple of 128 (got %lld)", who, (long long)I);
   BF8_CHECK(K % 16 == 0 && ldx % 16 == 0 && ldw % 16 == 0 && ldx >= K && ldw >= K,
@@ -776,8 +777,7 @@ static int geglu_entry(const char* who, const uint8_t* X, int64_t ldx, const uin
   p.C = H; p.ldc = ldh; p.GU = (uint16_t*)GU; p.partials = h_partials;
   p.h8_scale = h_scale; p.h8 = H8; p.h8t = H8t;
   Plan pl = choose_plan(M, 2 * I, K, true, 0);
-  return launch_plan(pl, p, EPI_GEGLU, BF8_OUT_BF16, BF8_E4M3, BF8_E4M3, nullptr,
-                     as_stream(stream));
+  return launch_plan(pl, p, EPI_GEGLU, BF8_OUT_BF16, fmt, fmt, nullptr, as_stream(stream));
 }
 
 int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw, int64_t M,
@@ -786,6 +786,17 @@ int bf8_gemm_geglu(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw,
                    void* stream) {
   return geglu_entry("bf8_gemm_geglu", X, ldx, W, ldw, M, I, K, x_scale_inv, w_scale_inv,
                      w_scale_stride, H, ldh, nullptr, nullptr, nullptr, GU, h_partials, stream);
+}
+
+int bf8_gemm_geglu_bf16(const void* X, int64_t ldx, const void* W, int64_t ldw, int64_t M,
+                        int64_t I, int64_t K, const float* x_scale, const float* w_scale,
+                        void* H, int64_t ldh, void* GU, uint32_t* h_partials, void* stream) {
+  BF8_CHECK(K >= 8 && K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0,
+            "bf8_gemm_geglu_bf16: need K, ldx, ldw multiples of 8 (K=%lld ldx=%lld ldw=%lld)",
+            (long long)K, (long long)ldx, (long long)ldw);
+  return geglu_entry("bf8_gemm_geglu_bf16", (const uint8_t*)X, 2 * ldx, (const uint8_t*)W,
+                     2 * ldw, M, I, 2 * K, x_scale, w_scale, 0, H, ldh, nullptr, nullptr, nullptr,
+                     GU, h_partials, stream, kFmtBf16);
 }
 
 int bf8_gemm_geglu_quant(const uint8_t* X, int64_t ldx, const uint8_t* W, int64_t ldw,

@@ -1219,6 +1219,12 @@ int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int
         }
       }
       using TG = typename FitTile<T, EPI_GEGLU, false>::type;
+      if (fmt_a == kFmtBf16 && fmt_b == kFmtBf16) {
+        // bf16 operands (NVFP4's exactly dequantized ones): the same epilogue on the sums
+        hipLaunchKernelGGL((gemm_kernel<TG, kFmtBf16, kFmtBf16, EPI_GEGLU, BF8_OUT_BF16>), grid,
+                           block, 0, stream, p);
+        return launch_status("gemm_kernel(geglu, bf16)");
+      }
       hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16>), grid, block, 0, stream, p);
       return launch_status("gemm_kernel(geglu)");
     } else if constexpr (T::WN == 1 && T::BN % 16 == 0 && T::BN % 64 != 0) {
@@ -1229,6 +1235,11 @@ int launch_gemm_tile(const GemmParams& p, int epi, int out_dtype, int fmt_a, int
         return BF8_EINVAL;
       }
       using TG = typename FitTile<T, EPI_GEGLU, false>::type;
+      if (fmt_a == kFmtBf16 && fmt_b == kFmtBf16) {
+        hipLaunchKernelGGL((gemm_kernel<TG, kFmtBf16, kFmtBf16, EPI_GEGLU, BF8_OUT_BF16>), grid,
+                           block, 0, stream, p);
+        return launch_status("gemm_kernel(geglu, bf16)");
+      }
       hipLaunchKernelGGL((gemm_kernel<TG, 0, 0, EPI_GEGLU, BF8_OUT_BF16>), grid, block, 0, stream, p);
       return launch_status("gemm_kernel(geglu)");
     } else {

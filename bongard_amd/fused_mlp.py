@@ -184,9 +184,8 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
 
 
     def _nvfp4_forward(self, x, flat, length, first):
-        """'nvfp4': the fused norm, fc1 as an NVFP4 GEMM, the bf16 gated GELU, fc2 as an
-        NVFP4 GEMM (no GEMM epilogue takes the activation: the operands are dequantized
-        to bf16 for the MFMA)."""
+        """'nvfp4': the fused norm, fc1 as an NVFP4 GEMM (operands dequantized exactly to
+        bf16 for the MFMA) with the gated GELU in its epilogue, fc2 as an NVFP4 GEMM."""
         if first:
             self._fp8_weights = (_linear.quantize_weight_nvfp4(self.fc1_weight),
                                  _linear.quantize_weight_nvfp4(self.fc2_weight))
@@ -199,8 +198,8 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
             normed = _FusedRMSNorm.apply(flat, self.layer_norm_weight, self.eps, parts)
         else:
             normed = _rms_norm(flat, self.layer_norm_weight, self.eps)
-        gu = _linear.Fp8LinearNvfp4Function.apply(normed, self.fc1_weight, gu_q)
-        h = _linear.GegluFunction.apply(gu)
+        h = _linear.GegluGateUpNvfp4Function.apply(normed, self.fc1_weight, gu_q,
+                                                    self.intermediate_size)
         out = _linear.Fp8LinearNvfp4Function.apply(h, self.fc2_weight, down_q)
         return out[:length].reshape_as(x)
 

@@ -298,6 +298,48 @@ class GegluFunction(torch.autograd.Function):
         return dGU
 
 
+class GegluGateUpNvfp4Function(_Fp8Function):
+    """H = geglu(X @ [W_gate; W_up]^T) under the NVFP4 recipe, the gated GELU in the
+    gate/up GEMM's epilogue: the NVFP4 operands dequantized exactly to bf16, the bf16
+    MFMA, g and u rounded to bf16 from the fp32 sums times the two S_dec, H = bf16(bf16(
+    gelu_tanh(g)) * u) (bf8_gemm_geglu_bf16). Equals Fp8LinearNvfp4Function followed by
+    GegluFunction bit for bit where that GEMM runs unsplit (the forward and, from the same
+    GU, the backward), without the [M, 2I] pre-activations' round trip when no gradient
+    is needed. x: bf16 [M, K]; w_gu [2I, K].
+
+    Reference: TEMLP's gate_up projection and F.gelu(gate, approximate='tanh') * up
+    (bongard/te_linear.py:98-103) and te.LayerNormMLP's fc1 + geglu (bongard/fused_mlp.py:
+    25-30) under the 'nvfp4' recipe (bongard/te_linear.py:17,38).
+    """
+
+    @staticmethod
+    def forward(ctx, x, w_gu, wq, intermediate):
+        need_dx, need_dw = _forward_needs(ctx, 2)
+        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw)
+        if wq is None:
+            wq = quantize_weight_nvfp4(w_gu, transpose=need_dx)
+        train = need_dx or need_dw
+        H, GU, _ = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, wq.data, wq.scales,
+                                        wq.meta, intermediate, keep_gu=train)
+        ctx.save_for_backward(GU, xq.data_t, xq.scales_t, xq.meta,
+                              wq.data_t if need_dx else None,
+                              wq.scales_t if need_dx else None, wq.meta)
+        return H
+
+    @staticmethod
+    def backward(ctx, dH):
+        GU, x4t, xst, x_meta, w4t, wst, w_meta = ctx.saved_tensors
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dGU, _ = ops.geglu_bwd(dH.contiguous(), GU)
+        dq = ops.quantize_nvfp4(dGU, rowwise=need_dx, colwise=need_dw)
+        dx = dw = None
+        if need_dx:
+            dx = ops.gemm_nvfp4(dq.data, dq.scales, dq.meta, w4t, wst, w_meta)
+        if need_dw:
+            dw = ops.gemm_nvfp4(dq.data_t, dq.scales_t, dq.meta, x4t, xst, x_meta)
+        return dx, dw, None, None
+
+
 def quantize_weight_mx(weight, *, transpose=True):
     """MXFP8 copy of a weight [N, K]: blocks along K (forward), and with ``transpose`` the
     [K, N] copy with blocks along N (the input-gradient GEMM's operand)."""

@@ -1045,6 +1045,42 @@ def gemm_bf16(a, b, a_sinv, b_sinv, *, out_dtype=torch.bfloat16):
     return out
 
 
+def gemm_geglu_bf16(a, b, a_sinv, b_sinv, intermediate, *, keep_gu=False, partials=None):
+    """:func:`gemm_geglu` on bf16 operands a [M, K], b [2I, K] (gate rows then up rows) with
+    device fp32 scalars a_sinv, b_sinv applied to the sums (bf8_gemm_geglu_bf16). Returns
+    ``(H bf16 [M, I], GU bf16 [M, 2I] or None, h_partials int32)``."""
+    _require_gpu(a, b, a_sinv, b_sinv)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise TypeError("gemm_geglu_bf16: a and b must be bfloat16")
+    if a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("gemm_geglu_bf16: a and b must be row-major")
+    M, K = a.shape
+    I = int(intermediate)
+    if tuple(b.shape) != (2 * I, K):
+        raise ValueError(f"gemm_geglu_bf16: weight must be [{2 * I}, {K}], got {tuple(b.shape)}")
+    H = torch.empty((M, I), dtype=torch.bfloat16, device=a.device)
+    GU = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=a.device) if keep_gu else None
+    count = _geglu_partials_cached(M, I, _tile_override())
+    if partials is None:
+        parts = torch.empty(count, dtype=torch.int32, device=a.device)
+    else:
+        if partials.numel() < count or partials.dtype != torch.int32:
+            raise ValueError(f"gemm_geglu_bf16: partials must be int32 with >= {count} entries")
+        parts = partials[:count]
+    _lib.check(_lib.lib().bf8_gemm_geglu_bf16(
+        _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, I, K, _ptr(a_sinv), _ptr(b_sinv),
+        _ptr(H), H.stride(0), _ptr(GU), _ptr(parts), _stream(a.device)), "bf8_gemm_geglu_bf16")
+    return H, GU, parts
+
+
+def gemm_geglu_nvfp4(a_data, a_scales, a_meta, b_data, b_scales, b_meta, intermediate, *,
+                     keep_gu=False):
+    """The NVFP4 gate/up projection with the gated GELU in its epilogue: both operands
+    dequantized exactly to bf16, then :func:`gemm_geglu_bf16` with the two S_dec."""
+    return gemm_geglu_bf16(dequant_nvfp4(a_data, a_scales), dequant_nvfp4(b_data, b_scales),
+                           a_meta[2:3], b_meta[2:3], intermediate, keep_gu=keep_gu)
+
+
 def gemm_nvfp4(a_data, a_scales, a_meta, b_data, b_scales, b_meta, *, out_dtype=torch.bfloat16):
     """``C = (A^ @ B^.T) * S_dec(a) * S_dec(b)`` for NVFP4 operands A [M, K], B [N, K]
     (blocks along K): both dequantized exactly to bf16, then the bf16 MFMA GEMM."""

@@ -26,8 +26,9 @@ without TE: every tensor in e2m1 blocks of 16 with e4m3 block scales under a per
 scale, round to nearest even, 1-D blocks along each GEMM's reduction dimension (TE's random
 Hadamard transform, stochastic rounding and 2-D weight blocks are not built). gfx950 has no
 MFMA for e4m3-scaled FP4 blocks, so the blocks are dequantized exactly to bf16 and multiplied
-on the bf16 MFMA, with the gated GELU between the projections as its own kernels
-(bongard_amd.linear.Fp8LinearNvfp4Function, GegluFunction); stateless, like 'mxfp8'.
+on the bf16 MFMA (bongard_amd.linear.Fp8LinearNvfp4Function), the gated GELU in the fused
+gate_up GEMM's epilogue (GegluGateUpNvfp4Function; the split projections use the elementwise
+GegluFunction); stateless, like 'mxfp8'.
 """
 
 import os
@@ -212,6 +213,23 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
         return first_microbatch
 
     @torch.compiler.disable
+    def geglu_forward(self, x, intermediate):
+        """Training forward of a gate_up projection ([W_gate; W_up]) under 'nvfp4' with the
+        gated GELU in the GEMM's epilogue: H [..., I] (rows padded and the weight cached as
+        in :meth:`forward`)."""
+        flat = x.reshape(-1, x.shape[-1])
+        first_microbatch = self._note_microbatch()
+        flat, length, aligned = _pad_rows(flat)
+        if flat.dtype != torch.bfloat16:
+            flat = flat.to(torch.bfloat16)
+        out = _linear.GegluGateUpNvfp4Function.apply(flat, self.weight,
+                                                     self.fp8_weight(first_microbatch),
+                                                     int(intermediate))
+        if aligned != length:
+            out = out[:length]
+        return out.reshape(*x.shape[:-1], out.shape[-1])
+
+    @torch.compiler.disable
     def forward(self, x):
         if not self.training:
             return F.linear(x, self.weight)
@@ -274,12 +292,12 @@ class TEMLP(torch.nn.Module):
     @torch.compiler.disable
     def _fp8_forward(self, x):
         if _is_nvfp4(self.down.recipe):
-            # NVFP4: the projections' own forwards (pad to 32, weight cache, NVFP4 GEMMs)
-            # around the bf16 gated GELU
+            # NVFP4: the projections' own forwards (pad to 32, weight cache, NVFP4 GEMMs);
+            # the fused gate_up GEMM takes the gated GELU into its epilogue, the split
+            # projections feed the elementwise one
             if self.fused_gate_up:
-                gu = self.gate_up(x)
-            else:
-                gu = torch.cat([self.gate_proj(x), self.up_proj(x)], -1)
+                return self.down(self.gate_up.geglu_forward(x, self.intermediate_size))
+            gu = torch.cat([self.gate_proj(x), self.up_proj(x)], -1)
             shape = gu.shape
             h = _linear.GegluFunction.apply(gu.reshape(-1, shape[-1]).contiguous())
             return self.down(h.reshape(*shape[:-1], shape[-1] // 2))

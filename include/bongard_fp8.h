@@ -384,6 +384,18 @@ size_t bf8_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K);
 int bf8_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
                   int64_t K, const float* a_scale_inv, const float* b_scale_inv, void* C,
                   int out_dtype, int64_t ldc, void* ws, size_t ws_bytes, void* stream);
+/* bf8_gemm_geglu on bf16 operands: the NVFP4 gate/up projection (X^ [M, K] and
+ * [W_gate; W_up]^ [2I, K], exactly dequantized, row strides ldx, ldw elements, K % 8 == 0)
+ * with the gated GELU of TEMLP / LayerNormMLP (bongard/te_linear.py:98-103,
+ * bongard/fused_mlp.py:25-30, under NVFP4BlockScaling: bongard/te_linear.py:17,38) in its
+ * epilogue: g and u are the bf16 roundings of the fp32 sums times x_scale * w_scale (the two
+ * S_dec), H = bf16(bf16(gelu_tanh(g)) * u) [M, I], GU the bf16 [g | u] [M, 2I] or NULL,
+ * h_partials the amax partials of |H| [bf8_geglu_partials(M, I)]; I % 128 == 0. H and GU
+ * equal bf8_gemm_bf16's bf16 output followed by bf8_geglu_bf16, bit for bit, where that
+ * GEMM runs unsplit. */
+int bf8_gemm_geglu_bf16(const void* X, int64_t ldx, const void* W, int64_t ldw, int64_t M,
+                        int64_t I, int64_t K, const float* x_scale, const float* w_scale,
+                        void* H, int64_t ldh, void* GU, uint32_t* h_partials, void* stream);
 
 /* C[m, n] = sum_b 2^(ea[m,b] + eb[n,b] - 254) * sum_{k in block b} A[m, k] * B[n, k]
  * (+ bias[n]), e4m3 operands, fp32 accumulation; TN like bf8_gemm, K % 32 == 0. Scale

@@ -18,7 +18,7 @@ import torch
 from torch import nn
 from transformers.models.t5gemma2.modeling_t5gemma2 import T5Gemma2MLP, T5Gemma2RMSNorm
 
-from bongard_amd import fused_mlp, ops, te_linear
+from bongard_amd import fused_mlp, linear, ops, te_linear
 from oracle import fp8_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -143,6 +143,37 @@ def test_telinear_nvfp4_fwd_bwd(gpu, rows):
     assert t.counts == {"weight_quantizations": 1}
     t(xg)
     assert t.counts == {"weight_quantizations": 1, "cached_weights": 1}
+
+
+@pytest.mark.parametrize("rows,K,I", [(512, 256, 512), (304, 512, 384), (64, 128, 256)])
+def test_geglu_gate_up_nvfp4_equals_unfused(gpu, rows, K, I):
+    """The gate/up GEMM with the gated GELU in its bf16 epilogue (bf8_gemm_geglu_bf16)
+    against the unfused chain on the same inputs (the NVFP4 linear, then the elementwise
+    gated GELU): H, and both gradients from the same dH, bit for bit (the GEMM plans here
+    run unsplit, so both sum every output in the same order); H also within the 1% bar of
+    the oracle's chain, and the no-grad forward (which keeps no GU) equal to the training
+    one."""
+    g = torch.Generator().manual_seed(rows + K + I)
+    x = _inputs(rows, K, rows + K)
+    w = (torch.randn(2 * I, K, generator=g) * 0.02).to(torch.bfloat16)
+    dH = (torch.randn(rows, I, generator=g) * 1e-3).to(torch.bfloat16).to(gpu)
+    x1, w1 = x.to(gpu).requires_grad_(True), w.to(gpu).requires_grad_(True)
+    H1 = linear.GegluGateUpNvfp4Function.apply(x1, w1, None, I)
+    H1.backward(dH)
+    x2, w2 = x.to(gpu).requires_grad_(True), w.to(gpu).requires_grad_(True)
+    H2 = linear.GegluFunction.apply(linear.Fp8LinearNvfp4Function.apply(x2, w2, None))
+    H2.backward(dH)
+    with torch.no_grad():
+        H0 = linear.GegluGateUpNvfp4Function.apply(x.to(gpu), w.to(gpu), None, I)
+    torch.cuda.synchronize()
+    assert H1.shape == (rows, I)
+    assert torch.equal(H1, H2), "H"
+    assert torch.equal(H0, H1), "H without grad"
+    assert torch.equal(x1.grad, x2.grad), "dx"
+    assert torch.equal(w1.grad, w2.grad), "dW"
+    gu = orc.linear_fwd_bwd_nvfp4(x, w, torch.zeros(rows, 2 * I, dtype=torch.bfloat16))[0]
+    _close(H1, orc.geglu(gu[:, :I].to(torch.bfloat16), gu[:, I:].to(torch.bfloat16)),
+           "nvfp4 fused gate/up H")
 
 
 def _mlp(hidden, inter, seed):
