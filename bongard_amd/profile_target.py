@@ -226,7 +226,7 @@ def _recipes(dev, iters):
         ops.quantize_axiswise(a, ops.E4M3, rowwise=True, colwise=True)
         ops.rmsnorm(a, gamma, 1e-6)
         xn, gn, dn = (ops.quantize_nvfp4(t) for t in (x, w_gu, w_d))
-        H, _ = ops.geglu(ops.gemm_nvfp4(xn.data, xn.scales, xn.meta, gn.data, gn.scales, gn.meta))
+        H, _, _ = ops.gemm_geglu_nvfp4(xn.data, xn.scales, xn.meta, gn.data, gn.scales, gn.meta, I)
         hn = ops.quantize_nvfp4(H)
         ops.gemm_nvfp4(hn.data, hn.scales, hn.meta, dn.data, dn.scales, dn.meta)
     torch.cuda.synchronize()
