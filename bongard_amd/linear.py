@@ -282,8 +282,9 @@ class Fp8LinearNvfp4Function(_Fp8Function):
 class GegluFunction(torch.autograd.Function):
     """H = bf16(bf16(gelu_tanh(gate)) * up) of the bf16 pre-activations GU [M, 2I] (gate |
     up) and its backward, on the elementwise kernels (bit-identical to the bf16 chain
-    F.gelu(gate, approximate='tanh') * up, bongard/te_linear.py:103): the activation between
-    two projections whose GEMMs cannot take it into their epilogue (the NVFP4 recipe)."""
+    F.gelu(gate, approximate='tanh') * up, bongard/te_linear.py:103): the activation after
+    two separate gate and up projections (the NVFP4 recipe's split layout, one tensor scale
+    per projection), whose GEMMs cannot take it into an epilogue."""
 
     @staticmethod
     def forward(ctx, GU):
