@@ -663,7 +663,7 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
     W_down quantized to NVFP4 (e2m1, 16-blocks, e4m3 block scales, per-tensor scale), each
     GEMM on the bf16 MFMA over the exactly dequantized operands, the gated GELU in the
     gate/up GEMM's epilogue (no [gate | up] stored without grad), H quantized to NVFP4 for
-    the down GEMM. The unfused step (the linear GEMM, then the elementwise gated GELU over
+    the down GEMM from the amax partials that epilogue wrote. The unfused step (the linear GEMM, then the elementwise gated GELU over
     the stored [gate | up], bit-identical H) is timed beside it."""
     c = workloads.config2()
     x = c["x"].to(dev)
@@ -677,9 +677,9 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
 
     def step():
         xq, gq, dq = q(x), q(w_gu), q(w_d)
-        H, _, _ = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, gq.data, gq.scales,
-                                       gq.meta, I)
-        hq = q(H)
+        H, _, hp = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, gq.data, gq.scales,
+                                        gq.meta, I)
+        hq = ops.quantize_nvfp4(H, rowwise=True, colwise=False, partials=hp)
         return ops.gemm_nvfp4(hq.data, hq.scales, hq.meta, dq.data, dq.scales, dq.meta)
 
     def step_unfused():

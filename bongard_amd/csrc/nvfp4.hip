@@ -177,42 +177,74 @@ unsigned stream_grid(int64_t items) {
 
 using namespace bf8;
 
-extern "C" {
-
-int bf8_quantize_nvfp4_bf16(const void* x, int64_t rows, int64_t cols, uint8_t* out,
-                            uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
-                            float* meta, uint32_t* partials, void* stream) {
-  BF8_CHECK(rows >= 0 && cols >= 0, "bf8_quantize_nvfp4_bf16: negative shape");
-  BF8_CHECK(out || out_t, "bf8_quantize_nvfp4_bf16: out and out_t are both NULL");
+// Argument checks shared by the NVFP4 quantize entry points (before anything launches).
+static int nvfp4_args(const char* who, const void* x, int64_t rows, int64_t cols,
+                      const uint8_t* out, const uint8_t* out_scales, const uint8_t* out_t,
+                      const uint8_t* out_t_scales, const float* meta) {
+  BF8_CHECK(rows >= 0 && cols >= 0, "%s: negative shape", who);
+  BF8_CHECK(out || out_t, "%s: out and out_t are both NULL", who);
   BF8_CHECK(!out || (out_scales && cols % 16 == 0),
-            "bf8_quantize_nvfp4_bf16: rowwise blocks need cols %% 16 == 0 (got %lld) and scales",
+            "%s: rowwise blocks need cols %% 16 == 0 (got %lld) and scales", who,
             (long long)cols);
   BF8_CHECK(!out_t || (out_t_scales && rows % 16 == 0),
-            "bf8_quantize_nvfp4_bf16: columnwise blocks need rows %% 16 == 0 (got %lld) and "
-            "scales", (long long)rows);
-  BF8_CHECK(meta && partials, "bf8_quantize_nvfp4_bf16: meta or partials is NULL");
+            "%s: columnwise blocks need rows %% 16 == 0 (got %lld) and scales", who,
+            (long long)rows);
+  BF8_CHECK(meta != nullptr, "%s: meta is NULL", who);
   BF8_CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 7) == 0 && ((uintptr_t)out_t & 7) == 0,
-            "bf8_quantize_nvfp4_bf16: x must be 16-byte and out, out_t 8-byte aligned");
+            "%s: x must be 16-byte and out, out_t 8-byte aligned", who);
+  BF8_CHECK(rows * cols == 0 || x != nullptr, "%s: x is NULL", who);
+  return BF8_OK;
+}
+
+// The rowwise and/or columnwise casts, the per-tensor amax reduced from np partials (maxima
+// of |x| as fp32 bits) that are already written.
+static int nvfp4_casts(const void* x, int64_t rows, int64_t cols, const uint32_t* partials,
+                       int64_t np, uint8_t* out, uint8_t* out_scales, uint8_t* out_t,
+                       uint8_t* out_t_scales, float* meta, hipStream_t s) {
   const int64_t n = rows * cols;
-  if (n == 0) return BF8_OK;
-  BF8_CHECK(x != nullptr, "bf8_quantize_nvfp4_bf16: x is NULL");
-  int rc = bf8_amax_bf16(x, n, partials, stream);
-  if (rc != BF8_OK) return rc;
-  const int64_t np = bf8_amax_partials(n);
-  hipStream_t s = as_stream(stream);
   if (out) {
     hipLaunchKernelGGL(nvfp4_rows_kernel, dim3(stream_grid(n / 16)), dim3(kNT), 0, s,
                        (const uint16_t*)x, rows, cols, partials, np, meta, out, out_scales);
-    rc = launch_status("nvfp4_rows_kernel");
+    const int rc = launch_status("nvfp4_rows_kernel");
     if (rc != BF8_OK) return rc;
   }
   if (out_t) {
     hipLaunchKernelGGL(nvfp4_cols_kernel, dim3(stream_grid(n / 16)), dim3(kNT), 0, s,
                        (const uint16_t*)x, rows, cols, partials, np, meta, out ? 0 : 1, out_t,
                        out_t_scales);
-    rc = launch_status("nvfp4_cols_kernel");
+    return launch_status("nvfp4_cols_kernel");
   }
-  return rc;
+  return BF8_OK;
+}
+
+extern "C" {
+
+int bf8_quantize_nvfp4_partials_bf16(const void* x, int64_t rows, int64_t cols,
+                                     const uint32_t* partials, int64_t n_partials, uint8_t* out,
+                                     uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
+                                     float* meta, void* stream) {
+  const char* who = "bf8_quantize_nvfp4_partials_bf16";
+  int rc = nvfp4_args(who, x, rows, cols, out, out_scales, out_t, out_t_scales, meta);
+  if (rc != BF8_OK) return rc;
+  BF8_CHECK(partials && n_partials >= 1, "%s: partials is NULL or empty", who);
+  if (rows * cols == 0) return BF8_OK;
+  return nvfp4_casts(x, rows, cols, partials, n_partials, out, out_scales, out_t, out_t_scales,
+                     meta, as_stream(stream));
+}
+
+int bf8_quantize_nvfp4_bf16(const void* x, int64_t rows, int64_t cols, uint8_t* out,
+                            uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
+                            float* meta, uint32_t* partials, void* stream) {
+  const char* who = "bf8_quantize_nvfp4_bf16";
+  int rc = nvfp4_args(who, x, rows, cols, out, out_scales, out_t, out_t_scales, meta);
+  if (rc != BF8_OK) return rc;
+  BF8_CHECK(partials, "%s: partials is NULL", who);
+  const int64_t n = rows * cols;
+  if (n == 0) return BF8_OK;
+  rc = bf8_amax_bf16(x, n, partials, stream);
+  if (rc != BF8_OK) return rc;
+  return nvfp4_casts(x, rows, cols, partials, bf8_amax_partials(n), out, out_scales, out_t,
+                     out_t_scales, meta, as_stream(stream));
 }
 
 int bf8_dequant_nvfp4(const uint8_t* q, const uint8_t* scales, int64_t rows, int64_t cols,

@@ -191,16 +191,18 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
                                  _linear.quantize_weight_nvfp4(self.fc2_weight))
         gu_q, down_q = self._fp8_weights
         flat = flat.to(torch.bfloat16).contiguous()
+        parts = None
         if _ops.rmsnorm_supported(flat.shape[1]):
-            # the norm's amax partials go unused: the NVFP4 quantizer finds its own amax
+            # the norm writes its output's amax partials: fc1's NVFP4 quantizer of the
+            # normed rows takes its tensor amax from them (no amax pass of its own)
             parts = torch.empty(_ops.rmsnorm_partials_count(flat.shape[0]), dtype=torch.int32,
                                 device=flat.device)
             normed = _FusedRMSNorm.apply(flat, self.layer_norm_weight, self.eps, parts)
         else:
             normed = _rms_norm(flat, self.layer_norm_weight, self.eps)
-        h = _linear.GegluGateUpNvfp4Function.apply(normed, self.fc1_weight, gu_q,
-                                                    self.intermediate_size)
-        out = _linear.Fp8LinearNvfp4Function.apply(h, self.fc2_weight, down_q)
+        h, h_partials = _linear.GegluGateUpNvfp4Function.apply(normed, self.fc1_weight, gu_q,
+                                                                self.intermediate_size, parts)
+        out = _linear.Fp8LinearNvfp4Function.apply(h, self.fc2_weight, down_q, h_partials)
         return out[:length].reshape_as(x)
 
 

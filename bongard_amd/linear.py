@@ -244,7 +244,8 @@ class Fp8LinearNvfp4Function(_Fp8Function):
     """y = x @ W^T under TE's NVFP4BlockScaling as built here (every tensor e2m1 in blocks
     of 16 along the GEMM's reduction dimension, e4m3 block scales, a per-tensor fp32 scale;
     round to nearest even, no Hadamard transform, no stochastic rounding); x: bf16 [M, K]
-    with M % 16 == 0 when the weight needs a gradient. Each GEMM dequantizes its NVFP4
+    with M % 16 == 0 when the weight needs a gradient; x_partials: amax partials of |x|
+    from its producer (no amax pass for x) or None. Each GEMM dequantizes its NVFP4
     operands exactly to bf16 and runs the bf16 MFMA, the two tensor scales in its epilogue.
 
       forward  y  = X^ . W^T           blocks along K on both
@@ -255,9 +256,9 @@ class Fp8LinearNvfp4Function(_Fp8Function):
     """
 
     @staticmethod
-    def forward(ctx, x, weight, wq):
+    def forward(ctx, x, weight, wq, x_partials=None):
         need_dx, need_dw = _forward_needs(ctx, 2)
-        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw)
+        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw, partials=x_partials)
         if wq is None:
             wq = quantize_weight_nvfp4(weight, transpose=need_dx)
         y = ops.gemm_nvfp4(xq.data, xq.scales, xq.meta, wq.data, wq.scales, wq.meta)
@@ -276,7 +277,7 @@ class Fp8LinearNvfp4Function(_Fp8Function):
             dx = ops.gemm_nvfp4(dyq.data, dyq.scales, dyq.meta, w4t, wst, w_meta)
         if need_dw:
             dw = ops.gemm_nvfp4(dyq.data_t, dyq.scales_t, dyq.meta, x4t, xst, x_meta)
-        return dx, dw, None
+        return dx, dw, None, None
 
 
 class GegluFunction(torch.autograd.Function):
@@ -306,7 +307,10 @@ class GegluGateUpNvfp4Function(_Fp8Function):
     gelu_tanh(g)) * u) (bf8_gemm_geglu_bf16). Equals Fp8LinearNvfp4Function followed by
     GegluFunction bit for bit where that GEMM runs unsplit (the forward and, from the same
     GU, the backward), without the [M, 2I] pre-activations' round trip when no gradient
-    is needed. x: bf16 [M, K]; w_gu [2I, K].
+    is needed. x: bf16 [M, K]; w_gu [2I, K]; x_partials: amax partials of |x| written by
+    its producer (the fused RMSNorm) or None. x and dGU are quantized from their producers'
+    amax partials, without an amax pass of their own. Returns ``(H, amax partials of |H|)``
+    (the partials for the down projection's quantizer; not differentiable).
 
     Reference: TEMLP's gate_up projection and F.gelu(gate, approximate='tanh') * up
     (bongard/te_linear.py:98-103) and te.LayerNormMLP's fc1 + geglu (bongard/fused_mlp.py:
@@ -314,31 +318,33 @@ class GegluGateUpNvfp4Function(_Fp8Function):
     """
 
     @staticmethod
-    def forward(ctx, x, w_gu, wq, intermediate):
+    def forward(ctx, x, w_gu, wq, intermediate, x_partials=None):
         need_dx, need_dw = _forward_needs(ctx, 2)
-        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw)
+        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw, partials=x_partials)
         if wq is None:
             wq = quantize_weight_nvfp4(w_gu, transpose=need_dx)
         train = need_dx or need_dw
-        H, GU, _ = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, wq.data, wq.scales,
-                                        wq.meta, intermediate, keep_gu=train)
+        H, GU, h_partials = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, wq.data,
+                                                 wq.scales, wq.meta, intermediate,
+                                                 keep_gu=train)
         ctx.save_for_backward(GU, xq.data_t, xq.scales_t, xq.meta,
                               wq.data_t if need_dx else None,
                               wq.scales_t if need_dx else None, wq.meta)
-        return H
+        ctx.mark_non_differentiable(h_partials)
+        return H, h_partials
 
     @staticmethod
-    def backward(ctx, dH):
+    def backward(ctx, dH, _d_partials):
         GU, x4t, xst, x_meta, w4t, wst, w_meta = ctx.saved_tensors
         need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        dGU, _ = ops.geglu_bwd(dH.contiguous(), GU)
-        dq = ops.quantize_nvfp4(dGU, rowwise=need_dx, colwise=need_dw)
+        dGU, dparts = ops.geglu_bwd(dH.contiguous(), GU)
+        dq = ops.quantize_nvfp4(dGU, rowwise=need_dx, colwise=need_dw, partials=dparts)
         dx = dw = None
         if need_dx:
             dx = ops.gemm_nvfp4(dq.data, dq.scales, dq.meta, w4t, wst, w_meta)
         if need_dw:
             dw = ops.gemm_nvfp4(dq.data_t, dq.scales_t, dq.meta, x4t, xst, x_meta)
-        return dx, dw, None, None
+        return dx, dw, None, None, None
 
 
 def quantize_weight_mx(weight, *, transpose=True):

@@ -988,10 +988,13 @@ class NvFp4Tensor:
     cols: int
 
 
-def quantize_nvfp4(x, *, rowwise=True, colwise=False):
+def quantize_nvfp4(x, *, rowwise=True, colwise=False, partials=None):
     """NVFP4 quantization of a bf16 tensor (flattened to 2-D): an amax pass and the block
-    quantization (rowwise needs cols % 16 == 0, columnwise rows % 16 == 0)."""
-    _require_gpu(x)
+    quantization (rowwise needs cols % 16 == 0, columnwise rows % 16 == 0). ``partials``:
+    the amax partials of |x| its producer wrote (int32 / uint32 fp32 bits: ``geglu_bwd``'s,
+    the fused RMSNorm's, the gated-GELU GEMM's); the amax pass is then skipped
+    (bf8_quantize_nvfp4_partials_bf16, the same outputs bit for bit)."""
+    _require_gpu(x, partials)
     x = _bf16_2d(x)
     rows, cols = x.shape
     dev = x.device
@@ -1002,6 +1005,14 @@ def quantize_nvfp4(x, *, rowwise=True, colwise=False):
     out_t = torch.empty((cols, rows // 2), dtype=u8, device=dev) if colwise else None
     sc_t = torch.empty((cols, rows // 16), dtype=u8, device=dev) if colwise else None
     L = _lib.lib()
+    if partials is not None:
+        if partials.dtype != torch.int32 or partials.dim() != 1 or partials.numel() < 1:
+            raise ValueError("quantize_nvfp4: partials must be a non-empty 1-D int32 tensor")
+        _lib.check(L.bf8_quantize_nvfp4_partials_bf16(
+            _ptr(x), rows, cols, _ptr(partials.contiguous()), partials.numel(), _ptr(out),
+            _ptr(sc), _ptr(out_t), _ptr(sc_t), _ptr(meta), _stream(dev)),
+            "bf8_quantize_nvfp4_partials_bf16")
+        return NvFp4Tensor(out, sc, out_t, sc_t, meta, rows, cols)
     parts = partials_buffer(max(1, int(L.bf8_amax_partials(rows * cols))), dev)
     _lib.check(L.bf8_quantize_nvfp4_bf16(_ptr(x), rows, cols, _ptr(out), _ptr(sc), _ptr(out_t),
                                          _ptr(sc_t), _ptr(meta), _ptr(parts), _stream(dev)),

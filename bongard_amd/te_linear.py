@@ -215,22 +215,26 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
     @torch.compiler.disable
     def geglu_forward(self, x, intermediate):
         """Training forward of a gate_up projection ([W_gate; W_up]) under 'nvfp4' with the
-        gated GELU in the GEMM's epilogue: H [..., I] (rows padded and the weight cached as
-        in :meth:`forward`)."""
+        gated GELU in the GEMM's epilogue: ``(H [..., I], amax partials of |H|)`` (rows
+        padded and the weight cached as in :meth:`forward`; the partials, over the padded
+        rows, whose H is zero, go to the down projection's ``x_partials``)."""
         flat = x.reshape(-1, x.shape[-1])
         first_microbatch = self._note_microbatch()
         flat, length, aligned = _pad_rows(flat)
         if flat.dtype != torch.bfloat16:
             flat = flat.to(torch.bfloat16)
-        out = _linear.GegluGateUpNvfp4Function.apply(flat, self.weight,
-                                                     self.fp8_weight(first_microbatch),
-                                                     int(intermediate))
+        out, parts = _linear.GegluGateUpNvfp4Function.apply(flat, self.weight,
+                                                            self.fp8_weight(first_microbatch),
+                                                            int(intermediate))
         if aligned != length:
             out = out[:length]
-        return out.reshape(*x.shape[:-1], out.shape[-1])
+        return out.reshape(*x.shape[:-1], out.shape[-1]), parts
 
     @torch.compiler.disable
-    def forward(self, x):
+    def forward(self, x, x_partials=None):
+        """``x_partials`` (the 'nvfp4' recipe only, else ignored): amax partials of |x| that
+        x's producer wrote (the gate/up GEMM's epilogue for H), so that x's quantizer needs
+        no amax pass of its own."""
         if not self.training:
             return F.linear(x, self.weight)
         flat = x.reshape(-1, x.shape[-1])
@@ -244,7 +248,8 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
                                                     self.fp8_weight(first_microbatch))
         elif _is_nvfp4(self.recipe):
             out = _linear.Fp8LinearNvfp4Function.apply(flat, self.weight,
-                                                       self.fp8_weight(first_microbatch))
+                                                       self.fp8_weight(first_microbatch),
+                                                       x_partials)
         else:
             out = _linear.Fp8LinearFunction.apply(flat, self.weight, None,
                                                   self.fp8_weight(first_microbatch), self.scaling)
@@ -296,7 +301,8 @@ class TEMLP(torch.nn.Module):
             # the fused gate_up GEMM takes the gated GELU into its epilogue, the split
             # projections feed the elementwise one
             if self.fused_gate_up:
-                return self.down(self.gate_up.geglu_forward(x, self.intermediate_size))
+                h, h_partials = self.gate_up.geglu_forward(x, self.intermediate_size)
+                return self.down(h, x_partials=h_partials)
             gu = torch.cat([self.gate_proj(x), self.up_proj(x)], -1)
             shape = gu.shape
             h = _linear.GegluFunction.apply(gu.reshape(-1, shape[-1]).contiguous())

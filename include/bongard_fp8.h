@@ -378,6 +378,15 @@ int bf8_quantize_mx_many_bf16(int count, const void* const* x, const int64_t* ro
 int bf8_quantize_nvfp4_bf16(const void* x, int64_t rows, int64_t cols, uint8_t* out,
                             uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
                             float* meta, uint32_t* partials, void* stream);
+/* bf8_quantize_nvfp4_bf16 without its amax pass: the per-tensor amax is the maximum of
+ * n_partials amax partials of |x| (fp32 bits) that x's producer already wrote (the gated
+ * GELU's backward for dGU, the fused RMSNorm for its output, the gate/up epilogue for H),
+ * as NVFP4BlockScaling's quantizer takes the amax of the same tensor (bongard/te_linear.py:
+ * 17,38; bongard/fused_mlp.py:9,32). Same outputs, bit for bit. */
+int bf8_quantize_nvfp4_partials_bf16(const void* x, int64_t rows, int64_t cols,
+                                     const uint32_t* partials, int64_t n_partials, uint8_t* out,
+                                     uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
+                                     float* meta, void* stream);
 int bf8_dequant_nvfp4(const uint8_t* q, const uint8_t* scales, int64_t rows, int64_t cols,
                       void* out, void* stream);
 size_t bf8_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K);

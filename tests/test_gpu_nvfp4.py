@@ -158,22 +158,56 @@ def test_geglu_gate_up_nvfp4_equals_unfused(gpu, rows, K, I):
     w = (torch.randn(2 * I, K, generator=g) * 0.02).to(torch.bfloat16)
     dH = (torch.randn(rows, I, generator=g) * 1e-3).to(torch.bfloat16).to(gpu)
     x1, w1 = x.to(gpu).requires_grad_(True), w.to(gpu).requires_grad_(True)
-    H1 = linear.GegluGateUpNvfp4Function.apply(x1, w1, None, I)
+    H1, hp1 = linear.GegluGateUpNvfp4Function.apply(x1, w1, None, I)
     H1.backward(dH)
     x2, w2 = x.to(gpu).requires_grad_(True), w.to(gpu).requires_grad_(True)
     H2 = linear.GegluFunction.apply(linear.Fp8LinearNvfp4Function.apply(x2, w2, None))
     H2.backward(dH)
     with torch.no_grad():
-        H0 = linear.GegluGateUpNvfp4Function.apply(x.to(gpu), w.to(gpu), None, I)
+        H0, _ = linear.GegluGateUpNvfp4Function.apply(x.to(gpu), w.to(gpu), None, I)
     torch.cuda.synchronize()
     assert H1.shape == (rows, I)
     assert torch.equal(H1, H2), "H"
     assert torch.equal(H0, H1), "H without grad"
     assert torch.equal(x1.grad, x2.grad), "dx"
     assert torch.equal(w1.grad, w2.grad), "dW"
+    assert not hp1.requires_grad
+    assert hp1.max().item() == H2.abs().float().max().view(torch.int32).item(), "H partials"
     gu = orc.linear_fwd_bwd_nvfp4(x, w, torch.zeros(rows, 2 * I, dtype=torch.bfloat16))[0]
     _close(H1, orc.geglu(gu[:, :I].to(torch.bfloat16), gu[:, I:].to(torch.bfloat16)),
            "nvfp4 fused gate/up H")
+
+
+@pytest.mark.parametrize("rows", [96, 80])
+def test_quantize_nvfp4_from_producer_partials(gpu, rows):
+    """The NVFP4 quantizer fed the amax partials its producer wrote (geglu_bwd's for dGU,
+    the gated-GELU GEMM's epilogue for H, the fused RMSNorm's for its output) against its
+    own amax pass: codes, block scales (both directions) and meta bit for bit. rows = 80 is
+    not a whole number of GEMM tiles (the rows past M must add nothing to H's partials)."""
+    g = torch.Generator().manual_seed(rows)
+    I, K = 256, 128
+    GU = (torch.randn(rows, 2 * I, generator=g) * 2).to(torch.bfloat16).to(gpu)
+    dH = (torch.randn(rows, I, generator=g) * 1e-3).to(torch.bfloat16).to(gpu)
+    x = _inputs(rows, K, rows + 1).to(gpu)
+    w = (torch.randn(2 * I, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    gamma = (torch.randn(K, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    dGU, dparts = ops.geglu_bwd(dH, GU)
+    xq, wq = ops.quantize_nvfp4(x), ops.quantize_nvfp4(w)
+    H, _, hparts = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, wq.data, wq.scales,
+                                        wq.meta, I)
+    normed, _, nparts = ops.rmsnorm(x, gamma, 1e-6)
+    for what, t, parts in (("dGU", dGU, dparts), ("H", H, hparts), ("normed", normed, nparts)):
+        for rw, cw in ((True, True), (True, False), (False, True)):
+            a = ops.quantize_nvfp4(t, rowwise=rw, colwise=cw)
+            b = ops.quantize_nvfp4(t, rowwise=rw, colwise=cw, partials=parts)
+            torch.cuda.synchronize()
+            for f in ("data", "scales", "data_t", "scales_t"):
+                fa, fb = getattr(a, f), getattr(b, f)
+                assert (fa is None) == (fb is None), (what, f)
+                assert fa is None or torch.equal(fa, fb), (what, rw, cw, f)
+            assert torch.equal(a.meta, b.meta), (what, rw, cw, "meta")
+    with pytest.raises(ValueError):
+        ops.quantize_nvfp4(H, partials=hparts.float())
 
 
 def _mlp(hidden, inter, seed):
