@@ -285,16 +285,19 @@ class GegluFunction(torch.autograd.Function):
     up) and its backward, on the elementwise kernels (bit-identical to the bf16 chain
     F.gelu(gate, approximate='tanh') * up, bongard/te_linear.py:103): the activation after
     two separate gate and up projections (the NVFP4 recipe's split layout, one tensor scale
-    per projection), whose GEMMs cannot take it into an epilogue."""
+    per projection), whose GEMMs cannot take it into an epilogue. Returns ``(H, amax
+    partials of |H|)`` (the partials for the down projection's quantizer; not
+    differentiable)."""
 
     @staticmethod
     def forward(ctx, GU):
-        H, _ = ops.geglu(GU)
+        H, parts = ops.geglu(GU)
         ctx.save_for_backward(GU)
-        return H
+        ctx.mark_non_differentiable(parts)
+        return H, parts
 
     @staticmethod
-    def backward(ctx, dH):
+    def backward(ctx, dH, _d_partials):
         (GU,) = ctx.saved_tensors
         dGU, _ = ops.geglu_bwd(dH.contiguous(), GU)
         return dGU

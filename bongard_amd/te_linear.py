@@ -305,8 +305,8 @@ class TEMLP(torch.nn.Module):
                 return self.down(h, x_partials=h_partials)
             gu = torch.cat([self.gate_proj(x), self.up_proj(x)], -1)
             shape = gu.shape
-            h = _linear.GegluFunction.apply(gu.reshape(-1, shape[-1]).contiguous())
-            return self.down(h.reshape(*shape[:-1], shape[-1] // 2))
+            h, h_partials = _linear.GegluFunction.apply(gu.reshape(-1, shape[-1]).contiguous())
+            return self.down(h.reshape(*shape[:-1], shape[-1] // 2), x_partials=h_partials)
         I = self.intermediate_size
         flat = x.reshape(-1, x.shape[-1])
         flat, length, aligned = _pad_rows(flat)

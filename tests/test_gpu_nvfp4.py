@@ -161,7 +161,7 @@ def test_geglu_gate_up_nvfp4_equals_unfused(gpu, rows, K, I):
     H1, hp1 = linear.GegluGateUpNvfp4Function.apply(x1, w1, None, I)
     H1.backward(dH)
     x2, w2 = x.to(gpu).requires_grad_(True), w.to(gpu).requires_grad_(True)
-    H2 = linear.GegluFunction.apply(linear.Fp8LinearNvfp4Function.apply(x2, w2, None))
+    H2, hp2 = linear.GegluFunction.apply(linear.Fp8LinearNvfp4Function.apply(x2, w2, None))
     H2.backward(dH)
     with torch.no_grad():
         H0, _ = linear.GegluGateUpNvfp4Function.apply(x.to(gpu), w.to(gpu), None, I)
@@ -173,6 +173,7 @@ def test_geglu_gate_up_nvfp4_equals_unfused(gpu, rows, K, I):
     assert torch.equal(w1.grad, w2.grad), "dW"
     assert not hp1.requires_grad
     assert hp1.max().item() == H2.abs().float().max().view(torch.int32).item(), "H partials"
+    assert hp2.max().item() == hp1.max().item() and not hp2.requires_grad
     gu = orc.linear_fwd_bwd_nvfp4(x, w, torch.zeros(rows, 2 * I, dtype=torch.bfloat16))[0]
     _close(H1, orc.geglu(gu[:, :I].to(torch.bfloat16), gu[:, I:].to(torch.bfloat16)),
            "nvfp4 fused gate/up H")
