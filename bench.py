@@ -689,11 +689,26 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
         hq = q(H)
         return ops.gemm_nvfp4(hq.data, hq.scales, hq.meta, dq.data, dq.scales, dq.meta)
 
+    gc, dc = q(w_gu), q(w_d)
+    gc.cache_dequant = dc.cache_dequant = True
+
+    def step_cached():
+        # weights cached across microbatches (TEMLP / FusedMLP): quantized and dequantized
+        # once, their bf16 operands kept
+        xq = q(x)
+        H, _, hp = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, gc.data, gc.scales,
+                                        gc.meta, I, b_deq=ops.nvfp4_dequant(gc))
+        hq = ops.quantize_nvfp4(H, rowwise=True, colwise=False, partials=hp)
+        return ops.gemm_nvfp4(hq.data, hq.scales, hq.meta, dc.data, dc.scales, dc.meta,
+                              b_deq=ops.nvfp4_dequant(dc))
+
     for _ in range(5):
         step()
         step_unfused()
+        step_cached()
     s = _timed(torch, step, steps, 3)
     su = _timed(torch, step_unfused, steps, 3)
+    sc = _timed(torch, step_cached, steps, 3)
     xq, gq, dq = q(x), q(w_gu), q(w_d)
     xb, gb = ops.dequant_nvfp4(xq.data, xq.scales), ops.dequant_nvfp4(gq.data, gq.scales)
     GU = ops.gemm_bf16(xb, gb, xq.meta[2:3], gq.meta[2:3])
@@ -714,6 +729,8 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
                         "epilogue)",
             "us_per_step": round(s * 1e6, 2), "tflops": round(flop / s / 1e12, 1),
             "us_per_step_unfused_geglu": round(su * 1e6, 2),
+            "us_per_step_cached_weights": round(sc * 1e6, 2),
+            "tflops_cached_weights": round(flop / sc / 1e12, 1),
             "gemm_gate_up_geglu_bf16_us": round(gg_s * 1e6, 2),
             "gemm_gate_up_geglu_frac_of_bf16_peak": round(2.0 * M * 2 * I * K / gg_s / 1e12
                                                           / BF16_PEAK_TFLOPS, 4),

@@ -187,8 +187,9 @@ class FusedMLP(_ScalingExtraState, torch.nn.Module):
         """'nvfp4': the fused norm, fc1 as an NVFP4 GEMM (operands dequantized exactly to
         bf16 for the MFMA) with the gated GELU in its epilogue, fc2 as an NVFP4 GEMM."""
         if first:
-            self._fp8_weights = (_linear.quantize_weight_nvfp4(self.fc1_weight),
-                                 _linear.quantize_weight_nvfp4(self.fc2_weight))
+            self._fp8_weights = (
+                _linear.quantize_weight_nvfp4(self.fc1_weight, cache_dequant=True),
+                _linear.quantize_weight_nvfp4(self.fc2_weight, cache_dequant=True))
         gu_q, down_q = self._fp8_weights
         flat = flat.to(torch.bfloat16).contiguous()
         parts = None

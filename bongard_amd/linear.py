@@ -234,10 +234,14 @@ class Fp8LinearAxiswiseFunction(_Fp8Function):
         return dx, dw, db, None
 
 
-def quantize_weight_nvfp4(weight, *, transpose=True):
+def quantize_weight_nvfp4(weight, *, transpose=True, cache_dequant=False):
     """NVFP4 copy of a weight [N, K]: blocks along K (forward), and with ``transpose`` the
-    columnwise copy [K, N] with blocks along N (the input-gradient GEMM's operand)."""
-    return ops.quantize_nvfp4(weight.detach(), rowwise=True, colwise=transpose)
+    columnwise copy [K, N] with blocks along N (the input-gradient GEMM's operand).
+    ``cache_dequant``: for a copy cached across microbatches, keep each copy's bf16
+    dequantization after its first GEMM (the GEMMs' operand; bit-identical)."""
+    q = ops.quantize_nvfp4(weight.detach(), rowwise=True, colwise=transpose)
+    q.cache_dequant = cache_dequant
+    return q
 
 
 class Fp8LinearNvfp4Function(_Fp8Function):
@@ -261,10 +265,13 @@ class Fp8LinearNvfp4Function(_Fp8Function):
         xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw, partials=x_partials)
         if wq is None:
             wq = quantize_weight_nvfp4(weight, transpose=need_dx)
-        y = ops.gemm_nvfp4(xq.data, xq.scales, xq.meta, wq.data, wq.scales, wq.meta)
+        y = ops.gemm_nvfp4(xq.data, xq.scales, xq.meta, wq.data, wq.scales, wq.meta,
+                           b_deq=ops.nvfp4_dequant(wq))
         ctx.save_for_backward(xq.data_t, xq.scales_t, xq.meta,
                               wq.data_t if need_dx else None,
                               wq.scales_t if need_dx else None, wq.meta)
+        # a cached weight lends the dgrad GEMM its kept bf16 columnwise operand
+        ctx.wq = wq if need_dx and wq.cache_dequant else None
         return y
 
     @staticmethod
@@ -274,7 +281,8 @@ class Fp8LinearNvfp4Function(_Fp8Function):
         dyq = ops.quantize_nvfp4(dy.contiguous(), rowwise=need_dx, colwise=need_dw)
         dx = dw = None
         if need_dx:
-            dx = ops.gemm_nvfp4(dyq.data, dyq.scales, dyq.meta, w4t, wst, w_meta)
+            wdt = ops.nvfp4_dequant(ctx.wq, transpose=True) if ctx.wq is not None else None
+            dx = ops.gemm_nvfp4(dyq.data, dyq.scales, dyq.meta, w4t, wst, w_meta, b_deq=wdt)
         if need_dw:
             dw = ops.gemm_nvfp4(dyq.data_t, dyq.scales_t, dyq.meta, x4t, xst, x_meta)
         return dx, dw, None, None
@@ -329,10 +337,11 @@ class GegluGateUpNvfp4Function(_Fp8Function):
         train = need_dx or need_dw
         H, GU, h_partials = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, wq.data,
                                                  wq.scales, wq.meta, intermediate,
-                                                 keep_gu=train)
+                                                 keep_gu=train, b_deq=ops.nvfp4_dequant(wq))
         ctx.save_for_backward(GU, xq.data_t, xq.scales_t, xq.meta,
                               wq.data_t if need_dx else None,
                               wq.scales_t if need_dx else None, wq.meta)
+        ctx.wq = wq if need_dx and wq.cache_dequant else None
         ctx.mark_non_differentiable(h_partials)
         return H, h_partials
 
@@ -344,7 +353,8 @@ class GegluGateUpNvfp4Function(_Fp8Function):
         dq = ops.quantize_nvfp4(dGU, rowwise=need_dx, colwise=need_dw, partials=dparts)
         dx = dw = None
         if need_dx:
-            dx = ops.gemm_nvfp4(dq.data, dq.scales, dq.meta, w4t, wst, w_meta)
+            wdt = ops.nvfp4_dequant(ctx.wq, transpose=True) if ctx.wq is not None else None
+            dx = ops.gemm_nvfp4(dq.data, dq.scales, dq.meta, w4t, wst, w_meta, b_deq=wdt)
         if need_dw:
             dw = ops.gemm_nvfp4(dq.data_t, dq.scales_t, dq.meta, x4t, xst, x_meta)
         return dx, dw, None, None, None

@@ -15,7 +15,7 @@ Float8CurrentScaling behind bongard/te_linear.py:38-39,73-74.
 import ctypes
 import functools
 import os
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Optional, Sequence
 
 import torch
@@ -977,7 +977,10 @@ class NvFp4Tensor:
     """An NVFP4 tensor of x [rows, cols]: ``data`` uint8 [rows, cols / 2] (two e2m1 codes a
     byte) with ``scales`` uint8 e4m3 [rows, cols / 16] (blocks along cols) and/or the
     columnwise copy ``data_t`` [cols, rows / 2] with ``scales_t`` [cols, rows / 16] (blocks
-    along rows), and ``meta`` fp32 [4] = {amax, S_enc, S_dec, 0}."""
+    along rows), and ``meta`` fp32 [4] = {amax, S_enc, S_dec, 0}. ``cache_dequant``: keep
+    the exact bf16 dequantization of each copy on the object after its first use (a weight
+    cached across microbatches: 2 bytes per element per copy, no dequantization pass per
+    GEMM afterwards)."""
 
     data: Optional[torch.Tensor]
     scales: Optional[torch.Tensor]
@@ -986,6 +989,22 @@ class NvFp4Tensor:
     meta: torch.Tensor
     rows: int
     cols: int
+    cache_dequant: bool = False
+    _deq: Optional[torch.Tensor] = field(default=None, repr=False)
+    _deq_t: Optional[torch.Tensor] = field(default=None, repr=False)
+
+
+def nvfp4_dequant(q, *, transpose=False):
+    """bf16 = e2m1(code) * s of ``q``'s rowwise copy (or with ``transpose`` its columnwise
+    copy), exact and without S_dec; kept on ``q`` when ``q.cache_dequant`` is set."""
+    if not q.cache_dequant:
+        return dequant_nvfp4(q.data_t, q.scales_t) if transpose else dequant_nvfp4(q.data, q.scales)
+    attr = "_deq_t" if transpose else "_deq"
+    d = getattr(q, attr)
+    if d is None:
+        d = dequant_nvfp4(q.data_t, q.scales_t) if transpose else dequant_nvfp4(q.data, q.scales)
+        setattr(q, attr, d)
+    return d
 
 
 def quantize_nvfp4(x, *, rowwise=True, colwise=False, partials=None):
@@ -1085,15 +1104,20 @@ def gemm_geglu_bf16(a, b, a_sinv, b_sinv, intermediate, *, keep_gu=False, partia
 
 
 def gemm_geglu_nvfp4(a_data, a_scales, a_meta, b_data, b_scales, b_meta, intermediate, *,
-                     keep_gu=False):
+                     keep_gu=False, b_deq=None):
     """The NVFP4 gate/up projection with the gated GELU in its epilogue: both operands
-    dequantized exactly to bf16, then :func:`gemm_geglu_bf16` with the two S_dec."""
-    return gemm_geglu_bf16(dequant_nvfp4(a_data, a_scales), dequant_nvfp4(b_data, b_scales),
-                           a_meta[2:3], b_meta[2:3], intermediate, keep_gu=keep_gu)
+    dequantized exactly to bf16, then :func:`gemm_geglu_bf16` with the two S_dec.
+    ``b_deq``: b's bf16 dequantization when the caller already holds it."""
+    b = b_deq if b_deq is not None else dequant_nvfp4(b_data, b_scales)
+    return gemm_geglu_bf16(dequant_nvfp4(a_data, a_scales), b, a_meta[2:3], b_meta[2:3],
+                           intermediate, keep_gu=keep_gu)
 
 
-def gemm_nvfp4(a_data, a_scales, a_meta, b_data, b_scales, b_meta, *, out_dtype=torch.bfloat16):
+def gemm_nvfp4(a_data, a_scales, a_meta, b_data, b_scales, b_meta, *, out_dtype=torch.bfloat16,
+               b_deq=None):
     """``C = (A^ @ B^.T) * S_dec(a) * S_dec(b)`` for NVFP4 operands A [M, K], B [N, K]
-    (blocks along K): both dequantized exactly to bf16, then the bf16 MFMA GEMM."""
-    return gemm_bf16(dequant_nvfp4(a_data, a_scales), dequant_nvfp4(b_data, b_scales),
-                     a_meta[2:3], b_meta[2:3], out_dtype=out_dtype)
+    (blocks along K): both dequantized exactly to bf16, then the bf16 MFMA GEMM.
+    ``b_deq``: B's bf16 dequantization when the caller already holds it."""
+    b = b_deq if b_deq is not None else dequant_nvfp4(b_data, b_scales)
+    return gemm_bf16(dequant_nvfp4(a_data, a_scales), b, a_meta[2:3], b_meta[2:3],
+                     out_dtype=out_dtype)

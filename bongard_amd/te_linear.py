@@ -196,7 +196,8 @@ class TELinear(_ScalingExtraState, torch.nn.Module):
             if _is_mx(self.recipe):
                 q = _linear.quantize_weight_mx(self.weight, transpose=True)
             elif _is_nvfp4(self.recipe):
-                q = _linear.quantize_weight_nvfp4(self.weight, transpose=True)
+                q = _linear.quantize_weight_nvfp4(self.weight, transpose=True,
+                                                  cache_dequant=is_first_microbatch is not None)
             else:
                 q = _linear.quantize_weight(self.weight,
                                             scaler=self.scaling and self.scaling.weight)

@@ -174,6 +174,20 @@ def test_geglu_gate_up_nvfp4_equals_unfused(gpu, rows, K, I):
     assert not hp1.requires_grad
     assert hp1.max().item() == H2.abs().float().max().view(torch.int32).item(), "H partials"
     assert hp2.max().item() == hp1.max().item() and not hp2.requires_grad
+    # a weight cached across microbatches keeps its bf16 dequantizations: the first call
+    # fills them, the second reads them; both equal the uncached path bit for bit
+    wq = linear.quantize_weight_nvfp4(w.to(gpu), cache_dequant=True)
+    for call in range(2):
+        x3, w3 = x.to(gpu).requires_grad_(True), w.to(gpu).requires_grad_(True)
+        H3, _ = linear.GegluGateUpNvfp4Function.apply(x3, w3, wq, I)
+        H3.backward(dH)
+        y3 = linear.Fp8LinearNvfp4Function.apply(x3.detach().requires_grad_(True), w3, wq)
+        torch.cuda.synchronize()
+        assert wq._deq is not None and wq._deq_t is not None, call
+        assert torch.equal(H3, H1) and torch.equal(x3.grad, x1.grad), call
+        assert torch.equal(w3.grad, w1.grad), call
+        y4 = linear.Fp8LinearNvfp4Function.apply(x.to(gpu), w.to(gpu), None)
+        assert torch.equal(y3, y4), call
     gu = orc.linear_fwd_bwd_nvfp4(x, w, torch.zeros(rows, 2 * I, dtype=torch.bfloat16))[0]
     _close(H1, orc.geglu(gu[:, :I].to(torch.bfloat16), gu[:, I:].to(torch.bfloat16)),
            "nvfp4 fused gate/up H")
