@@ -663,7 +663,8 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
     W_down quantized to NVFP4 (e2m1, 16-blocks, e4m3 block scales, per-tensor scale), each
     GEMM on the bf16 MFMA over the exactly dequantized operands, the gated GELU in the
     gate/up GEMM's epilogue (no [gate | up] stored without grad), H quantized to NVFP4 for
-    the down GEMM from the amax partials that epilogue wrote. The unfused step (the linear GEMM, then the elementwise gated GELU over
+    the down GEMM from the amax partials that epilogue wrote (X and H written as their exact
+    bf16 dequantization by the quantizer itself). The unfused step (the linear GEMM, then the elementwise gated GELU over
     the stored [gate | up], bit-identical H) is timed beside it."""
     c = workloads.config2()
     x = c["x"].to(dev)
@@ -675,12 +676,18 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
     def q(t):
         return ops.quantize_nvfp4(t, rowwise=True, colwise=False)
 
+    def qd(t, partials=None):
+        # an activation whose rowwise copy only feeds the next GEMM: written dequantized
+        return ops.quantize_nvfp4(t, rowwise=True, colwise=False, partials=partials,
+                                  dequant_rows=True)
+
     def step():
-        xq, gq, dq = q(x), q(w_gu), q(w_d)
-        H, _, hp = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, gq.data, gq.scales,
-                                        gq.meta, I)
-        hq = ops.quantize_nvfp4(H, rowwise=True, colwise=False, partials=hp)
-        return ops.gemm_nvfp4(hq.data, hq.scales, hq.meta, dq.data, dq.scales, dq.meta)
+        xq, gq, dq = qd(x), q(w_gu), q(w_d)
+        H, _, hp = ops.gemm_geglu_nvfp4(None, None, xq.meta, gq.data, gq.scales, gq.meta, I,
+                                        a_deq=ops.nvfp4_dequant(xq))
+        hq = qd(H, hp)
+        return ops.gemm_nvfp4(None, None, hq.meta, dq.data, dq.scales, dq.meta,
+                              a_deq=ops.nvfp4_dequant(hq))
 
     def step_unfused():
         xq, gq, dq = q(x), q(w_gu), q(w_d)
@@ -695,12 +702,13 @@ def _bench_c2_nvfp4(torch, ops, workloads, dev, steps=20):
     def step_cached():
         # weights cached across microbatches (TEMLP / FusedMLP): quantized and dequantized
         # once, their bf16 operands kept
-        xq = q(x)
-        H, _, hp = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, gc.data, gc.scales,
-                                        gc.meta, I, b_deq=ops.nvfp4_dequant(gc))
-        hq = ops.quantize_nvfp4(H, rowwise=True, colwise=False, partials=hp)
-        return ops.gemm_nvfp4(hq.data, hq.scales, hq.meta, dc.data, dc.scales, dc.meta,
-                              b_deq=ops.nvfp4_dequant(dc))
+        xq = qd(x)
+        H, _, hp = ops.gemm_geglu_nvfp4(None, None, xq.meta, gc.data, gc.scales, gc.meta, I,
+                                        a_deq=ops.nvfp4_dequant(xq),
+                                        b_deq=ops.nvfp4_dequant(gc))
+        hq = qd(H, hp)
+        return ops.gemm_nvfp4(None, None, hq.meta, dc.data, dc.scales, dc.meta,
+                              a_deq=ops.nvfp4_dequant(hq), b_deq=ops.nvfp4_dequant(dc))
 
     for _ in range(5):
         step()

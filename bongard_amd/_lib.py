@@ -9,7 +9,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p, POINTE
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libbongard_fp8.so")
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 # name -> (restype, argtypes); mirrors include/bongard_fp8.h one to one.
 SIGNATURES = {
@@ -78,6 +78,9 @@ SIGNATURES = {
     "bf8_quantize_nvfp4_partials_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64,
                                                  c_void_p, c_void_p, c_void_p, c_void_p,
                                                  c_void_p, c_void_p]),
+    "bf8_quantize_nvfp4_dequant_bf16": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64,
+                                                c_void_p, c_void_p, c_void_p, c_void_p,
+                                                c_void_p]),
     "bf8_dequant_nvfp4": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "bf8_gemm_bf16_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
     "bf8_gemm_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,

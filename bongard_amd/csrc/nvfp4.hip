@@ -82,14 +82,32 @@ __device__ __forceinline__ uint2 pack16(const uint32_t (&w)[8], float mult) {
   return make_uint2(r[0], r[1]);
 }
 
+// 8 packed code bytes of a block with scale value s -> its 16 bf16 values e2m1(code) * s
+// (two uint4). e2m1 x e4m3 has at most 6 significant bits: the fp32 product is exact, and so
+// is its bf16 (upper half).
+__device__ __forceinline__ void dequant16(uint2 c, float s, uint4& d0, uint4& d1) {
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t byte = ((i < 4 ? c.x : c.y) >> (8 * (i & 3))) & 0xFFu;
+    const uint32_t lo = __float_as_uint(e2m1_value(byte & 0xFu) * s) >> 16;
+    const uint32_t hi = __float_as_uint(e2m1_value(byte >> 4) * s) >> 16;
+    o[i] = lo | (hi << 16);
+  }
+  d0 = make_uint4(o[0], o[1], o[2], o[3]);
+  d1 = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
 // Rowwise: blocks of 16 consecutive elements of a row; one block per thread (grid-stride).
-// out [rows, cols / 2], scales [rows, cols / 16]. Block 0 publishes the meta record.
+// out [rows, cols / 2], scales [rows, cols / 16]; or, with deq set, the blocks' exact bf16
+// dequantization deq [rows, cols] in their place. Block 0 publishes the meta record.
 __global__ __launch_bounds__(kNT) void nvfp4_rows_kernel(const uint16_t* __restrict__ x,
                                                          int64_t rows, int64_t cols,
                                                          const uint32_t* __restrict__ partials,
                                                          int64_t np, float* __restrict__ meta,
                                                          uint8_t* __restrict__ out,
-                                                         uint8_t* __restrict__ scales) {
+                                                         uint8_t* __restrict__ scales,
+                                                         uint16_t* __restrict__ deq) {
   const float s_enc = scale_from_partials_block<kNT>(partials, np, kNvfp4Global, meta, false,
                                                      blockIdx.x == 0);
   const int64_t per_row = cols / 16;
@@ -103,8 +121,17 @@ __global__ __launch_bounds__(kNT) void nvfp4_rows_kernel(const uint16_t* __restr
     uint32_t sbyte;
     float mult;
     block_scale(key, s_enc, sbyte, mult);
-    *reinterpret_cast<uint2*>(out + b * 8) = pack16(w, mult);
-    scales[b] = (uint8_t)sbyte;
+    const uint2 c = pack16(w, mult);
+    if (deq) {
+      uint4 d0, d1;
+      dequant16(c, e4m3_value(sbyte), d0, d1);
+      uint4* dst = reinterpret_cast<uint4*>(deq + b * 16);
+      dst[0] = d0;
+      dst[1] = d1;
+    } else {
+      *reinterpret_cast<uint2*>(out + b * 8) = c;
+      scales[b] = (uint8_t)sbyte;
+    }
   }
 }
 
@@ -148,21 +175,11 @@ __global__ __launch_bounds__(kNT) void nvfp4_dequant_kernel(const uint8_t* __res
                                                             uint16_t* __restrict__ out) {
   for (int64_t b = (int64_t)blockIdx.x * kNT + threadIdx.x; b < nblk;
        b += (int64_t)gridDim.x * kNT) {
-    const uint2 c = *reinterpret_cast<const uint2*>(q + b * 8);
-    const float s = e4m3_value(scales[b]);
-    uint32_t o[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t byte = ((i < 4 ? c.x : c.y) >> (8 * (i & 3))) & 0xFFu;
-      // e2m1 x e4m3 has at most 6 significant bits: the fp32 product is exact, and so is
-      // its bf16 (upper half)
-      const uint32_t lo = __float_as_uint(e2m1_value(byte & 0xFu) * s) >> 16;
-      const uint32_t hi = __float_as_uint(e2m1_value(byte >> 4) * s) >> 16;
-      o[i] = lo | (hi << 16);
-    }
+    uint4 d0, d1;
+    dequant16(*reinterpret_cast<const uint2*>(q + b * 8), e4m3_value(scales[b]), d0, d1);
     uint4* dst = reinterpret_cast<uint4*>(out + b * 16);
-    dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-    dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    dst[0] = d0;
+    dst[1] = d1;
   }
 }
 
@@ -200,18 +217,20 @@ static int nvfp4_args(const char* who, const void* x, int64_t rows, int64_t cols
 // of |x| as fp32 bits) that are already written.
 static int nvfp4_casts(const void* x, int64_t rows, int64_t cols, const uint32_t* partials,
                        int64_t np, uint8_t* out, uint8_t* out_scales, uint8_t* out_t,
-                       uint8_t* out_t_scales, float* meta, hipStream_t s) {
+                       uint8_t* out_t_scales, float* meta, hipStream_t s,
+                       void* deq = nullptr) {
   const int64_t n = rows * cols;
-  if (out) {
+  if (out || deq) {
     hipLaunchKernelGGL(nvfp4_rows_kernel, dim3(stream_grid(n / 16)), dim3(kNT), 0, s,
-                       (const uint16_t*)x, rows, cols, partials, np, meta, out, out_scales);
+                       (const uint16_t*)x, rows, cols, partials, np, meta, out, out_scales,
+                       (uint16_t*)deq);
     const int rc = launch_status("nvfp4_rows_kernel");
     if (rc != BF8_OK) return rc;
   }
   if (out_t) {
     hipLaunchKernelGGL(nvfp4_cols_kernel, dim3(stream_grid(n / 16)), dim3(kNT), 0, s,
-                       (const uint16_t*)x, rows, cols, partials, np, meta, out ? 0 : 1, out_t,
-                       out_t_scales);
+                       (const uint16_t*)x, rows, cols, partials, np, meta,
+                       (out || deq) ? 0 : 1, out_t, out_t_scales);
     return launch_status("nvfp4_cols_kernel");
   }
   return BF8_OK;
@@ -245,6 +264,34 @@ int bf8_quantize_nvfp4_bf16(const void* x, int64_t rows, int64_t cols, uint8_t* 
   if (rc != BF8_OK) return rc;
   return nvfp4_casts(x, rows, cols, partials, bf8_amax_partials(n), out, out_scales, out_t,
                      out_t_scales, meta, as_stream(stream));
+}
+
+int bf8_quantize_nvfp4_dequant_bf16(const void* x, int64_t rows, int64_t cols,
+                                    uint32_t* partials, int64_t n_partials, void* deq,
+                                    uint8_t* out_t, uint8_t* out_t_scales, float* meta,
+                                    void* stream) {
+  const char* who = "bf8_quantize_nvfp4_dequant_bf16";
+  BF8_CHECK(rows >= 0 && cols >= 0, "%s: negative shape", who);
+  BF8_CHECK(deq != nullptr && cols % 16 == 0,
+            "%s: needs deq and cols %% 16 == 0 (got %lld)", who, (long long)cols);
+  BF8_CHECK(!out_t || (out_t_scales && rows % 16 == 0),
+            "%s: columnwise blocks need rows %% 16 == 0 (got %lld) and scales", who,
+            (long long)rows);
+  BF8_CHECK(meta != nullptr && partials != nullptr && n_partials >= 0,
+            "%s: meta or partials is NULL", who);
+  BF8_CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)deq & 15) == 0 && ((uintptr_t)out_t & 7) == 0,
+            "%s: x and deq must be 16-byte and out_t 8-byte aligned", who);
+  BF8_CHECK(rows * cols == 0 || x != nullptr, "%s: x is NULL", who);
+  int rc = BF8_OK;
+  const int64_t n = rows * cols;
+  if (n == 0) return BF8_OK;
+  if (n_partials == 0) {
+    rc = bf8_amax_bf16(x, n, partials, stream);
+    if (rc != BF8_OK) return rc;
+    n_partials = bf8_amax_partials(n);
+  }
+  return nvfp4_casts(x, rows, cols, partials, n_partials, nullptr, nullptr, out_t, out_t_scales,
+                     meta, as_stream(stream), deq);
 }
 
 int bf8_dequant_nvfp4(const uint8_t* q, const uint8_t* scales, int64_t rows, int64_t cols,

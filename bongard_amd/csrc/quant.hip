@@ -636,7 +636,7 @@ using namespace bf8;
 extern "C" {
 
 const char* bf8_last_error(void) { return bf8::g_err; }
-int bf8_abi_version(void) { return 17; }
+int bf8_abi_version(void) { return 18; }
 
 int64_t bf8_amax_partials(int64_t n) { return amax_blocks(n); }
 

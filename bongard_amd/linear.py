@@ -262,11 +262,12 @@ class Fp8LinearNvfp4Function(_Fp8Function):
     @staticmethod
     def forward(ctx, x, weight, wq, x_partials=None):
         need_dx, need_dw = _forward_needs(ctx, 2)
-        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw, partials=x_partials)
+        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw, partials=x_partials,
+                                dequant_rows=True)
         if wq is None:
             wq = quantize_weight_nvfp4(weight, transpose=need_dx)
-        y = ops.gemm_nvfp4(xq.data, xq.scales, xq.meta, wq.data, wq.scales, wq.meta,
-                           b_deq=ops.nvfp4_dequant(wq))
+        y = ops.gemm_nvfp4(None, None, xq.meta, wq.data, wq.scales, wq.meta,
+                           a_deq=ops.nvfp4_dequant(xq), b_deq=ops.nvfp4_dequant(wq))
         ctx.save_for_backward(xq.data_t, xq.scales_t, xq.meta,
                               wq.data_t if need_dx else None,
                               wq.scales_t if need_dx else None, wq.meta)
@@ -278,11 +279,13 @@ class Fp8LinearNvfp4Function(_Fp8Function):
     def backward(ctx, dy):
         x4t, xst, x_meta, w4t, wst, w_meta = ctx.saved_tensors
         need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        dyq = ops.quantize_nvfp4(dy.contiguous(), rowwise=need_dx, colwise=need_dw)
+        dyq = ops.quantize_nvfp4(dy.contiguous(), rowwise=need_dx, colwise=need_dw,
+                                 dequant_rows=True)
         dx = dw = None
         if need_dx:
             wdt = ops.nvfp4_dequant(ctx.wq, transpose=True) if ctx.wq is not None else None
-            dx = ops.gemm_nvfp4(dyq.data, dyq.scales, dyq.meta, w4t, wst, w_meta, b_deq=wdt)
+            dx = ops.gemm_nvfp4(None, None, dyq.meta, w4t, wst, w_meta,
+                                a_deq=ops.nvfp4_dequant(dyq), b_deq=wdt)
         if need_dw:
             dw = ops.gemm_nvfp4(dyq.data_t, dyq.scales_t, dyq.meta, x4t, xst, x_meta)
         return dx, dw, None, None
@@ -331,13 +334,15 @@ class GegluGateUpNvfp4Function(_Fp8Function):
     @staticmethod
     def forward(ctx, x, w_gu, wq, intermediate, x_partials=None):
         need_dx, need_dw = _forward_needs(ctx, 2)
-        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw, partials=x_partials)
+        xq = ops.quantize_nvfp4(x, rowwise=True, colwise=need_dw, partials=x_partials,
+                                dequant_rows=True)
         if wq is None:
             wq = quantize_weight_nvfp4(w_gu, transpose=need_dx)
         train = need_dx or need_dw
-        H, GU, h_partials = ops.gemm_geglu_nvfp4(xq.data, xq.scales, xq.meta, wq.data,
-                                                 wq.scales, wq.meta, intermediate,
-                                                 keep_gu=train, b_deq=ops.nvfp4_dequant(wq))
+        H, GU, h_partials = ops.gemm_geglu_nvfp4(None, None, xq.meta, wq.data, wq.scales,
+                                                 wq.meta, intermediate, keep_gu=train,
+                                                 a_deq=ops.nvfp4_dequant(xq),
+                                                 b_deq=ops.nvfp4_dequant(wq))
         ctx.save_for_backward(GU, xq.data_t, xq.scales_t, xq.meta,
                               wq.data_t if need_dx else None,
                               wq.scales_t if need_dx else None, wq.meta)
@@ -350,11 +355,13 @@ class GegluGateUpNvfp4Function(_Fp8Function):
         GU, x4t, xst, x_meta, w4t, wst, w_meta = ctx.saved_tensors
         need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         dGU, dparts = ops.geglu_bwd(dH.contiguous(), GU)
-        dq = ops.quantize_nvfp4(dGU, rowwise=need_dx, colwise=need_dw, partials=dparts)
+        dq = ops.quantize_nvfp4(dGU, rowwise=need_dx, colwise=need_dw, partials=dparts,
+                                dequant_rows=True)
         dx = dw = None
         if need_dx:
             wdt = ops.nvfp4_dequant(ctx.wq, transpose=True) if ctx.wq is not None else None
-            dx = ops.gemm_nvfp4(dq.data, dq.scales, dq.meta, w4t, wst, w_meta, b_deq=wdt)
+            dx = ops.gemm_nvfp4(None, None, dq.meta, w4t, wst, w_meta,
+                                a_deq=ops.nvfp4_dequant(dq), b_deq=wdt)
         if need_dw:
             dw = ops.gemm_nvfp4(dq.data_t, dq.scales_t, dq.meta, x4t, xst, x_meta)
         return dx, dw, None, None, None

@@ -996,10 +996,11 @@ class NvFp4Tensor:
 
 def nvfp4_dequant(q, *, transpose=False):
     """bf16 = e2m1(code) * s of ``q``'s rowwise copy (or with ``transpose`` its columnwise
-    copy), exact and without S_dec; kept on ``q`` when ``q.cache_dequant`` is set."""
-    if not q.cache_dequant:
-        return dequant_nvfp4(q.data_t, q.scales_t) if transpose else dequant_nvfp4(q.data, q.scales)
+    copy), exact and without S_dec; kept on ``q`` when ``q.cache_dequant`` is set, or
+    written by the quantizer itself (``quantize_nvfp4(dequant_rows=True)``)."""
     attr = "_deq_t" if transpose else "_deq"
+    if getattr(q, attr) is None and not q.cache_dequant:
+        return dequant_nvfp4(q.data_t, q.scales_t) if transpose else dequant_nvfp4(q.data, q.scales)
     d = getattr(q, attr)
     if d is None:
         d = dequant_nvfp4(q.data_t, q.scales_t) if transpose else dequant_nvfp4(q.data, q.scales)
@@ -1007,26 +1008,41 @@ def nvfp4_dequant(q, *, transpose=False):
     return d
 
 
-def quantize_nvfp4(x, *, rowwise=True, colwise=False, partials=None):
+def quantize_nvfp4(x, *, rowwise=True, colwise=False, partials=None, dequant_rows=False):
     """NVFP4 quantization of a bf16 tensor (flattened to 2-D): an amax pass and the block
     quantization (rowwise needs cols % 16 == 0, columnwise rows % 16 == 0). ``partials``:
     the amax partials of |x| its producer wrote (int32 / uint32 fp32 bits: ``geglu_bwd``'s,
     the fused RMSNorm's, the gated-GELU GEMM's); the amax pass is then skipped
-    (bf8_quantize_nvfp4_partials_bf16, the same outputs bit for bit)."""
+    (bf8_quantize_nvfp4_partials_bf16, the same outputs bit for bit). ``dequant_rows``: the
+    rowwise copy is kept only as its exact bf16 dequantization (``nvfp4_dequant(q)``; data
+    and scales None), for a tensor whose rowwise copy only feeds the next GEMM
+    (bf8_quantize_nvfp4_dequant_bf16)."""
     _require_gpu(x, partials)
     x = _bf16_2d(x)
     rows, cols = x.shape
     dev = x.device
     meta = new_meta(dev)
     u8 = torch.uint8
-    out = torch.empty((rows, cols // 2), dtype=u8, device=dev) if rowwise else None
-    sc = torch.empty((rows, cols // 16), dtype=u8, device=dev) if rowwise else None
+    codes = rowwise and not dequant_rows
+    out = torch.empty((rows, cols // 2), dtype=u8, device=dev) if codes else None
+    sc = torch.empty((rows, cols // 16), dtype=u8, device=dev) if codes else None
     out_t = torch.empty((cols, rows // 2), dtype=u8, device=dev) if colwise else None
     sc_t = torch.empty((cols, rows // 16), dtype=u8, device=dev) if colwise else None
     L = _lib.lib()
     if partials is not None:
         if partials.dtype != torch.int32 or partials.dim() != 1 or partials.numel() < 1:
             raise ValueError("quantize_nvfp4: partials must be a non-empty 1-D int32 tensor")
+    if dequant_rows and rowwise:
+        deq = torch.empty((rows, cols), dtype=torch.bfloat16, device=dev)
+        if partials is not None:
+            parts, n_parts = partials.contiguous(), partials.numel()
+        else:
+            parts, n_parts = partials_buffer(max(1, int(L.bf8_amax_partials(rows * cols))), dev), 0
+        _lib.check(L.bf8_quantize_nvfp4_dequant_bf16(
+            _ptr(x), rows, cols, _ptr(parts), n_parts, _ptr(deq), _ptr(out_t), _ptr(sc_t),
+            _ptr(meta), _stream(dev)), "bf8_quantize_nvfp4_dequant_bf16")
+        return NvFp4Tensor(None, None, out_t, sc_t, meta, rows, cols, _deq=deq)
+    if partials is not None:
         _lib.check(L.bf8_quantize_nvfp4_partials_bf16(
             _ptr(x), rows, cols, _ptr(partials.contiguous()), partials.numel(), _ptr(out),
             _ptr(sc), _ptr(out_t), _ptr(sc_t), _ptr(meta), _stream(dev)),
@@ -1104,20 +1120,20 @@ def gemm_geglu_bf16(a, b, a_sinv, b_sinv, intermediate, *, keep_gu=False, partia
 
 
 def gemm_geglu_nvfp4(a_data, a_scales, a_meta, b_data, b_scales, b_meta, intermediate, *,
-                     keep_gu=False, b_deq=None):
+                     keep_gu=False, a_deq=None, b_deq=None):
     """The NVFP4 gate/up projection with the gated GELU in its epilogue: both operands
     dequantized exactly to bf16, then :func:`gemm_geglu_bf16` with the two S_dec.
-    ``b_deq``: b's bf16 dequantization when the caller already holds it."""
+    ``a_deq`` / ``b_deq``: an operand's bf16 dequantization when the caller holds it."""
+    a = a_deq if a_deq is not None else dequant_nvfp4(a_data, a_scales)
     b = b_deq if b_deq is not None else dequant_nvfp4(b_data, b_scales)
-    return gemm_geglu_bf16(dequant_nvfp4(a_data, a_scales), b, a_meta[2:3], b_meta[2:3],
-                           intermediate, keep_gu=keep_gu)
+    return gemm_geglu_bf16(a, b, a_meta[2:3], b_meta[2:3], intermediate, keep_gu=keep_gu)
 
 
 def gemm_nvfp4(a_data, a_scales, a_meta, b_data, b_scales, b_meta, *, out_dtype=torch.bfloat16,
-               b_deq=None):
+               a_deq=None, b_deq=None):
     """``C = (A^ @ B^.T) * S_dec(a) * S_dec(b)`` for NVFP4 operands A [M, K], B [N, K]
     (blocks along K): both dequantized exactly to bf16, then the bf16 MFMA GEMM.
-    ``b_deq``: B's bf16 dequantization when the caller already holds it."""
+    ``a_deq`` / ``b_deq``: an operand's bf16 dequantization when the caller holds it."""
+    a = a_deq if a_deq is not None else dequant_nvfp4(a_data, a_scales)
     b = b_deq if b_deq is not None else dequant_nvfp4(b_data, b_scales)
-    return gemm_bf16(dequant_nvfp4(a_data, a_scales), b, a_meta[2:3], b_meta[2:3],
-                     out_dtype=out_dtype)
+    return gemm_bf16(a, b, a_meta[2:3], b_meta[2:3], out_dtype=out_dtype)

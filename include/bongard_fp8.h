@@ -387,6 +387,19 @@ int bf8_quantize_nvfp4_partials_bf16(const void* x, int64_t rows, int64_t cols,
                                      const uint32_t* partials, int64_t n_partials, uint8_t* out,
                                      uint8_t* out_scales, uint8_t* out_t, uint8_t* out_t_scales,
                                      float* meta, void* stream);
+/* The NVFP4 quantizer whose rowwise copy is written as its exact bf16 dequantization deq
+ * [rows, cols] (e2m1(code) * block scale, S_dec left to the GEMM: bf8_dequant_nvfp4's output
+ * bit for bit) in place of the codes and scale bytes, for a tensor whose rowwise copy only
+ * feeds the next GEMM (the forward's input, H, the backward's gradients under
+ * NVFP4BlockScaling: bongard/te_linear.py:17,38; bongard/fused_mlp.py:9,32); out_t /
+ * out_t_scales: the columnwise codes as in bf8_quantize_nvfp4_bf16, or NULL.
+ * n_partials > 0: the amax comes from that many producer partials (as
+ * bf8_quantize_nvfp4_partials_bf16); n_partials == 0: an amax pass writes partials
+ * [bf8_amax_partials(rows * cols)] first. */
+int bf8_quantize_nvfp4_dequant_bf16(const void* x, int64_t rows, int64_t cols,
+                                    uint32_t* partials, int64_t n_partials, void* deq,
+                                    uint8_t* out_t, uint8_t* out_t_scales, float* meta,
+                                    void* stream);
 int bf8_dequant_nvfp4(const uint8_t* q, const uint8_t* scales, int64_t rows, int64_t cols,
                       void* out, void* stream);
 size_t bf8_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K);

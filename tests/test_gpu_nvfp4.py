@@ -57,7 +57,13 @@ def test_quantize_nvfp4_bit_exact(gpu, rows, cols):
         pt, st, _, _, _ = orc.quantize_nvfp4(x, axis=0)
         assert torch.equal(q.data_t.cpu(), pt) and torch.equal(q.scales_t.cpu(), st)
     deq = ops.dequant_nvfp4(q.data, q.scales)
+    # the quantizer writing its rowwise copy as the bf16 dequantization directly
+    qd = ops.quantize_nvfp4(x.to(gpu), rowwise=True, colwise=rows % 16 == 0, dequant_rows=True)
     torch.cuda.synchronize()
+    assert qd.data is None and qd.scales is None
+    assert torch.equal(ops.nvfp4_dequant(qd), deq) and torch.equal(qd.meta, q.meta)
+    if rows % 16 == 0:
+        assert torch.equal(qd.data_t, q.data_t) and torch.equal(qd.scales_t, q.scales_t)
     ref = orc.dequant_nvfp4(p, sb)
     assert torch.equal(deq.cpu().float(), ref)        # e2m1 x e4m3 is exact in bf16
 
@@ -221,6 +227,12 @@ def test_quantize_nvfp4_from_producer_partials(gpu, rows):
                 assert (fa is None) == (fb is None), (what, f)
                 assert fa is None or torch.equal(fa, fb), (what, rw, cw, f)
             assert torch.equal(a.meta, b.meta), (what, rw, cw, "meta")
+            if rw:
+                c = ops.quantize_nvfp4(t, rowwise=True, colwise=cw, partials=parts,
+                                       dequant_rows=True)
+                torch.cuda.synchronize()
+                assert torch.equal(ops.nvfp4_dequant(c), ops.dequant_nvfp4(a.data, a.scales))
+                assert torch.equal(c.meta, a.meta) and (not cw or torch.equal(c.data_t, a.data_t))
     with pytest.raises(ValueError):
         ops.quantize_nvfp4(H, partials=hparts.float())
 
