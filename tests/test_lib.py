@@ -177,3 +177,37 @@ def test_kmajor_workspace_covers_transposed_b(monkeypatch):
         assert L.bf8_gemm_kmajor_workspace(M, N, K) == L.bf8_gemm_workspace(M, N, K)
     monkeypatch.setenv("BONGARD_FP8_GEMM_TILE", "256x256w8")
     assert L.bf8_gemm_kmajor_workspace(512, 2560, 2048) == 0
+
+
+def test_nvfp4_and_bf16_geglu_entries_reject_bad_arguments():
+    """The NVFP4 quantizer variants (producer partials, dequantized rowwise copy) and the
+    bf16 gated-GELU GEMM check their arguments on the host, before any launch."""
+    L = _lib.lib()
+    null = ctypes.c_void_p(0)
+    buf = ctypes.create_string_buffer(1 << 12)
+    ptr = ctypes.c_void_p((ctypes.addressof(buf) + 255) // 256 * 256)
+    odd = ctypes.c_void_p(ptr.value + 8)
+    # producer partials: at least one, and the rowwise blocks need cols % 16 == 0
+    rc = L.bf8_quantize_nvfp4_partials_bf16(ptr, 16, 32, ptr, 0, ptr, ptr, null, null, ptr, null)
+    assert rc == 1 and b"partials is NULL or empty" in L.bf8_last_error()
+    rc = L.bf8_quantize_nvfp4_partials_bf16(ptr, 16, 24, ptr, 4, ptr, ptr, null, null, ptr, null)
+    assert rc == 1 and b"cols % 16" in L.bf8_last_error()
+    rc = L.bf8_quantize_nvfp4_partials_bf16(ptr, 16, 32, ptr, 4, null, null, null, null, ptr,
+                                            null)
+    assert rc == 1 and b"both NULL" in L.bf8_last_error()
+    # dequantized rowwise copy: deq required and 16-byte aligned, columnwise rows % 16
+    rc = L.bf8_quantize_nvfp4_dequant_bf16(ptr, 16, 32, ptr, 0, null, null, null, ptr, null)
+    assert rc == 1 and b"needs deq" in L.bf8_last_error()
+    rc = L.bf8_quantize_nvfp4_dequant_bf16(ptr, 16, 32, ptr, 0, odd, null, null, ptr, null)
+    assert rc == 1 and b"16-byte" in L.bf8_last_error()
+    rc = L.bf8_quantize_nvfp4_dequant_bf16(ptr, 24, 32, ptr, 0, ptr, ptr, ptr, ptr, null)
+    assert rc == 1 and b"rows % 16" in L.bf8_last_error()
+    rc = L.bf8_quantize_nvfp4_dequant_bf16(ptr, 16, 32, ptr, -1, ptr, null, null, ptr, null)
+    assert rc == 1 and b"partials is NULL" in L.bf8_last_error()
+    # bf16 gated-GELU GEMM: K % 8, and I a multiple of 128
+    rc = L.bf8_gemm_geglu_bf16(ptr, 36, ptr, 36, 32, 128, 36, ptr, ptr, ptr, 128, null, ptr,
+                               null)
+    assert rc == 1 and b"bf8_gemm_geglu_bf16" in L.bf8_last_error()
+    rc = L.bf8_gemm_geglu_bf16(ptr, 32, ptr, 32, 32, 100, 32, ptr, ptr, ptr, 128, null, ptr,
+                               null)
+    assert rc == 1 and b"multiple of 128" in L.bf8_last_error()
