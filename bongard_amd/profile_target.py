@@ -225,10 +225,15 @@ def _recipes(dev, iters):
         ops.gemm_mx(hq.data, hq.scales, dq.data, dq.scales)
         ops.quantize_axiswise(a, ops.E4M3, rowwise=True, colwise=True)
         ops.rmsnorm(a, gamma, 1e-6)
-        xn, gn, dn = (ops.quantize_nvfp4(t) for t in (x, w_gu, w_d))
-        H, _, _ = ops.gemm_geglu_nvfp4(xn.data, xn.scales, xn.meta, gn.data, gn.scales, gn.meta, I)
-        hn = ops.quantize_nvfp4(H)
-        ops.gemm_nvfp4(hn.data, hn.scales, hn.meta, dn.data, dn.scales, dn.meta)
+        # NVFP4 as the modules run it: X and H written as their bf16 dequantization, H's
+        # amax from the gate/up epilogue's partials, the weights quantized per iteration
+        xn = ops.quantize_nvfp4(x, dequant_rows=True)
+        gn, dn = ops.quantize_nvfp4(w_gu), ops.quantize_nvfp4(w_d)
+        H, _, hp = ops.gemm_geglu_nvfp4(None, None, xn.meta, gn.data, gn.scales, gn.meta, I,
+                                        a_deq=ops.nvfp4_dequant(xn))
+        hn = ops.quantize_nvfp4(H, partials=hp, dequant_rows=True)
+        ops.gemm_nvfp4(None, None, hn.meta, dn.data, dn.scales, dn.meta,
+                       a_deq=ops.nvfp4_dequant(hn))
     torch.cuda.synchronize()
     print(f"profile_target done: {iters} iterations (recipes), copy {COPY_BYTES} bytes", flush=True)
 
